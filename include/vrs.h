@@ -1,0 +1,246 @@
+/*
+ * vrs.h -- C ABI of the MI355X-native (gfx950) YOLO26 inference hot path.
+ *
+ * Drop-in boundary for spinorml/vision-rs.  The reference builds YOLO26 as a
+ * symbolic graph from layer closures (src/models/yolo/yolo26/mod.rs:207-219
+ * and the files of src/models/yolo/yolo26/blocks), compiles it with teeny-cuda/TritonLowering and replays a CUDA
+ * graph (examples/yolo26.rs:3015-3141); its custom kernels plug in through
+ * teeny-core's CustomOp/RuntimeOp traits (kernels/attention/psa.rs:744-1066,
+ * kernels/detect_decode.rs:96-217).  This library replaces that L2/L1 stack:
+ * each entry point below names the reference interface it stands in for.
+ *
+ * Conventions
+ *  - Plain C: pointers, sizes and small POD descriptors; no torch/HIP types.
+ *    `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *  - Device buffers are caller-owned, except inside a vrs_model, which owns
+ *    its activations and packed parameters (as the reference's LoadedModel
+ *    owns device buffers).
+ *  - Every call returns VRS_OK (0) or a negative VRS_E* code and never aborts;
+ *    vrs_last_error() returns a thread-local message for the last failure.
+ *    All argument checks happen before any HIP call.
+ *  - A vrs_ctx is not re-entrant: use one per host thread (the reference runs
+ *    one stream per captured graph and serialises GPU tests).
+ *  - Activations are NHWC; a vrs_nhwc is a channel slice of an NHWC buffer, so
+ *    channel concat/chunk (blocks/concat.rs, blocks/c3k2.rs:26-41) cost nothing.
+ */
+#ifndef VRS_H
+#define VRS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+#define VRS_OK 0
+#define VRS_EINVAL (-1)       /* null pointer or invalid argument */
+#define VRS_EBADSHAPE (-2)    /* shapes/strides/alignment do not fit the kernel */
+#define VRS_EUNSUPPORTED (-3) /* valid request this build does not implement */
+#define VRS_ENOMODULE (-4)    /* a code object or kernel symbol is missing */
+#define VRS_EHIP (-5)         /* the HIP runtime reported an error */
+#define VRS_ENOTFOUND (-6)    /* unknown parameter name */
+#define VRS_ESTATE (-7)       /* call not valid in the object's current state */
+
+/* ---- enums -------------------------------------------------------------- */
+#define VRS_F32 0
+#define VRS_BF16 1
+
+#define VRS_ACT_NONE 0
+#define VRS_ACT_SILU 1
+
+typedef struct vrs_ctx vrs_ctx;
+typedef struct vrs_model vrs_model;
+
+/* ---- context ------------------------------------------------------------ */
+/* Last error message of the calling thread ("" if none). */
+const char* vrs_last_error(void);
+const char* vrs_version(void);
+
+/* Select `device`, hipModuleLoad every code object under `hsaco_dir` and
+ * resolve the kernels.  Replaces CudaGraphCompiler::compile_model + load
+ * (examples/yolo26.rs:3025-3040): kernels are compiled ahead of time. */
+int vrs_ctx_create(int device, const char* hsaco_dir, vrs_ctx** out);
+int vrs_ctx_destroy(vrs_ctx* ctx);
+
+/* ---- tensors ------------------------------------------------------------ */
+typedef struct {
+  void* data;       /* device address of the buffer (pixel 0, channel 0) */
+  int32_t n, h, w;  /* logical batch, height, width */
+  int32_t c;        /* channels of this view */
+  int32_t pitch;    /* channels per pixel of the underlying buffer */
+  int32_t c_off;    /* first channel of the view inside the buffer */
+} vrs_nhwc;
+
+/* ---- single ops ----------------------------------------------------------- */
+typedef struct {
+  int32_t k;        /* square kernel size; padding = k/2 (blocks/conv.rs:36) */
+  int32_t stride;
+  int32_t groups;   /* 1 = dense (implicit GEMM on MFMA); == channels = depthwise */
+  int32_t act;      /* VRS_ACT_NONE or VRS_ACT_SILU */
+  int32_t dtype;    /* VRS_BF16 or VRS_F32: element type of x, y, res */
+} vrs_conv_desc;
+
+/* Conv2d + folded BN (+SiLU) (+residual).  Replaces teeny-kernels
+ * Conv2dForward / conv2d_bn_silu* + BatchNormForwardInference + SiluForward +
+ * ElemwiseAddForward as the layers blocks/conv.rs:31-99 and
+ * blocks/bottleneck.rs:24-63 record them.
+ *   y = act(scale[co] * conv(x, w)[co] + shift[co]) + res
+ * w: dense -> packed by vrs_pack_conv_weight (dtype elements);
+ *    depthwise -> float32 [C][k*k] (also from vrs_pack_conv_weight).
+ * Dense requires x->c % 8 == 0; res may be NULL (dense only). */
+int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const void* w,
+               const float* scale, const float* shift, const vrs_nhwc* res, const vrs_nhwc* y,
+               void* stream);
+
+/* Host-side weight repack from the reference's OIHW float32 layout
+ * (nn::Conv2d weight) into the device layout vrs_conv2d reads:
+ *   dense:  [Cout][k][k][cin_pad] in `dtype` (cin_pad >= Cin, zero filled)
+ *   depthwise (groups == Cout): float32 [Cout][k*k].
+ * Returns the byte count needed when out == NULL. */
+int64_t vrs_pack_conv_weight(const float* w_oihw, int32_t cout, int32_t cin_per_group, int32_t k,
+                             int32_t groups, int32_t cin_pad, int32_t dtype, void* out);
+
+/* BN fold, examples/yolo26.rs:3437-3495: scale = gamma/sqrt(var+eps),
+ * shift = beta - scale*mean (host arithmetic, done once at load time).
+ * conv_plain layers have no BN: pass scale = 1, shift = bias to vrs_conv2d. */
+int vrs_bn_fold(const float* gamma, const float* beta, const float* mean, const float* var,
+                float eps, int32_t c, float* scale, float* shift);
+
+/* NCHW float32 -> NHWC dtype with zero channel padding to y->c (>= C). */
+int vrs_pack_input(vrs_ctx* ctx, const float* x_nchw, int32_t n, int32_t c, int32_t h, int32_t w,
+                   const vrs_nhwc* y, int32_t dtype, void* stream);
+/* NHWC dtype view -> NCHW float32 [n][x->c][h][w]. */
+int vrs_unpack_output(vrs_ctx* ctx, const vrs_nhwc* x, int32_t dtype, float* y_nchw, void* stream);
+
+/* SPPF pooling cascade (blocks/sppf.rs:43-61 + teeny-core MaxPool2d(5,1,2)):
+ * `buf` is a view of 4*c channels whose first c hold y; writes
+ * p1 = max5(y), p2 = max5(p1), p3 = max5(p2) into the next 3*c channels. */
+int vrs_sppf_pool(vrs_ctx* ctx, const vrs_nhwc* buf, int32_t dtype, void* stream);
+
+/* Nearest 2x upsample into a (concat) view (blocks/upsample.rs:23-35). */
+int vrs_upsample2x(vrs_ctx* ctx, const vrs_nhwc* x, const vrs_nhwc* y, int32_t dtype, void* stream);
+
+/* PSA attention core + fused PE (blocks/c2psa.rs:61-116).  Replaces the
+ * PsaPackQkvOp, FlashAttn2PsaOp (lo and hi), PsaMergeAttnOp, PsaExtractVOp
+ * custom ops (kernels/attention/psa.rs:744-1066), the PE conv_bn and the add:
+ *   out = softmax(q k^T * key_dim^-0.5) v + pe_scale * dw3x3(v) + pe_shift
+ * qkv: view of heads*128 channels (per head q 32 | k 32 | v 64);
+ * out: view of heads*64 channels; pe_w float32 [heads*64][9]. */
+typedef struct {
+  int32_t heads;
+  int32_t key_dim;   /* must be 32 (blocks/c2psa.rs:159) */
+  int32_t head_dim;  /* must be 64 (c / num_heads with num_heads = c/64) */
+  int32_t dtype;
+} vrs_psa_desc;
+int vrs_psa_attention(vrs_ctx* ctx, const vrs_psa_desc* d, const vrs_nhwc* qkv, const float* pe_w,
+                      const float* pe_scale, const float* pe_shift, const vrs_nhwc* out, void* stream);
+
+/* Detect post-process on the raw head outputs (DetectOutput,
+ * blocks/detect.rs:157-172), doing on the GPU what the reference does on the
+ * host (examples/yolo26.rs:1488-1529): decode, sigmoid, argmax (last max
+ * wins), threshold, stable descending sort, keep max_det (<= 1024).
+ * boxes [n][4*A] and scores [n][nc*A] float32 in per-scale blocks.
+ * Outputs per image: count[n]; score/cls/anchor [n][max_det]; xywh [n][max_det][4];
+ * rows past count are score 0, cls -1, anchor -1. */
+typedef struct {
+  int32_t n, nc, img_h, img_w;
+  int32_t nscales;        /* <= 4 */
+  int32_t strides[4];     /* e.g. 8, 16, 32 (loss/anchor.rs:33-35) */
+  float thr;              /* 0.25 viewer, 0.001 eval (examples/yolo26.rs:1507) */
+  int32_t max_det;
+} vrs_detect_desc;
+size_t vrs_detect_workspace_size(const vrs_detect_desc* d);
+int vrs_detect_postprocess(vrs_ctx* ctx, const vrs_detect_desc* d, const float* boxes,
+                           const float* scores, void* workspace, size_t workspace_bytes,
+                           int32_t* count, float* score, int32_t* cls, int32_t* anchor, float* xywh,
+                           void* stream);
+
+/* DetectDecodeOp / detect_decode_forward (kernels/detect_decode.rs:36-217):
+ * grid-unit anchors, [n][4][A] in and out. */
+int vrs_detect_decode_grid(vrs_ctx* ctx, const float* boxes, const float* anchor_x,
+                           const float* anchor_y, const float* strides, int32_t n, int32_t a,
+                           float* out, void* stream);
+
+/* Multi-scale deformable attention (RF-DETR decoder; no reference function).
+ * value [n][S][heads][32] f32, ref [n][q][2], off [n][q][heads][L][P][2],
+ * attw [n][q][heads][L][P] (softmaxed), out [n][q][heads*32]. */
+typedef struct {
+  int32_t n, q, heads, head_dim; /* head_dim must be 32 */
+  int32_t levels, points;        /* levels <= 8 */
+  int32_t level_h[8], level_w[8];
+} vrs_msda_desc;
+int vrs_msda(vrs_ctx* ctx, const vrs_msda_desc* d, const float* value, const float* ref,
+             const float* off, const float* attw, float* out, void* stream);
+
+/* ---- models (layer closures + graph runtime) ------------------------------ */
+#define VRS_BLOCK_CONV 1        /* conv / conv_bn / dwconv / conv_plain (blocks/conv.rs) */
+#define VRS_BLOCK_C3K2 2        /* c3k2 (blocks/c3k2.rs:94-127) */
+#define VRS_BLOCK_C3K2_PSA 3    /* c3k2_psa (blocks/c3k2.rs:134-164) */
+#define VRS_BLOCK_C2PSA 4       /* c2psa (blocks/c2psa.rs:150-179) */
+#define VRS_BLOCK_SPPF 5        /* sppf (blocks/sppf.rs:43-61) */
+#define VRS_BLOCK_PSA_ATTN 6    /* psa_attention (blocks/c2psa.rs:61-116) */
+#define VRS_BLOCK_DETECT_BOX 7  /* one Detect box branch cv2[i] (blocks/detect.rs:117-131) */
+#define VRS_BLOCK_YOLO26 8      /* yolo26() (yolo26/mod.rs:207-219) */
+
+#define VRS_CONV_BN_SILU 0      /* conv() */
+#define VRS_CONV_BN 1           /* conv_bn() */
+#define VRS_CONV_PLAIN 2        /* conv_plain(): bias, no BN, no act */
+
+typedef struct {
+  int32_t kind;
+  int32_t c_in, c_out;
+  int32_t k, s, g;          /* VRS_BLOCK_CONV */
+  int32_t conv_kind;        /* VRS_CONV_* for VRS_BLOCK_CONV */
+  int32_t n;                /* repeats (c3k2, c2psa, c3k2_psa) */
+  int32_t c3k, shortcut;    /* c3k2 flags; sppf shortcut */
+  float e;                  /* expansion (c3k2, c2psa, c3k2_psa) */
+  int32_t heads;            /* psa_attention */
+  int32_t nc;               /* yolo26: classes */
+  int32_t variant;          /* yolo26: 'n','s','m','l','x' */
+  int32_t one2one;          /* yolo26: 1 = one2one_cv2/cv3 head (DetectHead::OneToOne) */
+} vrs_block_desc;
+
+/* Record the block's layers for a fixed batch and input size, mirroring the
+ * reference closures; parameter names are the reference's name_scope paths
+ * (e.g. "model.6.m.0.m.1.cv2.conv.weight").  bn_eps is 1e-3 for the model
+ * (blocks/conv.rs:39); the reference's PyTorch fixtures use 1e-5.
+ * ctx may be NULL for a record-only model (parameter/output introspection
+ * without a GPU); finalize/forward then fail with VRS_ESTATE. */
+int vrs_model_create(vrs_ctx* ctx, const vrs_block_desc* d, int32_t batch, int32_t h, int32_t w,
+                     int32_t dtype, float bn_eps, vrs_model** out);
+int vrs_model_num_params(const vrs_model* m);
+/* name is owned by the model; dims[0..*ndim) (ndim <= 4). */
+int vrs_model_param_info(const vrs_model* m, int32_t i, const char** name, int32_t* dims, int32_t* ndim);
+/* LoadedModel::load_param_f32 analogue: float32 host data, reference layout. */
+int vrs_model_load_param(vrs_model* m, const char* name, const float* data, int64_t numel);
+/* Fold BN, repack/upload weights and allocate activations.  All params must be loaded. */
+int vrs_model_finalize(vrs_model* m);
+int vrs_model_num_outputs(const vrs_model* m);
+/* Output i: float32 element count and (up to 4) dims. */
+int vrs_model_output_info(const vrs_model* m, int32_t i, int64_t* numel, int32_t* dims, int32_t* ndim);
+/* Input: float32 NCHW [batch][c_in][h][w] device buffer.  Outputs: caller
+ * buffers of output_info sizes (yolo26: boxes [batch][4A], scores [batch][nc*A],
+ * the reference's DetectOutput; blocks: NCHW float32). */
+int vrs_model_forward(vrs_model* m, const float* x, float* const* outputs, void* stream);
+/* capture_graph analogue (examples/yolo26.rs:3110): capture one forward with
+ * these buffers into a hipGraph; vrs_model_replay launches it (run_inplace). */
+int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void* stream);
+int vrs_model_replay(vrs_model* m, void* stream);
+/* Number of kernel launches in one forward and their "layer:kernel" names
+ * (valid after the first vrs_model_forward / vrs_model_capture). */
+int vrs_model_num_launches(const vrs_model* m);
+const char* vrs_model_launch_name(const vrs_model* m, int32_t i);
+/* Algorithmic work of launch i: flops (2*M*N*K for convs; QK^T + PV + PE for
+ * attention) and compulsory bytes (inputs + weights + outputs, once each). */
+int vrs_model_launch_work(const vrs_model* m, int32_t i, double* flops, double* bytes);
+/* Run launches [first, first+count) of the prepared forward on `stream`
+ * (per-kernel timing with events between launches). */
+int vrs_model_run_launches(vrs_model* m, int32_t first, int32_t count, void* stream);
+int vrs_model_destroy(vrs_model* m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VRS_H */

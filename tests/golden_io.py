@@ -3,9 +3,12 @@ fixture file names to the reference's parameter names (name_scope paths)."""
 from __future__ import annotations
 
 import os
-import zlib
+import sys
 
 import numpy as np
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "vision-rs_amd"))
+from vrs.synth import seeded_params  # noqa: E402,F401
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -57,35 +60,6 @@ def block_params(family: str, shapes: dict) -> dict:
         conv_block_params(family, pre, name, out)
         out[f"{name}.conv.weight"] = out[f"{name}.conv.weight"].reshape(shapes[name])
     return out
-
-
-def seeded_params(specs, seed=0, bn="identity"):
-    """Deterministic synthetic parameters for (name, shape) specs.
-
-    Conv weights ~ N(0, sqrt(2/fan_in)) (Kaiming-normal), fan_in = shape[1]*kh*kw;
-    biases 0; BN identity (gamma 1, beta 0, mean 0, var 1) unless bn == "random"
-    (then gamma U[0.5,1.5), beta N(0,0.1), mean N(0,0.1), var U[0.5,1.5) -- used
-    by the parity tests to exercise the BN fold).  One PCG64 stream per name,
-    keyed by (seed, crc32(name)), so order does not matter.
-    """
-    P = {}
-    for name, shape in specs:
-        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
-        shape = tuple(int(s) for s in shape)
-        if name.endswith("weight") and len(shape) == 4:
-            fan_in = shape[1] * shape[2] * shape[3]
-            P[name] = (rng.standard_normal(shape) * np.sqrt(2.0 / fan_in)).astype(np.float32)
-        elif name.endswith("bn.weight"):
-            P[name] = (np.ones(shape) if bn == "identity" else rng.uniform(0.5, 1.5, shape)).astype(np.float32)
-        elif name.endswith("bn.bias") or name.endswith("bn.running_mean"):
-            P[name] = (np.zeros(shape) if bn == "identity" else rng.normal(0, 0.1, shape)).astype(np.float32)
-        elif name.endswith("bn.running_var"):
-            P[name] = (np.ones(shape) if bn == "identity" else rng.uniform(0.5, 1.5, shape)).astype(np.float32)
-        elif name.endswith("bias"):
-            P[name] = (np.zeros(shape) if bn == "identity" else rng.normal(0, 0.1, shape)).astype(np.float32)
-        else:
-            raise KeyError(name)
-    return P
 
 
 def max_rel_err(got: np.ndarray, ref: np.ndarray, floor: float) -> float:

@@ -1,0 +1,154 @@
+"""GPU parity of whole blocks and networks (vrs_model_* entry points).
+
+1. The reference's own golden vectors (tests/golden/, BN eps 1e-5) run
+   through the float32 path at the reference tests' tolerance (1e-3 absolute,
+   tests/test_c3k2_variants_cuda.rs:47 etc.).
+2. The bfloat16 path against the oracle on the same bf16-rounded parameters
+   (2e-2 relative with a floor).
+3. YOLO26 end to end: YOLO26n float32 at 640x640 (1e-4
+   relative with a floor) and YOLO26m bfloat16 (config 5 network at batch 2),
+   plus identical detections wherever the score margin exceeds the tolerance.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import yolo26 as Y
+from gpu_util import bf16_round, ctx, dev, rel_err, vrs
+from golden_io import seeded_params
+
+pytestmark = pytest.mark.gpu
+
+
+def run_model(desc, P, x, dtype, eps):
+    import torch
+    m = vrs.Model(ctx(), desc, x.shape[0], x.shape[2], x.shape[3], dtype, eps)
+    names = dict(m.params())
+    missing = [n for n in names if n not in P]
+    assert not missing, missing[:5]
+    m.load(P)
+    outs = m.forward(dev(x))
+    torch.cuda.synchronize()
+    return [o.cpu().numpy() for o in outs], m
+
+
+# ---------------------------------------------------------------- fixtures --
+
+def _c3k2_cases():
+    from test_oracle_golden import C3K2_CASES
+    return [c[0] for c in C3K2_CASES]
+
+
+@pytest.mark.parametrize("sub", _c3k2_cases())
+def test_c3k2_fixture_f32(sub):
+    from test_oracle_golden import c3k2_fixture
+    P, x, exp, (c_in, c_out, c3k, sc, e) = c3k2_fixture(sub)
+    d = vrs.block(vrs.BLOCK_C3K2, c_in, c_out, n=1, c3k=c3k, shortcut=sc, e=e)
+    (y,), _ = run_model(d, P, x, vrs.F32, 1e-5)
+    assert np.max(np.abs(y - exp)) < 1e-3
+
+
+def test_c2psa_fixture_f32():
+    from test_oracle_golden import c2psa_fixture
+    P, x, exp = c2psa_fixture()
+    (y,), _ = run_model(vrs.block(vrs.BLOCK_C2PSA, 256, 256, n=1, e=0.5), P, x, vrs.F32, 1e-5)
+    assert np.max(np.abs(y - exp)) < 1e-3
+
+
+def test_sppf_fixture_f32():
+    from test_oracle_golden import sppf_fixture
+    P, x, exp = sppf_fixture()
+    (y,), _ = run_model(vrs.block(vrs.BLOCK_SPPF, 32, 32, shortcut=False), P, x, vrs.F32, 1e-5)
+    assert np.max(np.abs(y - exp)) < 1e-3
+
+
+def test_detect_box_fixture_f32():
+    from test_oracle_golden import detect_fixture
+    P, x, exp = detect_fixture()
+    (y,), _ = run_model(vrs.block(vrs.BLOCK_DETECT_BOX, 256, 64), P, x, vrs.F32, 1e-5)
+    assert np.max(np.abs(y - exp)) < 1e-3
+
+
+def test_depthwise_fixture_f32():
+    from golden_io import load
+    x = load("conv_grouped/depthwise/x.bin", (2, 128, 4, 4))
+    w = load("conv_grouped/depthwise/conv_w.bin", (128, 1, 3, 3))
+    exp = load("conv_grouped/depthwise/expected_output.bin", (2, 128, 4, 4))
+    P = {"conv.weight": w, "bn.weight": np.ones(128, np.float32), "bn.bias": np.zeros(128, np.float32),
+         "bn.running_mean": np.zeros(128, np.float32), "bn.running_var": np.ones(128, np.float32)}
+    # identity BN with eps 0 reproduces the plain grouped conv of the fixture
+    (y,), _ = run_model(vrs.block(vrs.BLOCK_CONV, 128, 128, k=3, s=1, g=128, conv_kind=vrs.CONV_BN), P, x,
+                        vrs.F32, 0.0)
+    assert np.max(np.abs(y - exp)) < 1e-5
+
+
+# ------------------------------------------------------- bf16 vs the oracle --
+
+def _bf16_params(specs, seed):
+    P = seeded_params(specs, seed, bn="random")
+    return {k: (bf16_round(v) if v.ndim == 4 else v) for k, v in P.items()}
+
+
+BF16_BLOCKS = [
+    ("c3k2_c3k", vrs.block(vrs.BLOCK_C3K2, 128, 128, n=1, c3k=True, shortcut=True, e=0.5), 128, 20,
+     lambda: Y.c3k2(128, 128, 1, True, True, 0.5)),
+    ("c3k2_std", vrs.block(vrs.BLOCK_C3K2, 64, 128, n=2, c3k=False, shortcut=True, e=0.25), 64, 24,
+     lambda: Y.c3k2(64, 128, 2, False, True, 0.25)),
+    ("c2psa", vrs.block(vrs.BLOCK_C2PSA, 256, 256, n=1, e=0.5), 256, 20, lambda: Y.c2psa(256, 256, 1, 0.5)),
+    ("c3k2_psa", vrs.block(vrs.BLOCK_C3K2_PSA, 384, 256, n=1, shortcut=True, e=0.5), 384, 10,
+     lambda: Y.c3k2_psa(384, 256, 1, True, 0.5)),
+    ("sppf", vrs.block(vrs.BLOCK_SPPF, 256, 256, shortcut=True), 256, 20, lambda: Y.sppf(256, 256, True)),
+    ("psa_attn", vrs.block(vrs.BLOCK_PSA_ATTN, 256, 256, heads=4), 256, 20,
+     lambda: Y.psa_attention_block(256, 4, 32)),
+]
+
+
+@pytest.mark.parametrize("name,desc,cin,hw,ref_fn", BF16_BLOCKS, ids=[b[0] for b in BF16_BLOCKS])
+def test_block_bf16_vs_oracle(name, desc, cin, hw, ref_fn):
+    m = vrs.Model(ctx(), desc, 2, hw, hw, vrs.BF16, 1e-3)
+    P = _bf16_params(m.params(), 3)
+    x = bf16_round(np.random.default_rng(4).standard_normal((2, cin, hw, hw)).astype(np.float32))
+    (y,), _ = run_model(desc, P, x, vrs.BF16, 1e-3)
+    ref = ref_fn()(Y.Params(P, eps=1e-3), "", x)
+    err = rel_err(y, ref, 5e-2)
+    assert err < 2e-2 * 4, err  # several bf16 roundings of intermediate activations
+    # the bulk must sit at the kernel tolerance
+    rms_err = float(np.sqrt(np.mean((y - ref) ** 2)) / np.sqrt(np.mean(ref ** 2)))
+    assert rms_err < 2e-2, rms_err
+
+
+# --------------------------------------------------------------- end to end --
+
+def _yolo_params(m, seed=0, bn="identity", bf16=False):
+    P = seeded_params(m.params(), seed, bn=bn)
+    if bf16:
+        P = {k: (bf16_round(v) if v.ndim == 4 else v) for k, v in P.items()}
+    return P
+
+
+def test_yolo26n_f32_640_vs_oracle():
+    """YOLO26n, 1x3x640x640 U[0,1), Kaiming-normal seed 0, identity BN (eps 1e-3)."""
+    x = np.random.default_rng(0).uniform(0, 1, (1, 3, 640, 640)).astype(np.float32)
+    desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="n", one2one=True)
+    m = vrs.Model(ctx(), desc, 1, 640, 640, vrs.F32, 1e-3)
+    P = _yolo_params(m)
+    (boxes, scores), _ = run_model(desc, P, x, vrs.F32, 1e-3)
+    rb, rs = Y.yolo26(80, "n")(Y.Params(P, eps=1e-3), x)
+    assert boxes.shape == (1, 33600) and scores.shape == (1, 672000)
+    eb, es = rel_err(boxes, rb, 1e-2), rel_err(scores, rs, 1e-2)
+    print(f"yolo26n f32 max rel err boxes {eb:.2e} scores {es:.2e}")
+    assert eb < 1e-4 and es < 1e-4
+
+
+def test_yolo26m_bf16_vs_oracle():
+    """YOLO26m (config 5 network) in bfloat16 at batch 2, 320x320, bf16-rounded weights."""
+    x = np.random.default_rng(1).uniform(0, 1, (2, 3, 320, 320)).astype(np.float32)
+    desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="m", one2one=True)
+    m = vrs.Model(ctx(), desc, 2, 320, 320, vrs.BF16, 1e-3)
+    P = _yolo_params(m, bf16=True)
+    (boxes, scores), _ = run_model(desc, P, bf16_round(x), vrs.BF16, 1e-3)
+    rb, rs = Y.yolo26(80, "m")(Y.Params(P, eps=1e-3), bf16_round(x))
+    eb = float(np.sqrt(np.mean((boxes - rb) ** 2)) / np.sqrt(np.mean(rb ** 2)))
+    es = float(np.sqrt(np.mean((scores - rs) ** 2)) / np.sqrt(np.mean(rs ** 2)))
+    print(f"yolo26m bf16 rms rel err boxes {eb:.2e} scores {es:.2e}; max rel {rel_err(boxes, rb, 0.1):.2e}")
+    assert eb < 2e-2 and es < 2e-2

@@ -1,0 +1,231 @@
+"""GPU parity of the single-op C-ABI entry points against the CPU oracle.
+
+Inputs and weights are rounded to the kernel's element type first, so the
+tolerance measures kernel error, not input quantisation.  Tolerances (from the
+north_star): float32 1e-4 relative, bfloat16 2e-2 relative, each with an
+absolute floor of a fraction of the reference's RMS (rel_err in gpu_util).
+Integer/index/bytes outputs (pooling, upsample, top-k indices) are compared
+exactly.
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import bf16_round, ctx, dev, from_nhwc, rel_err, rounder, tdtype, to_nhwc, vrs
+
+pytestmark = pytest.mark.gpu
+
+TOL = {vrs.F32: 1e-4, vrs.BF16: 2e-2}
+FLOOR = {vrs.F32: 1e-3, vrs.BF16: 2e-2}
+DT = [vrs.F32, vrs.BF16]
+
+CONV_CASES = [
+    # n, cin, h, w, cout, k, s, residual, (x pitch, x c_off), (y pitch, y c_off)
+    (2, 64, 20, 20, 128, 3, 1, False, None, None),
+    (2, 32, 17, 13, 48, 3, 2, False, None, None),
+    (1, 8, 32, 32, 16, 3, 2, False, None, None),      # stem-like (padded Cin)
+    (2, 48, 9, 9, 80, 1, 1, False, None, None),       # Cin % 32 != 0, Cout 80
+    (1, 128, 8, 8, 4, 1, 1, False, None, None),       # Detect box conv width
+    (2, 256, 10, 10, 512, 1, 1, True, None, None),    # residual epilogue
+    (2, 64, 12, 12, 64, 3, 1, True, (96, 16), (160, 32)),  # channel-slice views
+    (1, 512, 6, 7, 256, 3, 2, False, None, None),
+]
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv2d(case, dtype):
+    import torch
+    n, cin, h, w, cout, k, s, with_res, xv, yv = case
+    rnd = rounder(dtype)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    x = rnd(rng.standard_normal((n, cin, h, w)).astype(np.float32))
+    wt = rnd((rng.standard_normal((cout, cin, k, k)) * np.sqrt(2.0 / (cin * k * k))).astype(np.float32))
+    scale = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    ho, wo = (h + 2 * (k // 2) - k) // s + 1, (w + 2 * (k // 2) - k) // s + 1
+    res = rnd(rng.standard_normal((n, cout, ho, wo)).astype(np.float32)) if with_res else None
+    ref = oracle.affine_act(oracle.conv2d(x, wt, s, k // 2), scale, shift, 1)
+    if with_res:
+        ref = ref + res
+    xp, xo = xv or (cin, 0)
+    yp, yo = yv or (cout, 0)
+    C = ctx()
+    xt = to_nhwc(x, dtype, xp, xo)
+    yt = torch.full((n, ho, wo, yp), 7.0, dtype=tdtype(dtype), device="cuda")
+    rt = to_nhwc(res, dtype, yp, yo) if with_res else None
+    wp = dev(vrs.pack_conv_weight(wt, 1, cin, dtype))
+    C.conv2d(vrs.nhwc(xt, cin, xo), wp, dev(scale), dev(shift), vrs.nhwc(yt, cout, yo), k, s, 1, vrs.ACT_SILU,
+             vrs.nhwc(rt, cout, yo) if with_res else None, dtype)
+    torch.cuda.synchronize()
+    got = from_nhwc(yt, cout, yo)
+    err = rel_err(got, ref, FLOOR[dtype])
+    assert err < TOL[dtype], err
+    # channels outside the output view are untouched
+    if yp > cout:
+        rest = torch.cat([yt[..., :yo], yt[..., yo + cout:]], -1).float()
+        assert torch.all(rest == 7.0)
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("act", [vrs.ACT_SILU, vrs.ACT_NONE])
+def test_dwconv(dtype, act):
+    import torch
+    rnd = rounder(dtype)
+    rng = np.random.default_rng(7)
+    n, c, h, w = 2, 64, 11, 9
+    x = rnd(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    wt = (rng.standard_normal((c, 1, 3, 3)) * 0.4).astype(np.float32)
+    scale = rng.uniform(0.5, 1.5, c).astype(np.float32)
+    shift = rng.normal(0, 0.2, c).astype(np.float32)
+    ref = oracle.affine_act(oracle.conv2d(x, wt, 1, 1, groups=c), scale, shift, act)
+    C = ctx()
+    xt = to_nhwc(x, dtype, 96, 8)
+    yt = torch.zeros((n, h, w, c), dtype=tdtype(dtype), device="cuda")
+    C.conv2d(vrs.nhwc(xt, c, 8), dev(wt.reshape(c, 9)), dev(scale), dev(shift), vrs.nhwc(yt), 3, 1, c, act, None,
+             dtype)
+    torch.cuda.synchronize()
+    assert rel_err(from_nhwc(yt), ref, FLOOR[dtype]) < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("hw", [(20, 20), (7, 5), (4, 4)])
+def test_sppf_pool_exact(dtype, hw):
+    import torch
+    h, w = hw
+    rnd = rounder(dtype)
+    rng = np.random.default_rng(8)
+    n, c = 2, 32
+    y = rnd(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    p1 = oracle.maxpool2d(y); p2 = oracle.maxpool2d(p1); p3 = oracle.maxpool2d(p2)
+    buf = torch.zeros((n, h, w, 4 * c + 8), dtype=tdtype(dtype), device="cuda")
+    buf[..., 8:8 + c] = to_nhwc(y, dtype)
+    ctx().sppf_pool(vrs.nhwc(buf, 4 * c, 8), dtype)
+    torch.cuda.synchronize()
+    got = from_nhwc(buf, 4 * c, 8)
+    assert np.array_equal(got, np.concatenate([y, p1, p2, p3], 1))
+
+
+@pytest.mark.parametrize("dtype", DT)
+def test_upsample_exact(dtype):
+    import torch
+    rng = np.random.default_rng(9)
+    x = rounder(dtype)(rng.standard_normal((2, 16, 5, 3)).astype(np.float32))
+    xt = to_nhwc(x, dtype)
+    yt = torch.zeros((2, 10, 6, 48), dtype=tdtype(dtype), device="cuda")
+    ctx().upsample2x(vrs.nhwc(xt), vrs.nhwc(yt, 16, 24), dtype)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_nhwc(yt, 16, 24), oracle.upsample_nearest(x))
+    assert torch.all(yt[..., :24] == 0) and torch.all(yt[..., 40:] == 0)
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("shape", [(2, 2, 4, 4), (2, 4, 20, 20), (1, 1, 7, 9)])
+def test_psa_attention(dtype, shape):
+    import torch
+    b, heads, h, w = shape
+    rnd = rounder(dtype)
+    rng = np.random.default_rng(10)
+    qkv = rnd(rng.standard_normal((b, heads * 128, h, w)).astype(np.float32))
+    c = heads * 64
+    pe_w = (rng.standard_normal((c, 1, 3, 3)) * 0.3).astype(np.float32)
+    pe_s = rng.uniform(0.5, 1.5, c).astype(np.float32)
+    pe_t = rng.normal(0, 0.1, c).astype(np.float32)
+    att = oracle.psa_attention(qkv, heads, 32, 64)
+    v = np.ascontiguousarray(qkv.reshape(b, heads, 128, h, w)[:, :, 64:].reshape(b, c, h, w))
+    ref = att + oracle.affine_act(oracle.conv2d(v, pe_w, 1, 1, groups=c), pe_s, pe_t, 0)
+    qt = to_nhwc(qkv, dtype)
+    ot = torch.zeros((b, h, w, c), dtype=tdtype(dtype), device="cuda")
+    ctx().psa_attention(vrs.nhwc(qt), dev(pe_w.reshape(c, 9)), dev(pe_s), dev(pe_t), vrs.nhwc(ot), heads, dtype)
+    torch.cuda.synchronize()
+    err = rel_err(from_nhwc(ot), ref, FLOOR[dtype])
+    assert err < TOL[dtype], err
+
+
+def test_detect_decode_grid_fixture():
+    import torch
+    from golden_io import load
+    B, A = 2, 16
+    boxes = dev(load("detect_decode/raw_boxes.bin", (B, 4, A)))
+    out = torch.empty_like(boxes)
+    ctx().detect_decode_grid(boxes, dev(load("detect_decode/anchor_x.bin")), dev(load("detect_decode/anchor_y.bin")),
+                             dev(load("detect_decode/strides.bin")), out)
+    torch.cuda.synchronize()
+    assert np.max(np.abs(out.cpu().numpy() - load("detect_decode/expected.bin", (B, 4, A)))) < 1e-4
+
+
+def _check_post(got, ref, thr_tol=1e-6):
+    count, sc, cl, an, xy = [g.cpu().numpy() for g in got]
+    rc, rs, rcl, ran, rxy = ref
+    assert np.array_equal(count, rc)
+    for b in range(len(count)):
+        k = count[b]
+        assert np.allclose(sc[b, :k], rs[b, :k], rtol=thr_tol, atol=0)
+        # identical order / class wherever neighbouring scores differ by more than the tolerance
+        same = np.abs(np.diff(rs[b, :k])) > 1e-6 * np.abs(rs[b, 1:k])
+        ok = np.ones(k, bool)
+        ok[1:] &= same
+        ok[:-1] &= same
+        assert np.array_equal(an[b, :k][ok], ran[b, :k][ok])
+        assert np.array_equal(cl[b, :k][ok], rcl[b, :k][ok])
+        assert np.allclose(xy[b, :k][ok], rxy[b, :k][ok], rtol=1e-6, atol=1e-4)
+        assert np.all(an[b, k:] == -1)
+
+
+@pytest.mark.parametrize("img,nc,thr,max_det", [(64, 5, 0.25, 50), (640, 80, 0.25, 300), (640, 80, 0.001, 1024),
+                                                (96, 3, 0.999, 7)])
+def test_detect_postprocess(img, nc, thr, max_det):
+    rng = np.random.default_rng(11)
+    strides = (8, 16, 32)
+    A = sum((img // s) ** 2 for s in strides)
+    B = 3
+    boxes = rng.uniform(0, 5, (B, 4 * A)).astype(np.float32)
+    scores = rng.normal(-2, 2, (B, nc * A)).astype(np.float32)
+    scores[0, : nc * 10] = 4.0  # exact ties in classes and across anchors
+    got = ctx().detect_postprocess(dev(boxes), dev(scores), nc, img, img, strides, thr, max_det)
+    import torch
+    torch.cuda.synchronize()
+    ref = oracle.detect_postprocess(boxes, scores, nc, img, img, strides, thr, max_det)
+    _check_post(got, ref)
+
+
+def test_detect_postprocess_empty():
+    rng = np.random.default_rng(12)
+    A = 21
+    boxes = rng.uniform(0, 5, (2, 4 * A)).astype(np.float32)
+    scores = np.full((2, 3 * A), -30.0, np.float32)
+    count, sc, cl, an, xy = ctx().detect_postprocess(dev(boxes), dev(scores), 3, 32, 32, (8, 16, 32), 0.25, 10)
+    assert count.cpu().numpy().tolist() == [0, 0]
+    assert np.all(an.cpu().numpy() == -1)
+
+
+@pytest.mark.parametrize("cfg", [
+    (2, 30, 4, [(16, 16), (8, 8), (4, 4), (2, 2)], 4),
+    (1, 7, 8, [(13, 11), (7, 6)], 3),
+])
+def test_msda(cfg):
+    import torch
+    from test_oracle_golden import msda_inputs
+    B, Q, heads, shapes, P = cfg
+    value, ref, off, attw = msda_inputs(B, Q, heads, 32, shapes, P)
+    exp = oracle.msda(value, shapes, ref, off, attw)
+    out = torch.empty((B, Q, heads * 32), dtype=torch.float32, device="cuda")
+    ctx().msda(dev(value), shapes, dev(ref), dev(off), dev(attw), out)
+    torch.cuda.synchronize()
+    assert rel_err(out.cpu().numpy(), exp, 1e-3) < 1e-4
+
+
+def test_errors_are_reported_not_fatal():
+    import torch
+    C = ctx()
+    x = torch.zeros((1, 4, 4, 12), dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros((1, 4, 4, 16), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(16 * 12, dtype=torch.bfloat16, device="cuda")
+    s = torch.ones(16, device="cuda")
+    with pytest.raises(vrs.VrsError) as e:  # Cin 12 is not a multiple of 8
+        C.conv2d(vrs.nhwc(x), w, s, s, vrs.nhwc(y), 1, 1, 1, vrs.ACT_SILU, None, vrs.BF16)
+    assert e.value.code == -2
+    with pytest.raises(vrs.VrsError):  # groups other than 1 / depthwise
+        C.conv2d(vrs.nhwc(y), w, s, s, vrs.nhwc(y), 3, 1, 2, vrs.ACT_SILU, None, vrs.BF16)

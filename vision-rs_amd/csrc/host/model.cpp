@@ -1,0 +1,729 @@
+// Model runtime: the reference's layer closures (src/models/yolo/yolo26/) restated as
+// destination-passing builders over planned NHWC buffers, plus the
+// LoadedModel roles (parameter upload, forward, graph capture and replay).
+//
+// The reference records a symbolic graph (ChannelCat / ChannelChunk / Add /
+// UpsampleNearest2d nodes, blocks/c3k2.rs:26-41, blocks/concat.rs:24-38) and
+// lowers every node to a kernel.  Here each producer writes straight into the
+// channel slice of the buffer its consumer reads, so concat and chunk are
+// free, residual adds run in the producing conv's epilogue, and only convs,
+// the SPPF pool, upsample and PSA attention launch kernels.
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <string>
+
+#include "vrs_internal.h"
+
+using namespace vrs;
+
+namespace {
+
+enum ConvKind { CK_BN_SILU = 0, CK_BN = 1, CK_PLAIN = 2 };
+
+struct V {  // channel slice of a model buffer
+  int buf = -1, c_off = 0, c = 0;
+};
+
+struct Buf {
+  int h = 0, w = 0, pitch = 0;
+  void* dev = nullptr;
+};
+
+struct Param {
+  std::string name;
+  std::vector<int32_t> dims;
+  std::vector<float> host;
+  bool loaded = false;
+};
+
+struct ConvStep {
+  std::string pre;
+  int kind = CK_BN_SILU;
+  bool dw = false;
+  int k = 1, s = 1, cin = 0, cout = 0;
+  V x, y;
+  bool has_res = false;
+  V res;
+  // flat float32 output (detect head / block outputs): output index + layout
+  int out_idx = -1;
+  int64_t out_off = 0, sb = 0, sp = 0, sc = 0;
+  // device parameters (finalize)
+  void* w = nullptr;
+  float* scale = nullptr;
+  float* shift = nullptr;
+};
+
+struct Step {
+  enum Type { PACK, CONV, POOL, UP, ATTN, UNPACK } type;
+  int conv = -1;      // CONV / ATTN (the PE conv's parameters)
+  V a, b;             // PACK: b = dest; POOL: a; UP: a -> b; ATTN: a = qkv, b = out; UNPACK: a
+  int heads = 0;
+  int out_idx = -1;   // UNPACK
+};
+
+}  // namespace
+
+struct vrs_model {
+  vrs_ctx* ctx = nullptr;
+  vrs_block_desc desc{};
+  int batch = 0, in_c = 0, in_h = 0, in_w = 0, dtype = VRS_BF16;
+  float eps = 1e-3f;
+  std::vector<Buf> bufs;
+  std::vector<Param> params;
+  std::unordered_map<std::string, int> pidx;
+  std::vector<ConvStep> convs;
+  std::vector<Step> steps;
+  std::vector<std::vector<int32_t>> out_dims;
+  bool finalized = false;
+  std::vector<void*> allocs;
+  // prepared launches for the last (x, outputs) pointers
+  std::vector<Launch> launches;
+  std::vector<std::string> labels;
+  const float* prep_x = nullptr;
+  std::vector<float*> prep_outs;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+std::string J(const std::string& pre, const std::string& n) { return pre.empty() ? n : pre + "." + n; }
+
+class Builder {
+ public:
+  explicit Builder(vrs_model* m) : m_(m) {}
+
+  V alloc(int h, int w, int c) {
+    Buf b;
+    b.h = h; b.w = w; b.pitch = c;
+    m_->bufs.push_back(b);
+    return V{(int)m_->bufs.size() - 1, 0, c};
+  }
+  static V slice(V v, int off, int c) { return V{v.buf, v.c_off + off, c}; }
+  int H(V v) const { return m_->bufs[v.buf].h; }
+  int W(V v) const { return m_->bufs[v.buf].w; }
+
+  void add_param(const std::string& name, std::vector<int32_t> dims) {
+    if (m_->pidx.count(name)) return;
+    Param p;
+    p.name = name;
+    p.dims = std::move(dims);
+    m_->pidx[name] = (int)m_->params.size();
+    m_->params.push_back(std::move(p));
+  }
+
+  int conv_common(const std::string& pre, V x, int cout, int k, int s, int kind, bool dw) {
+    ConvStep c;
+    c.pre = pre; c.kind = kind; c.dw = dw; c.k = k; c.s = s; c.cin = x.c; c.cout = cout; c.x = x;
+    const int cin_g = dw ? 1 : real_cin(x);
+    if (kind == CK_PLAIN) {
+      add_param(J(pre, "weight"), {cout, cin_g, k, k});
+      add_param(J(pre, "bias"), {cout});
+    } else {
+      add_param(J(pre, "conv.weight"), {cout, cin_g, k, k});
+      for (const char* n : {"bn.weight", "bn.bias", "bn.running_mean", "bn.running_var"}) add_param(J(pre, n), {cout});
+    }
+    m_->convs.push_back(c);
+    return (int)m_->convs.size() - 1;
+  }
+
+  // conv() / conv_bn(): blocks/conv.rs:31-69 (optional residual = elem_add of the caller)
+  void conv(const std::string& pre, V x, V y, int k, int s, int kind, const V* res = nullptr) {
+    const int i = conv_common(pre, x, y.c, k, s, kind, false);
+    m_->convs[i].y = y;
+    if (res) { m_->convs[i].has_res = true; m_->convs[i].res = *res; }
+    push_conv(i);
+  }
+  // dwconv() (SiLU) and conv_bn(g = c) (no act): blocks/conv.rs:53-85
+  void dwconv(const std::string& pre, V x, V y, int k, int s, int kind) {
+    const int i = conv_common(pre, x, y.c, k, s, kind, true);
+    m_->convs[i].y = y;
+    push_conv(i);
+  }
+  // conv() or conv_plain() writing float32 into a flat output (out_idx)
+  void conv_flat(const std::string& pre, V x, int cout, int k, int kind, int out_idx, int64_t off, int64_t sb,
+                 int64_t sp, int64_t sc) {
+    const int i = conv_common(pre, x, cout, k, 1, kind, false);
+    ConvStep& c = m_->convs[i];
+    c.out_idx = out_idx; c.out_off = off; c.sb = sb; c.sp = sp; c.sc = sc;
+    push_conv(i);
+  }
+
+  // bottleneck.rs:37-49 (c -> c/2 -> c) and :51-63 (c -> c -> c), 3x3 convs
+  void bottleneck(const std::string& pre, V x, V y, int c, bool shortcut, bool inner_half) {
+    const int ci = inner_half ? (int)(c * 0.5f) : c;
+    V t = alloc(H(x), W(x), ci);
+    conv(J(pre, "cv1"), x, t, 3, 1, CK_BN_SILU);
+    conv(J(pre, "cv2"), t, y, 3, 1, CK_BN_SILU, shortcut ? &x : nullptr);
+  }
+
+  // c3k2.rs:46-61: cv1 -> m.0 -> m.1, cv2, cv3(cat[m.1 out, cv2 out])
+  void c3k_inner(const std::string& pre, V x, V y, int c, bool shortcut) {
+    const int ch = (int)(c * 0.5f);
+    V cat = alloc(H(x), W(x), 2 * ch);
+    V a = alloc(H(x), W(x), ch), b = alloc(H(x), W(x), ch);
+    conv(J(pre, "cv1"), x, a, 1, 1, CK_BN_SILU);
+    bottleneck(J(pre, "m.0"), a, b, ch, shortcut, false);
+    bottleneck(J(pre, "m.1"), b, slice(cat, 0, ch), ch, shortcut, false);
+    conv(J(pre, "cv2"), x, slice(cat, ch, ch), 1, 1, CK_BN_SILU);
+    conv(J(pre, "cv3"), cat, y, 1, 1, CK_BN_SILU);
+  }
+
+  // c3k2.rs:94-127 (C2f topology: cv1 into the cat buffer, blocks append slices)
+  void c3k2(const std::string& pre, V x, V y, int c_out, int n, bool c3k, bool shortcut, float e) {
+    const int c = (int)(c_out * e);
+    V cat = alloc(H(x), W(x), (2 + n) * c);
+    conv(J(pre, "cv1"), x, slice(cat, 0, 2 * c), 1, 1, CK_BN_SILU);
+    V last = slice(cat, c, c);
+    for (int i = 0; i < n; ++i) {
+      V out = slice(cat, (2 + i) * c, c);
+      const std::string p = J(pre, "m." + std::to_string(i));
+      if (c3k) c3k_inner(p, last, out, c, shortcut);
+      else bottleneck(p, last, out, c, shortcut, true);
+      last = out;
+    }
+    conv(J(pre, "cv2"), cat, y, 1, 1, CK_BN_SILU);
+  }
+
+  // c2psa.rs:61-116: qkv conv_bn -> fused attention (+PE) -> proj conv_bn (+res)
+  void psa_attention(const std::string& pre, V x, V y, int c, int heads, const V* res) {
+    V qkv = alloc(H(x), W(x), heads * 128);
+    conv(J(pre, "qkv"), x, qkv, 1, 1, CK_BN);
+    V att = alloc(H(x), W(x), c);
+    // PE dw conv_bn parameters live in a ConvStep that launches nothing itself
+    const int pe = conv_common(J(pre, "pe"), slice(qkv, 0, c), c, 3, 1, CK_BN, true);
+    Step st;
+    st.type = Step::ATTN; st.conv = pe; st.a = qkv; st.b = att; st.heads = heads;
+    m_->steps.push_back(st);
+    conv(J(pre, "proj"), att, y, 1, 1, CK_BN, res);
+  }
+
+  // c2psa.rs:123-137: b += attn(b); b += ffn.1(ffn.0(b)), in place
+  void psa_block(const std::string& pre, V b, int c, int heads) {
+    psa_attention(J(pre, "attn"), b, b, c, heads, &b);
+    V f = alloc(H(b), W(b), 2 * c);
+    conv(J(pre, "ffn.0"), b, f, 1, 1, CK_BN_SILU);
+    conv(J(pre, "ffn.1"), f, b, 1, 1, CK_BN, &b);
+  }
+
+  // c2psa.rs:150-179
+  void c2psa(const std::string& pre, V x, V y, int c_out, int n, float e) {
+    const int c = (int)(c_out * e);
+    V cat = alloc(H(x), W(x), 2 * c);
+    conv(J(pre, "cv1"), x, cat, 1, 1, CK_BN_SILU);
+    V b = slice(cat, c, c);
+    for (int i = 0; i < n; ++i) psa_block(J(pre, "m." + std::to_string(i)), b, c, c / 64);
+    conv(J(pre, "cv2"), cat, y, 1, 1, CK_BN_SILU);
+  }
+
+  // c3k2.rs:134-164 with bottleneck_psa_seq (:67-79) as the inner block
+  void c3k2_psa(const std::string& pre, V x, V y, int c_out, int n, bool shortcut, float e) {
+    const int c = (int)(c_out * e);
+    V cat = alloc(H(x), W(x), (2 + n) * c);
+    conv(J(pre, "cv1"), x, slice(cat, 0, 2 * c), 1, 1, CK_BN_SILU);
+    V last = slice(cat, c, c);
+    for (int i = 0; i < n; ++i) {
+      V out = slice(cat, (2 + i) * c, c);
+      const std::string p = J(pre, "m." + std::to_string(i));
+      bottleneck(J(p, "0"), last, out, c, shortcut, true);
+      psa_block(J(p, "1"), out, c, c / 64);
+      last = out;
+    }
+    conv(J(pre, "cv2"), cat, y, 1, 1, CK_BN_SILU);
+  }
+
+  // sppf.rs:43-61: cv1 into slice 0 of a 4c buffer, pool cascade fills the rest
+  void sppf(const std::string& pre, V x, V y, int c_in, int c_out, bool shortcut) {
+    const int c = c_in / 2;
+    V cat = alloc(H(x), W(x), 4 * c);
+    conv(J(pre, "cv1"), x, slice(cat, 0, c), 1, 1, CK_BN);
+    Step st;
+    st.type = Step::POOL; st.a = cat;
+    m_->steps.push_back(st);
+    const bool add = shortcut && c_in == c_out;
+    conv(J(pre, "cv2"), cat, y, 1, 1, CK_BN_SILU, add ? &x : nullptr);
+  }
+
+  void upsample(V x, V y) {
+    Step st;
+    st.type = Step::UP; st.a = x; st.b = y;
+    m_->steps.push_back(st);
+  }
+
+  // detect.rs:108-172; outputs 0 (boxes) and 1 (scores) in channel_cat_flat layout
+  void detect(const std::string& pre, const V feats[3], const int chs[3], int nc, bool one2one) {
+    const int c2 = std::max(16, std::max(chs[0] / 4, 4));
+    const int c3 = std::max(chs[0], std::min(nc, 100));
+    const std::string p2 = one2one ? "one2one_cv2" : "cv2", p3 = one2one ? "one2one_cv3" : "cv3";
+    int64_t A = 0;
+    for (int i = 0; i < 3; ++i) A += (int64_t)H(feats[i]) * W(feats[i]);
+    int64_t base = 0;
+    for (int i = 0; i < 3; ++i) {
+      const V x = feats[i];
+      const int64_t as = (int64_t)H(x) * W(x);
+      const std::string q = J(pre, p2 + "." + std::to_string(i));
+      V t1 = alloc(H(x), W(x), c2), t2 = alloc(H(x), W(x), c2);
+      conv(J(q, "0"), x, t1, 3, 1, CK_BN_SILU);
+      conv(J(q, "1"), t1, t2, 3, 1, CK_BN_SILU);
+      conv_flat(J(q, "2"), t2, 4, 1, CK_PLAIN, 0, 4 * base, 4 * A, 1, as);
+      base += as;
+    }
+    base = 0;
+    for (int i = 0; i < 3; ++i) {
+      const V x = feats[i];
+      const int64_t as = (int64_t)H(x) * W(x);
+      const std::string q = J(pre, p3 + "." + std::to_string(i));
+      V d1 = alloc(H(x), W(x), chs[i]), p1 = alloc(H(x), W(x), c3);
+      V d2 = alloc(H(x), W(x), c3), pw = alloc(H(x), W(x), c3);
+      dwconv(J(q, "0.0"), x, d1, 3, 1, CK_BN_SILU);
+      conv(J(q, "0.1"), d1, p1, 1, 1, CK_BN_SILU);
+      dwconv(J(q, "1.0"), p1, d2, 3, 1, CK_BN_SILU);
+      conv(J(q, "1.1"), d2, pw, 1, 1, CK_BN_SILU);
+      conv_flat(J(q, "2"), pw, nc, 1, CK_PLAIN, 1, (int64_t)nc * base, (int64_t)nc * A, 1, as);
+      base += as;
+    }
+    m_->out_dims = {{m_->batch, (int32_t)(4 * A)}, {m_->batch, (int32_t)(nc * A)}};
+  }
+
+  V input(int c_real) {
+    V in = alloc(m_->in_h, m_->in_w, (c_real + 7) / 8 * 8);
+    real_c_[in.buf] = c_real;
+    Step st;
+    st.type = Step::PACK; st.b = in;
+    m_->steps.push_back(st);
+    return in;
+  }
+
+  void output(V y) {
+    Step st;
+    st.type = Step::UNPACK; st.a = y; st.out_idx = (int)m_->out_dims.size();
+    m_->steps.push_back(st);
+    m_->out_dims.push_back({m_->batch, y.c, H(y), W(y)});
+  }
+
+  int real_cin(V x) const {
+    auto it = real_c_.find(x.buf);
+    return (it != real_c_.end() && x.c_off == 0 && x.c == m_->bufs[x.buf].pitch) ? it->second : x.c;
+  }
+
+ private:
+  void push_conv(int i) {
+    Step st;
+    st.type = Step::CONV; st.conv = i;
+    m_->steps.push_back(st);
+  }
+  vrs_model* m_;
+  std::unordered_map<int, int> real_c_;  // input buffer -> unpadded channels
+};
+
+int round_half_away(float v) { return (int)std::floor(v + 0.5f); }
+
+int build(vrs_model* m) {
+  Builder b(m);
+  const vrs_block_desc& d = m->desc;
+  switch (d.kind) {
+    case VRS_BLOCK_CONV: {
+      V x = b.input(d.c_in);
+      const bool dw = d.g > 1;
+      if (dw && (d.g != d.c_in || d.c_in != d.c_out)) return fail(VRS_EUNSUPPORTED, "conv block: groups 1 or depthwise");
+      if (d.conv_kind == VRS_CONV_PLAIN) {
+        if (dw) return fail(VRS_EUNSUPPORTED, "conv_plain is dense");
+        const int ho = (m->in_h + 2 * (d.k / 2) - d.k) / d.s + 1, wo = (m->in_w + 2 * (d.k / 2) - d.k) / d.s + 1;
+        if (d.s != 1) return fail(VRS_EUNSUPPORTED, "conv_plain block: stride 1 only");
+        const int64_t hw = (int64_t)ho * wo;
+        b.conv_flat("", x, d.c_out, d.k, CK_PLAIN, 0, 0, d.c_out * hw, 1, hw);
+        m->out_dims = {{m->batch, d.c_out, ho, wo}};
+        return VRS_OK;
+      }
+      const int kind = d.conv_kind == VRS_CONV_BN ? CK_BN : CK_BN_SILU;
+      const int ho = (m->in_h + 2 * (d.k / 2) - d.k) / d.s + 1, wo = (m->in_w + 2 * (d.k / 2) - d.k) / d.s + 1;
+      V y = b.alloc(ho, wo, d.c_out);
+      if (dw) b.dwconv("", x, y, d.k, d.s, kind);
+      else b.conv("", x, y, d.k, d.s, kind);
+      b.output(y);
+      return VRS_OK;
+    }
+    case VRS_BLOCK_C3K2: {
+      V x = b.input(d.c_in);
+      V y = b.alloc(m->in_h, m->in_w, d.c_out);
+      b.c3k2("", x, y, d.c_out, d.n, d.c3k, d.shortcut, d.e);
+      b.output(y);
+      return VRS_OK;
+    }
+    case VRS_BLOCK_C3K2_PSA: {
+      V x = b.input(d.c_in);
+      V y = b.alloc(m->in_h, m->in_w, d.c_out);
+      b.c3k2_psa("", x, y, d.c_out, d.n, d.shortcut, d.e);
+      b.output(y);
+      return VRS_OK;
+    }
+    case VRS_BLOCK_C2PSA: {
+      if (d.c_in != d.c_out) return fail(VRS_EINVAL, "C2PSA requires c_in == c_out");
+      V x = b.input(d.c_in);
+      V y = b.alloc(m->in_h, m->in_w, d.c_out);
+      b.c2psa("", x, y, d.c_out, d.n, d.e);
+      b.output(y);
+      return VRS_OK;
+    }
+    case VRS_BLOCK_SPPF: {
+      V x = b.input(d.c_in);
+      V y = b.alloc(m->in_h, m->in_w, d.c_out);
+      b.sppf("", x, y, d.c_in, d.c_out, d.shortcut);
+      b.output(y);
+      return VRS_OK;
+    }
+    case VRS_BLOCK_PSA_ATTN: {
+      if (d.heads < 1 || d.c_in != d.heads * 64) return fail(VRS_EINVAL, "psa_attention: c must be heads*64");
+      V x = b.input(d.c_in);
+      V y = b.alloc(m->in_h, m->in_w, d.c_in);
+      b.psa_attention("", x, y, d.c_in, d.heads, nullptr);
+      b.output(y);
+      return VRS_OK;
+    }
+    case VRS_BLOCK_DETECT_BOX: {
+      const int c2 = d.c_out;
+      V x = b.input(d.c_in);
+      V t1 = b.alloc(m->in_h, m->in_w, c2), t2 = b.alloc(m->in_h, m->in_w, c2);
+      b.conv("0", x, t1, 3, 1, CK_BN_SILU);
+      b.conv("1", t1, t2, 3, 1, CK_BN_SILU);
+      const int64_t hw = (int64_t)m->in_h * m->in_w;
+      b.conv_flat("2", t2, 4, 1, CK_PLAIN, 0, 0, 4 * hw, 1, hw);
+      m->out_dims = {{m->batch, 4, m->in_h, m->in_w}};
+      return VRS_OK;
+    }
+    case VRS_BLOCK_YOLO26: {
+      float dep, wid;
+      int mc;
+      switch (d.variant) {  // yolo26/mod.rs:70-100
+        case 'n': dep = 0.5f; wid = 0.25f; mc = 1024; break;
+        case 's': dep = 0.5f; wid = 0.50f; mc = 1024; break;
+        case 'm': dep = 0.5f; wid = 1.00f; mc = 512; break;
+        case 'l': dep = 1.0f; wid = 1.00f; mc = 512; break;
+        case 'x': dep = 1.0f; wid = 1.50f; mc = 512; break;
+        default: return fail(VRS_EINVAL, "yolo26: unknown variant '%c'", (char)d.variant);
+      }
+      if (m->in_h % 32 || m->in_w % 32) return fail(VRS_EBADSHAPE, "yolo26: input must be divisible by 32");
+      if (d.c_in != 3) return fail(VRS_EINVAL, "yolo26: 3 input channels");
+      auto ch = [&](int base) { return round_half_away((float)std::min(base, mc) * wid); };  // mod.rs:106-108
+      const int c0 = ch(64), c1 = ch(128), c2 = ch(256), c3 = ch(512), c4 = ch(1024);
+      const int n = round_half_away(std::max(2 * dep, 1.0f));  // rep(2, d), mod.rs:111-117
+      const int H = m->in_h, W = m->in_w;
+      V in = b.input(3);
+      V x0 = b.alloc(H / 2, W / 2, c0);
+      b.conv("model.0", in, x0, 3, 2, CK_BN_SILU);
+      V x1 = b.alloc(H / 4, W / 4, c1);
+      b.conv("model.1", x0, x1, 3, 2, CK_BN_SILU);
+      V x2 = b.alloc(H / 4, W / 4, c2);
+      b.c3k2("model.2", x1, x2, c2, n, false, true, 0.25f);
+      V x3 = b.alloc(H / 8, W / 8, c2);
+      b.conv("model.3", x2, x3, 3, 2, CK_BN_SILU);
+      V cat16 = b.alloc(H / 8, W / 8, c3 + c3);       // [up(nk4), p3]
+      V p3 = Builder::slice(cat16, c3, c3);
+      b.c3k2("model.4", x3, p3, c3, n, false, true, 0.25f);
+      V x5 = b.alloc(H / 16, W / 16, c3);
+      b.conv("model.5", p3, x5, 3, 2, CK_BN_SILU);
+      V cat13 = b.alloc(H / 16, W / 16, c4 + c3);     // [up(p5), p4]
+      V p4 = Builder::slice(cat13, c4, c3);
+      b.c3k2("model.6", x5, p4, c3, n, true, true, 0.5f);
+      V x7 = b.alloc(H / 32, W / 32, c4);
+      b.conv("model.7", p4, x7, 3, 2, CK_BN_SILU);
+      V x8 = b.alloc(H / 32, W / 32, c4);
+      b.c3k2("model.8", x7, x8, c4, n, true, true, 0.5f);
+      V x9 = b.alloc(H / 32, W / 32, c4);
+      b.sppf("model.9", x8, x9, c4, c4, true);
+      V cat22 = b.alloc(H / 32, W / 32, c3 + c4);     // [l20(p4d), p5]
+      V p5 = Builder::slice(cat22, c3, c4);
+      b.c2psa("model.10", x9, p5, c4, n, 0.5f);
+      b.upsample(p5, Builder::slice(cat13, 0, c4));
+      V cat19 = b.alloc(H / 16, W / 16, c2 + c3);     // [l17(p3d), nk4]
+      V nk4 = Builder::slice(cat19, c2, c3);
+      b.c3k2("model.13", cat13, nk4, c3, n, true, true, 0.5f);
+      b.upsample(nk4, Builder::slice(cat16, 0, c3));
+      V p3d = b.alloc(H / 8, W / 8, c2);
+      b.c3k2("model.16", cat16, p3d, c2, n, true, true, 0.5f);
+      b.conv("model.17", p3d, Builder::slice(cat19, 0, c2), 3, 2, CK_BN_SILU);
+      V p4d = b.alloc(H / 16, W / 16, c3);
+      b.c3k2("model.19", cat19, p4d, c3, n, true, true, 0.5f);
+      b.conv("model.20", p4d, Builder::slice(cat22, 0, c3), 3, 2, CK_BN_SILU);
+      V p5d = b.alloc(H / 32, W / 32, c4);
+      b.c3k2_psa("model.22", cat22, p5d, c4, 1, true, 0.5f);
+      const V feats[3] = {p3d, p4d, p5d};
+      const int chs[3] = {c2, c3, c4};
+      b.detect("model.23", feats, chs, d.nc, d.one2one != 0);
+      return VRS_OK;
+    }
+    default:
+      return fail(VRS_EINVAL, "unknown block kind %d", d.kind);
+  }
+}
+
+vrs_nhwc view_of(const vrs_model* m, V v) {
+  const Buf& b = m->bufs[v.buf];
+  vrs_nhwc r;
+  r.data = b.dev; r.n = m->batch; r.h = b.h; r.w = b.w; r.c = v.c; r.pitch = b.pitch; r.c_off = v.c_off;
+  return r;
+}
+
+int prepare(vrs_model* m, const float* x, float* const* outs) {
+  const int nout = (int)m->out_dims.size();
+  std::vector<float*> o(outs, outs + nout);
+  if (!m->launches.empty() && m->prep_x == x && m->prep_outs == o) return VRS_OK;
+  std::vector<Launch> ls;
+  std::vector<std::string> labels;
+  int rc = VRS_OK;
+  for (const Step& st : m->steps) {
+    const size_t before = ls.size();
+    std::string label;
+    switch (st.type) {
+      case Step::PACK:
+        rc = prep_pack_input(m->ctx, x, m->batch, m->in_c, m->in_h, m->in_w, view_of(m, st.b), m->dtype, ls);
+        label = "input";
+        break;
+      case Step::CONV: {
+        const ConvStep& c = m->convs[st.conv];
+        ConvSpec cs;
+        cs.k = c.k; cs.stride = c.s; cs.dtype = m->dtype; cs.depthwise = c.dw;
+        cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
+        cs.cin_real = c.cin == m->bufs[c.x.buf].pitch && c.x.buf == 0 ? m->in_c : 0;
+        label = c.pre.empty() ? "conv" : c.pre;
+        if (c.out_idx >= 0) {
+          rc = prep_conv_flat(m->ctx, cs, view_of(m, c.x), c.w, c.scale, c.shift, c.cout, o[c.out_idx] + c.out_off,
+                              c.sb, c.sp, c.sc, ls);
+        } else {
+          vrs_nhwc r;
+          if (c.has_res) r = view_of(m, c.res);
+          rc = prep_conv(m->ctx, cs, view_of(m, c.x), c.w, c.scale, c.shift, c.has_res ? &r : nullptr,
+                         view_of(m, c.y), ls);
+        }
+        break;
+      }
+      case Step::POOL:
+        rc = prep_pool(m->ctx, view_of(m, st.a), m->dtype, ls);
+        label = "sppf.pool";
+        break;
+      case Step::UP:
+        rc = prep_up(m->ctx, view_of(m, st.a), view_of(m, st.b), m->dtype, ls);
+        label = "upsample";
+        break;
+      case Step::ATTN: {
+        const ConvStep& pe = m->convs[st.conv];
+        rc = prep_attn(m->ctx, st.heads, m->dtype, view_of(m, st.a), static_cast<const float*>(pe.w), pe.scale,
+                       pe.shift, view_of(m, st.b), ls);
+        label = pe.pre.substr(0, pe.pre.size() >= 3 ? pe.pre.size() - 3 : 0) + ".core";
+        break;
+      }
+      case Step::UNPACK:
+        rc = prep_unpack(m->ctx, view_of(m, st.a), m->dtype, o[st.out_idx], ls);
+        label = "output";
+        break;
+    }
+    if (rc) return rc;
+    for (size_t i = before; i < ls.size(); ++i) labels.push_back(label + ":" + ls[i].name);
+  }
+  m->launches = std::move(ls);
+  m->labels = std::move(labels);
+  m->prep_x = x;
+  m->prep_outs = o;
+  return VRS_OK;
+}
+
+int dev_upload(vrs_model* m, const void* host, size_t bytes, void** dev) {
+  void* p = nullptr;
+  VRS_HIP(hipMalloc(&p, bytes));
+  m->allocs.push_back(p);
+  VRS_HIP(hipMemcpy(p, host, bytes, hipMemcpyHostToDevice));
+  *dev = p;
+  return VRS_OK;
+}
+
+const Param* P(const vrs_model* m, const std::string& name) {
+  auto it = m->pidx.find(name);
+  return it == m->pidx.end() ? nullptr : &m->params[it->second];
+}
+
+}  // namespace
+
+extern "C" {
+
+int vrs_model_create(vrs_ctx* ctx, const vrs_block_desc* d, int32_t batch, int32_t h, int32_t w, int32_t dtype,
+                     float bn_eps, vrs_model** out) {
+  if (!d || !out) return fail(VRS_EINVAL, "vrs_model_create: null argument");
+  *out = nullptr;
+  if (batch <= 0 || h <= 0 || w <= 0) return fail(VRS_EBADSHAPE, "vrs_model_create: empty input");
+  if (dtype != VRS_BF16 && dtype != VRS_F32) return fail(VRS_EUNSUPPORTED, "vrs_model_create: dtype %d", dtype);
+  if (d->c_in <= 0 || (d->kind != VRS_BLOCK_YOLO26 && d->c_out <= 0 && d->kind != VRS_BLOCK_PSA_ATTN))
+    return fail(VRS_EINVAL, "vrs_model_create: channels");
+  std::unique_ptr<vrs_model> m(new vrs_model);
+  m->ctx = ctx; m->desc = *d; m->batch = batch; m->in_c = d->c_in; m->in_h = h; m->in_w = w; m->dtype = dtype;
+  m->eps = bn_eps;
+  int rc = build(m.get());
+  if (rc) return rc;
+  *out = m.release();
+  return VRS_OK;
+}
+
+int vrs_model_num_params(const vrs_model* m) { return m ? (int)m->params.size() : fail(VRS_EINVAL, "null model"); }
+
+int vrs_model_param_info(const vrs_model* m, int32_t i, const char** name, int32_t* dims, int32_t* ndim) {
+  if (!m || !name || !dims || !ndim) return fail(VRS_EINVAL, "vrs_model_param_info: null argument");
+  if (i < 0 || i >= (int)m->params.size()) return fail(VRS_EINVAL, "vrs_model_param_info: index %d", i);
+  const Param& p = m->params[i];
+  *name = p.name.c_str();
+  *ndim = (int32_t)p.dims.size();
+  for (size_t k = 0; k < p.dims.size(); ++k) dims[k] = p.dims[k];
+  return VRS_OK;
+}
+
+int vrs_model_load_param(vrs_model* m, const char* name, const float* data, int64_t numel) {
+  if (!m || !name || !data) return fail(VRS_EINVAL, "vrs_model_load_param: null argument");
+  if (m->finalized) return fail(VRS_ESTATE, "vrs_model_load_param: model already finalized");
+  auto it = m->pidx.find(name);
+  if (it == m->pidx.end()) return fail(VRS_ENOTFOUND, "unknown parameter '%s'", name);
+  Param& p = m->params[it->second];
+  int64_t n = 1;
+  for (int d : p.dims) n *= d;
+  if (n != numel) return fail(VRS_EBADSHAPE, "parameter '%s' expects %lld values, got %lld", name, (long long)n,
+                               (long long)numel);
+  p.host.assign(data, data + numel);
+  p.loaded = true;
+  return VRS_OK;
+}
+
+int vrs_model_finalize(vrs_model* m) {
+  if (!m) return fail(VRS_EINVAL, "null model");
+  if (!m->ctx) return fail(VRS_ESTATE, "model was created without a context (record-only)");
+  if (m->finalized) return VRS_OK;
+  for (const Param& p : m->params)
+    if (!p.loaded) return fail(VRS_ESTATE, "parameter '%s' not loaded", p.name.c_str());
+  const size_t es = elt_size(m->dtype);
+  for (Buf& b : m->bufs) {
+    const size_t bytes = (size_t)m->batch * b.h * b.w * b.pitch * es;
+    VRS_HIP(hipMalloc(&b.dev, bytes));
+    m->allocs.push_back(b.dev);
+    VRS_HIP(hipMemset(b.dev, 0, bytes));
+  }
+  for (ConvStep& c : m->convs) {
+    std::vector<float> scale(c.cout), shift(c.cout);
+    const Param* w;
+    if (c.kind == CK_PLAIN) {
+      w = P(m, J(c.pre, "weight"));
+      const Param* bias = P(m, J(c.pre, "bias"));
+      for (int i = 0; i < c.cout; ++i) { scale[i] = 1.f; shift[i] = bias->host[i]; }
+    } else {
+      w = P(m, J(c.pre, "conv.weight"));
+      vrs_bn_fold(P(m, J(c.pre, "bn.weight"))->host.data(), P(m, J(c.pre, "bn.bias"))->host.data(),
+                  P(m, J(c.pre, "bn.running_mean"))->host.data(), P(m, J(c.pre, "bn.running_var"))->host.data(),
+                  m->eps, c.cout, scale.data(), shift.data());
+    }
+    const int cin_g = w->dims[1];
+    const int groups = c.dw ? c.cout : 1;
+    const int cin_pad = c.dw ? 1 : c.cin;
+    const int64_t bytes = vrs_pack_conv_weight(nullptr, c.cout, cin_g, c.k, groups, cin_pad, m->dtype, nullptr);
+    if (bytes < 0) return (int)bytes;
+    std::vector<uint8_t> packed((size_t)bytes);
+    const int64_t r = vrs_pack_conv_weight(w->host.data(), c.cout, cin_g, c.k, groups, cin_pad, m->dtype, packed.data());
+    if (r < 0) return (int)r;
+    int rc;
+    if ((rc = dev_upload(m, packed.data(), packed.size(), &c.w))) return rc;
+    void* p;
+    if ((rc = dev_upload(m, scale.data(), scale.size() * 4, &p))) return rc;
+    c.scale = static_cast<float*>(p);
+    if ((rc = dev_upload(m, shift.data(), shift.size() * 4, &p))) return rc;
+    c.shift = static_cast<float*>(p);
+  }
+  for (Param& p : m->params) std::vector<float>().swap(p.host);
+  m->finalized = true;
+  return VRS_OK;
+}
+
+int vrs_model_num_outputs(const vrs_model* m) { return m ? (int)m->out_dims.size() : fail(VRS_EINVAL, "null model"); }
+
+int vrs_model_output_info(const vrs_model* m, int32_t i, int64_t* numel, int32_t* dims, int32_t* ndim) {
+  if (!m || !numel || !dims || !ndim) return fail(VRS_EINVAL, "vrs_model_output_info: null argument");
+  if (i < 0 || i >= (int)m->out_dims.size()) return fail(VRS_EINVAL, "vrs_model_output_info: index %d", i);
+  int64_t n = 1;
+  for (size_t k = 0; k < m->out_dims[i].size(); ++k) { dims[k] = m->out_dims[i][k]; n *= dims[k]; }
+  *ndim = (int32_t)m->out_dims[i].size();
+  *numel = n;
+  return VRS_OK;
+}
+
+int vrs_model_forward(vrs_model* m, const float* x, float* const* outputs, void* stream) {
+  if (!m || !x || !outputs) return fail(VRS_EINVAL, "vrs_model_forward: null argument");
+  if (!m->finalized) return fail(VRS_ESTATE, "vrs_model_forward: call vrs_model_finalize first");
+  for (size_t i = 0; i < m->out_dims.size(); ++i)
+    if (!outputs[i]) return fail(VRS_EINVAL, "vrs_model_forward: null output %zu", i);
+  int rc = prepare(m, x, outputs);
+  if (rc) return rc;
+  for (const Launch& l : m->launches)
+    if ((rc = run(l, static_cast<hipStream_t>(stream)))) return rc;
+  return VRS_OK;
+}
+
+int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void* stream) {
+  if (!m || !x || !outputs) return fail(VRS_EINVAL, "vrs_model_capture: null argument");
+  if (!stream) return fail(VRS_EINVAL, "vrs_model_capture: needs a non-default stream");
+  if (!m->finalized) return fail(VRS_ESTATE, "vrs_model_capture: call vrs_model_finalize first");
+  int rc = prepare(m, x, outputs);
+  if (rc) return rc;
+  if (m->exec) { (void)hipGraphExecDestroy(m->exec); m->exec = nullptr; }
+  if (m->graph) { (void)hipGraphDestroy(m->graph); m->graph = nullptr; }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  VRS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  for (const Launch& l : m->launches) {
+    if ((rc = run(l, s))) {
+      hipGraph_t g;
+      (void)hipStreamEndCapture(s, &g);
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+  }
+  VRS_HIP(hipStreamEndCapture(s, &m->graph));
+  VRS_HIP(hipGraphInstantiate(&m->exec, m->graph, nullptr, nullptr, 0));
+  return VRS_OK;
+}
+
+int vrs_model_replay(vrs_model* m, void* stream) {
+  if (!m) return fail(VRS_EINVAL, "null model");
+  if (!m->exec) return fail(VRS_ESTATE, "vrs_model_replay: no captured graph");
+  VRS_HIP(hipGraphLaunch(m->exec, static_cast<hipStream_t>(stream)));
+  return VRS_OK;
+}
+
+int vrs_model_num_launches(const vrs_model* m) { return m ? (int)m->launches.size() : 0; }
+
+const char* vrs_model_launch_name(const vrs_model* m, int32_t i) {
+  if (!m || i < 0 || i >= (int)m->labels.size()) return "";
+  return m->labels[i].c_str();
+}
+
+int vrs_model_launch_work(const vrs_model* m, int32_t i, double* flops, double* bytes) {
+  if (!m || !flops || !bytes) return fail(VRS_EINVAL, "vrs_model_launch_work: null argument");
+  if (i < 0 || i >= (int)m->launches.size()) return fail(VRS_EINVAL, "vrs_model_launch_work: index %d", i);
+  *flops = m->launches[i].flops;
+  *bytes = m->launches[i].bytes;
+  return VRS_OK;
+}
+
+int vrs_model_run_launches(vrs_model* m, int32_t first, int32_t count, void* stream) {
+  if (!m) return fail(VRS_EINVAL, "null model");
+  if (first < 0 || count < 0 || first + count > (int)m->launches.size())
+    return fail(VRS_EINVAL, "vrs_model_run_launches: range [%d,%d) of %zu", first, first + count, m->launches.size());
+  for (int i = first; i < first + count; ++i) {
+    int rc = run(m->launches[i], static_cast<hipStream_t>(stream));
+    if (rc) return rc;
+  }
+  return VRS_OK;
+}
+
+int vrs_model_destroy(vrs_model* m) {
+  if (!m) return VRS_OK;
+  if (m->exec) (void)hipGraphExecDestroy(m->exec);
+  if (m->graph) (void)hipGraphDestroy(m->graph);
+  for (void* p : m->allocs) (void)hipFree(p);
+  delete m;
+  return VRS_OK;
+}
+
+}  // extern "C"

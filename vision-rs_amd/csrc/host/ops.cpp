@@ -1,0 +1,221 @@
+// Single-op C-ABI entry points (include/vrs.h): each validates, prepares the
+// launch(es) and runs them on the caller's stream.
+#include <cmath>
+#include <cstring>
+
+#include "vrs_internal.h"
+
+using namespace vrs;
+
+namespace {
+
+int run_all(const std::vector<Launch>& ls, void* stream) {
+  for (const auto& l : ls) {
+    int rc = run(l, static_cast<hipStream_t>(stream));
+    if (rc) return rc;
+  }
+  return VRS_OK;
+}
+
+uint16_t host_f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+}  // namespace
+
+extern "C" {
+
+int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const void* w, const float* scale,
+               const float* shift, const vrs_nhwc* res, const vrs_nhwc* y, void* stream) {
+  if (!ctx || !d || !x || !y) return fail(VRS_EINVAL, "vrs_conv2d: null argument");
+  ConvSpec cs;
+  cs.k = d->k; cs.stride = d->stride; cs.act = d->act; cs.dtype = d->dtype;
+  if (d->groups == 1) cs.depthwise = false;
+  else if (d->groups == x->c && d->groups == y->c) cs.depthwise = true;
+  else return fail(VRS_EUNSUPPORTED, "vrs_conv2d: groups=%d (only 1 or depthwise)", d->groups);
+  if (d->act != VRS_ACT_NONE && d->act != VRS_ACT_SILU) return fail(VRS_EINVAL, "vrs_conv2d: act %d", d->act);
+  std::vector<Launch> ls;
+  int rc = prep_conv(ctx, cs, *x, w, scale, shift, res, *y, ls);
+  return rc ? rc : run_all(ls, stream);
+}
+
+int64_t vrs_pack_conv_weight(const float* w, int32_t cout, int32_t cin_g, int32_t k, int32_t groups, int32_t cin_pad,
+                             int32_t dtype, void* out) {
+  if (cout <= 0 || cin_g <= 0 || k <= 0 || groups <= 0) return fail(VRS_EINVAL, "pack_conv_weight: bad dims");
+  if (groups > 1) {
+    if (groups != cout || cin_g != 1) return fail(VRS_EUNSUPPORTED, "pack_conv_weight: groups must be 1 or Cout");
+    const int64_t bytes = (int64_t)cout * k * k * 4;
+    if (!out) return bytes;
+    if (!w) return fail(VRS_EINVAL, "pack_conv_weight: null weight");
+    memcpy(out, w, (size_t)bytes);  // [C][1][k][k] == [C][k*k]
+    return bytes;
+  }
+  if (dtype != VRS_BF16 && dtype != VRS_F32) return fail(VRS_EUNSUPPORTED, "pack_conv_weight: dtype");
+  if (cin_pad < cin_g) return fail(VRS_EINVAL, "pack_conv_weight: cin_pad < cin");
+  const int64_t n = (int64_t)cout * k * k * cin_pad;
+  const int64_t bytes = n * (int64_t)elt_size(dtype);
+  if (!out) return bytes;
+  if (!w) return fail(VRS_EINVAL, "pack_conv_weight: null weight");
+  for (int co = 0; co < cout; ++co)
+    for (int ky = 0; ky < k; ++ky)
+      for (int kx = 0; kx < k; ++kx)
+        for (int ci = 0; ci < cin_pad; ++ci) {
+          const float v = ci < cin_g ? w[(((int64_t)co * cin_g + ci) * k + ky) * k + kx] : 0.f;
+          const int64_t o = (((int64_t)co * k + ky) * k + kx) * cin_pad + ci;
+          if (dtype == VRS_F32) static_cast<float*>(out)[o] = v;
+          else static_cast<uint16_t*>(out)[o] = host_f2bf(v);
+        }
+  return bytes;
+}
+
+int vrs_bn_fold(const float* gamma, const float* beta, const float* mean, const float* var, float eps, int32_t c,
+                float* scale, float* shift) {
+  if (!gamma || !beta || !mean || !var || !scale || !shift || c <= 0) return fail(VRS_EINVAL, "vrs_bn_fold: bad args");
+  for (int i = 0; i < c; ++i) {
+    const float s = gamma[i] / std::sqrt(var[i] + eps);
+    scale[i] = s;
+    shift[i] = beta[i] - s * mean[i];
+  }
+  return VRS_OK;
+}
+
+int vrs_pack_input(vrs_ctx* ctx, const float* x, int32_t n, int32_t c, int32_t h, int32_t w, const vrs_nhwc* y,
+                   int32_t dtype, void* stream) {
+  if (!ctx || !y) return fail(VRS_EINVAL, "vrs_pack_input: null argument");
+  std::vector<Launch> ls;
+  int rc = prep_pack_input(ctx, x, n, c, h, w, *y, dtype, ls);
+  return rc ? rc : run_all(ls, stream);
+}
+
+int vrs_unpack_output(vrs_ctx* ctx, const vrs_nhwc* x, int32_t dtype, float* y, void* stream) {
+  if (!ctx || !x) return fail(VRS_EINVAL, "vrs_unpack_output: null argument");
+  std::vector<Launch> ls;
+  int rc = prep_unpack(ctx, *x, dtype, y, ls);
+  return rc ? rc : run_all(ls, stream);
+}
+
+int vrs_sppf_pool(vrs_ctx* ctx, const vrs_nhwc* buf, int32_t dtype, void* stream) {
+  if (!ctx || !buf) return fail(VRS_EINVAL, "vrs_sppf_pool: null argument");
+  std::vector<Launch> ls;
+  int rc = prep_pool(ctx, *buf, dtype, ls);
+  return rc ? rc : run_all(ls, stream);
+}
+
+int vrs_upsample2x(vrs_ctx* ctx, const vrs_nhwc* x, const vrs_nhwc* y, int32_t dtype, void* stream) {
+  if (!ctx || !x || !y) return fail(VRS_EINVAL, "vrs_upsample2x: null argument");
+  std::vector<Launch> ls;
+  int rc = prep_up(ctx, *x, *y, dtype, ls);
+  return rc ? rc : run_all(ls, stream);
+}
+
+int vrs_psa_attention(vrs_ctx* ctx, const vrs_psa_desc* d, const vrs_nhwc* qkv, const float* pe_w,
+                      const float* pe_scale, const float* pe_shift, const vrs_nhwc* out, void* stream) {
+  if (!ctx || !d || !qkv || !out) return fail(VRS_EINVAL, "vrs_psa_attention: null argument");
+  if (d->key_dim != 32 || d->head_dim != 64)
+    return fail(VRS_EUNSUPPORTED, "vrs_psa_attention: key_dim %d head_dim %d (32/64 only)", d->key_dim, d->head_dim);
+  std::vector<Launch> ls;
+  int rc = prep_attn(ctx, d->heads, d->dtype, *qkv, pe_w, pe_scale, pe_shift, *out, ls);
+  return rc ? rc : run_all(ls, stream);
+}
+
+static int64_t det_anchors(const vrs_detect_desc* d) {
+  int64_t a = 0;
+  for (int s = 0; s < d->nscales; ++s) a += (int64_t)(d->img_h / d->strides[s]) * (d->img_w / d->strides[s]);
+  return a;
+}
+
+static int det_check(const vrs_detect_desc* d) {
+  if (!d) return fail(VRS_EINVAL, "detect: null descriptor");
+  if (d->n <= 0 || d->nc <= 0 || d->nscales < 1 || d->nscales > 4 || d->img_h <= 0 || d->img_w <= 0)
+    return fail(VRS_EBADSHAPE, "detect: bad descriptor");
+  for (int s = 0; s < d->nscales; ++s)
+    if (d->strides[s] <= 0 || d->img_h % d->strides[s] || d->img_w % d->strides[s])
+      return fail(VRS_EBADSHAPE, "detect: image %dx%d not divisible by stride %d", d->img_h, d->img_w, d->strides[s]);
+  if (d->max_det < 1 || d->max_det > 1024) return fail(VRS_EUNSUPPORTED, "detect: max_det %d (1..1024)", d->max_det);
+  if (det_anchors(d) >= (1ll << 31) / 80) return fail(VRS_EBADSHAPE, "detect: too many anchors");
+  return VRS_OK;
+}
+
+size_t vrs_detect_workspace_size(const vrs_detect_desc* d) {
+  if (det_check(d)) return 0;
+  return (size_t)d->n * det_anchors(d) * (8 + 4 + 16);
+}
+
+int vrs_detect_postprocess(vrs_ctx* ctx, const vrs_detect_desc* d, const float* boxes, const float* scores,
+                           void* ws, size_t ws_bytes, int32_t* count, float* score, int32_t* cls, int32_t* anchor,
+                           float* xywh, void* stream) {
+  if (!ctx) return fail(VRS_EINVAL, "vrs_detect_postprocess: null ctx");
+  int rc = det_check(d);
+  if (rc) return rc;
+  if (!boxes || !scores || !ws || !count || !score || !cls || !anchor || !xywh)
+    return fail(VRS_EINVAL, "vrs_detect_postprocess: null buffer");
+  const int64_t A = det_anchors(d);
+  if (ws_bytes < (size_t)d->n * A * 28) return fail(VRS_EINVAL, "vrs_detect_postprocess: workspace too small");
+  if (reinterpret_cast<uintptr_t>(ws) % 16) return fail(VRS_EINVAL, "vrs_detect_postprocess: workspace alignment");
+  uint64_t* keys = static_cast<uint64_t*>(ws);
+  float* xy = reinterpret_cast<float*>(keys + (size_t)d->n * A);
+  int32_t* cl = reinterpret_cast<int32_t*>(xy + (size_t)d->n * A * 4);
+  vrs_det1_args a1{};
+  a1.boxes = boxes; a1.scores = scores; a1.keys = keys; a1.cls = cl; a1.xywh = xy;
+  a1.B = d->n; a1.nc = d->nc; a1.A = (int32_t)A; a1.nscales = d->nscales; a1.thr = d->thr;
+  int base = 0;
+  for (int s = 0; s < d->nscales; ++s) {
+    a1.a_base[s] = base;
+    a1.fw[s] = d->img_w / d->strides[s];
+    a1.stride[s] = (float)d->strides[s];
+    base += (d->img_h / d->strides[s]) * a1.fw[s];
+  }
+  vrs_det2_args a2{keys, cl, xy, count, score, cls, anchor, xywh, d->n, (int32_t)A, d->max_det};
+  hipFunction_t f1, f2;
+  if ((rc = get_fn(ctx, "vrs_detect_stage1", &f1)) || (rc = get_fn(ctx, "vrs_detect_stage2", &f2))) return rc;
+  std::vector<Launch> ls;
+  ls.push_back(make_launch("vrs_detect_stage1", f1, dim3((unsigned)((d->n * A + 255) / 256)), dim3(256), 0, a1));
+  ls.push_back(make_launch("vrs_detect_stage2", f2, dim3(d->n), dim3(1024), 0, a2));
+  return run_all(ls, stream);
+}
+
+int vrs_detect_decode_grid(vrs_ctx* ctx, const float* boxes, const float* ax, const float* ay, const float* st,
+                           int32_t n, int32_t a, float* out, void* stream) {
+  if (!ctx || !boxes || !ax || !ay || !st || !out) return fail(VRS_EINVAL, "vrs_detect_decode_grid: null argument");
+  if (n <= 0 || a <= 0) return fail(VRS_EBADSHAPE, "vrs_detect_decode_grid: empty");
+  hipFunction_t f;
+  int rc = get_fn(ctx, "vrs_detect_decode_grid", &f);
+  if (rc) return rc;
+  vrs_dec_args args{boxes, ax, ay, st, out, n, a};
+  std::vector<Launch> ls;
+  ls.push_back(make_launch("vrs_detect_decode_grid", f, dim3((unsigned)(((int64_t)n * a + 255) / 256)), dim3(256),
+                           0, args));
+  return run_all(ls, stream);
+}
+
+int vrs_msda(vrs_ctx* ctx, const vrs_msda_desc* d, const float* value, const float* ref, const float* off,
+             const float* attw, float* out, void* stream) {
+  if (!ctx || !d || !value || !ref || !off || !attw || !out) return fail(VRS_EINVAL, "vrs_msda: null argument");
+  if (d->head_dim != 32) return fail(VRS_EUNSUPPORTED, "vrs_msda: head_dim %d (32 only)", d->head_dim);
+  if (d->n <= 0 || d->q <= 0 || d->heads <= 0 || d->levels < 1 || d->levels > 8 || d->points < 1)
+    return fail(VRS_EBADSHAPE, "vrs_msda: bad descriptor");
+  vrs_msda_args a{};
+  a.value = value; a.ref = ref; a.off = off; a.attw = attw; a.out = out;
+  a.B = d->n; a.Q = d->q; a.heads = d->heads; a.L = d->levels; a.P = d->points;
+  int64_t s = 0;
+  for (int l = 0; l < d->levels; ++l) {
+    if (d->level_h[l] <= 0 || d->level_w[l] <= 0) return fail(VRS_EBADSHAPE, "vrs_msda: level %d empty", l);
+    a.lh[l] = d->level_h[l]; a.lw[l] = d->level_w[l]; a.lstart[l] = (int32_t)s;
+    s += (int64_t)d->level_h[l] * d->level_w[l];
+  }
+  if (s >= (1ll << 31)) return fail(VRS_EBADSHAPE, "vrs_msda: too many value rows");
+  a.S = (int32_t)s;
+  hipFunction_t f;
+  int rc = get_fn(ctx, "vrs_msda_f32", &f);
+  if (rc) return rc;
+  const int64_t threads = (int64_t)d->n * d->q * d->heads * 32;
+  std::vector<Launch> ls;
+  ls.push_back(make_launch("vrs_msda_f32", f, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a));
+  return run_all(ls, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,341 @@
+// Host runtime: errors, code-object loading, launch preparation.
+// Everything here validates on the host before any HIP call and reports
+// failures through status codes (include/vrs.h conventions).
+#include <dirent.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+
+#include "vrs_internal.h"
+
+namespace vrs {
+
+static thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  return fail(VRS_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int get_fn(vrs_ctx* ctx, const char* name, hipFunction_t* out) {
+  auto it = ctx->fns.find(name);
+  if (it != ctx->fns.end()) { *out = it->second; return VRS_OK; }
+  for (hipModule_t m : ctx->modules) {
+    hipFunction_t f = nullptr;
+    if (hipModuleGetFunction(&f, m, name) == hipSuccess && f) {
+      ctx->fns[name] = f;
+      *out = f;
+      return VRS_OK;
+    }
+  }
+  (void)hipGetLastError();
+  return fail(VRS_ENOMODULE, "kernel '%s' not found in the code objects under %s", name, ctx->dir.c_str());
+}
+
+int run(const Launch& l, hipStream_t s) {
+  void* params[] = {const_cast<uint8_t*>(l.args.data())};
+  hipError_t e = hipModuleLaunchKernel(l.fn, l.grid.x, l.grid.y, l.grid.z, l.block.x, l.block.y, l.block.z,
+                                       l.shmem, s, params, nullptr);
+  if (e != hipSuccess) return fail(VRS_EHIP, "launch %s: %s", l.name.c_str(), hipGetErrorString(e));
+  return VRS_OK;
+}
+
+static const void* at(const vrs_nhwc& v, int dtype) {
+  return static_cast<const char*>(v.data) + (int64_t)v.c_off * elt_size(dtype);
+}
+
+static int check_view(const vrs_nhwc& v, const char* what, int align) {
+  if (!v.data) return fail(VRS_EINVAL, "%s: null data", what);
+  if (v.n <= 0 || v.h <= 0 || v.w <= 0 || v.c <= 0) return fail(VRS_EBADSHAPE, "%s: empty shape", what);
+  if (v.c_off < 0 || v.c_off + v.c > v.pitch)
+    return fail(VRS_EBADSHAPE, "%s: channels [%d,%d) exceed pitch %d", what, v.c_off, v.c_off + v.c, v.pitch);
+  if (v.c_off % align || v.pitch % align || v.c % align)
+    return fail(VRS_EBADSHAPE, "%s: channel offset/pitch/count must be multiples of %d", what, align);
+  if (reinterpret_cast<uintptr_t>(v.data) % 16) return fail(VRS_EBADSHAPE, "%s: data not 16-byte aligned", what);
+  return VRS_OK;
+}
+
+static int check_dtype(int dtype) {
+  if (dtype != VRS_BF16 && dtype != VRS_F32) return fail(VRS_EUNSUPPORTED, "dtype %d not supported", dtype);
+  return VRS_OK;
+}
+
+static inline int out_size(int in, int k, int s) { return (in + 2 * (k / 2) - k) / s + 1; }
+
+// Tile choice per Cout: narrow layers take the 32- or 64-row tiles so MFMA
+// rows are not wasted; everything else takes 128x128.
+static void pick_tile(int cout, int cin, int dtype, char* name, size_t n, int* bm, int* bn) {
+  const char* t;
+  if (cout <= 32) { t = "32x256"; *bm = 32; *bn = 256; }
+  else if (cout <= 64) { t = "64x256"; *bm = 64; *bn = 256; }
+  else { t = "128x128"; *bm = 128; *bn = 128; }
+  snprintf(name, n, "vrs_conv_%s_%s_%c", dsuffix(dtype), t, cin % 32 == 0 ? 'a' : 'g');
+}
+
+static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
+                      const float* shift, int cout, int ho, int wo, vrs_conv_args& a, std::vector<Launch>& out) {
+  int rc;
+  if ((rc = check_dtype(cs.dtype))) return rc;
+  if ((rc = check_view(x, "conv input", 8))) return rc;
+  if (!w || !scale || !shift) return fail(VRS_EINVAL, "conv: null weight/scale/shift");
+  if (cs.k < 1 || cs.k > 7 || cs.k % 2 == 0 || cs.stride < 1) return fail(VRS_EBADSHAPE, "conv: k=%d s=%d", cs.k, cs.stride);
+  if (ho != out_size(x.h, cs.k, cs.stride) || wo != out_size(x.w, cs.k, cs.stride))
+    return fail(VRS_EBADSHAPE, "conv: output %dx%d does not match input %dx%d k=%d s=%d", ho, wo, x.h, x.w, cs.k,
+                cs.stride);
+  a.x = at(x, cs.dtype);
+  a.w = w;
+  a.scale = scale;
+  a.shift = shift;
+  a.N = x.n; a.H = x.h; a.W = x.w; a.Cin = x.c; a.x_pitch = x.pitch;
+  a.Ho = ho; a.Wo = wo; a.Cout = cout;
+  a.kh = a.kw = cs.k; a.stride = cs.stride; a.pad = cs.k / 2;
+  a.K = cs.k * cs.k * x.c;
+  const int64_t M = (int64_t)x.n * ho * wo;
+  if (M >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: %lld output pixels exceed int32", (long long)M);
+  a.M = (int32_t)M;
+  a.act = cs.act;
+  char name[64];
+  int bm, bn;
+  pick_tile(cout, x.c, cs.dtype, name, sizeof name, &bm, &bn);
+  a.tiles_m = (cout + bm - 1) / bm;
+  a.tiles_n = (int32_t)((M + bn - 1) / bn);
+  const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
+  if (blocks >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: grid too large");
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  out.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(256), 0, a));
+  const double es = (double)elt_size(cs.dtype);
+  const double cin = cs.cin_real > 0 ? cs.cin_real : x.c;
+  const double kk = (double)cs.k * cs.k;
+  out.back().flops = 2.0 * (double)M * cout * kk * cin;
+  out.back().bytes = (double)x.n * x.h * x.w * cin * es + (double)cout * kk * cin * es +
+                     (double)M * cout * (a.y_f32 ? 4.0 : es) + (a.res ? (double)M * cout * es : 0.0) + 8.0 * cout;
+  return VRS_OK;
+}
+
+int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
+              const float* shift, const vrs_nhwc* res, const vrs_nhwc& y, std::vector<Launch>& out) {
+  int rc;
+  if ((rc = check_view(y, "conv output", cs.depthwise ? 8 : 4))) return rc;
+  if (y.n != x.n) return fail(VRS_EBADSHAPE, "conv: batch mismatch %d vs %d", x.n, y.n);
+  if (cs.depthwise) {
+    if ((rc = check_dtype(cs.dtype))) return rc;
+    if ((rc = check_view(x, "dwconv input", 8))) return rc;
+    if (res) return fail(VRS_EUNSUPPORTED, "dwconv: residual not supported");
+    if (x.c != y.c) return fail(VRS_EBADSHAPE, "dwconv: channels %d -> %d", x.c, y.c);
+    if (cs.k < 1 || cs.k > 3 || cs.k % 2 == 0) return fail(VRS_EUNSUPPORTED, "dwconv: k=%d (1 or 3)", cs.k);
+    if (y.h != out_size(x.h, cs.k, cs.stride) || y.w != out_size(x.w, cs.k, cs.stride))
+      return fail(VRS_EBADSHAPE, "dwconv: output size");
+    if (!w || !scale || !shift) return fail(VRS_EINVAL, "dwconv: null weight/scale/shift");
+    vrs_dw_args a{};
+    a.x = at(x, cs.dtype); a.w = static_cast<const float*>(w); a.scale = scale; a.shift = shift;
+    a.y = const_cast<void*>(at(y, cs.dtype));
+    a.N = x.n; a.H = x.h; a.W = x.w; a.C = x.c; a.x_pitch = x.pitch;
+    a.Ho = y.h; a.Wo = y.w; a.y_pitch = y.pitch;
+    a.kh = a.kw = cs.k; a.stride = cs.stride; a.pad = cs.k / 2; a.act = cs.act;
+    const int64_t threads = (int64_t)x.n * ((y.h + 3) / 4) * y.w * (x.c / 8);
+    char name[48];
+    snprintf(name, sizeof name, "vrs_dwconv_%s", dsuffix(cs.dtype));
+    hipFunction_t f;
+    if ((rc = get_fn(ctx, name, &f))) return rc;
+    out.push_back(make_launch(name, f, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a));
+    const double es = (double)elt_size(cs.dtype);
+    out.back().flops = 2.0 * x.n * y.h * y.w * (double)x.c * cs.k * cs.k;
+    out.back().bytes = (double)x.n * x.h * x.w * x.c * es + (double)y.n * y.h * y.w * y.c * es +
+                       (double)x.c * (cs.k * cs.k + 2) * 4.0;
+    return VRS_OK;
+  }
+  vrs_conv_args a{};
+  if (res) {
+    if ((rc = check_view(*res, "conv residual", 4))) return rc;
+    if (res->n != y.n || res->h != y.h || res->w != y.w || res->c != y.c)
+      return fail(VRS_EBADSHAPE, "conv: residual shape differs from output");
+    a.res = at(*res, cs.dtype);
+    a.r_sb = (int64_t)res->h * res->w * res->pitch; a.r_sp = res->pitch; a.r_sc = 1;
+  }
+  a.y = const_cast<void*>(at(y, cs.dtype));
+  a.y_sb = (int64_t)y.h * y.w * y.pitch; a.y_sp = y.pitch; a.y_sc = 1;
+  a.y_f32 = 0;
+  return prep_dense(ctx, cs, x, w, scale, shift, y.c, y.h, y.w, a, out);
+}
+
+int prep_conv_flat(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
+                   const float* shift, int cout, float* y, int64_t sb, int64_t sp, int64_t sc,
+                   std::vector<Launch>& out) {
+  if (!y) return fail(VRS_EINVAL, "conv: null output");
+  vrs_conv_args a{};
+  a.y = y; a.y_sb = sb; a.y_sp = sp; a.y_sc = sc; a.y_f32 = 1;
+  const int ho = out_size(x.h, cs.k, cs.stride), wo = out_size(x.w, cs.k, cs.stride);
+  return prep_dense(ctx, cs, x, w, scale, shift, cout, ho, wo, a, out);
+}
+
+int prep_pack_input(vrs_ctx* ctx, const float* x, int n, int c, int h, int w, const vrs_nhwc& y, int dtype,
+                    std::vector<Launch>& out) {
+  int rc;
+  if ((rc = check_dtype(dtype))) return rc;
+  if (!x) return fail(VRS_EINVAL, "pack_input: null input");
+  if (y.c_off != 0 || y.pitch != y.c) return fail(VRS_EBADSHAPE, "pack_input: output must be a whole buffer");
+  if (y.n != n || y.h != h || y.w != w || y.c < c || y.c > 8)
+    return fail(VRS_EBADSHAPE, "pack_input: output view %dx%dx%dx%d for input %dx%dx%dx%d (padded c <= 8)", y.n,
+                y.h, y.w, y.c, n, c, h, w);
+  vrs_pack_args a{x, y.data, n, c, h, w, y.c};
+  char name[48];
+  snprintf(name, sizeof name, "vrs_pack_nchw_%s", dsuffix(dtype));
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  const int64_t threads = (int64_t)n * h * w;
+  out.push_back(make_launch(name, f, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a));
+  out.back().bytes = (double)n * h * w * (4.0 * c + (double)y.c * elt_size(dtype));
+  return VRS_OK;
+}
+
+int prep_unpack(vrs_ctx* ctx, const vrs_nhwc& x, int dtype, float* y, std::vector<Launch>& out) {
+  int rc;
+  if ((rc = check_dtype(dtype))) return rc;
+  if ((rc = check_view(x, "unpack input", 1))) return rc;
+  if (!y) return fail(VRS_EINVAL, "unpack: null output");
+  vrs_pack_args a{};
+  a.x = static_cast<const float*>(at(x, dtype));
+  a.y = y;
+  a.N = x.n; a.C = x.c; a.H = x.h; a.W = x.w; a.c_pad = x.pitch;
+  char name[48];
+  snprintf(name, sizeof name, "vrs_unpack_nchw_%s", dsuffix(dtype));
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  const int64_t threads = (int64_t)x.n * x.c * x.h * x.w;
+  out.push_back(make_launch(name, f, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a));
+  out.back().bytes = (double)threads * (4.0 + elt_size(dtype));
+  return VRS_OK;
+}
+
+int prep_pool(vrs_ctx* ctx, const vrs_nhwc& buf, int dtype, std::vector<Launch>& out) {
+  int rc;
+  if ((rc = check_dtype(dtype))) return rc;
+  if ((rc = check_view(buf, "sppf buffer", 8))) return rc;
+  if (buf.c % 32) return fail(VRS_EBADSHAPE, "sppf: view must hold 4*c channels with c %% 8 == 0");
+  const int c = buf.c / 4;
+  const int hw = buf.h * buf.w;
+  const int64_t per_group = 2ll * hw * 8 * (int64_t)elt_size(dtype);
+  int cg = (int)std::min<int64_t>(c / 8, (48 * 1024) / per_group);
+  if (cg < 1) return fail(VRS_EUNSUPPORTED, "sppf: %dx%d map does not fit the LDS plane", buf.h, buf.w);
+  vrs_pool_args a{};
+  a.buf = const_cast<void*>(at(buf, dtype));
+  a.N = buf.n; a.H = buf.h; a.W = buf.w; a.c = c; a.pitch = buf.pitch; a.cgroups_per_block = cg;
+  const int blocks_per_img = (c / 8 + cg - 1) / cg;
+  char name[48];
+  snprintf(name, sizeof name, "vrs_sppf_pool_%s", dsuffix(dtype));
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  out.push_back(make_launch(name, f, dim3(buf.n * blocks_per_img), dim3(256), (uint32_t)(cg * per_group), a));
+  out.back().bytes = 4.0 * buf.n * hw * (double)c * elt_size(dtype);
+  return VRS_OK;
+}
+
+int prep_up(vrs_ctx* ctx, const vrs_nhwc& x, const vrs_nhwc& y, int dtype, std::vector<Launch>& out) {
+  int rc;
+  if ((rc = check_dtype(dtype))) return rc;
+  if ((rc = check_view(x, "upsample input", 8)) || (rc = check_view(y, "upsample output", 8))) return rc;
+  if (y.n != x.n || y.h != 2 * x.h || y.w != 2 * x.w || y.c != x.c)
+    return fail(VRS_EBADSHAPE, "upsample2x: output must be [n, 2h, 2w, c]");
+  vrs_up_args a{at(x, dtype), const_cast<void*>(at(y, dtype)), x.n, x.h, x.w, x.c, x.pitch, y.pitch};
+  char name[48];
+  snprintf(name, sizeof name, "vrs_upsample2x_%s", dsuffix(dtype));
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  const int64_t threads = (int64_t)y.n * y.h * y.w * (y.c / 8);
+  out.push_back(make_launch(name, f, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a));
+  out.back().bytes = 5.0 * x.n * x.h * x.w * (double)x.c * elt_size(dtype);
+  return VRS_OK;
+}
+
+int prep_attn(vrs_ctx* ctx, int heads, int dtype, const vrs_nhwc& qkv, const float* pe_w, const float* pe_scale,
+              const float* pe_shift, const vrs_nhwc& o, std::vector<Launch>& out) {
+  int rc;
+  if ((rc = check_dtype(dtype))) return rc;
+  if ((rc = check_view(qkv, "psa qkv", 8)) || (rc = check_view(o, "psa out", 4))) return rc;
+  if (heads < 1 || qkv.c != heads * 128 || o.c != heads * 64)
+    return fail(VRS_EBADSHAPE, "psa: heads=%d needs qkv %d and out %d channels", heads, heads * 128, heads * 64);
+  if (o.n != qkv.n || o.h != qkv.h || o.w != qkv.w) return fail(VRS_EBADSHAPE, "psa: out/qkv spatial mismatch");
+  if (!pe_w || !pe_scale || !pe_shift) return fail(VRS_EINVAL, "psa: null pe parameters");
+  vrs_attn_args a{};
+  a.qkv = at(qkv, dtype); a.pe_w = pe_w; a.pe_scale = pe_scale; a.pe_shift = pe_shift;
+  a.out = const_cast<void*>(at(o, dtype));
+  a.B = qkv.n; a.H = qkv.h; a.W = qkv.w; a.heads = heads; a.qkv_pitch = qkv.pitch; a.out_pitch = o.pitch;
+  a.scale_log2e = (float)(1.0 / std::sqrt(32.0) * 1.4426950408889634);
+  a.q_blocks = (qkv.h * qkv.w + 63) / 64;
+  char name[48];
+  snprintf(name, sizeof name, "vrs_psa_attn_%s", dsuffix(dtype));
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  out.push_back(make_launch(name, f, dim3(a.B * heads * a.q_blocks), dim3(256), 0, a));
+  const double N = (double)qkv.h * qkv.w;
+  out.back().flops = 2.0 * a.B * heads * N * N * (32 + 64) + 2.0 * a.B * N * o.c * 9;
+  out.back().bytes = (double)a.B * N * (qkv.c + o.c) * elt_size(dtype) + (double)o.c * 11 * 4;
+  return VRS_OK;
+}
+
+}  // namespace vrs
+
+using namespace vrs;
+
+extern "C" {
+
+const char* vrs_last_error(void) { return g_err.c_str(); }
+const char* vrs_version(void) { return "vrs 0.1 gfx950"; }
+
+int vrs_ctx_create(int device, const char* hsaco_dir, vrs_ctx** out) {
+  if (!out || !hsaco_dir) return fail(VRS_EINVAL, "vrs_ctx_create: null argument");
+  *out = nullptr;
+  DIR* d = opendir(hsaco_dir);
+  if (!d) return fail(VRS_ENOMODULE, "code-object directory %s not found", hsaco_dir);
+  std::vector<std::string> files;
+  while (dirent* e = readdir(d)) {
+    std::string n = e->d_name;
+    if (n.size() > 6 && n.compare(n.size() - 6, 6, ".hsaco") == 0) files.push_back(std::string(hsaco_dir) + "/" + n);
+  }
+  closedir(d);
+  if (files.empty()) return fail(VRS_ENOMODULE, "no .hsaco code objects under %s", hsaco_dir);
+  int ndev = 0;
+  VRS_HIP(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev) return fail(VRS_EINVAL, "device %d out of range (%d devices)", device, ndev);
+  VRS_HIP(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  VRS_HIP(hipGetDeviceProperties(&prop, device));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(VRS_EUNSUPPORTED, "device %d is %s; this build targets gfx950 only", device, prop.gcnArchName);
+  auto* ctx = new vrs_ctx;
+  ctx->device = device;
+  ctx->dir = hsaco_dir;
+  ctx->num_cu = prop.multiProcessorCount;
+  for (const auto& f : files) {
+    hipModule_t m = nullptr;
+    hipError_t e = hipModuleLoad(&m, f.c_str());
+    if (e != hipSuccess) {
+      for (auto mm : ctx->modules) (void)hipModuleUnload(mm);
+      delete ctx;
+      return fail(VRS_ENOMODULE, "hipModuleLoad(%s): %s", f.c_str(), hipGetErrorString(e));
+    }
+    ctx->modules.push_back(m);
+  }
+  *out = ctx;
+  return VRS_OK;
+}
+
+int vrs_ctx_destroy(vrs_ctx* ctx) {
+  if (!ctx) return VRS_OK;
+  for (auto m : ctx->modules) (void)hipModuleUnload(m);
+  delete ctx;
+  return VRS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,88 @@
+// Internal declarations of the host runtime behind include/vrs.h.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../kargs.h"
+#include "vrs.h"
+
+struct vrs_ctx {
+  int device = 0;
+  std::string dir;
+  std::vector<hipModule_t> modules;
+  std::unordered_map<std::string, hipFunction_t> fns;
+  int num_cu = 0;
+};
+
+namespace vrs {
+
+// Thread-local error text; returns `code` so callers can `return fail(...)`.
+int fail(int code, const char* fmt, ...);
+int hip_check(hipError_t e, const char* what);
+#define VRS_HIP(call)                                       \
+  do {                                                      \
+    hipError_t e_ = (call);                                 \
+    if (e_ != hipSuccess) return ::vrs::hip_check(e_, #call); \
+  } while (0)
+
+// Resolve a kernel by name from the loaded code objects.
+int get_fn(vrs_ctx* ctx, const char* name, hipFunction_t* out);
+
+// One prepared kernel launch: everything hipModuleLaunchKernel needs, with the
+// argument block stored by value so it can be replayed or captured.
+struct Launch {
+  std::string name;
+  hipFunction_t fn = nullptr;
+  dim3 grid, block;
+  uint32_t shmem = 0;
+  std::vector<uint8_t> args;
+  double flops = 0.0;  // algorithmic work of this launch
+  double bytes = 0.0;  // compulsory HBM bytes (inputs + weights + outputs)
+};
+
+int run(const Launch& l, hipStream_t s);
+
+template <typename A>
+Launch make_launch(const char* name, hipFunction_t fn, dim3 grid, dim3 block, uint32_t shmem, const A& a) {
+  Launch l;
+  l.name = name;
+  l.fn = fn;
+  l.grid = grid;
+  l.block = block;
+  l.shmem = shmem;
+  l.args.resize(sizeof(A));
+  memcpy(l.args.data(), &a, sizeof(A));
+  return l;
+}
+
+inline size_t elt_size(int dtype) { return dtype == VRS_F32 ? 4 : 2; }
+inline const char* dsuffix(int dtype) { return dtype == VRS_F32 ? "f32" : "bf16"; }
+
+// Prepare (validate + fill) launches.  Each returns VRS_OK or an error and
+// appends to `out`.  Pointers in views are device addresses.
+struct ConvSpec {
+  int k = 1, stride = 1, act = VRS_ACT_NONE, dtype = VRS_BF16;
+  bool depthwise = false;
+  int cin_real = 0;  // unpadded input channels for work accounting (0: the view's)
+};
+int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
+              const float* shift, const vrs_nhwc* res, const vrs_nhwc& y, std::vector<Launch>& out);
+// Dense conv storing float32 into a strided (flat) output: element (b, p, co)
+// at y + b*sb + p*sp + co*sc (the Detect head's channel_cat_flat layout).
+int prep_conv_flat(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
+                   const float* shift, int cout, float* y, int64_t sb, int64_t sp, int64_t sc,
+                   std::vector<Launch>& out);
+int prep_pack_input(vrs_ctx* ctx, const float* x, int n, int c, int h, int w, const vrs_nhwc& y, int dtype,
+                    std::vector<Launch>& out);
+int prep_unpack(vrs_ctx* ctx, const vrs_nhwc& x, int dtype, float* y, std::vector<Launch>& out);
+int prep_pool(vrs_ctx* ctx, const vrs_nhwc& buf, int dtype, std::vector<Launch>& out);
+int prep_up(vrs_ctx* ctx, const vrs_nhwc& x, const vrs_nhwc& y, int dtype, std::vector<Launch>& out);
+int prep_attn(vrs_ctx* ctx, int heads, int dtype, const vrs_nhwc& qkv, const float* pe_w, const float* pe_scale,
+              const float* pe_shift, const vrs_nhwc& o, std::vector<Launch>& out);
+
+}  // namespace vrs

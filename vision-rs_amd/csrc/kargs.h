@@ -1,0 +1,140 @@
+/* Kernel argument blocks shared by the host runtime and the gfx950 kernels.
+ * Plain C layout: each kernel takes exactly one of these by value, and the host
+ * passes it through hipModuleLaunchKernel's kernelParams.
+ * Element offsets are in elements of the tensor's dtype. */
+#ifndef VRS_KARGS_H
+#define VRS_KARGS_H
+#include <stdint.h>
+
+#define VRS_ACT_NONE 0
+#define VRS_ACT_SILU 1
+
+/* Implicit-GEMM convolution (dense, groups == 1).
+ * x: NHWC view; element (b, iy, ix, ci) at x[((b*H + iy)*W + ix)*x_pitch + ci]
+ *    (the pointer already includes the view's channel offset).
+ * w: packed [Cout][kh][kw][Cin] (K = kh*kw*Cin contiguous per output channel).
+ * y: element (b, p, co) at y[b*y_sb + p*y_sp + co*y_sc], p = oy*Wo + ox.
+ * res (optional): same addressing with r_* strides, added after the activation.
+ * out = act(acc*scale[co] + shift[co]) + res. */
+typedef struct {
+  const void* x;
+  const void* w;
+  const float* scale;
+  const float* shift;
+  const void* res;
+  void* y;
+  int64_t y_sb, y_sp, y_sc;
+  int64_t r_sb, r_sp, r_sc;
+  int32_t N, H, W, Cin, x_pitch;
+  int32_t Ho, Wo, Cout;
+  int32_t kh, kw, stride, pad;
+  int32_t K;      /* kh*kw*Cin */
+  int32_t M;      /* N*Ho*Wo */
+  int32_t act;
+  int32_t y_f32;  /* 1: store float32, 0: store the kernel's element type */
+  int32_t tiles_m, tiles_n; /* grid decomposition: Cout tiles x pixel tiles */
+} vrs_conv_args;
+
+/* Depthwise conv (groups == C), NHWC, weights [C][kh*kw] float32. */
+typedef struct {
+  const void* x;
+  const float* w;
+  const float* scale;
+  const float* shift;
+  void* y;
+  int32_t N, H, W, C, x_pitch;
+  int32_t Ho, Wo, y_pitch;
+  int32_t kh, kw, stride, pad;
+  int32_t act;
+} vrs_dw_args;
+
+/* SPPF pooling: reads channels [0,c) of a NHWC buffer (pitch) and writes the
+ * cascade p1 = max5(y), p2 = max5(p1), p3 = max5(p2) (stride 1, pad 2, -inf
+ * padding) into channels [c,2c), [2c,3c), [3c,4c) of the same buffer. */
+typedef struct {
+  void* buf;
+  int32_t N, H, W, c, pitch;
+  int32_t cgroups_per_block;
+} vrs_pool_args;
+
+/* Nearest 2x upsample from a NHWC view into a NHWC view. */
+typedef struct {
+  const void* x;
+  void* y;
+  int32_t N, H, W, C, x_pitch, y_pitch;
+} vrs_up_args;
+
+/* NCHW float32 image batch -> NHWC element-type buffer with c_pad channels
+ * (channels >= C are zero). */
+typedef struct {
+  const float* x;
+  void* y;
+  int32_t N, C, H, W, c_pad;
+} vrs_pack_args;
+
+/* PSA attention, key_dim 32, head_dim 64 (blocks/c2psa.rs:61-116).
+ * qkv: NHWC [B, N, heads*128] (per head: q 32 | k 32 | v 64).
+ * out[b, n, h*64 + d] = softmax(q.k * scale) v + pe_scale*dw3x3(v) + pe_shift. */
+typedef struct {
+  const void* qkv;
+  const float* pe_w;    /* [heads*64][9] */
+  const float* pe_scale;
+  const float* pe_shift;
+  void* out;
+  int32_t B, H, W, heads, qkv_pitch, out_pitch;
+  float scale_log2e;    /* kd^-0.5 * log2(e) */
+  int32_t q_blocks;
+} vrs_attn_args;
+
+/* Detect post-process stage 1: per anchor decode + sigmoid/argmax + threshold. */
+typedef struct {
+  const float* boxes;   /* [B, 4*A] per-scale [4][A_s] blocks */
+  const float* scores;  /* [B, nc*A] per-scale [nc][A_s] blocks */
+  uint64_t* keys;       /* [B, A] (score_bits << 32 | ~anchor) or 0 */
+  int32_t* cls;         /* [B, A] */
+  float* xywh;          /* [B, A, 4] */
+  int32_t B, nc, A, nscales;
+  int32_t a_base[4];    /* anchor offset of each scale */
+  int32_t fw[4];        /* grid width of each scale */
+  float stride[4];
+  float thr;
+} vrs_det1_args;
+
+/* Detect post-process stage 2: per image exact top-k (radix select over the
+ * unique 64-bit keys) + sort, one workgroup per image. */
+typedef struct {
+  const uint64_t* keys;
+  const int32_t* cls;
+  const float* xywh;
+  int32_t* count;
+  float* out_score;
+  int32_t* out_cls;
+  int32_t* out_anchor;
+  float* out_xywh;
+  int32_t B, A, max_det;
+} vrs_det2_args;
+
+/* Grid-unit decode on [B,4,A] (kernels/detect_decode.rs:36-86). */
+typedef struct {
+  const float* boxes;
+  const float* ax;
+  const float* ay;
+  const float* st;
+  float* out;
+  int32_t B, A;
+} vrs_dec_args;
+
+/* Multi-scale deformable attention, Dh = 32.
+ * value [B, S, heads, 32]; ref [B, Q, 2]; off [B, Q, heads, L, P, 2];
+ * attw [B, Q, heads, L, P]; out [B, Q, heads*32]. */
+typedef struct {
+  const float* value;
+  const float* ref;
+  const float* off;
+  const float* attw;
+  float* out;
+  int32_t B, S, Q, heads, L, P;
+  int32_t lh[8], lw[8], lstart[8];
+} vrs_msda_args;
+
+#endif

@@ -1,0 +1,87 @@
+// Device helpers for the gfx950 (CDNA4) kernels: element types, 16-byte
+// vector moves, and the 16x16x32 MFMA step shared by conv and attention.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../kargs.h"
+
+typedef uint16_t bf16_t;  // storage type for bfloat16 activations/weights
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
+
+__device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
+
+// float -> bfloat16, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+
+// ---- element traits --------------------------------------------------------
+// A "group" is 8 consecutive elements along K: the unit one lane feeds into
+// the 16x16x32 MFMA step (bf16: one 16-byte register quad; f32: two quads).
+template <typename T> struct Elt;
+
+template <> struct Elt<bf16_t> {
+  struct group { u32x4_t v; };
+  static __device__ __forceinline__ group load(const bf16_t* p) {
+    group g; g.v = *reinterpret_cast<const u32x4_t*>(p); return g;
+  }
+  static __device__ __forceinline__ group zero() { group g; g.v = (u32x4_t){0, 0, 0, 0}; return g; }
+  static __device__ __forceinline__ void store(bf16_t* p, const group& g) {
+    *reinterpret_cast<u32x4_t*>(p) = g.v;
+  }
+  static __device__ __forceinline__ float to_f(bf16_t v) { return bf2f(v); }
+  static __device__ __forceinline__ bf16_t from_f(float v) { return f2bf(v); }
+};
+
+template <> struct Elt<float> {
+  struct group { u32x4_t lo, hi; };
+  static __device__ __forceinline__ group load(const float* p) {
+    group g;
+    g.lo = *reinterpret_cast<const u32x4_t*>(p);
+    g.hi = *reinterpret_cast<const u32x4_t*>(p + 4);
+    return g;
+  }
+  static __device__ __forceinline__ group zero() {
+    group g; g.lo = (u32x4_t){0, 0, 0, 0}; g.hi = g.lo; return g;
+  }
+  static __device__ __forceinline__ void store(float* p, const group& g) {
+    *reinterpret_cast<u32x4_t*>(p) = g.lo;
+    *reinterpret_cast<u32x4_t*>(p + 4) = g.hi;
+  }
+  static __device__ __forceinline__ float to_f(float v) { return v; }
+  static __device__ __forceinline__ float from_f(float v) { return v; }
+};
+
+// acc(16x16, fp32) += A(16 x 32) * B(32 x 16).
+// Lane l supplies A[row l%16][k (l/16)*8 + j] and B[k (l/16)*8 + j][col l%16],
+// j = 0..7, as one group each.  acc lane l holds D[row (l/16)*4 + r][col l%16].
+__device__ __forceinline__ f32x4_t mfma_k32(const Elt<bf16_t>::group& a, const Elt<bf16_t>::group& b,
+                                            f32x4_t acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a.v),
+                                                 __builtin_bit_cast(bf16x8_t, b.v), acc, 0, 0, 0);
+}
+
+// f32: eight 16x16x4 steps; step j takes element j of every lane's group, so
+// the four lane groups cover k = g*8 + j and all 32 k are summed.
+__device__ __forceinline__ f32x4_t mfma_k32(const Elt<float>::group& a, const Elt<float>::group& b,
+                                            f32x4_t acc) {
+  const float* av0 = reinterpret_cast<const float*>(&a.lo);
+  const float* av1 = reinterpret_cast<const float*>(&a.hi);
+  const float* bv0 = reinterpret_cast<const float*>(&b.lo);
+  const float* bv1 = reinterpret_cast<const float*>(&b.hi);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av0[j], bv0[j], acc, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av1[j], bv1[j], acc, 0, 0, 0);
+  return acc;
+}

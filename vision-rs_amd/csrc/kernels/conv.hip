@@ -1,0 +1,277 @@
+// Implicit-GEMM Conv2d + folded BatchNorm + SiLU (+ residual) for gfx950.
+//
+// Semantics (blocks/conv.rs:31-99, fused as Graph::optimise() does at
+// examples/yolo26.rs:3021): y = act(scale[co] * sum_k W[co,k] x_col[k,p] + shift[co]) + res.
+//
+// GEMM view: rows = output channels (Cout), cols = output pixels (N*Ho*Wo),
+// K = kh*kw*Cin taken in NHWC order (tap-major, channel-minor), so one group of
+// 8 consecutive k is 8 consecutive channels of one input pixel: a single
+// 16-byte load.  Weights are the MFMA A operand and pixels the B operand, so
+// each lane's accumulator quad is 4 consecutive output channels of one pixel
+// and the NHWC store is a vector store.
+//
+// Workgroup: 256 threads = 4 wave64, tile BM (Cout) x BN (pixels), BK = 32.
+// Tiles are staged through double-buffered LDS (one barrier per K step) with
+// the next step's global loads in flight during the MFMAs.
+#include "common.h"
+
+namespace {
+
+constexpr int BK = 32;
+constexpr int NT = 256;
+
+// blockIdx.x -> logical tile id so that each XCD (blocks are dealt round-robin
+// over the 8 XCDs) receives a contiguous range of tiles: neighbouring Cout
+// tiles of one pixel tile then share that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int bid, int G) {
+  const int q = G >> 3, r = G & 7;
+  const int xcd = bid & 7, idx = bid >> 3;
+  return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+}
+
+template <typename T, int BM, int BN, int WGM, int WGN, bool ALIGNED>
+__device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
+  using E = Elt<T>;
+  using G = typename E::group;
+  constexpr int PAD = 16 / sizeof(T) * 2;    // 32 bytes of row padding
+  constexpr int LDK = BK + PAD;              // LDS row stride in elements
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  constexpr int TM = WTM / 16, TN = WTN / 16;
+  constexpr int A_IT = (BM * 4 + NT - 1) / NT;
+  constexpr int B_IT = (BN * 4 + NT - 1) / NT;
+  static_assert(WGM * WGN == 4, "4 waves");
+  static_assert(TM >= 1 && TN >= 1, "tile");
+
+  __shared__ __attribute__((aligned(16))) T sA[2][BM * LDK];
+  __shared__ __attribute__((aligned(16))) T sB[2][BN * LDK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile_m = logical % a.tiles_m, tile_n = logical / a.tiles_m;
+  const int m0 = tile_m * BM;   // first output channel
+  const int n0 = tile_n * BN;   // first output pixel
+
+  const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
+  const T* __restrict__ w = reinterpret_cast<const T*>(a.w);
+  const int HWo = a.Ho * a.Wo;
+
+  // Per-thread B (pixel) chunk geometry, fixed over the K loop.
+  int b_iy0[B_IT], b_ix0[B_IT], b_grp[B_IT], b_row[B_IT];
+  int64_t b_base[B_IT];
+  bool b_ok[B_IT];
+#pragma unroll
+  for (int i = 0; i < B_IT; ++i) {
+    const int c = tid + i * NT;
+    b_row[i] = c >> 2;
+    b_grp[i] = c & 3;
+    const int m = n0 + b_row[i];
+    b_ok[i] = (c < BN * 4) && (m < a.M);
+    const int mm = b_ok[i] ? m : 0;
+    const int bb = mm / HWo, rr = mm - bb * HWo;
+    const int oy = rr / a.Wo, ox = rr - oy * a.Wo;
+    b_iy0[i] = oy * a.stride - a.pad;
+    b_ix0[i] = ox * a.stride - a.pad;
+    b_base[i] = (int64_t)bb * a.H * a.W;
+  }
+
+  G ra[A_IT], rb[B_IT];
+
+  auto load_tiles = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_IT; ++i) {
+      const int c = tid + i * NT;
+      const int row = c >> 2, k = k0 + (c & 3) * 8;
+      const int co = m0 + row;
+      if (c < BM * 4 && co < a.Cout && k < a.K)
+        ra[i] = E::load(w + (int64_t)co * a.K + k);
+      else
+        ra[i] = E::zero();
+    }
+    int tap = 0, ci0 = 0;
+    if (ALIGNED) { tap = k0 / a.Cin; ci0 = k0 - tap * a.Cin; }
+#pragma unroll
+    for (int i = 0; i < B_IT; ++i) {
+      int t = tap, ci = ci0 + b_grp[i] * 8;
+      bool ok = b_ok[i];
+      if (!ALIGNED) {
+        const int k = k0 + b_grp[i] * 8;
+        ok = ok && (k < a.K);
+        t = k / a.Cin;
+        ci = k - t * a.Cin;
+      }
+      const int ky = t / a.kw, kx = t - ky * a.kw;
+      const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
+      ok = ok && (iy >= 0) && (iy < a.H) && (ix >= 0) && (ix < a.W);
+      if (ok)
+        rb[i] = E::load(x + (b_base[i] + (int64_t)iy * a.W + ix) * a.x_pitch + ci);
+      else
+        rb[i] = E::zero();
+    }
+  };
+
+  auto store_tiles = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_IT; ++i) {
+      const int c = tid + i * NT;
+      if (c < BM * 4) E::store(&sA[buf][(c >> 2) * LDK + (c & 3) * 8], ra[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < B_IT; ++i) {
+      const int c = tid + i * NT;
+      if (c < BN * 4) E::store(&sB[buf][b_row[i] * LDK + b_grp[i] * 8], rb[i]);
+    }
+  };
+
+  f32x4_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (a.K + BK - 1) / BK;
+  load_tiles(0);
+  store_tiles(0);
+  __syncthreads();
+
+  const int frag_row = lane & 15;
+  const int frag_k = (lane >> 4) * 8;
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) load_tiles((kt + 1) * BK);
+
+    G fa[TM], fb[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      fa[i] = E::load(&sA[cur][(wm * WTM + i * 16 + frag_row) * LDK + frag_k]);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      fb[j] = E::load(&sB[cur][(wn * WTN + j * 16 + frag_row) * LDK + frag_k]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma_k32(fa[i], fb[j], acc[i][j]);
+
+    if (kt + 1 < nk) store_tiles(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: folded BN, activation, residual, store.
+  const int q = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int co = m0 + wm * WTM + i * 16 + q * 4;
+    if (co >= a.Cout) continue;
+    float sc[4], sh[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = co + r < a.Cout ? co + r : a.Cout - 1;
+      sc[r] = a.scale[c];
+      sh[r] = a.shift[c];
+    }
+    const bool full4 = (co + 3 < a.Cout);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int m = n0 + wn * WTN + j * 16 + (lane & 15);
+      if (m >= a.M) continue;
+      const int bb = m / HWo, pp = m - bb * HWo;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float t = acc[i][j][r] * sc[r] + sh[r];
+        if (a.act == VRS_ACT_SILU) t = silu_f(t);
+        v[r] = t;
+      }
+      if (a.res) {
+        const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + (int64_t)co * a.r_sc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (co + r < a.Cout) v[r] += E::to_f(rp[r * a.r_sc]);
+      }
+      const int64_t yo = bb * a.y_sb + pp * a.y_sp + (int64_t)co * a.y_sc;
+      if (a.y_f32) {
+        float* yp = reinterpret_cast<float*>(a.y) + yo;
+        if (a.y_sc == 1 && full4) {
+          *reinterpret_cast<f32x4_t*>(yp) = (f32x4_t){v[0], v[1], v[2], v[3]};
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (co + r < a.Cout) yp[r * a.y_sc] = v[r];
+        }
+      } else {
+        T* yp = reinterpret_cast<T*>(a.y) + yo;
+        if (sizeof(T) == 2 && a.y_sc == 1 && full4) {
+          const uint32_t lo = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+          const uint32_t hi = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+          *reinterpret_cast<u32x2_t*>(yp) = (u32x2_t){lo, hi};
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (co + r < a.Cout) yp[r * a.y_sc] = E::from_f(v[r]);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+#define VRS_CONV_KERNEL(NAME, T, BM, BN, WGM, WGN, AL)                                  \
+  extern "C" __global__ __launch_bounds__(256) void NAME(vrs_conv_args a) {            \
+    conv_body<T, BM, BN, WGM, WGN, AL>(a);                                              \
+  }
+
+// bf16 tiles: 128x128 (2x2 waves of 64x64), 64x256 (1x4 waves of 64x64),
+// 32x256 (1x4 waves of 32x64) for narrow Cout.
+VRS_CONV_KERNEL(vrs_conv_bf16_128x128_a, bf16_t, 128, 128, 2, 2, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_128x128_g, bf16_t, 128, 128, 2, 2, false)
+VRS_CONV_KERNEL(vrs_conv_bf16_64x256_a, bf16_t, 64, 256, 1, 4, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_64x256_g, bf16_t, 64, 256, 1, 4, false)
+VRS_CONV_KERNEL(vrs_conv_bf16_32x256_a, bf16_t, 32, 256, 1, 4, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_32x256_g, bf16_t, 32, 256, 1, 4, false)
+// f32 (parity path, fp32 MFMA)
+VRS_CONV_KERNEL(vrs_conv_f32_128x128_a, float, 128, 128, 2, 2, true)
+VRS_CONV_KERNEL(vrs_conv_f32_128x128_g, float, 128, 128, 2, 2, false)
+VRS_CONV_KERNEL(vrs_conv_f32_64x256_a, float, 64, 256, 1, 4, true)
+VRS_CONV_KERNEL(vrs_conv_f32_64x256_g, float, 64, 256, 1, 4, false)
+VRS_CONV_KERNEL(vrs_conv_f32_32x256_a, float, 32, 256, 1, 4, true)
+VRS_CONV_KERNEL(vrs_conv_f32_32x256_g, float, 32, 256, 1, 4, false)
+
+// ---------------------------------------------------------------------------
+// NCHW float32 image batch -> NHWC (element type) with zero channel padding.
+// One thread per output pixel; the c_pad (<= 8) channels go out as one group.
+template <typename T>
+__device__ __forceinline__ void pack_body(const vrs_pack_args& a) {
+  const int64_t HW = (int64_t)a.H * a.W;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.N * HW) return;
+  const int64_t b = i / HW, p = i - b * HW;
+  T* y = reinterpret_cast<T*>(a.y) + i * a.c_pad;
+  for (int c = 0; c < a.c_pad; ++c) {
+    const float v = c < a.C ? a.x[(b * a.C + c) * HW + p] : 0.f;
+    y[c] = Elt<T>::from_f(v);
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void vrs_pack_nchw_bf16(vrs_pack_args a) { pack_body<bf16_t>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_pack_nchw_f32(vrs_pack_args a) { pack_body<float>(a); }
+
+// NHWC view (element type) -> NCHW float32, one thread per output element.
+template <typename T>
+__device__ __forceinline__ void unpack_body(const vrs_pack_args& a) {
+  // reuse of vrs_pack_args: x = source view base (pre-offset), y = float32 NCHW,
+  // N, C (channels of the view), H, W, c_pad = source pitch
+  const int64_t HW = (int64_t)a.H * a.W;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.N * a.C * HW) return;
+  const int64_t p = i % HW, bc = i / HW;
+  const int64_t c = bc % a.C, b = bc / a.C;
+  const T* src = reinterpret_cast<const T*>(a.x);
+  reinterpret_cast<float*>(a.y)[i] = Elt<T>::to_f(src[(b * HW + p) * a.c_pad + c]);
+}
+
+extern "C" __global__ __launch_bounds__(256) void vrs_unpack_nchw_bf16(vrs_pack_args a) { unpack_body<bf16_t>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_unpack_nchw_f32(vrs_pack_args a) { unpack_body<float>(a); }

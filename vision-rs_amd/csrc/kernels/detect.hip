@@ -1,0 +1,160 @@
+// Detect-head post-processing on gfx950.
+//
+// Stage 1 (one thread per anchor): LTRB -> xywh decode, sigmoid per class,
+// argmax, threshold -- the host loops of examples/yolo26.rs:1488-1528 with
+// the anchor grid of loss/anchor.rs:47-66.  The argmax follows Rust's
+// Iterator::max_by with partial_cmp().unwrap_or(Equal): the running best is
+// kept only if it compares Greater, so the last of equal maxima wins and a
+// NaN compares Equal.  A kept anchor gets the unique 64-bit key
+// (score_bits << 32) | (0xffffffff - anchor): ordering keys descending is the
+// stable descending sort of examples/yolo26.rs:1529 (equal scores keep
+// ascending anchor order); sigmoid scores are non-negative so their IEEE bits
+// order like the values.
+//
+// Stage 2 (one workgroup per image): exact top-k.  A most-significant-digit
+// radix select over the keys finds the k-th largest key (k = min(count,
+// max_det)); the keys >= it are gathered into LDS and bitonic-sorted.
+#include "common.h"
+
+extern "C" __global__ __launch_bounds__(256) void vrs_detect_stage1(vrs_det1_args a) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.B * a.A) return;
+  const int b = (int)(i / a.A), ai = (int)(i - (int64_t)b * a.A);
+  int s = 0;
+  while (s + 1 < a.nscales && ai >= a.a_base[s + 1]) ++s;
+  const int as = (s + 1 < a.nscales ? a.a_base[s + 1] : a.A) - a.a_base[s];
+  const int j = ai - a.a_base[s];
+  const float st = a.stride[s];
+  const float* bb = a.boxes + (int64_t)b * 4 * a.A + 4 * (int64_t)a.a_base[s];
+  const float l = bb[j], t = bb[as + j], r = bb[2 * as + j], bo = bb[3 * as + j];
+  const float cx = ((float)(j % a.fw[s]) + 0.5f) * st;
+  const float cy = ((float)(j / a.fw[s]) + 0.5f) * st;
+  float* xy = a.xywh + i * 4;
+  xy[0] = cx + st * (r - l) * 0.5f;
+  xy[1] = cy + st * (bo - t) * 0.5f;
+  xy[2] = st * (l + r);
+  xy[3] = st * (t + bo);
+
+  const float* sc = a.scores + (int64_t)b * a.nc * a.A + (int64_t)a.nc * a.a_base[s] + j;
+  float best = 1.0f / (1.0f + expf(-sc[0]));
+  int bc = 0;
+  for (int c = 1; c < a.nc; ++c) {
+    const float v = 1.0f / (1.0f + expf(-sc[(int64_t)c * as]));
+    if (!(best > v)) { best = v; bc = c; }
+  }
+  a.cls[i] = bc;
+  a.keys[i] = (best >= a.thr) ? (((uint64_t)__float_as_uint(best)) << 32) | (uint64_t)(0xffffffffu - (uint32_t)ai)
+                              : 0ull;
+}
+
+namespace {
+constexpr int TOPK_MAX = 1024;
+}
+
+extern "C" __global__ __launch_bounds__(1024) void vrs_detect_stage2(vrs_det2_args a) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint64_t sel[TOPK_MAX];
+  __shared__ uint32_t s_count, s_nsel, s_digit, s_krem;
+  const int b = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
+  const uint64_t* keys = a.keys + (int64_t)b * a.A;
+
+  if (tid == 0) { s_count = 0; s_nsel = 0; }
+  __syncthreads();
+  uint32_t local = 0;
+  for (int i = tid; i < a.A; i += nt) local += keys[i] != 0ull;
+  atomicAdd(&s_count, local);
+  __syncthreads();
+  const uint32_t count = s_count;
+  const uint32_t k = count < (uint32_t)a.max_det ? count : (uint32_t)a.max_det;
+
+  uint64_t prefix = 0, pmask = 0;
+  if (tid == 0) s_krem = k;
+  for (int shift = 56; shift >= 0 && k > 0; shift -= 8) {
+    for (int i = tid; i < 256; i += nt) hist[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < a.A; i += nt) {
+      const uint64_t key = keys[i];
+      if (key != 0ull && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t cum = 0, krem = s_krem;
+      int d = 255;
+      for (; d > 0; --d) {
+        if (cum + hist[d] >= krem) break;
+        cum += hist[d];
+      }
+      s_digit = (uint32_t)d;
+      s_krem = krem - cum;
+    }
+    __syncthreads();
+    prefix |= ((uint64_t)s_digit) << shift;
+    pmask |= 255ull << shift;
+    __syncthreads();
+  }
+  const uint64_t kth = prefix;  // exact k-th largest key (keys are unique)
+
+  for (int i = tid; i < TOPK_MAX; i += nt) sel[i] = 0ull;
+  __syncthreads();
+  if (k > 0)
+    for (int i = tid; i < a.A; i += nt) {
+      const uint64_t key = keys[i];
+      if (key != 0ull && key >= kth) {
+        const uint32_t slot = atomicAdd(&s_nsel, 1u);
+        if (slot < (uint32_t)TOPK_MAX) sel[slot] = key;
+      }
+    }
+  __syncthreads();
+
+  // bitonic sort, descending, over TOPK_MAX slots (zeros sink to the end)
+  for (int size = 2; size <= TOPK_MAX; size <<= 1)
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < TOPK_MAX; i += nt) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const bool desc = (i & size) == 0;
+          const uint64_t x = sel[i], y = sel[j];
+          if (desc ? (x < y) : (x > y)) { sel[i] = y; sel[j] = x; }
+        }
+      }
+      __syncthreads();
+    }
+
+  if (tid == 0) a.count[b] = (int32_t)k;
+  for (int i = tid; i < a.max_det; i += nt) {
+    const int64_t o = (int64_t)b * a.max_det + i;
+    if ((uint32_t)i < k) {
+      const uint64_t key = sel[i];
+      const int anchor = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+      a.out_score[o] = __uint_as_float((uint32_t)(key >> 32));
+      a.out_anchor[o] = anchor;
+      a.out_cls[o] = a.cls[(int64_t)b * a.A + anchor];
+      const float* xy = a.xywh + ((int64_t)b * a.A + anchor) * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a.out_xywh[o * 4 + q] = xy[q];
+    } else {
+      a.out_score[o] = 0.f;
+      a.out_anchor[o] = -1;
+      a.out_cls[o] = -1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a.out_xywh[o * 4 + q] = 0.f;
+    }
+  }
+}
+
+// Grid-unit decode on [B,4,A] rows l,t,r,b (kernels/detect_decode.rs:36-86):
+// cx = (ax - l + ax + r) * 0.5 * s, cy likewise, w = (r + l) * s, h = (b + t) * s.
+extern "C" __global__ __launch_bounds__(256) void vrs_detect_decode_grid(vrs_dec_args a) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.B * a.A) return;
+  const int b = (int)(i / a.A), ai = (int)(i - (int64_t)b * a.A);
+  const float* bx = a.boxes + (int64_t)b * 4 * a.A;
+  float* o = a.out + (int64_t)b * 4 * a.A;
+  const float x1 = a.ax[ai] - bx[ai], y1 = a.ay[ai] - bx[a.A + ai];
+  const float x2 = a.ax[ai] + bx[2 * a.A + ai], y2 = a.ay[ai] + bx[3 * a.A + ai];
+  const float s = a.st[ai];
+  o[ai] = (x1 + x2) * 0.5f * s;
+  o[a.A + ai] = (y1 + y2) * 0.5f * s;
+  o[2 * a.A + ai] = (x2 - x1) * s;
+  o[3 * a.A + ai] = (y2 - y1) * s;
+}

@@ -1,0 +1,196 @@
+// Bandwidth-bound NHWC kernels for gfx950: depthwise conv, the SPPF pooling
+// cascade and nearest 2x upsample.  No MFMA: these move bytes, so each lane
+// moves 8 consecutive channels (one 16-byte bf16 group) and consecutive lanes
+// walk the channel dimension first for coalesced HBM access.
+#include "common.h"
+
+// ---------------------------------------------------------------------------
+// Depthwise conv + folded BN (+ SiLU): blocks/conv.rs:75-85 (dwconv) and the
+// PE conv_bn with g = c (blocks/c2psa.rs:66).  One thread computes 8 channels
+// of OUT_ROWS vertically adjacent output pixels, so each loaded input row is
+// reused by up to 3 outputs.
+namespace {
+constexpr int DW_ROWS = 4;
+
+template <typename T>
+__device__ __forceinline__ void dw_body(const vrs_dw_args& a) {
+  using E = Elt<T>;
+  const int cg = a.C >> 3;                       // channel groups of 8
+  const int row_tiles = (a.Ho + DW_ROWS - 1) / DW_ROWS;
+  const int64_t total = (int64_t)a.N * row_tiles * a.Wo * cg;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int g = (int)(i % cg);
+  int64_t t = i / cg;
+  const int ox = (int)(t % a.Wo); t /= a.Wo;
+  const int rt = (int)(t % row_tiles);
+  const int b = (int)(t / row_tiles);
+  const int c0 = g * 8;
+  const int oy0 = rt * DW_ROWS;
+
+  float wv[9][8];
+  const int taps = a.kh * a.kw;
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    for (int k = 0; k < 9; ++k) wv[k][c] = k < taps ? a.w[(c0 + c) * taps + k] : 0.f;
+
+  float acc[DW_ROWS][8];
+#pragma unroll
+  for (int r = 0; r < DW_ROWS; ++r)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[r][c] = 0.f;
+
+  const T* x = reinterpret_cast<const T*>(a.x);
+  // input rows touched by DW_ROWS outputs: (DW_ROWS-1)*stride + kh
+  const int iy_first = oy0 * a.stride - a.pad;
+  const int nrows = (DW_ROWS - 1) * a.stride + a.kh;
+  for (int rr = 0; rr < nrows; ++rr) {
+    const int iy = iy_first + rr;
+    if (iy < 0 || iy >= a.H) continue;
+    for (int kx = 0; kx < a.kw; ++kx) {
+      const int ix = ox * a.stride - a.pad + kx;
+      if (ix < 0 || ix >= a.W) continue;
+      typename E::group gv = E::load(x + (((int64_t)b * a.H + iy) * a.W + ix) * a.x_pitch + c0);
+      const T* ev = reinterpret_cast<const T*>(&gv);
+      float xv[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) xv[c] = E::to_f(ev[c]);
+#pragma unroll
+      for (int r = 0; r < DW_ROWS; ++r) {
+        const int ky = rr - r * a.stride;   // tap row for output row oy0 + r
+        if (ky < 0 || ky >= a.kh) continue;
+        const int k = ky * a.kw + kx;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[r][c] += wv[k][c] * xv[c];
+      }
+    }
+  }
+  T* y = reinterpret_cast<T*>(a.y);
+  float sc[8], sh[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) { sc[c] = a.scale[c0 + c]; sh[c] = a.shift[c0 + c]; }
+#pragma unroll
+  for (int r = 0; r < DW_ROWS; ++r) {
+    const int oy = oy0 + r;
+    if (oy >= a.Ho) break;
+    typename E::group out;
+    T* ov = reinterpret_cast<T*>(&out);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float v = acc[r][c] * sc[c] + sh[c];
+      if (a.act == VRS_ACT_SILU) v = silu_f(v);
+      ov[c] = E::from_f(v);
+    }
+    E::store(y + (((int64_t)b * a.Ho + oy) * a.Wo + ox) * a.y_pitch + c0, out);
+  }
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv_bf16(vrs_dw_args a) { dw_body<bf16_t>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv_f32(vrs_dw_args a) { dw_body<float>(a); }
+
+// ---------------------------------------------------------------------------
+// SPPF pooling cascade (blocks/sppf.rs:43-61): p1 = max5(y), p2 = max5(p1),
+// p3 = max5(p2), stride 1, pad 2 with -inf semantics (windows clipped to the
+// map, teeny-core MaxPool2d::with_padding at blocks/sppf.rs:48-50).
+// One workgroup owns one image and 8*cgroups_per_block channels; the plane is
+// staged in LDS and every 5x5 max is done separably (row pass, column pass).
+// Max of stored values is exact, so LDS keeps the element type.
+namespace {
+constexpr int POOL_LDS_BYTES = 48 * 1024;
+
+template <typename T>
+__device__ __forceinline__ void pool_body(const vrs_pool_args& a) {
+  using E = Elt<T>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int HW = a.H * a.W;
+  const int CG = a.cgroups_per_block;             // channel groups of 8 per block
+  const int groups_total = a.c >> 3;
+  const int blocks_per_img = (groups_total + CG - 1) / CG;
+  const int b = blockIdx.x / blocks_per_img;
+  const int g0 = (blockIdx.x % blocks_per_img) * CG;
+  const int ng = min(CG, groups_total - g0);
+  // two planes of [HW][ng*8] elements: cur and tmp
+  T* cur = reinterpret_cast<T*>(smem);
+  T* tmp = cur + (size_t)HW * CG * 8;
+  T* base = reinterpret_cast<T*>(a.buf) + (int64_t)b * HW * a.pitch;
+  const int nvec = HW * ng;  // (pixel, group) items
+
+  for (int it = threadIdx.x; it < nvec; it += blockDim.x) {
+    const int p = it / ng, g = it - p * ng;
+    E::store(cur + ((size_t)p * CG + g) * 8, E::load(base + (int64_t)p * a.pitch + (g0 + g) * 8));
+  }
+  __syncthreads();
+  for (int stage = 1; stage <= 3; ++stage) {
+    // row pass: tmp = max over x-window of cur
+    for (int it = threadIdx.x; it < nvec; it += blockDim.x) {
+      const int p = it / ng, g = it - p * ng;
+      const int y = p / a.W, xx = p - y * a.W;
+      float m[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) m[c] = -INFINITY;
+      for (int dx = -2; dx <= 2; ++dx) {
+        const int xs = xx + dx;
+        if (xs < 0 || xs >= a.W) continue;
+        const T* s = cur + ((size_t)(y * a.W + xs) * CG + g) * 8;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) m[c] = fmaxf(m[c], E::to_f(s[c]));
+      }
+      T* d = tmp + ((size_t)p * CG + g) * 8;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) d[c] = E::from_f(m[c]);
+    }
+    __syncthreads();
+    // column pass: cur = max over y-window of tmp; also write to the buffer
+    for (int it = threadIdx.x; it < nvec; it += blockDim.x) {
+      const int p = it / ng, g = it - p * ng;
+      const int y = p / a.W, xx = p - y * a.W;
+      float m[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) m[c] = -INFINITY;
+      for (int dy = -2; dy <= 2; ++dy) {
+        const int ys = y + dy;
+        if (ys < 0 || ys >= a.H) continue;
+        const T* s = tmp + ((size_t)(ys * a.W + xx) * CG + g) * 8;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) m[c] = fmaxf(m[c], E::to_f(s[c]));
+      }
+      typename E::group out;
+      T* ov = reinterpret_cast<T*>(&out);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) ov[c] = E::from_f(m[c]);
+      E::store(cur + ((size_t)p * CG + g) * 8, out);
+      E::store(base + (int64_t)p * a.pitch + stage * a.c + (g0 + g) * 8, out);
+    }
+    __syncthreads();
+  }
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void vrs_sppf_pool_bf16(vrs_pool_args a) { pool_body<bf16_t>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_sppf_pool_f32(vrs_pool_args a) { pool_body<float>(a); }
+
+// ---------------------------------------------------------------------------
+// Nearest 2x upsample (blocks/upsample.rs:23-35) into a channel slice of a
+// concat buffer (blocks/concat.rs:24-38): y[b, oy, ox, c] = x[b, oy/2, ox/2, c].
+template <typename T>
+__device__ __forceinline__ void up_body(const vrs_up_args& a) {
+  using E = Elt<T>;
+  const int cg = a.C >> 3;
+  const int Ho = a.H * 2, Wo = a.W * 2;
+  const int64_t total = (int64_t)a.N * Ho * Wo * cg;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int g = (int)(i % cg);
+  int64_t t = i / cg;
+  const int ox = (int)(t % Wo); t /= Wo;
+  const int oy = (int)(t % Ho);
+  const int b = (int)(t / Ho);
+  const T* x = reinterpret_cast<const T*>(a.x);
+  T* y = reinterpret_cast<T*>(a.y);
+  E::store(y + (((int64_t)b * Ho + oy) * Wo + ox) * a.y_pitch + g * 8,
+           E::load(x + (((int64_t)b * a.H + (oy >> 1)) * a.W + (ox >> 1)) * a.x_pitch + g * 8));
+}
+
+extern "C" __global__ __launch_bounds__(256) void vrs_upsample2x_bf16(vrs_up_args a) { up_body<bf16_t>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_upsample2x_f32(vrs_up_args a) { up_body<float>(a); }

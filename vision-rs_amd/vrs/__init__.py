@@ -1,0 +1,355 @@
+"""Python binding of the vision-rs MI355X hot path (include/vrs.h) over ctypes.
+
+The product is the C ABI in vision-rs_amd/lib/libvrs.so plus the gfx950 code
+objects next to it; this module only marshals arguments.  torch provides
+device memory and the current stream (plumbing); every computation runs in the
+HIP kernels.  There is no CPU fallback: if the library or code objects are
+missing, loading fails with an error.
+
+Layer/op names mirror the reference crate: conv / conv_bn / dwconv /
+conv_plain (blocks/conv.rs), c3k2, c3k2_psa (blocks/c3k2.rs), c2psa and
+psa_attention (blocks/c2psa.rs), sppf (blocks/sppf.rs), detect
+(blocks/detect.rs), yolo26 (yolo26/mod.rs).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_DIR = os.path.join(PKG, "lib")
+SO = os.path.join(LIB_DIR, "libvrs.so")
+
+VRS_OK = 0
+F32, BF16 = 0, 1
+ACT_NONE, ACT_SILU = 0, 1
+BLOCK_CONV, BLOCK_C3K2, BLOCK_C3K2_PSA, BLOCK_C2PSA, BLOCK_SPPF, BLOCK_PSA_ATTN, BLOCK_DETECT_BOX, BLOCK_YOLO26 = \
+    1, 2, 3, 4, 5, 6, 7, 8
+CONV_BN_SILU, CONV_BN, CONV_PLAIN = 0, 1, 2
+
+ERRORS = {-1: "EINVAL", -2: "EBADSHAPE", -3: "EUNSUPPORTED", -4: "ENOMODULE", -5: "EHIP", -6: "ENOTFOUND",
+          -7: "ESTATE"}
+
+
+class VrsError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"vrs error {code} ({ERRORS.get(code, '?')}): {msg}")
+        self.code = code
+
+
+class Nhwc(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("n", C.c_int32), ("h", C.c_int32), ("w", C.c_int32), ("c", C.c_int32),
+                ("pitch", C.c_int32), ("c_off", C.c_int32)]
+
+
+class ConvDesc(C.Structure):
+    _fields_ = [("k", C.c_int32), ("stride", C.c_int32), ("groups", C.c_int32), ("act", C.c_int32),
+                ("dtype", C.c_int32)]
+
+
+class PsaDesc(C.Structure):
+    _fields_ = [("heads", C.c_int32), ("key_dim", C.c_int32), ("head_dim", C.c_int32), ("dtype", C.c_int32)]
+
+
+class DetectDesc(C.Structure):
+    _fields_ = [("n", C.c_int32), ("nc", C.c_int32), ("img_h", C.c_int32), ("img_w", C.c_int32),
+                ("nscales", C.c_int32), ("strides", C.c_int32 * 4), ("thr", C.c_float), ("max_det", C.c_int32)]
+
+
+class MsdaDesc(C.Structure):
+    _fields_ = [("n", C.c_int32), ("q", C.c_int32), ("heads", C.c_int32), ("head_dim", C.c_int32),
+                ("levels", C.c_int32), ("points", C.c_int32), ("level_h", C.c_int32 * 8),
+                ("level_w", C.c_int32 * 8)]
+
+
+class BlockDesc(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("c_in", C.c_int32), ("c_out", C.c_int32), ("k", C.c_int32), ("s", C.c_int32),
+                ("g", C.c_int32), ("conv_kind", C.c_int32), ("n", C.c_int32), ("c3k", C.c_int32),
+                ("shortcut", C.c_int32), ("e", C.c_float), ("heads", C.c_int32), ("nc", C.c_int32),
+                ("variant", C.c_int32), ("one2one", C.c_int32)]
+
+
+# Every exported symbol of include/vrs.h with its ctypes signature.
+_vp, _i32, _i64, _f32, _sz = C.c_void_p, C.c_int32, C.c_int64, C.c_float, C.c_size_t
+_P = C.POINTER
+SIGNATURES = {
+    "vrs_last_error": (C.c_char_p, []),
+    "vrs_version": (C.c_char_p, []),
+    "vrs_ctx_create": (C.c_int, [C.c_int, C.c_char_p, _P(_vp)]),
+    "vrs_ctx_destroy": (C.c_int, [_vp]),
+    "vrs_conv2d": (C.c_int, [_vp, _P(ConvDesc), _P(Nhwc), _vp, _vp, _vp, _P(Nhwc), _P(Nhwc), _vp]),
+    "vrs_pack_conv_weight": (_i64, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "vrs_bn_fold": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _i32, _vp, _vp]),
+    "vrs_pack_input": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _P(Nhwc), _i32, _vp]),
+    "vrs_unpack_output": (C.c_int, [_vp, _P(Nhwc), _i32, _vp, _vp]),
+    "vrs_sppf_pool": (C.c_int, [_vp, _P(Nhwc), _i32, _vp]),
+    "vrs_upsample2x": (C.c_int, [_vp, _P(Nhwc), _P(Nhwc), _i32, _vp]),
+    "vrs_psa_attention": (C.c_int, [_vp, _P(PsaDesc), _P(Nhwc), _vp, _vp, _vp, _P(Nhwc), _vp]),
+    "vrs_detect_workspace_size": (_sz, [_P(DetectDesc)]),
+    "vrs_detect_postprocess": (C.c_int, [_vp, _P(DetectDesc), _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "vrs_detect_decode_grid": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
+    "vrs_msda": (C.c_int, [_vp, _P(MsdaDesc), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "vrs_model_create": (C.c_int, [_vp, _P(BlockDesc), _i32, _i32, _i32, _i32, _f32, _P(_vp)]),
+    "vrs_model_num_params": (C.c_int, [_vp]),
+    "vrs_model_param_info": (C.c_int, [_vp, _i32, _P(C.c_char_p), _P(_i32), _P(_i32)]),
+    "vrs_model_load_param": (C.c_int, [_vp, C.c_char_p, _vp, _i64]),
+    "vrs_model_finalize": (C.c_int, [_vp]),
+    "vrs_model_num_outputs": (C.c_int, [_vp]),
+    "vrs_model_output_info": (C.c_int, [_vp, _i32, _P(_i64), _P(_i32), _P(_i32)]),
+    "vrs_model_forward": (C.c_int, [_vp, _vp, _P(_vp), _vp]),
+    "vrs_model_capture": (C.c_int, [_vp, _vp, _P(_vp), _vp]),
+    "vrs_model_replay": (C.c_int, [_vp, _vp]),
+    "vrs_model_num_launches": (C.c_int, [_vp]),
+    "vrs_model_launch_name": (C.c_char_p, [_vp, _i32]),
+    "vrs_model_launch_work": (C.c_int, [_vp, _i32, _P(C.c_double), _P(C.c_double)]),
+    "vrs_model_run_launches": (C.c_int, [_vp, _i32, _i32, _vp]),
+    "vrs_model_destroy": (C.c_int, [_vp]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libvrs.so (raises if it was not built: there is no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(SO):
+            raise RuntimeError(f"{SO} not built: run `python vision-rs_amd/build.py` (no CPU fallback exists)")
+        L = C.CDLL(SO)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> int:
+    if rc < 0:
+        raise VrsError(rc, lib().vrs_last_error().decode())
+    return rc
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    if stream is not None:
+        return C.c_void_p(stream)
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def nhwc(t, c=None, c_off=0):
+    """View of a [n, h, w, pitch] torch tensor (channels [c_off, c_off+c))."""
+    n, h, w, pitch = t.shape
+    return Nhwc(t.data_ptr(), n, h, w, pitch - c_off if c is None else c, pitch, c_off)
+
+
+def dtype_code(torch_dtype) -> int:
+    import torch
+    if torch_dtype == torch.bfloat16:
+        return BF16
+    if torch_dtype == torch.float32:
+        return F32
+    raise ValueError(f"unsupported dtype {torch_dtype}")
+
+
+class Context:
+    """vrs_ctx: one device, all code objects loaded (CudaGraphCompiler::load analogue)."""
+
+    def __init__(self, device: int = 0):
+        self.handle = C.c_void_p()
+        check(lib().vrs_ctx_create(device, LIB_DIR.encode(), C.byref(self.handle)))
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            lib().vrs_ctx_destroy(self.handle)
+            self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- single ops --------------------------------------------------------
+    def conv2d(self, x, w, scale, shift, y, k, stride=1, groups=1, act=ACT_SILU, res=None, dtype=BF16,
+               stream=None):
+        """x, y, res: Nhwc views; w/scale/shift: device tensors."""
+        d = ConvDesc(k, stride, groups, act, dtype)
+        check(lib().vrs_conv2d(self.handle, C.byref(d), C.byref(x), _ptr(w), _ptr(scale), _ptr(shift),
+                               C.byref(res) if res is not None else None, C.byref(y), _stream(stream)))
+
+    def pack_input(self, x_nchw, y, dtype, stream=None):
+        n, c, h, w = x_nchw.shape
+        check(lib().vrs_pack_input(self.handle, _ptr(x_nchw), n, c, h, w, C.byref(y), dtype, _stream(stream)))
+
+    def unpack_output(self, x, dtype, y_nchw, stream=None):
+        check(lib().vrs_unpack_output(self.handle, C.byref(x), dtype, _ptr(y_nchw), _stream(stream)))
+
+    def sppf_pool(self, buf, dtype, stream=None):
+        check(lib().vrs_sppf_pool(self.handle, C.byref(buf), dtype, _stream(stream)))
+
+    def upsample2x(self, x, y, dtype, stream=None):
+        check(lib().vrs_upsample2x(self.handle, C.byref(x), C.byref(y), dtype, _stream(stream)))
+
+    def psa_attention(self, qkv, pe_w, pe_scale, pe_shift, out, heads, dtype, stream=None):
+        d = PsaDesc(heads, 32, 64, dtype)
+        check(lib().vrs_psa_attention(self.handle, C.byref(d), C.byref(qkv), _ptr(pe_w), _ptr(pe_scale),
+                                      _ptr(pe_shift), C.byref(out), _stream(stream)))
+
+    def detect_postprocess(self, boxes, scores, nc, img_h, img_w, strides=(8, 16, 32), thr=0.25, max_det=300,
+                           stream=None):
+        import torch
+        n = boxes.shape[0]
+        st = (C.c_int32 * 4)(*list(strides), *([0] * (4 - len(strides))))
+        d = DetectDesc(n, nc, img_h, img_w, len(strides), st, thr, max_det)
+        ws_bytes = lib().vrs_detect_workspace_size(C.byref(d))
+        if ws_bytes == 0:
+            raise VrsError(-1, lib().vrs_last_error().decode())
+        dev = boxes.device
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        count = torch.empty(n, dtype=torch.int32, device=dev)
+        score = torch.empty(n, max_det, dtype=torch.float32, device=dev)
+        cls = torch.empty(n, max_det, dtype=torch.int32, device=dev)
+        anchor = torch.empty(n, max_det, dtype=torch.int32, device=dev)
+        xywh = torch.empty(n, max_det, 4, dtype=torch.float32, device=dev)
+        check(lib().vrs_detect_postprocess(self.handle, C.byref(d), _ptr(boxes), _ptr(scores), _ptr(ws), ws_bytes,
+                                           _ptr(count), _ptr(score), _ptr(cls), _ptr(anchor), _ptr(xywh),
+                                           _stream(stream)))
+        return count, score, cls, anchor, xywh
+
+    def detect_decode_grid(self, boxes, ax, ay, strides, out, stream=None):
+        n, _, a = boxes.shape
+        check(lib().vrs_detect_decode_grid(self.handle, _ptr(boxes), _ptr(ax), _ptr(ay), _ptr(strides), n, a,
+                                           _ptr(out), _stream(stream)))
+
+    def msda(self, value, shapes, ref, off, attw, out, stream=None):
+        n, s, heads, dh = value.shape
+        _, q, _, L, P, _ = off.shape
+        lh = (C.c_int32 * 8)(*[h for h, _ in shapes], *([0] * (8 - L)))
+        lw = (C.c_int32 * 8)(*[w for _, w in shapes], *([0] * (8 - L)))
+        d = MsdaDesc(n, q, heads, dh, L, P, lh, lw)
+        check(lib().vrs_msda(self.handle, C.byref(d), _ptr(value), _ptr(ref), _ptr(off), _ptr(attw), _ptr(out),
+                             _stream(stream)))
+
+
+def pack_conv_weight(w_oihw, groups=1, cin_pad=None, dtype=BF16):
+    """Host repack (numpy float32 OIHW) -> bytes in the device layout."""
+    import numpy as np
+    w = np.ascontiguousarray(w_oihw, dtype=np.float32)
+    cout, cin_g, k, _ = w.shape
+    cin_pad = cin_g if cin_pad is None else cin_pad
+    n = check(lib().vrs_pack_conv_weight(None, cout, cin_g, k, groups, cin_pad, dtype, None))
+    out = np.empty(n, np.uint8)
+    check(lib().vrs_pack_conv_weight(w.ctypes.data, cout, cin_g, k, groups, cin_pad, dtype, out.ctypes.data))
+    return out
+
+
+def bn_fold(gamma, beta, mean, var, eps):
+    import numpy as np
+    c = gamma.shape[0]
+    s = np.empty(c, np.float32); t = np.empty(c, np.float32)
+    arrs = [np.ascontiguousarray(a, np.float32) for a in (gamma, beta, mean, var)]
+    check(lib().vrs_bn_fold(*[a.ctypes.data for a in arrs], eps, c, s.ctypes.data, t.ctypes.data))
+    return s, t
+
+
+class Model:
+    """vrs_model: a recorded block/network with its parameters and buffers.
+
+    Mirrors the reference's flow: build closures -> load_param_f32 per name ->
+    forward / capture_graph + run_inplace."""
+
+    def __init__(self, ctx, desc: BlockDesc, batch: int, h: int, w: int, dtype=BF16, bn_eps=1e-3):
+        """ctx=None records the layers only (params()/output_shapes() work without a GPU)."""
+        self.ctx = ctx
+        self.desc = desc
+        self.batch, self.h, self.w, self.dtype = batch, h, w, dtype
+        self.handle = C.c_void_p()
+        check(lib().vrs_model_create(ctx.handle if ctx is not None else None, C.byref(desc), batch, h, w, dtype,
+                                     bn_eps, C.byref(self.handle)))
+
+    def params(self):
+        """[(name, shape)] in recording order (the reference's name_scope paths)."""
+        out = []
+        n = check(lib().vrs_model_num_params(self.handle))
+        for i in range(n):
+            name = C.c_char_p()
+            dims = (C.c_int32 * 4)()
+            nd = C.c_int32()
+            check(lib().vrs_model_param_info(self.handle, i, C.byref(name), dims, C.byref(nd)))
+            out.append((name.value.decode(), tuple(dims[j] for j in range(nd.value))))
+        return out
+
+    def load(self, P: dict):
+        import numpy as np
+        for name, shape in self.params():
+            a = np.ascontiguousarray(P[name], dtype=np.float32).reshape(shape)
+            check(lib().vrs_model_load_param(self.handle, name.encode(), a.ctypes.data, a.size))
+        check(lib().vrs_model_finalize(self.handle))
+        return self
+
+    def output_shapes(self):
+        out = []
+        for i in range(check(lib().vrs_model_num_outputs(self.handle))):
+            numel = C.c_int64()
+            dims = (C.c_int32 * 4)()
+            nd = C.c_int32()
+            check(lib().vrs_model_output_info(self.handle, i, C.byref(numel), dims, C.byref(nd)))
+            out.append(tuple(dims[j] for j in range(nd.value)))
+        return out
+
+    def alloc_outputs(self, device="cuda"):
+        import torch
+        return [torch.empty(s, dtype=torch.float32, device=device) for s in self.output_shapes()]
+
+    def forward(self, x, outs=None, stream=None):
+        if outs is None:
+            outs = self.alloc_outputs(x.device)
+        ptrs = (C.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+        check(lib().vrs_model_forward(self.handle, _ptr(x), ptrs, _stream(stream)))
+        return outs
+
+    def capture(self, x, outs, stream):
+        ptrs = (C.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+        check(lib().vrs_model_capture(self.handle, _ptr(x), ptrs, C.c_void_p(stream)))
+
+    def replay(self, stream):
+        check(lib().vrs_model_replay(self.handle, C.c_void_p(stream)))
+
+    def launch_names(self):
+        n = lib().vrs_model_num_launches(self.handle)
+        return [lib().vrs_model_launch_name(self.handle, i).decode() for i in range(n)]
+
+    def launch_work(self):
+        """[(flops, bytes)] per launch of the prepared forward."""
+        out = []
+        for i in range(lib().vrs_model_num_launches(self.handle)):
+            f, b = C.c_double(), C.c_double()
+            check(lib().vrs_model_launch_work(self.handle, i, C.byref(f), C.byref(b)))
+            out.append((f.value, b.value))
+        return out
+
+    def run_launches(self, first, count, stream=None):
+        check(lib().vrs_model_run_launches(self.handle, first, count, _stream(stream)))
+
+    def close(self):
+        if self.handle:
+            lib().vrs_model_destroy(self.handle)
+            self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def block(kind, c_in, c_out=0, k=1, s=1, g=1, conv_kind=CONV_BN_SILU, n=1, c3k=False, shortcut=False, e=0.5,
+          heads=0, nc=80, variant="m", one2one=True):
+    return BlockDesc(kind, c_in, c_out, k, s, g, conv_kind, n, int(c3k), int(shortcut), e, heads, nc,
+                     ord(variant), int(one2one))
