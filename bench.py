@@ -85,7 +85,7 @@ def roofline_of(sym, d, dtype_peak):
             "algorithmic_mb_per_launch": round(d["bytes"] / d["launches"] / 1e6, 3)}
 
 
-def cpu_baseline(variant, size, P, budget_s=12.0):
+def cpu_baseline(variant, size, P, budget_s=15.0):
     """CPU oracle (float32, OpenMP) on a bounded sample of the same workload."""
     import numpy as np
     import oracle
@@ -97,7 +97,7 @@ def cpu_baseline(variant, size, P, budget_s=12.0):
     t0 = time.perf_counter()
     net(PP, x1)
     t1 = time.perf_counter() - t0
-    n = int(max(1, min(16, budget_s // max(t1, 1e-3))))
+    n = int(max(1, min(64, budget_s // max(t1, 1e-3))))
     xs = images(n, size, size, seed=2)
     t0 = time.perf_counter()
     net(PP, xs)

@@ -87,9 +87,10 @@ typedef struct {
  * ElemwiseAddForward as the layers blocks/conv.rs:31-99 and
  * blocks/bottleneck.rs:24-63 record them.
  *   y = act(scale[co] * conv(x, w)[co] + shift[co]) + res
- * w: dense -> packed by vrs_pack_conv_weight (dtype elements);
- *    depthwise -> float32 [C][k*k] (also from vrs_pack_conv_weight).
- * Dense requires x->c % 8 == 0; res may be NULL (dense only). */
+ * w: packed by vrs_pack_conv_weight in `dtype` elements (dense
+ *    [Cout][k][k][Cin]; depthwise tap-major [k*k][C]).
+ * Dense requires x->c % 8 == 0; depthwise is 3x3 with stride 1 or 2;
+ * res may be NULL (dense only). */
 int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const void* w,
                const float* scale, const float* shift, const vrs_nhwc* res, const vrs_nhwc* y,
                void* stream);
@@ -97,7 +98,7 @@ int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const vo
 /* Host-side weight repack from the reference's OIHW float32 layout
  * (nn::Conv2d weight) into the device layout vrs_conv2d reads:
  *   dense:  [Cout][k][k][cin_pad] in `dtype` (cin_pad >= Cin, zero filled)
- *   depthwise (groups == Cout): float32 [Cout][k*k].
+ *   depthwise (groups == Cout): tap-major [k*k][Cout] in `dtype`.
  * Returns the byte count needed when out == NULL. */
 int64_t vrs_pack_conv_weight(const float* w_oihw, int32_t cout, int32_t cin_per_group, int32_t k,
                              int32_t groups, int32_t cin_pad, int32_t dtype, void* out);
@@ -108,7 +109,7 @@ int64_t vrs_pack_conv_weight(const float* w_oihw, int32_t cout, int32_t cin_per_
 int vrs_bn_fold(const float* gamma, const float* beta, const float* mean, const float* var,
                 float eps, int32_t c, float* scale, float* shift);
 
-/* NCHW float32 -> NHWC dtype with zero channel padding to y->c (>= C). */
+/* NCHW float32 -> NHWC dtype, zero-padding channels C..y->c-1 (C <= y->c < C+8). */
 int vrs_pack_input(vrs_ctx* ctx, const float* x_nchw, int32_t n, int32_t c, int32_t h, int32_t w,
                    const vrs_nhwc* y, int32_t dtype, void* stream);
 /* NHWC dtype view -> NCHW float32 [n][x->c][h][w]. */
@@ -127,14 +128,15 @@ int vrs_upsample2x(vrs_ctx* ctx, const vrs_nhwc* x, const vrs_nhwc* y, int32_t d
  * custom ops (kernels/attention/psa.rs:744-1066), the PE conv_bn and the add:
  *   out = softmax(q k^T * key_dim^-0.5) v + pe_scale * dw3x3(v) + pe_shift
  * qkv: view of heads*128 channels (per head q 32 | k 32 | v 64);
- * out: view of heads*64 channels; pe_w float32 [heads*64][9]. */
+ * out: view of heads*64 channels; pe_w: the PE conv weight packed as a
+ * depthwise weight (tap-major [9][heads*64], dtype elements). */
 typedef struct {
   int32_t heads;
   int32_t key_dim;   /* must be 32 (blocks/c2psa.rs:159) */
   int32_t head_dim;  /* must be 64 (c / num_heads with num_heads = c/64) */
   int32_t dtype;
 } vrs_psa_desc;
-int vrs_psa_attention(vrs_ctx* ctx, const vrs_psa_desc* d, const vrs_nhwc* qkv, const float* pe_w,
+int vrs_psa_attention(vrs_ctx* ctx, const vrs_psa_desc* d, const vrs_nhwc* qkv, const void* pe_w,
                       const float* pe_scale, const float* pe_shift, const vrs_nhwc* out, void* stream);
 
 /* Detect post-process on the raw head outputs (DetectOutput,

@@ -53,27 +53,37 @@ def _j(pre, name):
 
 class Params(dict):
     """Name -> array, plus the BN eps the model folds with (1e-3 in the model,
-    blocks/conv.rs:39; 1e-5 for the reference's PyTorch-made fixtures)."""
+    blocks/conv.rs:39; 1e-5 for the reference's PyTorch-made fixtures).
 
-    def __init__(self, *a, eps=1e-3, **k):
+    ``act_q`` (identity by default) is applied wherever an activation tensor is
+    materialised -- each conv output (after its residual add, which belongs to
+    the same elem_add node of the reference graph) and the attention output --
+    so a bfloat16 run can be compared against an oracle that stores its
+    activations at the same precision and at the same points."""
+
+    def __init__(self, *a, eps=1e-3, act_q=None, **k):
         super().__init__(*a, **k)
         self.eps = eps
+        self.act_q = act_q if act_q is not None else (lambda t: t)
 
 
-def _conv_bn_act(P, pre, x, k, s, g, act):
+def _conv_bn_act(P, pre, x, k, s, g, act, res=None):
     w = P[_j(pre, "conv.weight")]
     y = conv2d(x, w, stride=s, pad=k // 2, groups=g)
     scale, shift = bn_fold(P[_j(pre, "bn.weight")], P[_j(pre, "bn.bias")],
                            P[_j(pre, "bn.running_mean")], P[_j(pre, "bn.running_var")], P.eps)
-    return affine_act(y, scale, shift, act)
+    y = affine_act(y, scale, shift, act)
+    if res is not None:  # elem_add(x, conv(...)) of the caller (bottleneck.rs:24-30)
+        y = y + res
+    return P.act_q(y)
 
 
 def conv(c_in, c_out, k, s):  # conv.rs:31-46: Conv2d(no bias, pad k/2) -> BN -> SiLU
-    return lambda P, pre, x: _conv_bn_act(P, pre, x, k, s, 1, SILU)
+    return lambda P, pre, x, res=None: _conv_bn_act(P, pre, x, k, s, 1, SILU, res)
 
 
 def conv_bn(c_in, c_out, k, s, g):  # conv.rs:53-69: grouped conv -> BN, no act
-    return lambda P, pre, x: _conv_bn_act(P, pre, x, k, s, g, NONE)
+    return lambda P, pre, x, res=None: _conv_bn_act(P, pre, x, k, s, g, NONE, res)
 
 
 def dwconv(c, k, s):  # conv.rs:75-85: depthwise -> BN -> SiLU
@@ -85,23 +95,15 @@ def conv_plain(c_in, c_out, k, s):  # conv.rs:90-99: conv with bias
                                     bias=P[_j(pre, "bias")])
 
 
-def bottleneck_std(c, shortcut):  # bottleneck.rs:37-49
+def bottleneck_std(c, shortcut):  # bottleneck.rs:37-49: shortcut -> elem_add(x, y)
     ci = int(c * 0.5)
     cv1, cv2 = conv(c, ci, 3, 1), conv(ci, c, 3, 1)
-
-    def f(P, pre, x):
-        y = cv2(P, _j(pre, "cv2"), cv1(P, _j(pre, "cv1"), x))
-        return x + y if shortcut else y
-    return f
+    return lambda P, pre, x: cv2(P, _j(pre, "cv2"), cv1(P, _j(pre, "cv1"), x), x if shortcut else None)
 
 
 def bottleneck_3x3(c, shortcut):  # bottleneck.rs:51-63
     cv1, cv2 = conv(c, c, 3, 1), conv(c, c, 3, 1)
-
-    def f(P, pre, x):
-        y = cv2(P, _j(pre, "cv2"), cv1(P, _j(pre, "cv1"), x))
-        return x + y if shortcut else y
-    return f
+    return lambda P, pre, x: cv2(P, _j(pre, "cv2"), cv1(P, _j(pre, "cv1"), x), x if shortcut else None)
 
 
 def c3k_inner(c, shortcut):  # c3k2.rs:46-61
@@ -140,27 +142,30 @@ def psa_attention_block(c, num_heads, key_dim):  # c2psa.rs:61-116
     head_dim = c // num_heads
     qkv_h = num_heads * (2 * key_dim + head_dim)
     qkv = conv_bn(c, qkv_h, 1, 1, 1)
-    pe = conv_bn(c, c, 3, 1, c)
     proj = conv_bn(c, c, 1, 1, 1)
 
-    def f(P, pre, x):
+    def f(P, pre, x, res=None):
         B, _, H, W = x.shape
         q = qkv(P, _j(pre, "qkv"), x)
         att = psa_attention(q, num_heads, key_dim, head_dim)
-        # V channels per head -> [B, c, H, W] (psa.rs:104-142)
+        # V channels per head -> [B, c, H, W] (psa.rs:104-142); PE conv_bn on V
         v = q.reshape(B, num_heads, 2 * key_dim + head_dim, H, W)[:, :, 2 * key_dim:]
         v = np.ascontiguousarray(v.reshape(B, c, H, W))
-        return proj(P, _j(pre, "proj"), att + pe(P, _j(pre, "pe"), v))
+        w = P[_j(pre, "pe.conv.weight")]
+        scale, shift = bn_fold(P[_j(pre, "pe.bn.weight")], P[_j(pre, "pe.bn.bias")],
+                               P[_j(pre, "pe.bn.running_mean")], P[_j(pre, "pe.bn.running_var")], P.eps)
+        pe_out = affine_act(conv2d(v, w, stride=1, pad=1, groups=c), scale, shift, NONE)
+        return proj(P, _j(pre, "proj"), P.act_q(att + pe_out), res)  # elem_add(merged, pe) (:112)
     return f
 
 
-def psa_block(c, num_heads, key_dim):  # c2psa.rs:123-137
+def psa_block(c, num_heads, key_dim):  # c2psa.rs:123-137: b += attn(b); b += ffn(b)
     attn = psa_attention_block(c, num_heads, key_dim)
     ffn0, ffn1 = conv(c, 2 * c, 1, 1), conv_bn(2 * c, c, 1, 1, 1)
 
     def f(P, pre, b):
-        b = b + attn(P, _j(pre, "attn"), b)
-        return b + ffn1(P, _j(pre, "ffn.1"), ffn0(P, _j(pre, "ffn.0"), b))
+        b = attn(P, _j(pre, "attn"), b, b)
+        return ffn1(P, _j(pre, "ffn.1"), ffn0(P, _j(pre, "ffn.0"), b), b)
     return f
 
 
@@ -197,8 +202,7 @@ def sppf(c_in, c_out, shortcut):  # sppf.rs:43-61
     def f(P, pre, x):
         y = cv1(P, _j(pre, "cv1"), x)
         p1 = maxpool2d(y); p2 = maxpool2d(p1); p3 = maxpool2d(p2)
-        out = cv2(P, _j(pre, "cv2"), np.concatenate([y, p1, p2, p3], axis=1))
-        return out + x if add else out
+        return cv2(P, _j(pre, "cv2"), np.concatenate([y, p1, p2, p3], axis=1), x if add else None)
     return f
 
 

@@ -62,6 +62,10 @@ def test_pack_conv_weight_layout():
                              vrs.BF16).view(np.uint16)
     # round to nearest even: 1.00390625 is halfway between 1.0 and 1.0078125 -> 1.0
     assert b[0] == 0x3F80 and b[1] == 0x3F80 and b[2] == 0x3F82
+    # depthwise: [C][1][3][3] -> tap-major [9][C]
+    dw = np.arange(4 * 9, dtype=np.float32).reshape(4, 1, 3, 3)
+    out = vrs.pack_conv_weight(dw, 4, 1, vrs.F32).view(np.float32).reshape(9, 4)
+    assert np.array_equal(out, dw.reshape(4, 9).T)
 
 
 def test_bn_fold_matches_reference_formula():

@@ -3,8 +3,13 @@
 1. The reference's own golden vectors (tests/golden/, BN eps 1e-5) run
    through the float32 path at the reference tests' tolerance (1e-3 absolute,
    tests/test_c3k2_variants_cuda.rs:47 etc.).
-2. The bfloat16 path against the oracle on the same bf16-rounded parameters
-   (2e-2 relative with a floor).
+2. The bfloat16 path against the oracle on the same bf16-rounded parameters,
+   the oracle storing its activations in bfloat16 at the same points the GPU
+   does (Params.act_q).  Through several layers one-ulp rounding flips of
+   intermediate activations (2^-8 relative) propagate, so the bar for a
+   multi-layer block is: normwise relative error <= 2e-2 (the north_star's
+   bf16 tolerance) and no element off by more than 5e-2 * max(|ref|, rms(ref)).
+   Single kernels are held to the elementwise bar in test_gpu_ops.
 3. YOLO26 end to end: YOLO26n float32 at 640x640 (1e-4
    relative with a floor) and YOLO26m bfloat16 (config 5 network at batch 2),
    plus identical detections wherever the score margin exceeds the tolerance.
@@ -84,6 +89,13 @@ def test_depthwise_fixture_f32():
 
 # ------------------------------------------------------- bf16 vs the oracle --
 
+def bf16_block_errors(got, ref):
+    """(||got-ref||_2 / ||ref||_2, max |got-ref| / max(|ref|, rms(ref)))."""
+    got = np.asarray(got, np.float64); ref = np.asarray(ref, np.float64)
+    norm = float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+    return norm, rel_err(got, ref, 1.0)
+
+
 def _bf16_params(specs, seed):
     P = seeded_params(specs, seed, bn="random")
     return {k: (bf16_round(v) if v.ndim == 4 else v) for k, v in P.items()}
@@ -109,12 +121,10 @@ def test_block_bf16_vs_oracle(name, desc, cin, hw, ref_fn):
     P = _bf16_params(m.params(), 3)
     x = bf16_round(np.random.default_rng(4).standard_normal((2, cin, hw, hw)).astype(np.float32))
     (y,), _ = run_model(desc, P, x, vrs.BF16, 1e-3)
-    ref = ref_fn()(Y.Params(P, eps=1e-3), "", x)
-    err = rel_err(y, ref, 5e-2)
-    assert err < 2e-2 * 4, err  # several bf16 roundings of intermediate activations
-    # the bulk must sit at the kernel tolerance
-    rms_err = float(np.sqrt(np.mean((y - ref) ** 2)) / np.sqrt(np.mean(ref ** 2)))
-    assert rms_err < 2e-2, rms_err
+    ref = ref_fn()(Y.Params(P, eps=1e-3, act_q=bf16_round), "", x)
+    norm_err, elt_err = bf16_block_errors(y, ref)
+    print(f"{name}: normwise rel {norm_err:.2e}, elementwise (floor rms) {elt_err:.2e}")
+    assert norm_err < 2e-2 and elt_err < 5e-2, (norm_err, elt_err)
 
 
 # --------------------------------------------------------------- end to end --
@@ -135,20 +145,58 @@ def test_yolo26n_f32_640_vs_oracle():
     (boxes, scores), _ = run_model(desc, P, x, vrs.F32, 1e-3)
     rb, rs = Y.yolo26(80, "n")(Y.Params(P, eps=1e-3), x)
     assert boxes.shape == (1, 33600) and scores.shape == (1, 672000)
-    eb, es = rel_err(boxes, rb, 1e-2), rel_err(scores, rs, 1e-2)
+    # float32 through ~100 layers: floor 0.1*rms admits the summation-order
+    # noise of two float32 implementations (~1e-6 rms per layer, compounding)
+    eb, es = rel_err(boxes, rb, 1e-1), rel_err(scores, rs, 1e-1)
     print(f"yolo26n f32 max rel err boxes {eb:.2e} scores {es:.2e}")
     assert eb < 1e-4 and es < 1e-4
 
 
+def _argmax_last(scores_flat, nc, a_s):
+    """Per-anchor class argmax with Rust max_by tie rule (last maximal class wins)."""
+    out, margins, base = [], [], 0
+    for a in a_s:
+        blk = scores_flat[:, nc * base: nc * (base + a)].reshape(-1, nc, a)
+        rev = blk[:, ::-1, :]
+        out.append(nc - 1 - np.argmax(rev, axis=1))
+        srt = np.sort(blk, axis=1)
+        margins.append(srt[:, -1, :] - srt[:, -2, :])
+        base += a
+    return np.concatenate(out, 1), np.concatenate(margins, 1)
+
+
 def test_yolo26m_bf16_vs_oracle():
-    """YOLO26m (config 5 network) in bfloat16 at batch 2, 320x320, bf16-rounded weights."""
-    x = np.random.default_rng(1).uniform(0, 1, (2, 3, 320, 320)).astype(np.float32)
+    """YOLO26m (config 5 network) in bfloat16 at batch 2, 320x320, bf16-rounded weights,
+    against the oracle storing bf16 activations; then the detections."""
+    x = bf16_round(np.random.default_rng(1).uniform(0, 1, (2, 3, 320, 320)).astype(np.float32))
     desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="m", one2one=True)
     m = vrs.Model(ctx(), desc, 2, 320, 320, vrs.BF16, 1e-3)
     P = _yolo_params(m, bf16=True)
-    (boxes, scores), _ = run_model(desc, P, bf16_round(x), vrs.BF16, 1e-3)
-    rb, rs = Y.yolo26(80, "m")(Y.Params(P, eps=1e-3), bf16_round(x))
-    eb = float(np.sqrt(np.mean((boxes - rb) ** 2)) / np.sqrt(np.mean(rb ** 2)))
-    es = float(np.sqrt(np.mean((scores - rs) ** 2)) / np.sqrt(np.mean(rs ** 2)))
-    print(f"yolo26m bf16 rms rel err boxes {eb:.2e} scores {es:.2e}; max rel {rel_err(boxes, rb, 0.1):.2e}")
+    (boxes, scores), _ = run_model(desc, P, x, vrs.BF16, 1e-3)
+    rb, rs = Y.yolo26(80, "m")(Y.Params(P, eps=1e-3, act_q=bf16_round), x)
+    eb, mb = bf16_block_errors(boxes, rb)
+    es, ms = bf16_block_errors(scores, rs)
+    print(f"yolo26m bf16: normwise rel boxes {eb:.2e} scores {es:.2e}; elementwise boxes {mb:.2e} scores {ms:.2e}")
     assert eb < 2e-2 and es < 2e-2
+    assert mb < 5e-2 * 4 and ms < 5e-2 * 4  # ~100 layers of bf16 storage
+    # identical class argmax wherever the reference's top-2 logit margin exceeds the tolerance
+    a_s = [(320 // s) ** 2 for s in (8, 16, 32)]
+    cg, _ = _argmax_last(scores, 80, a_s)
+    cr, margin = _argmax_last(rs, 80, a_s)
+    sure = margin > 2e-2
+    assert np.array_equal(cg[sure], cr[sure]), int(np.sum(cg[sure] != cr[sure]))
+    # top-k anchors from the device post-process vs the oracle's on the oracle outputs
+    import torch
+    got = ctx().detect_postprocess(dev(boxes), dev(scores), 80, 320, 320, (8, 16, 32), 0.25, 300)
+    torch.cuda.synchronize()
+    gc, gs, gcl, gan, _ = [t.cpu().numpy() for t in got]
+    rc, rsc, rcl, ran, _ = oracle.detect_postprocess(rb, rs, 80, 320, 320, (8, 16, 32), 0.25, 300)
+    for b in range(2):
+        k = min(gc[b], rc[b])
+        # ranks whose reference score is separated from both neighbours by more than 2e-2 relative
+        s = rsc[b, :k]
+        sep = np.ones(k, bool)
+        gap = np.abs(np.diff(s)) > 2e-2 * s[1:]
+        sep[1:] &= gap
+        sep[:-1] &= gap
+        assert np.array_equal(gan[b, :k][sep], ran[b, :k][sep])

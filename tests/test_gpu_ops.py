@@ -2,8 +2,13 @@
 
 Inputs and weights are rounded to the kernel's element type first, so the
 tolerance measures kernel error, not input quantisation.  Tolerances (from the
-north_star): float32 1e-4 relative, bfloat16 2e-2 relative, each with an
-absolute floor of a fraction of the reference's RMS (rel_err in gpu_util).
+north_star): float32 1e-4 relative, bfloat16 2e-2 relative, elementwise, with
+an absolute floor for elements near zero (rel_err in gpu_util):
+  |got - ref| <= tol * max(|ref|, floor * rms(ref))
+floor = 0.05 for float32: two float32 summations of K products differ by
+~eps*sqrt(K/2)*rms (~1e-6 rms at K = 576), which the floor must admit;
+floor = 0.1 for bfloat16: the attention's probabilities enter the PV MFMA as
+bfloat16 (8-bit mantissa), an absolute error of ~2^-9 * rms on every output.
 Integer/index/bytes outputs (pooling, upsample, top-k indices) are compared
 exactly.
 """
@@ -18,7 +23,7 @@ from gpu_util import bf16_round, ctx, dev, from_nhwc, rel_err, rounder, tdtype, 
 pytestmark = pytest.mark.gpu
 
 TOL = {vrs.F32: 1e-4, vrs.BF16: 2e-2}
-FLOOR = {vrs.F32: 1e-3, vrs.BF16: 2e-2}
+FLOOR = {vrs.F32: 5e-2, vrs.BF16: 1e-1}
 DT = [vrs.F32, vrs.BF16]
 
 CONV_CASES = [
@@ -77,17 +82,18 @@ def test_dwconv(dtype, act):
     rng = np.random.default_rng(7)
     n, c, h, w = 2, 64, 11, 9
     x = rnd(rng.standard_normal((n, c, h, w)).astype(np.float32))
-    wt = (rng.standard_normal((c, 1, 3, 3)) * 0.4).astype(np.float32)
+    wt = rnd((rng.standard_normal((c, 1, 3, 3)) * 0.4).astype(np.float32))
     scale = rng.uniform(0.5, 1.5, c).astype(np.float32)
     shift = rng.normal(0, 0.2, c).astype(np.float32)
-    ref = oracle.affine_act(oracle.conv2d(x, wt, 1, 1, groups=c), scale, shift, act)
     C = ctx()
     xt = to_nhwc(x, dtype, 96, 8)
-    yt = torch.zeros((n, h, w, c), dtype=tdtype(dtype), device="cuda")
-    C.conv2d(vrs.nhwc(xt, c, 8), dev(wt.reshape(c, 9)), dev(scale), dev(shift), vrs.nhwc(yt), 3, 1, c, act, None,
-             dtype)
-    torch.cuda.synchronize()
-    assert rel_err(from_nhwc(yt), ref, FLOOR[dtype]) < TOL[dtype]
+    for s in (1, 2):
+        ref = oracle.affine_act(oracle.conv2d(x, wt, s, 1, groups=c), scale, shift, act)
+        yt = torch.zeros((n, ref.shape[2], ref.shape[3], c), dtype=tdtype(dtype), device="cuda")
+        C.conv2d(vrs.nhwc(xt, c, 8), dev(vrs.pack_conv_weight(wt, c, 1, dtype)), dev(scale), dev(shift),
+                 vrs.nhwc(yt), 3, s, c, act, None, dtype)
+        torch.cuda.synchronize()
+        assert rel_err(from_nhwc(yt), ref, FLOOR[dtype]) < TOL[dtype], s
 
 
 @pytest.mark.parametrize("dtype", DT)
@@ -130,7 +136,7 @@ def test_psa_attention(dtype, shape):
     rng = np.random.default_rng(10)
     qkv = rnd(rng.standard_normal((b, heads * 128, h, w)).astype(np.float32))
     c = heads * 64
-    pe_w = (rng.standard_normal((c, 1, 3, 3)) * 0.3).astype(np.float32)
+    pe_w = rnd((rng.standard_normal((c, 1, 3, 3)) * 0.3).astype(np.float32))
     pe_s = rng.uniform(0.5, 1.5, c).astype(np.float32)
     pe_t = rng.normal(0, 0.1, c).astype(np.float32)
     att = oracle.psa_attention(qkv, heads, 32, 64)
@@ -138,7 +144,8 @@ def test_psa_attention(dtype, shape):
     ref = att + oracle.affine_act(oracle.conv2d(v, pe_w, 1, 1, groups=c), pe_s, pe_t, 0)
     qt = to_nhwc(qkv, dtype)
     ot = torch.zeros((b, h, w, c), dtype=tdtype(dtype), device="cuda")
-    ctx().psa_attention(vrs.nhwc(qt), dev(pe_w.reshape(c, 9)), dev(pe_s), dev(pe_t), vrs.nhwc(ot), heads, dtype)
+    ctx().psa_attention(vrs.nhwc(qt), dev(vrs.pack_conv_weight(pe_w, c, 1, dtype)), dev(pe_s), dev(pe_t),
+                        vrs.nhwc(ot), heads, dtype)
     torch.cuda.synchronize()
     err = rel_err(from_nhwc(ot), ref, FLOOR[dtype])
     assert err < TOL[dtype], err
@@ -214,7 +221,7 @@ def test_msda(cfg):
     out = torch.empty((B, Q, heads * 32), dtype=torch.float32, device="cuda")
     ctx().msda(dev(value), shapes, dev(ref), dev(off), dev(attw), out)
     torch.cuda.synchronize()
-    assert rel_err(out.cpu().numpy(), exp, 1e-3) < 1e-4
+    assert rel_err(out.cpu().numpy(), exp, FLOOR[vrs.F32]) < 1e-4
 
 
 def test_errors_are_reported_not_fatal():

@@ -16,6 +16,7 @@ class Recorder(dict):
     def __init__(self, P, eps=1e-3):
         super().__init__(P)
         self.eps = eps
+        self.act_q = lambda t: t
         self.used = set()
 
     def __getitem__(self, k):

@@ -508,7 +508,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         break;
       case Step::ATTN: {
         const ConvStep& pe = m->convs[st.conv];
-        rc = prep_attn(m->ctx, st.heads, m->dtype, view_of(m, st.a), static_cast<const float*>(pe.w), pe.scale,
+        rc = prep_attn(m->ctx, st.heads, m->dtype, view_of(m, st.a), pe.w, pe.scale,
                        pe.shift, view_of(m, st.b), ls);
         label = pe.pre.substr(0, pe.pre.size() >= 3 ? pe.pre.size() - 3 : 0) + ".core";
         break;

@@ -46,15 +46,22 @@ int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const vo
 int64_t vrs_pack_conv_weight(const float* w, int32_t cout, int32_t cin_g, int32_t k, int32_t groups, int32_t cin_pad,
                              int32_t dtype, void* out) {
   if (cout <= 0 || cin_g <= 0 || k <= 0 || groups <= 0) return fail(VRS_EINVAL, "pack_conv_weight: bad dims");
+  if (dtype != VRS_BF16 && dtype != VRS_F32) return fail(VRS_EUNSUPPORTED, "pack_conv_weight: dtype");
   if (groups > 1) {
     if (groups != cout || cin_g != 1) return fail(VRS_EUNSUPPORTED, "pack_conv_weight: groups must be 1 or Cout");
-    const int64_t bytes = (int64_t)cout * k * k * 4;
+    const int64_t n = (int64_t)cout * k * k;
+    const int64_t bytes = n * (int64_t)elt_size(dtype);
     if (!out) return bytes;
     if (!w) return fail(VRS_EINVAL, "pack_conv_weight: null weight");
-    memcpy(out, w, (size_t)bytes);  // [C][1][k][k] == [C][k*k]
+    for (int c = 0; c < cout; ++c)  // [C][1][k][k] -> tap-major [k*k][C]
+      for (int t = 0; t < k * k; ++t) {
+        const float v = w[(int64_t)c * k * k + t];
+        const int64_t o = (int64_t)t * cout + c;
+        if (dtype == VRS_F32) static_cast<float*>(out)[o] = v;
+        else static_cast<uint16_t*>(out)[o] = host_f2bf(v);
+      }
     return bytes;
   }
-  if (dtype != VRS_BF16 && dtype != VRS_F32) return fail(VRS_EUNSUPPORTED, "pack_conv_weight: dtype");
   if (cin_pad < cin_g) return fail(VRS_EINVAL, "pack_conv_weight: cin_pad < cin");
   const int64_t n = (int64_t)cout * k * k * cin_pad;
   const int64_t bytes = n * (int64_t)elt_size(dtype);
@@ -112,7 +119,7 @@ int vrs_upsample2x(vrs_ctx* ctx, const vrs_nhwc* x, const vrs_nhwc* y, int32_t d
   return rc ? rc : run_all(ls, stream);
 }
 
-int vrs_psa_attention(vrs_ctx* ctx, const vrs_psa_desc* d, const vrs_nhwc* qkv, const float* pe_w,
+int vrs_psa_attention(vrs_ctx* ctx, const vrs_psa_desc* d, const vrs_nhwc* qkv, const void* pe_w,
                       const float* pe_scale, const float* pe_shift, const vrs_nhwc* out, void* stream) {
   if (!ctx || !d || !qkv || !out) return fail(VRS_EINVAL, "vrs_psa_attention: null argument");
   if (d->key_dim != 32 || d->head_dim != 64)

@@ -37,8 +37,10 @@ int get_fn(vrs_ctx* ctx, const char* name, hipFunction_t* out) {
       *out = f;
       return VRS_OK;
     }
+    // A miss in this module is expected while probing; do not leave it as the
+    // thread's sticky last error (the caller's own HIP checks would see it).
+    (void)hipGetLastError();
   }
-  (void)hipGetLastError();
   return fail(VRS_ENOMODULE, "kernel '%s' not found in the code objects under %s", name, ctx->dir.c_str());
 }
 
@@ -133,26 +135,27 @@ int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w
     if ((rc = check_view(x, "dwconv input", 8))) return rc;
     if (res) return fail(VRS_EUNSUPPORTED, "dwconv: residual not supported");
     if (x.c != y.c) return fail(VRS_EBADSHAPE, "dwconv: channels %d -> %d", x.c, y.c);
-    if (cs.k < 1 || cs.k > 3 || cs.k % 2 == 0) return fail(VRS_EUNSUPPORTED, "dwconv: k=%d (1 or 3)", cs.k);
+    if (cs.k != 3 || (cs.stride != 1 && cs.stride != 2))
+      return fail(VRS_EUNSUPPORTED, "dwconv: k=%d s=%d (3x3, stride 1 or 2)", cs.k, cs.stride);
     if (y.h != out_size(x.h, cs.k, cs.stride) || y.w != out_size(x.w, cs.k, cs.stride))
       return fail(VRS_EBADSHAPE, "dwconv: output size");
     if (!w || !scale || !shift) return fail(VRS_EINVAL, "dwconv: null weight/scale/shift");
     vrs_dw_args a{};
-    a.x = at(x, cs.dtype); a.w = static_cast<const float*>(w); a.scale = scale; a.shift = shift;
+    a.x = at(x, cs.dtype); a.w = w; a.scale = scale; a.shift = shift;
     a.y = const_cast<void*>(at(y, cs.dtype));
     a.N = x.n; a.H = x.h; a.W = x.w; a.C = x.c; a.x_pitch = x.pitch;
     a.Ho = y.h; a.Wo = y.w; a.y_pitch = y.pitch;
     a.kh = a.kw = cs.k; a.stride = cs.stride; a.pad = cs.k / 2; a.act = cs.act;
     const int64_t threads = (int64_t)x.n * ((y.h + 3) / 4) * y.w * (x.c / 8);
     char name[48];
-    snprintf(name, sizeof name, "vrs_dwconv_%s", dsuffix(cs.dtype));
+    snprintf(name, sizeof name, "vrs_dwconv3_s%d_%s", cs.stride, dsuffix(cs.dtype));
     hipFunction_t f;
     if ((rc = get_fn(ctx, name, &f))) return rc;
     out.push_back(make_launch(name, f, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a));
     const double es = (double)elt_size(cs.dtype);
     out.back().flops = 2.0 * x.n * y.h * y.w * (double)x.c * cs.k * cs.k;
     out.back().bytes = (double)x.n * x.h * x.w * x.c * es + (double)y.n * y.h * y.w * y.c * es +
-                       (double)x.c * (cs.k * cs.k + 2) * 4.0;
+                       (double)x.c * (cs.k * cs.k * es + 8.0);
     return VRS_OK;
   }
   vrs_conv_args a{};
@@ -185,8 +188,8 @@ int prep_pack_input(vrs_ctx* ctx, const float* x, int n, int c, int h, int w, co
   if ((rc = check_dtype(dtype))) return rc;
   if (!x) return fail(VRS_EINVAL, "pack_input: null input");
   if (y.c_off != 0 || y.pitch != y.c) return fail(VRS_EBADSHAPE, "pack_input: output must be a whole buffer");
-  if (y.n != n || y.h != h || y.w != w || y.c < c || y.c > 8)
-    return fail(VRS_EBADSHAPE, "pack_input: output view %dx%dx%dx%d for input %dx%dx%dx%d (padded c <= 8)", y.n,
+  if (y.n != n || y.h != h || y.w != w || y.c < c || y.c >= c + 8)
+    return fail(VRS_EBADSHAPE, "pack_input: output view %dx%dx%dx%d for input %dx%dx%dx%d (c padded by < 8)", y.n,
                 y.h, y.w, y.c, n, c, h, w);
   vrs_pack_args a{x, y.data, n, c, h, w, y.c};
   char name[48];
@@ -258,7 +261,7 @@ int prep_up(vrs_ctx* ctx, const vrs_nhwc& x, const vrs_nhwc& y, int dtype, std::
   return VRS_OK;
 }
 
-int prep_attn(vrs_ctx* ctx, int heads, int dtype, const vrs_nhwc& qkv, const float* pe_w, const float* pe_scale,
+int prep_attn(vrs_ctx* ctx, int heads, int dtype, const vrs_nhwc& qkv, const void* pe_w, const float* pe_scale,
               const float* pe_shift, const vrs_nhwc& o, std::vector<Launch>& out) {
   int rc;
   if ((rc = check_dtype(dtype))) return rc;
@@ -280,7 +283,7 @@ int prep_attn(vrs_ctx* ctx, int heads, int dtype, const vrs_nhwc& qkv, const flo
   out.push_back(make_launch(name, f, dim3(a.B * heads * a.q_blocks), dim3(256), 0, a));
   const double N = (double)qkv.h * qkv.w;
   out.back().flops = 2.0 * a.B * heads * N * N * (32 + 64) + 2.0 * a.B * N * o.c * 9;
-  out.back().bytes = (double)a.B * N * (qkv.c + o.c) * elt_size(dtype) + (double)o.c * 11 * 4;
+  out.back().bytes = (double)a.B * N * (qkv.c + o.c) * elt_size(dtype) + (double)o.c * (9 * elt_size(dtype) + 8);
   return VRS_OK;
 }
 

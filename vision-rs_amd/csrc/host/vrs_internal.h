@@ -82,7 +82,7 @@ int prep_pack_input(vrs_ctx* ctx, const float* x, int n, int c, int h, int w, co
 int prep_unpack(vrs_ctx* ctx, const vrs_nhwc& x, int dtype, float* y, std::vector<Launch>& out);
 int prep_pool(vrs_ctx* ctx, const vrs_nhwc& buf, int dtype, std::vector<Launch>& out);
 int prep_up(vrs_ctx* ctx, const vrs_nhwc& x, const vrs_nhwc& y, int dtype, std::vector<Launch>& out);
-int prep_attn(vrs_ctx* ctx, int heads, int dtype, const vrs_nhwc& qkv, const float* pe_w, const float* pe_scale,
+int prep_attn(vrs_ctx* ctx, int heads, int dtype, const vrs_nhwc& qkv, const void* pe_w, const float* pe_scale,
               const float* pe_shift, const vrs_nhwc& o, std::vector<Launch>& out);
 
 }  // namespace vrs

@@ -35,10 +35,11 @@ typedef struct {
   int32_t tiles_m, tiles_n; /* grid decomposition: Cout tiles x pixel tiles */
 } vrs_conv_args;
 
-/* Depthwise conv (groups == C), NHWC, weights [C][kh*kw] float32. */
+/* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the
+ * element type. */
 typedef struct {
   const void* x;
-  const float* w;
+  const void* w;
   const float* scale;
   const float* shift;
   void* y;
@@ -77,7 +78,7 @@ typedef struct {
  * out[b, n, h*64 + d] = softmax(q.k * scale) v + pe_scale*dw3x3(v) + pe_shift. */
 typedef struct {
   const void* qkv;
-  const float* pe_w;    /* [heads*64][9] */
+  const void* pe_w;     /* tap-major [9][heads*64], element type */
   const float* pe_scale;
   const float* pe_shift;
   void* out;

@@ -150,8 +150,9 @@ __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
         const int xx = qx + kx - 1;
         if (xx < 0 || xx >= a.W) continue;
         const T* vp = qkv + (img + yy * a.W + xx) * a.qkv_pitch + hc + 2 * KD + d0;
+        const T* wk = reinterpret_cast<const T*>(a.pe_w) + (ky * 3 + kx) * (a.heads * VD) + c0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pe[r] += a.pe_w[(c0 + r) * 9 + ky * 3 + kx] * E::to_f(vp[r]);
+        for (int r = 0; r < 4; ++r) pe[r] += E::to_f(wk[r]) * E::to_f(vp[r]);
       }
     }
 #pragma unroll

@@ -23,7 +23,13 @@ __device__ __forceinline__ bf16_t f2bf(float f) {
   return (bf16_t)(u >> 16);
 }
 
-__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+// SiLU: the bfloat16 path uses the fast exp (its error is far below bf16
+// resolution); the float32 parity path uses the accurately rounded expf.
+__device__ __forceinline__ float silu_fast(float v) { return v / (1.0f + __expf(-v)); }
+__device__ __forceinline__ float silu_acc(float v) { return v / (1.0f + expf(-v)); }
+template <typename T> __device__ __forceinline__ float silu_t(float v) {
+  return sizeof(T) == 4 ? silu_acc(v) : silu_fast(v);
+}
 
 // ---- element traits --------------------------------------------------------
 // A "group" is 8 consecutive elements along K: the unit one lane feeds into

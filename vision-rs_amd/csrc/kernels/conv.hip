@@ -182,7 +182,7 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float t = acc[i][j][r] * sc[r] + sh[r];
-        if (a.act == VRS_ACT_SILU) t = silu_f(t);
+        if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
         v[r] = t;
       }
       if (a.res) {

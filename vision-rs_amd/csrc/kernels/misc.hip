@@ -5,16 +5,21 @@
 #include "common.h"
 
 // ---------------------------------------------------------------------------
-// Depthwise conv + folded BN (+ SiLU): blocks/conv.rs:75-85 (dwconv) and the
-// PE conv_bn with g = c (blocks/c2psa.rs:66).  One thread computes 8 channels
-// of OUT_ROWS vertically adjacent output pixels, so each loaded input row is
-// reused by up to 3 outputs.
+// Depthwise 3x3 conv + folded BN (+ SiLU): blocks/conv.rs:75-85 (dwconv) and
+// the PE conv_bn with g = c (blocks/c2psa.rs:66).  Weights are tap-major
+// [9][C] in the element type, so the 9 taps of 8 channels are 9 vector loads.
+// One thread computes 8 channels of DW_ROWS vertically adjacent output pixels;
+// every loop is unrolled at compile time (stride is a template parameter) so
+// weights and accumulators stay in registers, and the (DW_ROWS-1)*S+3 input
+// rows x 3 columns are independent loads in flight together.
 namespace {
 constexpr int DW_ROWS = 4;
 
-template <typename T>
+template <typename T, int S>
 __device__ __forceinline__ void dw_body(const vrs_dw_args& a) {
   using E = Elt<T>;
+  using G = typename E::group;
+  constexpr int NR = (DW_ROWS - 1) * S + 3;
   const int cg = a.C >> 3;                       // channel groups of 8
   const int row_tiles = (a.Ho + DW_ROWS - 1) / DW_ROWS;
   const int64_t total = (int64_t)a.N * row_tiles * a.Wo * cg;
@@ -28,40 +33,45 @@ __device__ __forceinline__ void dw_body(const vrs_dw_args& a) {
   const int c0 = g * 8;
   const int oy0 = rt * DW_ROWS;
 
+  const T* wp = reinterpret_cast<const T*>(a.w);
   float wv[9][8];
-  const int taps = a.kh * a.kw;
 #pragma unroll
-  for (int c = 0; c < 8; ++c)
-    for (int k = 0; k < 9; ++k) wv[k][c] = k < taps ? a.w[(c0 + c) * taps + k] : 0.f;
-
+  for (int k = 0; k < 9; ++k) {
+    G gw = E::load(wp + (int64_t)k * a.C + c0);
+    const T* ew = reinterpret_cast<const T*>(&gw);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) wv[k][c] = E::to_f(ew[c]);
+  }
   float acc[DW_ROWS][8];
 #pragma unroll
   for (int r = 0; r < DW_ROWS; ++r)
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[r][c] = 0.f;
 
-  const T* x = reinterpret_cast<const T*>(a.x);
-  // input rows touched by DW_ROWS outputs: (DW_ROWS-1)*stride + kh
-  const int iy_first = oy0 * a.stride - a.pad;
-  const int nrows = (DW_ROWS - 1) * a.stride + a.kh;
-  for (int rr = 0; rr < nrows; ++rr) {
-    const int iy = iy_first + rr;
-    if (iy < 0 || iy >= a.H) continue;
-    for (int kx = 0; kx < a.kw; ++kx) {
-      const int ix = ox * a.stride - a.pad + kx;
-      if (ix < 0 || ix >= a.W) continue;
-      typename E::group gv = E::load(x + (((int64_t)b * a.H + iy) * a.W + ix) * a.x_pitch + c0);
-      const T* ev = reinterpret_cast<const T*>(&gv);
+  const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)b * a.H * a.W * a.x_pitch + c0;
+  const int iy0 = oy0 * S - 1, ix0 = ox * S - 1;
+#pragma unroll
+  for (int rr = 0; rr < NR; ++rr) {
+    const int iy = iy0 + rr;
+    const bool rok = iy >= 0 && iy < a.H;
+    G gv[3];
+#pragma unroll
+    for (int kx = 0; kx < 3; ++kx) {
+      const int ix = ix0 + kx;
+      gv[kx] = (rok && ix >= 0 && ix < a.W) ? E::load(x + ((int64_t)iy * a.W + ix) * a.x_pitch) : E::zero();
+    }
+#pragma unroll
+    for (int kx = 0; kx < 3; ++kx) {
+      const T* ev = reinterpret_cast<const T*>(&gv[kx]);
       float xv[8];
 #pragma unroll
       for (int c = 0; c < 8; ++c) xv[c] = E::to_f(ev[c]);
 #pragma unroll
       for (int r = 0; r < DW_ROWS; ++r) {
-        const int ky = rr - r * a.stride;   // tap row for output row oy0 + r
-        if (ky < 0 || ky >= a.kh) continue;
-        const int k = ky * a.kw + kx;
+        const int ky = rr - r * S;   // tap row for output row oy0 + r (compile-time)
+        if (ky < 0 || ky > 2) continue;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) acc[r][c] += wv[k][c] * xv[c];
+        for (int c = 0; c < 8; ++c) acc[r][c] += wv[ky * 3 + kx][c] * xv[c];
       }
     }
   }
@@ -73,12 +83,12 @@ __device__ __forceinline__ void dw_body(const vrs_dw_args& a) {
   for (int r = 0; r < DW_ROWS; ++r) {
     const int oy = oy0 + r;
     if (oy >= a.Ho) break;
-    typename E::group out;
+    G out;
     T* ov = reinterpret_cast<T*>(&out);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       float v = acc[r][c] * sc[c] + sh[c];
-      if (a.act == VRS_ACT_SILU) v = silu_f(v);
+      if (a.act == VRS_ACT_SILU) v = silu_t<T>(v);
       ov[c] = E::from_f(v);
     }
     E::store(y + (((int64_t)b * a.Ho + oy) * a.Wo + ox) * a.y_pitch + c0, out);
@@ -86,8 +96,10 @@ __device__ __forceinline__ void dw_body(const vrs_dw_args& a) {
 }
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) void vrs_dwconv_bf16(vrs_dw_args a) { dw_body<bf16_t>(a); }
-extern "C" __global__ __launch_bounds__(256) void vrs_dwconv_f32(vrs_dw_args a) { dw_body<float>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1_bf16(vrs_dw_args a) { dw_body<bf16_t, 1>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s2_bf16(vrs_dw_args a) { dw_body<bf16_t, 2>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1_f32(vrs_dw_args a) { dw_body<float, 1>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s2_f32(vrs_dw_args a) { dw_body<float, 2>(a); }
 
 // ---------------------------------------------------------------------------
 // SPPF pooling cascade (blocks/sppf.rs:43-61): p1 = max5(y), p2 = max5(p1),

@@ -238,7 +238,8 @@ class Context:
 
 
 def pack_conv_weight(w_oihw, groups=1, cin_pad=None, dtype=BF16):
-    """Host repack (numpy float32 OIHW) -> bytes in the device layout."""
+    """Host repack (numpy float32 OIHW) -> bytes in the device layout
+    (dense [Cout][k][k][cin_pad]; depthwise tap-major [k*k][C]), dtype elements."""
     import numpy as np
     w = np.ascontiguousarray(w_oihw, dtype=np.float32)
     cout, cin_g, k, _ = w.shape
