@@ -74,12 +74,24 @@ typedef struct {
 } vrs_nhwc;
 
 /* ---- single ops ----------------------------------------------------------- */
+/* Dense-conv workgroup tiles (output channels x output pixels).  VRS_TILE_AUTO
+ * picks by shape; OR VRS_TILE_K32 to force the 32-deep reduction step (the
+ * 64-deep one is used when Cin % 64 == 0 and the tile has it). */
+#define VRS_TILE_AUTO 0
+#define VRS_TILE_128x128 1
+#define VRS_TILE_256x128 2
+#define VRS_TILE_128x256 3
+#define VRS_TILE_64x256 4
+#define VRS_TILE_32x256 5
+#define VRS_TILE_K32 0x100
+
 typedef struct {
   int32_t k;        /* square kernel size; padding = k/2 (blocks/conv.rs:36) */
   int32_t stride;
   int32_t groups;   /* 1 = dense (implicit GEMM on MFMA); == channels = depthwise */
   int32_t act;      /* VRS_ACT_NONE or VRS_ACT_SILU */
   int32_t dtype;    /* VRS_BF16 or VRS_F32: element type of x, y, res */
+  int32_t tile;     /* dense only: VRS_TILE_* (0 = automatic) */
 } vrs_conv_desc;
 
 /* Conv2d + folded BN (+SiLU) (+residual).  Replaces teeny-kernels
@@ -212,6 +224,10 @@ typedef struct {
  * without a GPU); finalize/forward then fail with VRS_ESTATE. */
 int vrs_model_create(vrs_ctx* ctx, const vrs_block_desc* d, int32_t batch, int32_t h, int32_t w,
                      int32_t dtype, float bn_eps, vrs_model** out);
+/* Per-layer tile autotuning at finalize (default on): every dense conv is
+ * timed with each applicable VRS_TILE_* on the model's own buffers and the
+ * fastest is kept.  Off: the shape heuristic of VRS_TILE_AUTO. */
+int vrs_model_set_autotune(vrs_model* m, int32_t on);
 int vrs_model_num_params(const vrs_model* m);
 /* name is owned by the model; dims[0..*ndim) (ndim <= 4). */
 int vrs_model_param_info(const vrs_model* m, int32_t i, const char** name, int32_t* dims, int32_t* ndim);

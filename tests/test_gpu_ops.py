@@ -74,6 +74,51 @@ def test_conv2d(case, dtype):
         assert torch.all(rest == 7.0)
 
 
+TILES_BF16 = [vrs.TILE_128x128, vrs.TILE_256x128, vrs.TILE_128x256, vrs.TILE_64x256, vrs.TILE_32x256]
+TILES_F32 = [vrs.TILE_128x128, vrs.TILE_64x256, vrs.TILE_32x256]
+
+
+@pytest.mark.parametrize("dtype,tile", [(vrs.BF16, t) for t in TILES_BF16] +
+                         [(vrs.BF16, t | vrs.TILE_K32) for t in TILES_BF16[:4]] +
+                         [(vrs.F32, t) for t in TILES_F32])
+@pytest.mark.parametrize("yview", [(264, 8), (260, 4)])  # staged (16-byte chunks) / direct epilogue
+def test_conv2d_every_tile(dtype, tile, yview):
+    import torch
+    n, cin, h, w, cout, k, s = 2, 128, 14, 10, 256, 3, 1
+    rnd = rounder(dtype)
+    rng = np.random.default_rng(21)
+    x = rnd(rng.standard_normal((n, cin, h, w)).astype(np.float32))
+    wt = rnd((rng.standard_normal((cout, cin, k, k)) * np.sqrt(2.0 / (cin * k * k))).astype(np.float32))
+    scale = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    res = rnd(rng.standard_normal((n, cout, h, w)).astype(np.float32))
+    ref = oracle.affine_act(oracle.conv2d(x, wt, s, k // 2), scale, shift, 1) + res
+    yp, yo = yview
+    xt = to_nhwc(x, dtype)
+    yt = torch.full((n, h, w, yp), 7.0, dtype=tdtype(dtype), device="cuda")
+    rt = to_nhwc(res, dtype, yp, yo)
+    wp = dev(vrs.pack_conv_weight(wt, 1, cin, dtype))
+    ctx().conv2d(vrs.nhwc(xt), wp, dev(scale), dev(shift), vrs.nhwc(yt, cout, yo), k, s, 1, vrs.ACT_SILU,
+                 vrs.nhwc(rt, cout, yo), dtype, tile=tile)
+    torch.cuda.synchronize()
+    assert rel_err(from_nhwc(yt, cout, yo), ref, FLOOR[dtype]) < TOL[dtype]
+    rest = torch.cat([yt[..., :yo], yt[..., yo + cout:]], -1).float()
+    assert torch.all(rest == 7.0)
+
+
+def test_conv2d_tile_rejections():
+    import torch
+    x = torch.zeros((1, 4, 4, 48), dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros((1, 4, 4, 64), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(64 * 48, dtype=torch.bfloat16, device="cuda")
+    s = torch.ones(64, device="cuda")
+    with pytest.raises(vrs.VrsError):  # 256x128 needs Cin % 32 == 0
+        ctx().conv2d(vrs.nhwc(x), w, s, s, vrs.nhwc(y), 1, 1, 1, vrs.ACT_SILU, None, vrs.BF16, tile=vrs.TILE_256x128)
+    with pytest.raises(vrs.VrsError):  # no float32 build of 128x256
+        ctx().conv2d(vrs.nhwc(x.float()), w, s, s, vrs.nhwc(y.float()), 1, 1, 1, vrs.ACT_SILU, None, vrs.F32,
+                     tile=vrs.TILE_128x256)
+
+
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("act", [vrs.ACT_SILU, vrs.ACT_NONE])
 def test_dwconv(dtype, act):

@@ -48,6 +48,7 @@ struct ConvStep {
   // flat float32 output (detect head / block outputs): output index + layout
   int out_idx = -1;
   int64_t out_off = 0, sb = 0, sp = 0, sc = 0;
+  int tile = VRS_TILE_AUTO;  // chosen at finalize (autotune) for dense NHWC convs
   // device parameters (finalize)
   void* w = nullptr;
   float* scale = nullptr;
@@ -76,6 +77,7 @@ struct vrs_model {
   std::vector<Step> steps;
   std::vector<std::vector<int32_t>> out_dims;
   bool finalized = false;
+  bool autotune = true;
   std::vector<void*> allocs;
   // prepared launches for the last (x, outputs) pointers
   std::vector<Launch> launches;
@@ -486,6 +488,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         cs.k = c.k; cs.stride = c.s; cs.dtype = m->dtype; cs.depthwise = c.dw;
         cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
         cs.cin_real = c.cin == m->bufs[c.x.buf].pitch && c.x.buf == 0 ? m->in_c : 0;
+        cs.tile = c.tile;
         label = c.pre.empty() ? "conv" : c.pre;
         if (c.out_idx >= 0) {
           rc = prep_conv_flat(m->ctx, cs, view_of(m, c.x), c.w, c.scale, c.shift, c.cout, o[c.out_idx] + c.out_off,
@@ -535,6 +538,54 @@ int dev_upload(vrs_model* m, const void* host, size_t bytes, void** dev) {
   VRS_HIP(hipMemcpy(p, host, bytes, hipMemcpyHostToDevice));
   *dev = p;
   return VRS_OK;
+}
+
+// Time every applicable tile of each dense NHWC conv on the model's own
+// buffers (contents do not matter for timing; a forward rewrites them all)
+// and keep the fastest.  Replaces the reference's shape-adaptive tile choice
+// in TritonLowering (examples/yolo26.rs:3027).
+int autotune_tiles(vrs_model* m) {
+  hipStream_t s;
+  VRS_HIP(hipStreamCreate(&s));
+  hipEvent_t e0, e1;
+  VRS_HIP(hipEventCreate(&e0));
+  VRS_HIP(hipEventCreate(&e1));
+  int rc = VRS_OK;
+  for (ConvStep& c : m->convs) {
+    if (c.dw || c.out_idx >= 0 || c.y.buf < 0) continue;
+    const std::vector<int> cand = conv_tile_candidates(c.cout, c.cin, m->dtype);
+    if (cand.size() < 2) continue;
+    ConvSpec cs;
+    cs.k = c.k; cs.stride = c.s; cs.dtype = m->dtype; cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
+    vrs_nhwc r;
+    if (c.has_res) r = view_of(m, c.res);
+    float best = 1e30f;
+    int best_tile = VRS_TILE_AUTO;
+    for (int t : cand) {
+      cs.tile = t;
+      std::vector<Launch> ls;
+      if (prep_conv(m->ctx, cs, view_of(m, c.x), c.w, c.scale, c.shift, c.has_res ? &r : nullptr, view_of(m, c.y),
+                    ls) != VRS_OK)
+        continue;
+      if ((rc = run(ls[0], s))) break;
+      VRS_HIP(hipEventRecord(e0, s));
+      for (int it = 0; it < 3; ++it)
+        if ((rc = run(ls[0], s))) break;
+      if (rc) break;
+      VRS_HIP(hipEventRecord(e1, s));
+      VRS_HIP(hipEventSynchronize(e1));
+      float ms = 0.f;
+      VRS_HIP(hipEventElapsedTime(&ms, e0, e1));
+      if (ms < best) { best = ms; best_tile = t; }
+    }
+    if (rc) break;
+    c.tile = best_tile;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipStreamDestroy(s);
+  (void)hipGetLastError();
+  return rc;
 }
 
 const Param* P(const vrs_model* m, const std::string& name) {
@@ -633,7 +684,18 @@ int vrs_model_finalize(vrs_model* m) {
     c.shift = static_cast<float*>(p);
   }
   for (Param& p : m->params) std::vector<float>().swap(p.host);
+  if (m->autotune) {
+    int rc = autotune_tiles(m);
+    if (rc) return rc;
+  }
   m->finalized = true;
+  return VRS_OK;
+}
+
+int vrs_model_set_autotune(vrs_model* m, int32_t on) {
+  if (!m) return fail(VRS_EINVAL, "null model");
+  if (m->finalized) return fail(VRS_ESTATE, "vrs_model_set_autotune: model already finalized");
+  m->autotune = on != 0;
   return VRS_OK;
 }
 

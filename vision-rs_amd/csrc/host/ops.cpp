@@ -33,7 +33,7 @@ int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const vo
                const float* shift, const vrs_nhwc* res, const vrs_nhwc* y, void* stream) {
   if (!ctx || !d || !x || !y) return fail(VRS_EINVAL, "vrs_conv2d: null argument");
   ConvSpec cs;
-  cs.k = d->k; cs.stride = d->stride; cs.act = d->act; cs.dtype = d->dtype;
+  cs.k = d->k; cs.stride = d->stride; cs.act = d->act; cs.dtype = d->dtype; cs.tile = d->tile;
   if (d->groups == 1) cs.depthwise = false;
   else if (d->groups == x->c && d->groups == y->c) cs.depthwise = true;
   else return fail(VRS_EUNSUPPORTED, "vrs_conv2d: groups=%d (only 1 or depthwise)", d->groups);

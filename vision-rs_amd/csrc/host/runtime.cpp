@@ -74,14 +74,62 @@ static int check_dtype(int dtype) {
 
 static inline int out_size(int in, int k, int s) { return (in + 2 * (k / 2) - k) / s + 1; }
 
-// Tile choice per Cout: narrow layers take the 32- or 64-row tiles so MFMA
-// rows are not wasted; everything else takes 128x128.
-static void pick_tile(int cout, int cin, int dtype, char* name, size_t n, int* bm, int* bn) {
-  const char* t;
-  if (cout <= 32) { t = "32x256"; *bm = 32; *bn = 256; }
-  else if (cout <= 64) { t = "64x256"; *bm = 64; *bn = 256; }
-  else { t = "128x128"; *bm = 128; *bn = 128; }
-  snprintf(name, n, "vrs_conv_%s_%s_%c", dsuffix(dtype), t, cin % 32 == 0 ? 'a' : 'g');
+// Dense-conv tiles.  bf16 has every tile with 32- and (when Cin % 64 == 0)
+// 64-deep K steps; the float32 parity path has 128x128, 64x256 and 32x256.
+struct TileInfo { int code, bm, bn; const char* tag; bool f32; };
+static const TileInfo kTiles[] = {
+    {VRS_TILE_128x128, 128, 128, "128x128", true}, {VRS_TILE_256x128, 256, 128, "256x128", false},
+    {VRS_TILE_128x256, 128, 256, "128x256", false}, {VRS_TILE_64x256, 64, 256, "64x256", true},
+    {VRS_TILE_32x256, 32, 256, "32x256", true},
+};
+
+static const TileInfo* tile_info(int code) {
+  for (const auto& t : kTiles)
+    if (t.code == (code & 0xff)) return &t;
+  return nullptr;
+}
+
+// Kernel name for a tile, or an error when the combination is not built.
+static int tile_kernel(int code, int cin, int dtype, char* name, size_t n, int* bm, int* bn) {
+  const TileInfo* t = tile_info(code);
+  if (!t) return fail(VRS_EINVAL, "conv: unknown tile code %d", code);
+  if (dtype == VRS_F32 && !t->f32) return fail(VRS_EUNSUPPORTED, "conv: tile %s has no float32 build", t->tag);
+  const bool g = cin % 32 != 0;
+  bool k64 = !(code & VRS_TILE_K32) && dtype == VRS_BF16 && cin % 64 == 0 && t->code != VRS_TILE_32x256;
+  if (g && t->code != VRS_TILE_128x128 && t->code != VRS_TILE_64x256 && t->code != VRS_TILE_32x256)
+    return fail(VRS_EUNSUPPORTED, "conv: tile %s needs Cin %% 32 == 0 (Cin=%d)", t->tag, cin);
+  snprintf(name, n, "vrs_conv_%s_%s_k%d_%c", dsuffix(dtype), t->tag, k64 ? 64 : 32, g ? 'g' : 'a');
+  *bm = t->bm;
+  *bn = t->bn;
+  return VRS_OK;
+}
+
+// Shape heuristic (VRS_TILE_AUTO): the widest tile that still gives the
+// 256-CU chip at least two workgroups per CU.
+static int auto_tile(int cout, int cin, int64_t M, int dtype, int num_cu) {
+  auto blocks = [&](int bm, int bn) { return (int64_t)((cout + bm - 1) / bm) * ((M + bn - 1) / bn); };
+  const int64_t want = 2ll * (num_cu > 0 ? num_cu : 256);
+  if (cout <= 32) return VRS_TILE_32x256;
+  if (cout <= 64) return VRS_TILE_64x256;
+  if (dtype == VRS_BF16 && cin % 32 == 0) {
+    if (cout <= 128 && blocks(128, 256) >= want) return VRS_TILE_128x256;
+    if (cout > 128 && blocks(256, 128) >= want) return VRS_TILE_256x128;
+  }
+  return VRS_TILE_128x128;
+}
+
+std::vector<int> conv_tile_candidates(int cout, int cin, int dtype) {
+  std::vector<int> c;
+  const bool g = cin % 32 != 0;
+  for (const auto& t : kTiles) {
+    if (dtype == VRS_F32 && !t.f32) continue;
+    if (g && t.code != VRS_TILE_128x128 && t.code != VRS_TILE_64x256 && t.code != VRS_TILE_32x256) continue;
+    if (t.bm >= 2 * 128 && cout <= 128) continue;   // mostly empty rows
+    if (t.bm <= 64 && cout > 4 * t.bm) continue;     // too many passes over the input
+    c.push_back(t.code);
+    if (dtype == VRS_BF16 && cin % 64 == 0 && t.code != VRS_TILE_32x256) c.push_back(t.code | VRS_TILE_K32);
+  }
+  return c;
 }
 
 static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
@@ -108,7 +156,8 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   a.act = cs.act;
   char name[64];
   int bm, bn;
-  pick_tile(cout, x.c, cs.dtype, name, sizeof name, &bm, &bn);
+  const int tile = cs.tile ? cs.tile : auto_tile(cout, x.c, M, cs.dtype, ctx->num_cu);
+  if ((rc = tile_kernel(tile, x.c, cs.dtype, name, sizeof name, &bm, &bn))) return rc;
   a.tiles_m = (cout + bm - 1) / bm;
   a.tiles_n = (int32_t)((M + bn - 1) / bn);
   const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
@@ -169,6 +218,9 @@ int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w
   a.y = const_cast<void*>(at(y, cs.dtype));
   a.y_sb = (int64_t)y.h * y.w * y.pitch; a.y_sp = y.pitch; a.y_sc = 1;
   a.y_f32 = 0;
+  // 16-byte chunks of 8 (bf16) or 4 (f32) channels must be whole and aligned
+  const int chunk = cs.dtype == VRS_F32 ? 4 : 8;
+  a.stage = (y.c % 8 == 0 && y.c_off % chunk == 0 && y.pitch % chunk == 0) ? 1 : 0;
   return prep_dense(ctx, cs, x, w, scale, shift, y.c, y.h, y.w, a, out);
 }
 

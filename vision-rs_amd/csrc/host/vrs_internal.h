@@ -69,7 +69,10 @@ struct ConvSpec {
   int k = 1, stride = 1, act = VRS_ACT_NONE, dtype = VRS_BF16;
   bool depthwise = false;
   int cin_real = 0;  // unpadded input channels for work accounting (0: the view's)
+  int tile = VRS_TILE_AUTO;  // dense conv tile (VRS_TILE_*)
 };
+// Dense conv tiles worth trying for a layer (autotuning candidates).
+std::vector<int> conv_tile_candidates(int cout, int cin, int dtype);
 int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
               const float* shift, const vrs_nhwc* res, const vrs_nhwc& y, std::vector<Launch>& out);
 // Dense conv storing float32 into a strided (flat) output: element (b, p, co)

@@ -33,6 +33,9 @@ typedef struct {
   int32_t act;
   int32_t y_f32;  /* 1: store float32, 0: store the kernel's element type */
   int32_t tiles_m, tiles_n; /* grid decomposition: Cout tiles x pixel tiles */
+  int32_t stage;  /* 1: NHWC output staged through LDS for 16-byte stores
+                     (element-type output, y_sc == 1, Cout % 8 == 0, 16-byte
+                     aligned channel offset and pitch) */
 } vrs_conv_args;
 
 /* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the

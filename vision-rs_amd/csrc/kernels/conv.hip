@@ -17,7 +17,6 @@
 
 namespace {
 
-constexpr int BK = 32;
 constexpr int NT = 256;
 
 // blockIdx.x -> logical tile id so that each XCD (blocks are dealt round-robin
@@ -29,21 +28,29 @@ __device__ __forceinline__ int xcd_remap(int bid, int G) {
   return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
 }
 
-template <typename T, int BM, int BN, int WGM, int WGN, bool ALIGNED>
+// BM output channels x BN pixels per workgroup, BK reduction elements per
+// pipeline step, WGM x WGN waves (wave tile (BM/WGM) x (BN/WGN)).
+// ALIGNED: Cin % BK == 0, so a K step never straddles two filter taps.
+template <typename T, int BM, int BN, int BK, int WGM, int WGN, bool ALIGNED>
 __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   using E = Elt<T>;
   using G = typename E::group;
-  constexpr int PAD = 16 / sizeof(T) * 2;    // 32 bytes of row padding
+  constexpr int PAD = 32 / (int)sizeof(T);   // 32 bytes of row padding
   constexpr int LDK = BK + PAD;              // LDS row stride in elements
+  constexpr int GPR = BK / 8;                // 8-element groups per tile row
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int TM = WTM / 16, TN = WTN / 16;
-  constexpr int A_IT = (BM * 4 + NT - 1) / NT;
-  constexpr int B_IT = (BN * 4 + NT - 1) / NT;
+  constexpr int A_IT = (BM * GPR + NT - 1) / NT;
+  constexpr int B_IT = (BN * GPR + NT - 1) / NT;
+  constexpr int TILE_ELEMS = (BM + BN) * LDK;            // one pipeline stage
+  // epilogue staging: per wave WTN pixels x (WTM + SPAD) channels
+  constexpr int SPAD = 16 / (int)sizeof(T);
+  constexpr int STAGE_ELEMS = 4 * WTN * (WTM + SPAD);
+  constexpr int SMEM_ELEMS = 2 * TILE_ELEMS > STAGE_ELEMS ? 2 * TILE_ELEMS : STAGE_ELEMS;
   static_assert(WGM * WGN == 4, "4 waves");
-  static_assert(TM >= 1 && TN >= 1, "tile");
+  static_assert(TM >= 1 && TN >= 1 && BK % 32 == 0, "tile");
 
-  __shared__ __attribute__((aligned(16))) T sA[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) T sB[2][BN * LDK];
+  __shared__ __attribute__((aligned(16))) T smem[SMEM_ELEMS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -59,16 +66,14 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   const int HWo = a.Ho * a.Wo;
 
   // Per-thread B (pixel) chunk geometry, fixed over the K loop.
-  int b_iy0[B_IT], b_ix0[B_IT], b_grp[B_IT], b_row[B_IT];
+  int b_iy0[B_IT], b_ix0[B_IT];
   int64_t b_base[B_IT];
   bool b_ok[B_IT];
 #pragma unroll
   for (int i = 0; i < B_IT; ++i) {
     const int c = tid + i * NT;
-    b_row[i] = c >> 2;
-    b_grp[i] = c & 3;
-    const int m = n0 + b_row[i];
-    b_ok[i] = (c < BN * 4) && (m < a.M);
+    const int m = n0 + c / GPR;
+    b_ok[i] = (c < BN * GPR) && (m < a.M);
     const int mm = b_ok[i] ? m : 0;
     const int bb = mm / HWo, rr = mm - bb * HWo;
     const int oy = rr / a.Wo, ox = rr - oy * a.Wo;
@@ -83,21 +88,18 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       const int c = tid + i * NT;
-      const int row = c >> 2, k = k0 + (c & 3) * 8;
-      const int co = m0 + row;
-      if (c < BM * 4 && co < a.Cout && k < a.K)
-        ra[i] = E::load(w + (int64_t)co * a.K + k);
-      else
-        ra[i] = E::zero();
+      const int co = m0 + c / GPR, k = k0 + (c % GPR) * 8;
+      ra[i] = (c < BM * GPR && co < a.Cout && k < a.K) ? E::load(w + (int64_t)co * a.K + k) : E::zero();
     }
     int tap = 0, ci0 = 0;
     if (ALIGNED) { tap = k0 / a.Cin; ci0 = k0 - tap * a.Cin; }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
-      int t = tap, ci = ci0 + b_grp[i] * 8;
+      const int grp = (tid + i * NT) % GPR;
+      int t = tap, ci = ci0 + grp * 8;
       bool ok = b_ok[i];
       if (!ALIGNED) {
-        const int k = k0 + b_grp[i] * 8;
+        const int k = k0 + grp * 8;
         ok = ok && (k < a.K);
         t = k / a.Cin;
         ci = k - t * a.Cin;
@@ -105,23 +107,22 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
       const int ky = t / a.kw, kx = t - ky * a.kw;
       const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
       ok = ok && (iy >= 0) && (iy < a.H) && (ix >= 0) && (ix < a.W);
-      if (ok)
-        rb[i] = E::load(x + (b_base[i] + (int64_t)iy * a.W + ix) * a.x_pitch + ci);
-      else
-        rb[i] = E::zero();
+      rb[i] = ok ? E::load(x + (b_base[i] + (int64_t)iy * a.W + ix) * a.x_pitch + ci) : E::zero();
     }
   };
 
   auto store_tiles = [&](int buf) {
+    T* sA = smem + buf * TILE_ELEMS;
+    T* sB = sA + BM * LDK;
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       const int c = tid + i * NT;
-      if (c < BM * 4) E::store(&sA[buf][(c >> 2) * LDK + (c & 3) * 8], ra[i]);
+      if (c < BM * GPR) E::store(&sA[(c / GPR) * LDK + (c % GPR) * 8], ra[i]);
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
       const int c = tid + i * NT;
-      if (c < BN * 4) E::store(&sB[buf][b_row[i] * LDK + b_grp[i] * 8], rb[i]);
+      if (c < BN * GPR) E::store(&sB[(c / GPR) * LDK + (c % GPR) * 8], rb[i]);
     }
   };
 
@@ -142,25 +143,81 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < nk) load_tiles((kt + 1) * BK);
-
-    G fa[TM], fb[TN];
+    const T* sA = smem + cur * TILE_ELEMS;
+    const T* sB = sA + BM * LDK;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-      fa[i] = E::load(&sA[cur][(wm * WTM + i * 16 + frag_row) * LDK + frag_k]);
+    for (int kk = 0; kk < BK / 32; ++kk) {
+      G fa[TM], fb[TN];
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-      fb[j] = E::load(&sB[cur][(wn * WTN + j * 16 + frag_row) * LDK + frag_k]);
+      for (int i = 0; i < TM; ++i)
+        fa[i] = E::load(&sA[(wm * WTM + i * 16 + frag_row) * LDK + kk * 32 + frag_k]);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j)
+        fb[j] = E::load(&sB[(wn * WTN + j * 16 + frag_row) * LDK + kk * 32 + frag_k]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = mfma_k32(fa[i], fb[j], acc[i][j]);
-
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_k32(fa[i], fb[j], acc[i][j]);
+    }
     if (kt + 1 < nk) store_tiles(cur ^ 1);
     __syncthreads();
   }
 
-  // Epilogue: folded BN, activation, residual, store.
+  // Epilogue: folded BN, activation, residual.
   const int q = lane >> 4;
+  if (a.stage) {
+    // Staged store: every wave writes its (WTN pixel x WTM channel) tile to
+    // LDS, then stores whole 16-byte channel chunks per lane, so consecutive
+    // lanes write contiguous bytes of a pixel's NHWC row.
+    T* st = smem + wave * WTN * (WTM + SPAD);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int cl = i * 16 + q * 4;          // channel within the wave tile
+      const int co = m0 + wm * WTM + cl;
+      float sc[4], sh[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int c = co + r < a.Cout ? co + r : a.Cout - 1;
+        sc[r] = a.scale[c];
+        sh[r] = a.shift[c];
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int pl = j * 16 + (lane & 15);
+        const int m = n0 + wn * WTN + pl;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float t = acc[i][j][r] * sc[r] + sh[r];
+          if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
+          v[r] = t;
+        }
+        if (a.res && m < a.M && co < a.Cout) {
+          const int bb = m / HWo, pp = m - bb * HWo;
+          const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + co;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] += E::to_f(rp[r]);
+        }
+        T* sp = st + pl * (WTM + SPAD) + cl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sp[r] = E::from_f(v[r]);
+      }
+    }
+    __syncthreads();
+    constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+    constexpr int CPP = WTM / EPC;            // chunks per pixel row
+    const int co_w = m0 + wm * WTM;
+    for (int c = lane; c < WTN * CPP; c += 64) {
+      const int pl = c / CPP, part = c % CPP;
+      const int m = n0 + wn * WTN + pl;
+      const int co = co_w + part * EPC;
+      if (m >= a.M || co >= a.Cout) continue;
+      const int bb = m / HWo, pp = m - bb * HWo;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + pl * (WTM + SPAD) + part * EPC);
+      *reinterpret_cast<u32x4_t*>(reinterpret_cast<T*>(a.y) + bb * a.y_sb + pp * a.y_sp + co) = v;
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int co = m0 + wm * WTM + i * 16 + q * 4;
@@ -219,26 +276,32 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
 
 }  // namespace
 
-#define VRS_CONV_KERNEL(NAME, T, BM, BN, WGM, WGN, AL)                                  \
+#define VRS_CONV_KERNEL(NAME, T, BM, BN, BK, WGM, WGN, AL)                              \
   extern "C" __global__ __launch_bounds__(256) void NAME(vrs_conv_args a) {            \
-    conv_body<T, BM, BN, WGM, WGN, AL>(a);                                              \
+    conv_body<T, BM, BN, BK, WGM, WGN, AL>(a);                                          \
   }
 
-// bf16 tiles: 128x128 (2x2 waves of 64x64), 64x256 (1x4 waves of 64x64),
-// 32x256 (1x4 waves of 32x64) for narrow Cout.
-VRS_CONV_KERNEL(vrs_conv_bf16_128x128_a, bf16_t, 128, 128, 2, 2, true)
-VRS_CONV_KERNEL(vrs_conv_bf16_128x128_g, bf16_t, 128, 128, 2, 2, false)
-VRS_CONV_KERNEL(vrs_conv_bf16_64x256_a, bf16_t, 64, 256, 1, 4, true)
-VRS_CONV_KERNEL(vrs_conv_bf16_64x256_g, bf16_t, 64, 256, 1, 4, false)
-VRS_CONV_KERNEL(vrs_conv_bf16_32x256_a, bf16_t, 32, 256, 1, 4, true)
-VRS_CONV_KERNEL(vrs_conv_bf16_32x256_g, bf16_t, 32, 256, 1, 4, false)
+// Kernel names: vrs_conv_<type>_<BM>x<BN>_k<BK>_<a|g>.  Wave tiles: 128x128
+// and 64x256 -> 64x64, 256x128 -> 128x64, 128x256 -> 64x128, 32x256 -> 32x64.
+VRS_CONV_KERNEL(vrs_conv_bf16_128x128_k32_a, bf16_t, 128, 128, 32, 2, 2, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_128x128_k32_g, bf16_t, 128, 128, 32, 2, 2, false)
+VRS_CONV_KERNEL(vrs_conv_bf16_128x128_k64_a, bf16_t, 128, 128, 64, 2, 2, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_256x128_k32_a, bf16_t, 256, 128, 32, 2, 2, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_256x128_k64_a, bf16_t, 256, 128, 64, 2, 2, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_128x256_k32_a, bf16_t, 128, 256, 32, 2, 2, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_128x256_k64_a, bf16_t, 128, 256, 64, 2, 2, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_64x256_k32_a, bf16_t, 64, 256, 32, 1, 4, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_64x256_k32_g, bf16_t, 64, 256, 32, 1, 4, false)
+VRS_CONV_KERNEL(vrs_conv_bf16_64x256_k64_a, bf16_t, 64, 256, 64, 1, 4, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_32x256_k32_a, bf16_t, 32, 256, 32, 1, 4, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_32x256_k32_g, bf16_t, 32, 256, 32, 1, 4, false)
 // f32 (parity path, fp32 MFMA)
-VRS_CONV_KERNEL(vrs_conv_f32_128x128_a, float, 128, 128, 2, 2, true)
-VRS_CONV_KERNEL(vrs_conv_f32_128x128_g, float, 128, 128, 2, 2, false)
-VRS_CONV_KERNEL(vrs_conv_f32_64x256_a, float, 64, 256, 1, 4, true)
-VRS_CONV_KERNEL(vrs_conv_f32_64x256_g, float, 64, 256, 1, 4, false)
-VRS_CONV_KERNEL(vrs_conv_f32_32x256_a, float, 32, 256, 1, 4, true)
-VRS_CONV_KERNEL(vrs_conv_f32_32x256_g, float, 32, 256, 1, 4, false)
+VRS_CONV_KERNEL(vrs_conv_f32_128x128_k32_a, float, 128, 128, 32, 2, 2, true)
+VRS_CONV_KERNEL(vrs_conv_f32_128x128_k32_g, float, 128, 128, 32, 2, 2, false)
+VRS_CONV_KERNEL(vrs_conv_f32_64x256_k32_a, float, 64, 256, 32, 1, 4, true)
+VRS_CONV_KERNEL(vrs_conv_f32_64x256_k32_g, float, 64, 256, 32, 1, 4, false)
+VRS_CONV_KERNEL(vrs_conv_f32_32x256_k32_a, float, 32, 256, 32, 1, 4, true)
+VRS_CONV_KERNEL(vrs_conv_f32_32x256_k32_g, float, 32, 256, 32, 1, 4, false)
 
 // ---------------------------------------------------------------------------
 // NCHW float32 image batch -> NHWC (element type) with zero channel padding.

@@ -26,6 +26,7 @@ ACT_NONE, ACT_SILU = 0, 1
 BLOCK_CONV, BLOCK_C3K2, BLOCK_C3K2_PSA, BLOCK_C2PSA, BLOCK_SPPF, BLOCK_PSA_ATTN, BLOCK_DETECT_BOX, BLOCK_YOLO26 = \
     1, 2, 3, 4, 5, 6, 7, 8
 CONV_BN_SILU, CONV_BN, CONV_PLAIN = 0, 1, 2
+TILE_AUTO, TILE_128x128, TILE_256x128, TILE_128x256, TILE_64x256, TILE_32x256, TILE_K32 = 0, 1, 2, 3, 4, 5, 0x100
 
 ERRORS = {-1: "EINVAL", -2: "EBADSHAPE", -3: "EUNSUPPORTED", -4: "ENOMODULE", -5: "EHIP", -6: "ENOTFOUND",
           -7: "ESTATE"}
@@ -44,7 +45,7 @@ class Nhwc(C.Structure):
 
 class ConvDesc(C.Structure):
     _fields_ = [("k", C.c_int32), ("stride", C.c_int32), ("groups", C.c_int32), ("act", C.c_int32),
-                ("dtype", C.c_int32)]
+                ("dtype", C.c_int32), ("tile", C.c_int32)]
 
 
 class PsaDesc(C.Structure):
@@ -90,6 +91,7 @@ SIGNATURES = {
     "vrs_detect_decode_grid": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "vrs_msda": (C.c_int, [_vp, _P(MsdaDesc), _vp, _vp, _vp, _vp, _vp, _vp]),
     "vrs_model_create": (C.c_int, [_vp, _P(BlockDesc), _i32, _i32, _i32, _i32, _f32, _P(_vp)]),
+    "vrs_model_set_autotune": (C.c_int, [_vp, _i32]),
     "vrs_model_num_params": (C.c_int, [_vp]),
     "vrs_model_param_info": (C.c_int, [_vp, _i32, _P(C.c_char_p), _P(_i32), _P(_i32)]),
     "vrs_model_load_param": (C.c_int, [_vp, C.c_char_p, _vp, _i64]),
@@ -177,9 +179,9 @@ class Context:
 
     # ---- single ops --------------------------------------------------------
     def conv2d(self, x, w, scale, shift, y, k, stride=1, groups=1, act=ACT_SILU, res=None, dtype=BF16,
-               stream=None):
+               stream=None, tile=TILE_AUTO):
         """x, y, res: Nhwc views; w/scale/shift: device tensors."""
-        d = ConvDesc(k, stride, groups, act, dtype)
+        d = ConvDesc(k, stride, groups, act, dtype, tile)
         check(lib().vrs_conv2d(self.handle, C.byref(d), C.byref(x), _ptr(w), _ptr(scale), _ptr(shift),
                                C.byref(res) if res is not None else None, C.byref(y), _stream(stream)))
 
@@ -265,7 +267,8 @@ class Model:
     Mirrors the reference's flow: build closures -> load_param_f32 per name ->
     forward / capture_graph + run_inplace."""
 
-    def __init__(self, ctx, desc: BlockDesc, batch: int, h: int, w: int, dtype=BF16, bn_eps=1e-3):
+    def __init__(self, ctx, desc: BlockDesc, batch: int, h: int, w: int, dtype=BF16, bn_eps=1e-3,
+                 autotune=True):
         """ctx=None records the layers only (params()/output_shapes() work without a GPU)."""
         self.ctx = ctx
         self.desc = desc
@@ -273,6 +276,7 @@ class Model:
         self.handle = C.c_void_p()
         check(lib().vrs_model_create(ctx.handle if ctx is not None else None, C.byref(desc), batch, h, w, dtype,
                                      bn_eps, C.byref(self.handle)))
+        check(lib().vrs_model_set_autotune(self.handle, int(autotune)))
 
     def params(self):
         """[(name, shape)] in recording order (the reference's name_scope paths)."""
