@@ -107,6 +107,138 @@ def cpu_baseline(variant, size, P, budget_s=15.0):
                       f"({dt:.1f} s) on the C oracle (oracle/vrs_oracle.c, OpenMP); the reference has no CPU path"}
 
 
+def _time_launches(fn, n_sets, iters=20, warmup=3):
+    """Average GPU time of fn(set_index) (one kernel launch each), measured with
+    events around every launch on the current stream."""
+    import torch
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn(i % n_sets)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for i, (e0, e1) in enumerate(evs):
+        e0.record(stream)
+        fn(i % n_sets)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in evs) / iters  # ms
+
+
+def micro(ctx, emit):
+    """BASELINE configs 2-4 as isolated kernels (bf16 unless stated)."""
+    import numpy as np
+    import torch
+    import vrs
+    from vrs.synth import seeded_params
+    dev = "cuda"
+    MALL = 256 * 2 ** 20  # Infinity Cache: rotate buffer sets beyond it for HBM-bound kernels
+
+    def sets_for(nbytes):
+        return max(1, int(np.ceil(2 * MALL / max(nbytes, 1))))
+
+    # copy of a known size: calibrates FETCH_SIZE / WRITE_SIZE counter readings
+    src = torch.empty(2 ** 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    emit({"config": "calibration copy", "bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4})
+    del src, dst
+
+    # ---- config 3: conv microbench, B=32, folded BN + SiLU epilogue ----------
+    convs = [("c3a 3x3 s1 128->128 @80", 128, 128, 80, 3, 1), ("c3b 3x3 s2 256->512 @40", 256, 512, 40, 3, 2),
+             ("c3d 1x1 1024->512 @20", 1024, 512, 20, 1, 1)]
+    B = 32
+    rng = np.random.default_rng(0)
+    for name, cin, cout, hw, k, s in convs:
+        ho = (hw + 2 * (k // 2) - k) // s + 1
+        wt = (rng.standard_normal((cout, cin, k, k)) * np.sqrt(2.0 / (cin * k * k))).astype(np.float32)
+        wp = torch.from_numpy(vrs.pack_conv_weight(wt, 1, cin, vrs.BF16)).to(dev)
+        sc = torch.full((cout,), 1.0 / np.sqrt(1.001), device=dev)
+        sh = torch.zeros(cout, device=dev)
+        in_b, out_b = B * hw * hw * cin * 2, B * ho * ho * cout * 2
+        n_sets = sets_for(in_b + out_b)
+        xs = [torch.nn.functional.silu(torch.randn(B, hw, hw, cin, device=dev)).to(torch.bfloat16) for _ in range(n_sets)]
+        ys = [torch.empty(B, ho, ho, cout, dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
+        flops = 2.0 * B * ho * ho * cout * cin * k * k
+        best = None
+        for tile in [vrs.TILE_128x128, vrs.TILE_128x128 | vrs.TILE_K32, vrs.TILE_256x128, vrs.TILE_128x256,
+                     vrs.TILE_64x256]:
+            try:
+                f = lambda i, t=tile: ctx.conv2d(vrs.nhwc(xs[i]), wp, sc, sh, vrs.nhwc(ys[i]), k, s, 1, vrs.ACT_SILU,
+                                                  None, vrs.BF16, tile=t)
+                ms = _time_launches(f, n_sets)
+            except vrs.VrsError:
+                continue
+            if best is None or ms < best[1]:
+                best = (tile, ms)
+        tile, ms = best
+        emit({"config": name, "batch": B, "us": round(ms * 1e3, 2), "tile": tile,
+              "gflop": round(flops / 1e9, 2), "tflops": round(flops / ms / 1e9, 1),
+              "frac_mfma": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+              "mb": round((in_b + out_b + cout * cin * k * k * 2) / 1e6, 1), "buffer_sets": n_sets})
+        del xs, ys
+
+    # (c) depthwise 3x3 512 @20x20, HBM-bound
+    C, hw = 512, 20
+    wdw = (rng.standard_normal((C, 1, 3, 3)) * np.sqrt(2.0 / 9)).astype(np.float32)
+    wp = torch.from_numpy(vrs.pack_conv_weight(wdw, C, 1, vrs.BF16)).to(dev)
+    sc = torch.full((C,), 1.0 / np.sqrt(1.001), device=dev)
+    sh = torch.zeros(C, device=dev)
+    nb = 2 * B * hw * hw * C * 2
+    n_sets = sets_for(nb)
+    xs = [torch.nn.functional.silu(torch.randn(B, hw, hw, C, device=dev)).to(torch.bfloat16) for _ in range(n_sets)]
+    ys = [torch.empty(B, hw, hw, C, dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
+    ms = _time_launches(lambda i: ctx.conv2d(vrs.nhwc(xs[i]), wp, sc, sh, vrs.nhwc(ys[i]), 3, 1, C, vrs.ACT_SILU,
+                                             None, vrs.BF16), n_sets, iters=60)
+    emit({"config": "c3c dw3x3 512 @20", "batch": B, "us": round(ms * 1e3, 2), "mb": round(nb / 1e6, 2),
+          "gbs": round(nb / ms / 1e6, 1), "frac_hbm": round(nb / ms / 1e6 / PEAK_HBM_GBS, 4), "buffer_sets": n_sets})
+    del xs, ys
+
+    # ---- config 2: isolated PSA attention block, B=32, 256 ch @20x20, 4 heads --
+    desc = vrs.block(vrs.BLOCK_PSA_ATTN, 256, 256, heads=4)
+    m = vrs.Model(ctx, desc, 32, 20, 20, vrs.BF16, 1e-3)
+    P = seeded_params(m.params(), seed=0)
+    for nme in P:  # N(0, 1/sqrt(C)) weights (BASELINE config 2)
+        if P[nme].ndim == 4:
+            P[nme] = (np.random.default_rng(1).standard_normal(P[nme].shape) / 16.0).astype(np.float32)
+    m.load(P)
+    x = torch.randn(32, 256, 20, 20, device=dev)
+    outs = m.forward(x)
+    torch.cuda.synchronize()
+    names = m.launch_names()
+    work = m.launch_work()
+    ai = [i for i, n in enumerate(names) if "psa_attn" in n][0]
+    ms_core = _time_launches(lambda i: m.run_launches(ai, 1), 1, iters=50)
+    ms_blk = _time_launches(lambda i: m.run_launches(1, len(names) - 2), 1, iters=20)  # qkv..proj, no pack/unpack
+    core_fl = work[ai][0]
+    blk_fl = sum(w[0] for w in work[1:len(names) - 1])
+    emit({"config": "c2 psa attention B32 256ch 20x20 4 heads", "core_us": round(ms_core * 1e3, 2),
+          "core_gflop": round(core_fl / 1e9, 3), "core_tflops": round(core_fl / ms_core / 1e9, 1),
+          "core_frac_mfma": round(core_fl / ms_core / 1e9 / PEAK_BF16_TFLOPS, 4),
+          "block_us": round(ms_blk * 1e3, 2), "block_gflop": round(blk_fl / 1e9, 3),
+          "block_tflops": round(blk_fl / ms_blk / 1e9, 1)})
+    m.close()
+
+    # ---- config 4: MSDA, fp32 value, B=8, Q=300, 8 heads, 4 levels x 4 points ----
+    shapes = [(80, 80), (40, 40), (20, 20), (10, 10)]
+    Bq, Q, Hh, L, Pp = 8, 300, 8, 4, 4
+    S = sum(h * w for h, w in shapes)
+    vbytes = Bq * S * Hh * 32 * 4
+    n_sets = sets_for(vbytes)
+    vals = [torch.randn(Bq, S, Hh, 32, device=dev) for _ in range(n_sets)]
+    ref = torch.rand(Bq, Q, 2, device=dev)
+    off = torch.randn(Bq, Q, Hh, L, Pp, 2, device=dev) * 0.05
+    attw = torch.softmax(torch.randn(Bq, Q, Hh, L * Pp, device=dev), -1).reshape(Bq, Q, Hh, L, Pp).contiguous()
+    out = torch.empty(Bq, Q, Hh * 32, device=dev)
+    ms = _time_launches(lambda i: ctx.msda(vals[i], shapes, ref, off, attw, out), n_sets, iters=60)
+    comp = vbytes + ref.numel() * 4 + off.numel() * 4 + attw.numel() * 4 + out.numel() * 4
+    issued = Bq * Q * Hh * L * Pp * 4 * 32 * 4
+    emit({"config": "c4 msda B8 Q300 8h 4L 4P fp32", "us": round(ms * 1e3, 2),
+          "compulsory_mb": round(comp / 1e6, 2), "gbs_compulsory": round(comp / ms / 1e6, 1),
+          "frac_hbm": round(comp / ms / 1e6 / PEAK_HBM_GBS, 4), "issued_gather_mb": round(issued / 1e6, 1),
+          "buffer_sets": n_sets})
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -118,6 +250,8 @@ def main() -> int:
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "f32"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--layers", action="store_true", help="also print the per-layer table to stderr")
+    ap.add_argument("--micro", action="store_true",
+                    help="instead: BASELINE configs 2-4 as isolated kernels, one JSON line each")
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -130,9 +264,12 @@ def main() -> int:
     import vrs
     from vrs.synth import images, seeded_params
 
-    log(f"[bench] YOLO26{a.variant} {a.dtype} bs{a.batch} {a.size}x{a.size}: building")
     torch.cuda.init()
     ctx = vrs.Context(0)
+    if a.micro:
+        micro(ctx, lambda d: print(json.dumps(d), flush=True))
+        return 0
+    log(f"[bench] YOLO26{a.variant} {a.dtype} bs{a.batch} {a.size}x{a.size}: building")
     dt = vrs.BF16 if a.dtype == "bf16" else vrs.F32
     desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant=a.variant, one2one=True)
     m = vrs.Model(ctx, desc, a.batch, a.size, a.size, dt, 1e-3)

@@ -146,12 +146,22 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   a.w = w;
   a.scale = scale;
   a.shift = shift;
+  {  // raw-buffer extents (the kernels use 32-bit byte offsets)
+    const int64_t xb = ((int64_t)x.n * x.h * x.w * x.pitch - x.c_off) * (int64_t)elt_size(cs.dtype);
+    const int64_t wb = (int64_t)cout * cs.k * cs.k * x.c * (int64_t)elt_size(cs.dtype);
+    if (xb >= (1ll << 31) || wb >= (1ll << 31))
+      return fail(VRS_EBADSHAPE, "conv: input buffer (%lld B) or weights (%lld B) exceed 2 GiB", (long long)xb,
+                  (long long)wb);
+    a.x_bytes = (int32_t)xb;
+    a.w_bytes = (int32_t)wb;
+  }
   a.N = x.n; a.H = x.h; a.W = x.w; a.Cin = x.c; a.x_pitch = x.pitch;
   a.Ho = ho; a.Wo = wo; a.Cout = cout;
   a.kh = a.kw = cs.k; a.stride = cs.stride; a.pad = cs.k / 2;
   a.K = cs.k * cs.k * x.c;
   const int64_t M = (int64_t)x.n * ho * wo;
-  if (M >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: %lld output pixels exceed int32", (long long)M);
+  if (M >= (1ll << 24))  // the kernels divide pixel indices through a float reciprocal
+    return fail(VRS_EBADSHAPE, "conv: %lld output pixels per launch exceed 2^24 (split the batch)", (long long)M);
   a.M = (int32_t)M;
   a.act = cs.act;
   char name[64];
@@ -195,12 +205,13 @@ int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w
     a.N = x.n; a.H = x.h; a.W = x.w; a.C = x.c; a.x_pitch = x.pitch;
     a.Ho = y.h; a.Wo = y.w; a.y_pitch = y.pitch;
     a.kh = a.kw = cs.k; a.stride = cs.stride; a.pad = cs.k / 2; a.act = cs.act;
-    const int64_t threads = (int64_t)x.n * ((y.h + 3) / 4) * y.w * (x.c / 8);
+    const int64_t per_img = (int64_t)((y.h + 3) / 4) * y.w * (x.c / 8);
+    if (per_img >= (1ll << 24)) return fail(VRS_EBADSHAPE, "dwconv: map too large for one grid row");
     char name[48];
     snprintf(name, sizeof name, "vrs_dwconv3_s%d_%s", cs.stride, dsuffix(cs.dtype));
     hipFunction_t f;
     if ((rc = get_fn(ctx, name, &f))) return rc;
-    out.push_back(make_launch(name, f, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a));
+    out.push_back(make_launch(name, f, dim3((unsigned)((per_img + 255) / 256), (unsigned)x.n), dim3(256), 0, a));
     const double es = (double)elt_size(cs.dtype);
     out.back().flops = 2.0 * x.n * y.h * y.w * (double)x.c * cs.k * cs.k;
     out.back().bytes = (double)x.n * x.h * x.w * x.c * es + (double)y.n * y.h * y.w * y.c * es +

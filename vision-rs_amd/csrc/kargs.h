@@ -36,6 +36,8 @@ typedef struct {
   int32_t stage;  /* 1: NHWC output staged through LDS for 16-byte stores
                      (element-type output, y_sc == 1, Cout % 8 == 0, 16-byte
                      aligned channel offset and pitch) */
+  int32_t x_bytes;  /* readable bytes from x to the end of its buffer (< 2^31) */
+  int32_t w_bytes;  /* bytes of the packed weights (< 2^31) */
 } vrs_conv_args;
 
 /* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the

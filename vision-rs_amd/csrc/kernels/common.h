@@ -15,21 +15,45 @@ typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
 
 __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
 
-// float -> bfloat16, round to nearest even (NaN stays NaN).
-__device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+typedef float f32x2_hw __attribute__((ext_vector_type(2)));
+
+// float -> bfloat16, round to nearest even (gfx950 v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+// Two floats -> packed bfloat16 pair (lo, hi) in one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_hw f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_hw));
 }
 
-// SiLU: the bfloat16 path uses the fast exp (its error is far below bf16
-// resolution); the float32 parity path uses the accurately rounded expf.
-__device__ __forceinline__ float silu_fast(float v) { return v / (1.0f + __expf(-v)); }
+// q = n / d and r = n % d for 0 <= n < 2^24 and d >= 1 from the float
+// reciprocal: n is exact in float and the float quotient is within one of
+// the true one, so a single correction step makes it exact.
+__device__ __forceinline__ int fdivmod(int n, int d, float inv_d, int& r) {
+  int q = (int)((float)n * inv_d);
+  r = n - q * d;
+  if (r < 0) { --q; r += d; } else if (r >= d) { ++q; r -= d; }
+  return q;
+}
+
+// SiLU: the bfloat16 path uses the hardware exp2 and reciprocal (v_exp_f32,
+// v_rcp_f32, ~1 ulp each -- far below bf16 resolution) instead of an
+// IEEE-exact division; the float32 parity path uses expf and a true divide.
+__device__ __forceinline__ float silu_fast(float v) {
+  const float e = __builtin_amdgcn_exp2f(-v * 1.4426950408889634f);
+  return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
 __device__ __forceinline__ float silu_acc(float v) { return v / (1.0f + expf(-v)); }
 template <typename T> __device__ __forceinline__ float silu_t(float v) {
   return sizeof(T) == 4 ? silu_acc(v) : silu_fast(v);
 }
+
+// Raw buffer resource over [base, base + bytes): a load whose offset is at or
+// past `bytes` returns zeros, so padding/halo lanes need no branch.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+constexpr uint32_t kOOB = 0x80000000u;  // an offset every resource here rejects
 
 // ---- element traits --------------------------------------------------------
 // A "group" is 8 consecutive elements along K: the unit one lane feeds into
@@ -38,6 +62,9 @@ template <typename T> struct Elt;
 
 template <> struct Elt<bf16_t> {
   struct group { u32x4_t v; };
+  static __device__ __forceinline__ group bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    group g; g.v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0); return g;
+  }
   static __device__ __forceinline__ group load(const bf16_t* p) {
     group g; g.v = *reinterpret_cast<const u32x4_t*>(p); return g;
   }
@@ -51,6 +78,12 @@ template <> struct Elt<bf16_t> {
 
 template <> struct Elt<float> {
   struct group { u32x4_t lo, hi; };
+  static __device__ __forceinline__ group bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    group g;
+    g.lo = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    g.hi = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16u, soff, 0);
+    return g;
+  }
   static __device__ __forceinline__ group load(const float* p) {
     group g;
     g.lo = *reinterpret_cast<const u32x4_t*>(p);

@@ -64,10 +64,25 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
   const T* __restrict__ w = reinterpret_cast<const T*>(a.w);
   const int HWo = a.Ho * a.Wo;
+  // pixel index -> (image, position): float-reciprocal divmod (M < 2^24 is
+  // checked on the host)
+  const float inv_hwo = 1.0f / (float)HWo, inv_wo = 1.0f / (float)a.Wo;
 
-  // Per-thread B (pixel) chunk geometry, fixed over the K loop.
+  // Per-thread chunk geometry, fixed over the K loop: the A pointer advances
+  // by k0; the B (pixel) pointer is the tap-(0,0) input pixel and each K step
+  // adds a wave-uniform tap offset, so the loop body does one 64-bit add and
+  // two range checks per chunk.
+  const T* a_ptr[A_IT];
+  bool a_ok[A_IT];
+#pragma unroll
+  for (int i = 0; i < A_IT; ++i) {
+    const int c = tid + i * NT;
+    const int co = m0 + c / GPR;
+    a_ok[i] = (c < BM * GPR) && (co < a.Cout);
+    a_ptr[i] = w + (int64_t)(a_ok[i] ? co : 0) * a.K + (c % GPR) * 8;
+  }
   int b_iy0[B_IT], b_ix0[B_IT];
-  int64_t b_base[B_IT];
+  const T* b_ptr[B_IT];
   bool b_ok[B_IT];
 #pragma unroll
   for (int i = 0; i < B_IT; ++i) {
@@ -75,39 +90,67 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
     const int m = n0 + c / GPR;
     b_ok[i] = (c < BN * GPR) && (m < a.M);
     const int mm = b_ok[i] ? m : 0;
-    const int bb = mm / HWo, rr = mm - bb * HWo;
-    const int oy = rr / a.Wo, ox = rr - oy * a.Wo;
+    int rr, ox;
+    const int bb = fdivmod(mm, HWo, inv_hwo, rr);
+    const int oy = fdivmod(rr, a.Wo, inv_wo, ox);
     b_iy0[i] = oy * a.stride - a.pad;
     b_ix0[i] = ox * a.stride - a.pad;
-    b_base[i] = (int64_t)bb * a.H * a.W;
+    b_ptr[i] = x + (((int64_t)bb * a.H + b_iy0[i]) * a.W + b_ix0[i]) * a.x_pitch + (c % GPR) * 8;
   }
 
   G ra[A_IT], rb[B_IT];
 
+  // ALIGNED path: raw buffer loads.  Weight rows: per-lane byte offset, the
+  // K step as the scalar offset.  Pixels: per-lane byte offset of the
+  // tap-(0,0) position plus a wave-uniform tap offset; lanes whose tap falls
+  // in the zero padding (or past the last pixel/row) use kOOB and read zeros.
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, a.w_bytes);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
+  uint32_t a_off[A_IT], b_off[B_IT];
+  if (ALIGNED) {
+#pragma unroll
+    for (int i = 0; i < A_IT; ++i)
+      a_off[i] = a_ok[i] ? (uint32_t)((a_ptr[i] - w) * (int)sizeof(T)) : kOOB;
+#pragma unroll
+    for (int i = 0; i < B_IT; ++i) b_off[i] = (uint32_t)((b_ptr[i] - x) * (int64_t)sizeof(T));
+  }
+
+  // (ky, kx, ci0) of the next step to load, advanced incrementally (ALIGNED:
+  // a step never crosses a tap, so ci0 wraps exactly at Cin).
+  int t_ky = 0, t_kx = 0, t_ci = 0;
   auto load_tiles = [&](int k0) {
+    if (ALIGNED) {
 #pragma unroll
-    for (int i = 0; i < A_IT; ++i) {
-      const int c = tid + i * NT;
-      const int co = m0 + c / GPR, k = k0 + (c % GPR) * 8;
-      ra[i] = (c < BM * GPR && co < a.Cout && k < a.K) ? E::load(w + (int64_t)co * a.K + k) : E::zero();
-    }
-    int tap = 0, ci0 = 0;
-    if (ALIGNED) { tap = k0 / a.Cin; ci0 = k0 - tap * a.Cin; }
-#pragma unroll
-    for (int i = 0; i < B_IT; ++i) {
-      const int grp = (tid + i * NT) % GPR;
-      int t = tap, ci = ci0 + grp * 8;
-      bool ok = b_ok[i];
-      if (!ALIGNED) {
-        const int k = k0 + grp * 8;
-        ok = ok && (k < a.K);
-        t = k / a.Cin;
-        ci = k - t * a.Cin;
+      for (int i = 0; i < A_IT; ++i) ra[i] = E::bload(rw, a_off[i], (uint32_t)k0 * sizeof(T));
+      const int ky = t_ky, kx = t_kx;
+      const uint32_t off = (uint32_t)((ky * a.W + kx) * a.x_pitch + t_ci) * sizeof(T);
+      t_ci += BK;
+      if (t_ci == a.Cin) {
+        t_ci = 0;
+        if (++t_kx == a.kw) { t_kx = 0; ++t_ky; }
       }
-      const int ky = t / a.kw, kx = t - ky * a.kw;
-      const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
-      ok = ok && (iy >= 0) && (iy < a.H) && (ix >= 0) && (ix < a.W);
-      rb[i] = ok ? E::load(x + (b_base[i] + (int64_t)iy * a.W + ix) * a.x_pitch + ci) : E::zero();
+#pragma unroll
+      for (int i = 0; i < B_IT; ++i) {
+        const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
+        const bool ok = b_ok[i] && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+        rb[i] = E::bload(rx, ok ? b_off[i] + off : kOOB, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_IT; ++i) {
+        const int k = k0 + ((tid + i * NT) % GPR) * 8;
+        ra[i] = (a_ok[i] && k < a.K) ? E::load(a_ptr[i] + k0) : E::zero();
+      }
+#pragma unroll
+      for (int i = 0; i < B_IT; ++i) {
+        const int grp = (tid + i * NT) % GPR;
+        const int k = k0 + grp * 8;
+        const int t = k / a.Cin, ci = k - t * a.Cin;
+        const int ky = t / a.kw, kx = t - ky * a.kw;
+        const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
+        const bool ok = b_ok[i] && (k < a.K) && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+        rb[i] = ok ? E::load(b_ptr[i] - grp * 8 + ((int64_t)ky * a.W + kx) * a.x_pitch + ci) : E::zero();
+      }
     }
   };
 
@@ -193,14 +236,18 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
           v[r] = t;
         }
         if (a.res && m < a.M && co < a.Cout) {
-          const int bb = m / HWo, pp = m - bb * HWo;
+          int pp;
+          const int bb = fdivmod(m, HWo, inv_hwo, pp);
           const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + co;
 #pragma unroll
           for (int r = 0; r < 4; ++r) v[r] += E::to_f(rp[r]);
         }
         T* sp = st + pl * (WTM + SPAD) + cl;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sp[r] = E::from_f(v[r]);
+        if (sizeof(T) == 2) {
+          *reinterpret_cast<u32x2_t*>(sp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        } else {
+          *reinterpret_cast<f32x4_t*>(sp) = (f32x4_t){v[0], v[1], v[2], v[3]};
+        }
       }
     }
     __syncthreads();
@@ -212,7 +259,8 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
       const int m = n0 + wn * WTN + pl;
       const int co = co_w + part * EPC;
       if (m >= a.M || co >= a.Cout) continue;
-      const int bb = m / HWo, pp = m - bb * HWo;
+      int pp;
+      const int bb = fdivmod(m, HWo, inv_hwo, pp);
       const u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + pl * (WTM + SPAD) + part * EPC);
       *reinterpret_cast<u32x4_t*>(reinterpret_cast<T*>(a.y) + bb * a.y_sb + pp * a.y_sp + co) = v;
     }
@@ -234,7 +282,8 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
     for (int j = 0; j < TN; ++j) {
       const int m = n0 + wn * WTN + j * 16 + (lane & 15);
       if (m >= a.M) continue;
-      const int bb = m / HWo, pp = m - bb * HWo;
+      int pp;
+      const int bb = fdivmod(m, HWo, inv_hwo, pp);
       float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -261,9 +310,7 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
       } else {
         T* yp = reinterpret_cast<T*>(a.y) + yo;
         if (sizeof(T) == 2 && a.y_sc == 1 && full4) {
-          const uint32_t lo = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-          const uint32_t hi = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-          *reinterpret_cast<u32x2_t*>(yp) = (u32x2_t){lo, hi};
+          *reinterpret_cast<u32x2_t*>(yp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r)

@@ -22,14 +22,13 @@ __device__ __forceinline__ void dw_body(const vrs_dw_args& a) {
   constexpr int NR = (DW_ROWS - 1) * S + 3;
   const int cg = a.C >> 3;                       // channel groups of 8
   const int row_tiles = (a.Ho + DW_ROWS - 1) / DW_ROWS;
-  const int64_t total = (int64_t)a.N * row_tiles * a.Wo * cg;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int g = (int)(i % cg);
-  int64_t t = i / cg;
-  const int ox = (int)(t % a.Wo); t /= a.Wo;
-  const int rt = (int)(t % row_tiles);
-  const int b = (int)(t / row_tiles);
+  const int per_img = row_tiles * a.Wo * cg;     // < 2^24, checked on the host
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= per_img) return;
+  const int b = blockIdx.y;                      // one grid row per image
+  int g, ox;
+  const int t = fdivmod(i, cg, 1.0f / (float)cg, g);
+  const int rt = fdivmod(t, a.Wo, 1.0f / (float)a.Wo, ox);
   const int c0 = g * 8;
   const int oy0 = rt * DW_ROWS;
 

@@ -161,9 +161,10 @@ def dtype_code(torch_dtype) -> int:
 class Context:
     """vrs_ctx: one device, all code objects loaded (CudaGraphCompiler::load analogue)."""
 
-    def __init__(self, device: int = 0):
+    def __init__(self, device: int = 0, hsaco_dir: str | None = None):
         self.handle = C.c_void_p()
-        check(lib().vrs_ctx_create(device, LIB_DIR.encode(), C.byref(self.handle)))
+        d = LIB_DIR if hsaco_dir is None else hsaco_dir
+        check(lib().vrs_ctx_create(device, d.encode(), C.byref(self.handle)))
         self.device = device
 
     def close(self):
