@@ -254,8 +254,9 @@ def test_detect_postprocess_empty():
 
 
 @pytest.mark.parametrize("cfg", [
-    (2, 30, 4, [(16, 16), (8, 8), (4, 4), (2, 2)], 4),
-    (1, 7, 8, [(13, 11), (7, 6)], 3),
+    (2, 30, 4, [(16, 16), (8, 8), (4, 4), (2, 2)], 4),   # unrolled 4-level x 4-point kernel
+    (1, 7, 8, [(13, 11), (7, 6)], 3),                    # generic kernel
+    (1, 5, 8, [(80, 80), (40, 40), (20, 20), (10, 10)], 4),  # BASELINE config 4 level shapes
 ])
 def test_msda(cfg):
     import torch

@@ -338,12 +338,12 @@ int prep_attn(vrs_ctx* ctx, int heads, int dtype, const vrs_nhwc& qkv, const voi
   a.out = const_cast<void*>(at(o, dtype));
   a.B = qkv.n; a.H = qkv.h; a.W = qkv.w; a.heads = heads; a.qkv_pitch = qkv.pitch; a.out_pitch = o.pitch;
   a.scale_log2e = (float)(1.0 / std::sqrt(32.0) * 1.4426950408889634);
-  a.q_blocks = (qkv.h * qkv.w + 63) / 64;
+  a.q_blocks = (qkv.h * qkv.w + 79) / 80;  // 5 waves x 16 queries per workgroup
   char name[48];
   snprintf(name, sizeof name, "vrs_psa_attn_%s", dsuffix(dtype));
   hipFunction_t f;
   if ((rc = get_fn(ctx, name, &f))) return rc;
-  out.push_back(make_launch(name, f, dim3(a.B * heads * a.q_blocks), dim3(256), 0, a));
+  out.push_back(make_launch(name, f, dim3(a.B * heads * a.q_blocks), dim3(320), 0, a));
   const double N = (double)qkv.h * qkv.w;
   out.back().flops = 2.0 * a.B * heads * N * N * (32 + 64) + 2.0 * a.B * N * o.c * 9;
   out.back().bytes = (double)a.B * N * (qkv.c + o.c) * elt_size(dtype) + (double)o.c * (9 * elt_size(dtype) + 8);

@@ -9,27 +9,29 @@
 // one pass, psa_merge_attn_nchw, psa_extract_v_nchw, the PE depthwise conv_bn
 // and the elem_add, fused.
 //
-// Workgroup = (b, h, block of 64 queries); each wave64 owns 16 queries.
+// Workgroup = (b, h, block of QW*16 queries); each wave64 owns 16 queries.
 // S^T = K Q^T on MFMA (keys are rows), so each lane holds 4 keys x 1 query and
 // softmax row statistics need only two cross-lane steps (xor 16, 32).  The
-// probabilities feed O^T += V^T P^T directly from registers: the k-slot order
+// probabilities feed O^T += V^T P^T straight from registers: the k-slot order
 // of P^T is the lane's natural key order and V^T is read from LDS in that same
-// order.  K/V are streamed through LDS 64 keys at a time.
+// order.  K and V^T are streamed through double-buffered LDS 64 keys at a
+// time (one barrier per chunk); V^T is written as packed key pairs so the
+// transposing store is free of bank conflicts.
 #include "common.h"
 
 namespace {
-constexpr int QB = 64;     // queries per workgroup
 constexpr int KC = 64;     // keys per LDS chunk
 constexpr int KD = 32, VD = 64;
 
-template <typename T>
+template <typename T, int QW>
 __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
   using E = Elt<T>;
   using G = typename E::group;
-  constexpr int LDK = KD + 16 / (int)sizeof(T) * 2;   // padded K row
-  constexpr int LDV = KC + 16 / (int)sizeof(T);       // padded V^T row
-  __shared__ __attribute__((aligned(16))) T sK[KC * LDK];
-  __shared__ __attribute__((aligned(16))) T sVt[VD * LDV];
+  constexpr int NT = QW * 64;
+  constexpr int LDK = KD + 16 / (int)sizeof(T) * 2;   // padded K row (elements)
+  constexpr int LDV = KC + 16 / (int)sizeof(T);       // padded V^T row (elements)
+  constexpr int BUF = KC * LDK + VD * LDV;
+  __shared__ __attribute__((aligned(16))) T smem[2 * BUF];
 
   const int N = a.H * a.W;
   const int qblk = blockIdx.x % a.q_blocks;
@@ -43,33 +45,52 @@ __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
   const int hc = h * (2 * KD + VD);
 
   // B operand Q^T: lane holds q[query lq][lg*8 .. +8]
-  const int qn = qblk * QB + wave * 16 + lq;
+  const int qn = qblk * (QW * 16) + wave * 16 + lq;
   G qf = qn < N ? E::load(qkv + (img + qn) * a.qkv_pitch + hc + lg * 8) : E::zero();
+
+  // Stage one chunk of K (row-major) and V^T (transposed) into buffer `buf`.
+  auto stage = [&](int kc, int buf) {
+    T* sK = smem + buf * BUF;
+    T* sVt = sK + KC * LDK;
+    for (int c = tid; c < KC * 4; c += NT) {  // K: 64 keys x 4 groups of 8
+      const int key = c >> 2, g = c & 3;
+      const int n = kc + key;
+      E::store(&sK[key * LDK + g * 8], n < N ? E::load(qkv + (img + n) * a.qkv_pitch + hc + KD + g * 8) : E::zero());
+    }
+    for (int c = tid; c < (KC / 2) * 8; c += NT) {  // V^T: 32 key pairs x 8 channel groups
+      const int kp = c & 31, dg = c >> 5;
+      const int n0 = kc + 2 * kp;
+      const T* vp = qkv + (img + n0) * a.qkv_pitch + hc + 2 * KD + dg * 8;
+      G v0 = n0 < N ? E::load(vp) : E::zero();
+      G v1 = n0 + 1 < N ? E::load(vp + a.qkv_pitch) : E::zero();
+      const T* e0 = reinterpret_cast<const T*>(&v0);
+      const T* e1 = reinterpret_cast<const T*>(&v1);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {  // one 4-byte (bf16) / 8-byte (f32) store per key pair
+        T* dst = &sVt[(dg * 8 + j) * LDV + 2 * kp];
+        if constexpr (sizeof(T) == 2) {
+          *reinterpret_cast<uint32_t*>(dst) =
+              (uint32_t)__builtin_bit_cast(uint16_t, e0[j]) | ((uint32_t)__builtin_bit_cast(uint16_t, e1[j]) << 16);
+        } else {
+          *reinterpret_cast<u32x2_t*>(dst) = (u32x2_t){__builtin_bit_cast(uint32_t, e0[j]), __builtin_bit_cast(uint32_t, e1[j])};
+        }
+      }
+    }
+  };
 
   f32x4_t o[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) o[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_part = 0.f;
 
-  for (int kc = 0; kc < N; kc += KC) {
-    __syncthreads();
-    {  // K chunk: 64 keys x 4 groups, one group per thread
-      const int key = tid >> 2, g = tid & 3;
-      const int n = kc + key;
-      G v = n < N ? E::load(qkv + (img + n) * a.qkv_pitch + hc + KD + g * 8) : E::zero();
-      E::store(&sK[key * LDK + g * 8], v);
-    }
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {  // V chunk transposed: 64 keys x 8 groups
-      const int c = tid + it * 256;
-      const int key = c >> 3, dg = c & 7;
-      const int n = kc + key;
-      G v = n < N ? E::load(qkv + (img + n) * a.qkv_pitch + hc + 2 * KD + dg * 8) : E::zero();
-      const T* ev = reinterpret_cast<const T*>(&v);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sVt[(dg * 8 + j) * LDV + key] = ev[j];
-    }
-    __syncthreads();
+  const int nchunks = (N + KC - 1) / KC;
+  stage(0, 0);
+  __syncthreads();
+  for (int ci = 0; ci < nchunks; ++ci) {
+    const int kc = ci * KC;
+    const T* sK = smem + (ci & 1) * BUF;
+    const T* sVt = sK + KC * LDK;
+    if (ci + 1 < nchunks) stage(kc + KC, (ci + 1) & 1);  // overlaps this chunk's math
 
     // S^T for 4 key tiles of 16
     f32x4_t s[4];
@@ -79,27 +100,27 @@ __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
       s[t] = mfma_k32(kf, qf, (f32x4_t){0.f, 0.f, 0.f, 0.f});
     }
     float cmax = -INFINITY;
+    const bool tail = kc + KC > N;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int key = kc + t * 16 + lg * 4 + r;
         float v = s[t][r] * a.scale_log2e;
-        v = key < N ? v : -INFINITY;
+        if (tail && kc + t * 16 + lg * 4 + r >= N) v = -INFINITY;
         s[t][r] = v;
         cmax = fmaxf(cmax, v);
       }
     cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
     cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
     const float m_new = fmaxf(m_run, cmax);
-    const float alpha = exp2f(m_run - m_new);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     m_run = m_new;
     float psum = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = exp2f(s[t][r] - m_new);
+        const float p = __builtin_amdgcn_exp2f(s[t][r] - m_new);
         s[t][r] = p;
         psum += p;
       }
@@ -111,22 +132,36 @@ __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       G pf;
-      T* pv = reinterpret_cast<T*>(&pf);
+      if constexpr (sizeof(T) == 2) {
+        u32x4_t pv = {pack_bf16x2(s[2 * kk][0], s[2 * kk][1]), pack_bf16x2(s[2 * kk][2], s[2 * kk][3]),
+                      pack_bf16x2(s[2 * kk + 1][0], s[2 * kk + 1][1]), pack_bf16x2(s[2 * kk + 1][2], s[2 * kk + 1][3])};
+        pf = *reinterpret_cast<G*>(&pv);
+      } else {
+        T* pv = reinterpret_cast<T*>(&pf);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pv[r] = E::from_f(s[2 * kk][r]);
-        pv[4 + r] = E::from_f(s[2 * kk + 1][r]);
+        for (int r = 0; r < 4; ++r) {
+          pv[r] = E::from_f(s[2 * kk][r]);
+          pv[4 + r] = E::from_f(s[2 * kk + 1][r]);
+        }
       }
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         const T* vrow = &sVt[(dt * 16 + lq) * LDV + kk * 32 + lg * 4];
         G vf;
-        T* vv = reinterpret_cast<T*>(&vf);
+        if constexpr (sizeof(T) == 2) {
+          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
+          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 16);
+          u32x4_t vv = {lo[0], lo[1], hi[0], hi[1]};
+          vf = *reinterpret_cast<G*>(&vv);
+        } else {
+          T* vv = reinterpret_cast<T*>(&vf);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) { vv[r] = vrow[r]; vv[4 + r] = vrow[16 + r]; }
+          for (int r = 0; r < 4; ++r) { vv[r] = vrow[r]; vv[4 + r] = vrow[16 + r]; }
+        }
         o[dt] = mfma_k32(vf, pf, o[dt]);
       }
     }
+    __syncthreads();  // next chunk staged; this chunk's buffer is free
   }
 
   float l_tot = l_part;
@@ -137,30 +172,51 @@ __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
 
   // Fused PE: depthwise 3x3 on V (pad 1) + folded BN, added to the attention.
   const int qy = qn / a.W, qx = qn - qy * a.W;
+  const int C = a.heads * VD;
   T* out = reinterpret_cast<T*>(a.out) + (img + qn) * a.out_pitch + h * VD;
+  const T* wpe = reinterpret_cast<const T*>(a.pe_w);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
     const int d0 = dt * 16 + lg * 4;
     const int c0 = h * VD + d0;
     float pe[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
     for (int ky = 0; ky < 3; ++ky) {
       const int yy = qy + ky - 1;
-      if (yy < 0 || yy >= a.H) continue;
+      if ((unsigned)yy >= (unsigned)a.H) continue;
+#pragma unroll
       for (int kx = 0; kx < 3; ++kx) {
         const int xx = qx + kx - 1;
-        if (xx < 0 || xx >= a.W) continue;
+        if ((unsigned)xx >= (unsigned)a.W) continue;
         const T* vp = qkv + (img + yy * a.W + xx) * a.qkv_pitch + hc + 2 * KD + d0;
-        const T* wk = reinterpret_cast<const T*>(a.pe_w) + (ky * 3 + kx) * (a.heads * VD) + c0;
+        const T* wk = wpe + (ky * 3 + kx) * C + c0;
+        if constexpr (sizeof(T) == 2) {
+          const u32x2_t vv = *reinterpret_cast<const u32x2_t*>(vp);
+          const u32x2_t ww = *reinterpret_cast<const u32x2_t*>(wk);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pe[r] += E::to_f(wk[r]) * E::to_f(vp[r]);
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t vw = vv[r >> 1] >> (16 * (r & 1)), wwv = ww[r >> 1] >> (16 * (r & 1));
+            pe[r] += bf2f((bf16_t)wwv) * bf2f((bf16_t)vw);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pe[r] += E::to_f(wk[r]) * E::to_f(vp[r]);
+        }
       }
     }
+    float res[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      out[d0 + r] = E::from_f(o[dt][r] * inv + pe[r] * a.pe_scale[c0 + r] + a.pe_shift[c0 + r]);
+    for (int r = 0; r < 4; ++r) res[r] = o[dt][r] * inv + pe[r] * a.pe_scale[c0 + r] + a.pe_shift[c0 + r];
+    if constexpr (sizeof(T) == 2) {
+      *reinterpret_cast<u32x2_t*>(out + d0) = (u32x2_t){pack_bf16x2(res[0], res[1]), pack_bf16x2(res[2], res[3])};
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out[d0 + r] = E::from_f(res[r]);
+    }
   }
 }
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) void vrs_psa_attn_bf16(vrs_attn_args a) { attn_body<bf16_t>(a); }
-extern "C" __global__ __launch_bounds__(256) void vrs_psa_attn_f32(vrs_attn_args a) { attn_body<float>(a); }
+// 5 waves x 16 queries: N = 400 (a 20x20 map) is exactly 5 workgroups per head.
+extern "C" __global__ __launch_bounds__(320) void vrs_psa_attn_bf16(vrs_attn_args a) { attn_body<bf16_t, 5>(a); }
+extern "C" __global__ __launch_bounds__(320) void vrs_psa_attn_f32(vrs_attn_args a) { attn_body<float, 5>(a); }

@@ -8,49 +8,100 @@
 // with zero padding outside the map (grid_sample bilinear, zeros,
 // align_corners=False).
 //
-// Gather-bound: the value tensor [B, S, heads, 32] keeps each (pixel, head)
-// row of 32 floats contiguous, so a corner fetch by the 32 lanes that own a
-// head is one 128-byte coalesced segment.  A wave64 serves two heads of the
-// same query; the per-sample location/weight loads are wave-uniform per half
-// and come from the scalar-broadcast path of the vector cache.
+// Gather-bound.  The value tensor [B, S, heads, 32] keeps each (pixel, head)
+// row of 32 floats (128 bytes) contiguous; 8 lanes own one head and fetch a
+// corner row as 8 x 16-byte loads, so one wave64 serves all 8 heads of one
+// query and every corner fetch is a full 128-byte segment per head.  The
+// level and point loops are unrolled at compile time (L <= 4, P <= 4 for the
+// fast kernel) so all corner fetches of a query are independent loads in
+// flight together; sampling locations and weights are read once per lane
+// group with 8-byte / 4-byte loads.
 #include "common.h"
 
-extern "C" __global__ __launch_bounds__(256) void vrs_msda_f32(vrs_msda_args a) {
+namespace {
+
+template <int L, int P>
+__device__ __forceinline__ void msda_body(const vrs_msda_args& a) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int d = (int)(gid & 31);
-  const int64_t bqh = gid >> 5;
+  const int part = (int)(gid & 7);          // which 4 of the 32 channels
+  const int64_t bqh = gid >> 3;
   if (bqh >= (int64_t)a.B * a.Q * a.heads) return;
   const int h = (int)(bqh % a.heads);
   const int64_t bq = bqh / a.heads;
   const int b = (int)(bq / a.Q);
   const float rx = a.ref[bq * 2 + 0], ry = a.ref[bq * 2 + 1];
-  const float* vb = a.value + (int64_t)b * a.S * a.heads * 32 + h * 32 + d;
-  const int64_t row = (int64_t)a.heads * 32;  // elements per pixel
+  const int64_t row = (int64_t)a.heads * 32;  // floats per value pixel
+  const float* vb = a.value + (int64_t)b * a.S * row + h * 32 + part * 4;
+  const int64_t obase = bqh * (L * P);
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int l = 0; l < L; ++l) {
+    const int Hl = a.lh[l], Wl = a.lw[l];
+    const float* vl = vb + (int64_t)a.lstart[l] * row;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t oi = obase + l * P + p;
+      const float2 off = *reinterpret_cast<const float2*>(a.off + 2 * oi);
+      const float w = a.attw[oi];
+      const float ix = (rx + off.x) * (float)Wl - 0.5f;
+      const float iy = (ry + off.y) * (float)Hl - 0.5f;
+      const float fx = floorf(ix), fy = floorf(iy);
+      const int x0 = (int)fx, y0 = (int)fy;
+      const float ax1 = ix - fx, ay1 = iy - fy;
+      const float ax0 = 1.f - ax1, ay0 = 1.f - ay1;
+      const bool xv0 = (unsigned)x0 < (unsigned)Wl, xv1 = (unsigned)(x0 + 1) < (unsigned)Wl;
+      const bool yv0 = (unsigned)y0 < (unsigned)Hl, yv1 = (unsigned)(y0 + 1) < (unsigned)Hl;
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      const f32x4_t v00 = (yv0 && xv0) ? *reinterpret_cast<const f32x4_t*>(vl + ((int64_t)y0 * Wl + x0) * row) : z;
+      const f32x4_t v01 = (yv0 && xv1) ? *reinterpret_cast<const f32x4_t*>(vl + ((int64_t)y0 * Wl + x0 + 1) * row) : z;
+      const f32x4_t v10 = (yv1 && xv0) ? *reinterpret_cast<const f32x4_t*>(vl + ((int64_t)(y0 + 1) * Wl + x0) * row) : z;
+      const f32x4_t v11 = (yv1 && xv1) ? *reinterpret_cast<const f32x4_t*>(vl + ((int64_t)(y0 + 1) * Wl + x0 + 1) * row) : z;
+      acc += w * (ay0 * (ax0 * v00 + ax1 * v01) + ay1 * (ax0 * v10 + ax1 * v11));
+    }
+  }
+  *reinterpret_cast<f32x4_t*>(a.out + bq * row + h * 32 + part * 4) = acc;
+}
+
+// Any L <= 8, P: runtime loops (the shapes the unrolled kernels do not cover).
+__device__ __forceinline__ void msda_any(const vrs_msda_args& a) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int part = (int)(gid & 7);
+  const int64_t bqh = gid >> 3;
+  if (bqh >= (int64_t)a.B * a.Q * a.heads) return;
+  const int h = (int)(bqh % a.heads);
+  const int64_t bq = bqh / a.heads;
+  const int b = (int)(bq / a.Q);
+  const float rx = a.ref[bq * 2 + 0], ry = a.ref[bq * 2 + 1];
+  const int64_t row = (int64_t)a.heads * 32;
+  const float* vb = a.value + (int64_t)b * a.S * row + h * 32 + part * 4;
   const int64_t obase = bqh * a.L * a.P;
-  float acc = 0.f;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   for (int l = 0; l < a.L; ++l) {
     const int Hl = a.lh[l], Wl = a.lw[l];
     const float* vl = vb + (int64_t)a.lstart[l] * row;
     for (int p = 0; p < a.P; ++p) {
       const int64_t oi = obase + l * a.P + p;
-      const float lx = rx + a.off[2 * oi + 0];
-      const float ly = ry + a.off[2 * oi + 1];
+      const float ix = (rx + a.off[2 * oi]) * (float)Wl - 0.5f;
+      const float iy = (ry + a.off[2 * oi + 1]) * (float)Hl - 0.5f;
       const float w = a.attw[oi];
-      const float ix = lx * (float)Wl - 0.5f;
-      const float iy = ly * (float)Hl - 0.5f;
       const float fx = floorf(ix), fy = floorf(iy);
       const int x0 = (int)fx, y0 = (int)fy;
       const float ax1 = ix - fx, ay1 = iy - fy;
       const float ax0 = 1.f - ax1, ay0 = 1.f - ay1;
-      const bool xv0 = x0 >= 0 && x0 < Wl, xv1 = x0 + 1 >= 0 && x0 + 1 < Wl;
-      const bool yv0 = y0 >= 0 && y0 < Hl, yv1 = y0 + 1 >= 0 && y0 + 1 < Hl;
-      float v00 = 0.f, v01 = 0.f, v10 = 0.f, v11 = 0.f;
-      if (yv0 && xv0) v00 = vl[((int64_t)y0 * Wl + x0) * row];
-      if (yv0 && xv1) v01 = vl[((int64_t)y0 * Wl + x0 + 1) * row];
-      if (yv1 && xv0) v10 = vl[((int64_t)(y0 + 1) * Wl + x0) * row];
-      if (yv1 && xv1) v11 = vl[((int64_t)(y0 + 1) * Wl + x0 + 1) * row];
-      acc += w * (ay0 * (ax0 * v00 + ax1 * v01) + ay1 * (ax0 * v10 + ax1 * v11));
+      const int xs[2] = {x0, x0 + 1}, ys[2] = {y0, y0 + 1};
+      const float wx[2] = {ax0, ax1}, wy[2] = {ay0, ay1};
+      for (int cy = 0; cy < 2; ++cy)
+        for (int cx = 0; cx < 2; ++cx) {
+          if ((unsigned)xs[cx] >= (unsigned)Wl || (unsigned)ys[cy] >= (unsigned)Hl) continue;
+          const f32x4_t v = *reinterpret_cast<const f32x4_t*>(vl + ((int64_t)ys[cy] * Wl + xs[cx]) * row);
+          acc += (w * wy[cy] * wx[cx]) * v;
+        }
     }
   }
-  a.out[bq * row + h * 32 + d] = acc;
+  *reinterpret_cast<f32x4_t*>(a.out + bq * row + h * 32 + part * 4) = acc;
 }
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void vrs_msda_l4p4_f32(vrs_msda_args a) { msda_body<4, 4>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_msda_f32(vrs_msda_args a) { msda_any(a); }
