@@ -85,6 +85,115 @@ def roofline_of(sym, d, dtype_peak):
             "algorithmic_mb_per_launch": round(d["bytes"] / d["launches"] / 1e6, 3)}
 
 
+TRAFFIC_MD = os.path.join(ROOT, "profiles", "yolo26m_bf16_bs64_traffic.md")
+
+
+def traffic_pass(a, ctx, labels_out):
+    """Workload for the two rocprofv3 --pmc passes: a 1 GiB copy (counter
+    calibration), model build + tile autotuning, then two eager forwards; the
+    last forward's dispatches are the ones the summary reads."""
+    import torch
+    import vrs
+    from vrs.synth import images, seeded_params
+    src = torch.empty(2 ** 28, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    dt = vrs.BF16 if a.dtype == "bf16" else vrs.F32
+    m = vrs.Model(ctx, vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant=a.variant, one2one=True),
+                  a.batch, a.size, a.size, dt, 1e-3)
+    m.load(seeded_params(m.params(), seed=0, bn="identity"))
+    x = torch.from_numpy(images(a.batch, a.size, a.size, seed=0)).cuda()
+    outs = m.alloc_outputs()
+    m.forward(x, outs)
+    m.forward(x, outs)
+    torch.cuda.synchronize()
+    with open(labels_out, "w") as f:
+        json.dump({"labels": m.launch_names(), "work": m.launch_work(), "copy_bytes": 2 ** 30}, f)
+    log(f"[traffic] {len(m.launch_names())} launches per forward -> {labels_out}")
+
+
+def _pmc_rows(csv_dir, counter):
+    import csv
+    import glob
+    rows = []
+    for fn in glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True):
+        with open(fn) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter:
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return rows
+
+
+def traffic_summary(fetch_dir, write_dir):
+    """Markdown table of HBM bytes per launch of the last forward, from the
+    FETCH_SIZE and WRITE_SIZE passes (each directory holds the pass's CSV and
+    the labels.json its --traffic-pass wrote), each counter scaled by what it
+    read for the calibration copy.  Launches whose autotuned kernel differs
+    between the two passes are left out."""
+    per, labs, factors = {}, {}, {}
+    for name, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        with open(os.path.join(d, "labels.json")) as f:
+            meta = json.load(f)
+        labels = meta["labels"]
+        rows = _pmc_rows(d, name)
+        cal = max(v for _, k, v in rows if "copy" in k.lower())
+        factors[name] = meta["copy_bytes"] / 1024.0 / cal
+        mine = [(k, v) for _, k, v in rows if k.startswith("vrs_")][-len(labels):]
+        if [k for k, _ in mine] != [lab.split(":")[-1] for lab in labels]:
+            raise SystemExit(f"{name}: the last {len(labels)} vrs_ dispatches do not match the forward's launches")
+        per[name] = [v for _, v in mine]
+        labs[name] = labels
+        work = meta["work"]
+    out = [f"Calibration (1 GiB device copy): FETCH_SIZE factor {factors['FETCH_SIZE']:.4f}, "
+           f"WRITE_SIZE factor {factors['WRITE_SIZE']:.4f}; HBM bytes = factor x KiB x 1024.", "",
+           "| launch | kernel | FETCH KiB | WRITE KiB | HBM MB | algorithmic MB | HBM / algorithmic |",
+           "|---|---|---|---|---|---|---|"]
+    sym_tot = {}
+    skipped = 0
+    for i, lab in enumerate(labs["FETCH_SIZE"]):
+        if i >= len(labs["WRITE_SIZE"]) or labs["WRITE_SIZE"][i] != lab:
+            skipped += 1
+            continue
+        fk, wk = per["FETCH_SIZE"][i], per["WRITE_SIZE"][i]
+        hbm = (fk * factors["FETCH_SIZE"] + wk * factors["WRITE_SIZE"]) * 1024.0
+        alg = work[i][1]
+        sym = lab.split(":")[-1]
+        t = sym_tot.setdefault(sym, [0, 0.0, 0.0])
+        t[0] += 1
+        t[1] += hbm
+        t[2] += alg
+        out.append(f"| {lab.rsplit(':', 1)[0]} | {sym} | {fk:.1f} | {wk:.1f} | {hbm / 1e6:.3f} | {alg / 1e6:.3f} | "
+                   f"{hbm / max(alg, 1.0):.2f} |")
+    out += ["", f"{skipped} launch(es) left out (different autotuned kernel in the two passes).", "",
+            "| kernel | launches | HBM MB per launch | algorithmic MB per launch | HBM / algorithmic |",
+            "|---|---|---|---|---|"]
+    for sym, (n, hbm, alg) in sorted(sym_tot.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"| {sym} | {n} | {hbm / n / 1e6:.3f} | {alg / n / 1e6:.3f} | {hbm / max(alg, 1.0):.2f} |")
+    return "\n".join(out)
+
+
+def traffic_lookup(sym, names):
+    """HBM bytes per launch of `sym` in this forward, from the committed
+    per-launch table (launches whose layer ran the same kernel there)."""
+    try:
+        with open(TRAFFIC_MD) as f:
+            table = {}
+            for line in f:
+                c = [x.strip() for x in line.strip().strip("|").split("|")]
+                if len(c) == 7 and c[1].startswith("vrs_"):
+                    table[(c[0], c[1])] = float(c[4]) * 1e6
+    except OSError:
+        return None, 0
+    mine = [lab.rsplit(":", 1)[0] for lab in names if lab.split(":")[-1] == sym]
+    got = [table[(l, sym)] for l in mine if (l, sym) in table]
+    if not got:
+        return None, 0
+    return sum(got) / len(got), len(got) / len(mine)
+
+
 def cpu_baseline(variant, size, P, budget_s=15.0):
     """CPU oracle (float32, OpenMP) on a bounded sample of the same workload."""
     import numpy as np
@@ -93,11 +202,13 @@ def cpu_baseline(variant, size, P, budget_s=15.0):
     from vrs.synth import images
     net = Y.yolo26(80, variant)
     PP = Y.Params(P, eps=1e-3)
-    x1 = images(1, size, size, seed=1)
+    # batches parallelise better than single images: size the sample from a
+    # 4-image probe so the timed batch is ~budget_s of CPU work (at most 64)
+    x4 = images(4, size, size, seed=1)
     t0 = time.perf_counter()
-    net(PP, x1)
-    t1 = time.perf_counter() - t0
-    n = int(max(1, min(64, budget_s // max(t1, 1e-3))))
+    net(PP, x4)
+    t4 = (time.perf_counter() - t0) / 4
+    n = int(max(1, min(64, budget_s // max(t4, 1e-3))))
     xs = images(n, size, size, seed=2)
     t0 = time.perf_counter()
     net(PP, xs)
@@ -252,7 +363,14 @@ def main() -> int:
     ap.add_argument("--layers", action="store_true", help="also print the per-layer table to stderr")
     ap.add_argument("--micro", action="store_true",
                     help="instead: BASELINE configs 2-4 as isolated kernels, one JSON line each")
+    ap.add_argument("--traffic-pass", metavar="LABELS_JSON",
+                    help="instead: the workload profiled by the rocprofv3 --pmc traffic passes")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="instead (no GPU): print the per-launch HBM traffic table from the two passes")
     a = ap.parse_args()
+    if a.traffic_summary:
+        print(traffic_summary(*a.traffic_summary))
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: every box in this build has one MI355X and the path shards by "
@@ -268,6 +386,9 @@ def main() -> int:
     ctx = vrs.Context(0)
     if a.micro:
         micro(ctx, lambda d: print(json.dumps(d), flush=True))
+        return 0
+    if a.traffic_pass:
+        traffic_pass(a, ctx, a.traffic_pass)
         return 0
     log(f"[bench] YOLO26{a.variant} {a.dtype} bs{a.batch} {a.size}x{a.size}: building")
     dt = vrs.BF16 if a.dtype == "bf16" else vrs.F32
@@ -299,6 +420,12 @@ def main() -> int:
     peak = PEAK_BF16_TFLOPS if dt == vrs.BF16 else PEAK_F32_TFLOPS
     dom = max(per_sym.items(), key=lambda kv: kv[1]["ms"])
     roof = roofline_of(dom[0], dom[1], peak)
+    if a.variant == "m" and a.batch == 64 and a.size == 640 and a.dtype == "bf16":
+        tr, cover = traffic_lookup(dom[0], m.launch_names())
+        if tr is not None:
+            roof["traffic"] = round(tr)
+            roof["traffic_source"] = (f"{os.path.relpath(TRAFFIC_MD, ROOT)}: rocprofv3 FETCH_SIZE/WRITE_SIZE, "
+                                      f"{cover:.0%} of this run's launches of the kernel")
     kern = {s: {"launches": d["launches"], "ms": round(d["ms"], 4),
                 "tflops": round(d["flops"] / max(d["ms"], 1e-9) / 1e9, 2),
                 "gbs": round(d["bytes"] / max(d["ms"], 1e-9) / 1e6, 1)} for s, d in
