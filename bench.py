@@ -272,7 +272,7 @@ def micro(ctx, emit):
         ys = [torch.empty(B, ho, ho, cout, dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
         flops = 2.0 * B * ho * ho * cout * cin * k * k
         best = None
-        for tile in [vrs.TILE_128x128, vrs.TILE_128x128 | vrs.TILE_K32, vrs.TILE_256x128, vrs.TILE_128x256,
+        for tile in [vrs.TILE_128x128, vrs.TILE_128x128 | vrs.TILE_K32, vrs.TILE_256x128, vrs.TILE_256x256, vrs.TILE_128x256,
                      vrs.TILE_64x256]:
             try:
                 f = lambda i, t=tile: ctx.conv2d(vrs.nhwc(xs[i]), wp, sc, sh, vrs.nhwc(ys[i]), k, s, 1, vrs.ACT_SILU,

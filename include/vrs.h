@@ -83,6 +83,7 @@ typedef struct {
 #define VRS_TILE_128x256 3
 #define VRS_TILE_64x256 4
 #define VRS_TILE_32x256 5
+#define VRS_TILE_256x256 6   /* 512 threads; bf16, Cin % 64 == 0 */
 #define VRS_TILE_K32 0x100
 
 typedef struct {

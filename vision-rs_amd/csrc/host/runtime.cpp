@@ -76,11 +76,12 @@ static inline int out_size(int in, int k, int s) { return (in + 2 * (k / 2) - k)
 
 // Dense-conv tiles.  bf16 has every tile with 32- and (when Cin % 64 == 0)
 // 64-deep K steps; the float32 parity path has 128x128, 64x256 and 32x256.
-struct TileInfo { int code, bm, bn; const char* tag; bool f32; };
+struct TileInfo { int code, bm, bn; const char* tag; bool f32; bool k32; int threads; };
 static const TileInfo kTiles[] = {
-    {VRS_TILE_128x128, 128, 128, "128x128", true}, {VRS_TILE_256x128, 256, 128, "256x128", false},
-    {VRS_TILE_128x256, 128, 256, "128x256", false}, {VRS_TILE_64x256, 64, 256, "64x256", true},
-    {VRS_TILE_32x256, 32, 256, "32x256", true},
+    {VRS_TILE_128x128, 128, 128, "128x128", true, true, 256}, {VRS_TILE_256x128, 256, 128, "256x128", false, true, 256},
+    {VRS_TILE_128x256, 128, 256, "128x256", false, true, 256}, {VRS_TILE_64x256, 64, 256, "64x256", true, true, 256},
+    {VRS_TILE_32x256, 32, 256, "32x256", true, true, 256},
+    {VRS_TILE_256x256, 256, 256, "256x256", false, false, 512},  // 64-deep K steps only
 };
 
 static const TileInfo* tile_info(int code) {
@@ -90,17 +91,20 @@ static const TileInfo* tile_info(int code) {
 }
 
 // Kernel name for a tile, or an error when the combination is not built.
-static int tile_kernel(int code, int cin, int dtype, char* name, size_t n, int* bm, int* bn) {
+static int tile_kernel(int code, int cin, int dtype, char* name, size_t n, int* bm, int* bn, int* threads) {
   const TileInfo* t = tile_info(code);
   if (!t) return fail(VRS_EINVAL, "conv: unknown tile code %d", code);
   if (dtype == VRS_F32 && !t->f32) return fail(VRS_EUNSUPPORTED, "conv: tile %s has no float32 build", t->tag);
   const bool g = cin % 32 != 0;
   bool k64 = !(code & VRS_TILE_K32) && dtype == VRS_BF16 && cin % 64 == 0 && t->code != VRS_TILE_32x256;
+  if (!t->k32 && (!k64 || g))
+    return fail(VRS_EUNSUPPORTED, "conv: tile %s needs Cin %% 64 == 0 and 64-deep steps (Cin=%d)", t->tag, cin);
   if (g && t->code != VRS_TILE_128x128 && t->code != VRS_TILE_64x256 && t->code != VRS_TILE_32x256)
     return fail(VRS_EUNSUPPORTED, "conv: tile %s needs Cin %% 32 == 0 (Cin=%d)", t->tag, cin);
   snprintf(name, n, "vrs_conv_%s_%s_k%d_%c", dsuffix(dtype), t->tag, k64 ? 64 : 32, g ? 'g' : 'a');
   *bm = t->bm;
   *bn = t->bn;
+  *threads = t->threads;
   return VRS_OK;
 }
 
@@ -126,6 +130,10 @@ std::vector<int> conv_tile_candidates(int cout, int cin, int dtype) {
     if (g && t.code != VRS_TILE_128x128 && t.code != VRS_TILE_64x256 && t.code != VRS_TILE_32x256) continue;
     if (t.bm >= 2 * 128 && cout <= 128) continue;   // mostly empty rows
     if (t.bm <= 64 && cout > 4 * t.bm) continue;     // too many passes over the input
+    if (!t.k32) {  // 64-deep only
+      if (dtype == VRS_BF16 && cin % 64 == 0 && cout >= t.bm) c.push_back(t.code);
+      continue;
+    }
     c.push_back(t.code);
     if (dtype == VRS_BF16 && cin % 64 == 0 && t.code != VRS_TILE_32x256) c.push_back(t.code | VRS_TILE_K32);
   }
@@ -165,16 +173,16 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   a.M = (int32_t)M;
   a.act = cs.act;
   char name[64];
-  int bm, bn;
+  int bm, bn, threads;
   const int tile = cs.tile ? cs.tile : auto_tile(cout, x.c, M, cs.dtype, ctx->num_cu);
-  if ((rc = tile_kernel(tile, x.c, cs.dtype, name, sizeof name, &bm, &bn))) return rc;
+  if ((rc = tile_kernel(tile, x.c, cs.dtype, name, sizeof name, &bm, &bn, &threads))) return rc;
   a.tiles_m = (cout + bm - 1) / bm;
   a.tiles_n = (int32_t)((M + bn - 1) / bn);
   const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
   if (blocks >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: grid too large");
   hipFunction_t f;
   if ((rc = get_fn(ctx, name, &f))) return rc;
-  out.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(256), 0, a));
+  out.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(threads), 0, a));
   const double es = (double)elt_size(cs.dtype);
   const double cin = cs.cin_real > 0 ? cs.cin_real : x.c;
   const double kk = (double)cs.k * cs.k;

@@ -10,6 +10,7 @@ typedef uint16_t bf16_t;  // storage type for bfloat16 activations/weights
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
 typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
 
@@ -122,5 +123,30 @@ __device__ __forceinline__ f32x4_t mfma_k32(const Elt<float>::group& a, const El
   for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av0[j], bv0[j], acc, 0, 0, 0);
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av1[j], bv1[j], acc, 0, 0, 0);
+  return acc;
+}
+
+// 32x32x16 step (the full-rate bf16 MFMA on gfx950: 16x16x32 issues at half
+// the flop rate).  Lane l supplies A[row l%32][k (l/32)*8 + j] and
+// B[k (l/32)*8 + j][col l%32], j = 0..7, as one group each; accumulator
+// register r of lane l holds D[row (r/4)*8 + (l/32)*4 + r%4][col l%32].
+__device__ __forceinline__ f32x16_t mfma32_k16(const Elt<bf16_t>::group& a, const Elt<bf16_t>::group& b,
+                                               f32x16_t acc) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a.v),
+                                                 __builtin_bit_cast(bf16x8_t, b.v), acc, 0, 0, 0);
+}
+
+// f32: eight 32x32x2 steps; step j takes element j of every lane's group, so
+// the two lane groups cover k = g*8 + j and all 16 k are summed.
+__device__ __forceinline__ f32x16_t mfma32_k16(const Elt<float>::group& a, const Elt<float>::group& b,
+                                               f32x16_t acc) {
+  const float* av0 = reinterpret_cast<const float*>(&a.lo);
+  const float* av1 = reinterpret_cast<const float*>(&a.hi);
+  const float* bv0 = reinterpret_cast<const float*>(&b.lo);
+  const float* bv1 = reinterpret_cast<const float*>(&b.hi);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[j], bv0[j], acc, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[j], bv1[j], acc, 0, 0, 0);
   return acc;
 }

@@ -17,7 +17,6 @@
 
 namespace {
 
-constexpr int NT = 256;
 
 // blockIdx.x -> logical tile id so that each XCD (blocks are dealt round-robin
 // over the 8 XCDs) receives a contiguous range of tiles: neighbouring Cout
@@ -28,6 +27,32 @@ __device__ __forceinline__ int xcd_remap(int bid, int G) {
   return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
 }
 
+// Instruction interleave of one pipelined K step (NM MFMAs, NRK fragment
+// reads per 16-deep k slice of NMK MFMAs, NX global loads and as many LDS
+// writes): the fragment reads of slice kk+1 ride on the MFMAs of slice kk,
+// the global loads of step k+2 go out during the first half of the MFMAs and
+// the LDS writes of step k+1 (whose loads then had a whole step to land)
+// during the second half.
+template <int I, int NM, int NRK, int NMK, int NX>
+__device__ __forceinline__ void pipe_schedule_at() {
+  if constexpr (I < NM) {
+    constexpr int KS = NM / NMK, kk = I / NMK, j = I % NMK, H = NM / 2;
+    constexpr int nr = kk + 1 < KS ? (j + 1) * NRK / NMK - j * NRK / NMK : 0;
+    constexpr int nv = I < H ? (I + 1) * NX / H - I * NX / H : 0;
+    constexpr int nw = I >= H ? (I - H + 1) * NX / (NM - H) - (I - H) * NX / (NM - H) : 0;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);  // DS read
+    if constexpr (nv > 0) __builtin_amdgcn_sched_group_barrier(0x020, nv, 0);  // VMEM read
+    if constexpr (nw > 0) __builtin_amdgcn_sched_group_barrier(0x200, nw, 0);  // DS write
+    pipe_schedule_at<I + 1, NM, NRK, NMK, NX>();
+  }
+}
+template <int NM, int NRK, int NMK, int NX>
+__device__ __forceinline__ void pipe_schedule() {
+  __builtin_amdgcn_sched_group_barrier(0x100, NRK, 0);  // slice 0 fragments
+  pipe_schedule_at<0, NM, NRK, NMK, NX>();
+}
+
 // BM output channels x BN pixels per workgroup, BK reduction elements per
 // pipeline step, WGM x WGN waves (wave tile (BM/WGM) x (BN/WGN)).
 // ALIGNED: Cin % BK == 0, so a K step never straddles two filter taps.
@@ -35,26 +60,41 @@ template <typename T, int BM, int BN, int BK, int WGM, int WGN, bool ALIGNED>
 __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   using E = Elt<T>;
   using G = typename E::group;
-  constexpr int PAD = 32 / (int)sizeof(T);   // 32 bytes of row padding
+  // LDS rows of BK + 8 elements: the 32 rows a half-wave reads with
+  // ds_read_b128 (row stride 144 B for BK=64 bf16) start on distinct 4-bank
+  // groups of the 64 banks (measured: 4% conflict cycles vs 34% at +16).
+  constexpr int PAD = 8;
   constexpr int LDK = BK + PAD;              // LDS row stride in elements
   constexpr int GPR = BK / 8;                // 8-element groups per tile row
+  constexpr int NT = 64 * WGM * WGN;         // threads per workgroup
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
-  constexpr int TM = WTM / 16, TN = WTN / 16;
+  constexpr int TM = WTM / 32, TN = WTN / 32;   // 32x32 MFMA tiles per wave
   constexpr int A_IT = (BM * GPR + NT - 1) / NT;
   constexpr int B_IT = (BN * GPR + NT - 1) / NT;
+  constexpr bool A_FULL = (BM * GPR) % NT == 0;   // every thread owns A_IT chunks
+  constexpr bool B_FULL = (BN * GPR) % NT == 0;
+  // Branch-free software pipeline (two register sets, interleaved schedule)
+  // when every thread loads whole chunks; otherwise the plain loop.
+  constexpr bool PIPE = ALIGNED && A_FULL && B_FULL;
   constexpr int TILE_ELEMS = (BM + BN) * LDK;            // one pipeline stage
   // epilogue staging: per wave WTN pixels x (WTM + SPAD) channels
   constexpr int SPAD = 16 / (int)sizeof(T);
-  constexpr int STAGE_ELEMS = 4 * WTN * (WTM + SPAD);
-  constexpr int SMEM_ELEMS = 2 * TILE_ELEMS > STAGE_ELEMS ? 2 * TILE_ELEMS : STAGE_ELEMS;
-  static_assert(WGM * WGN == 4, "4 waves");
+  constexpr int STAGE2 = (WGM * WGN / 2) * WTN * (WTM + SPAD);   // half the waves' staging
+  constexpr int BUF_ELEMS = TILE_ELEMS > STAGE2 ? TILE_ELEMS : STAGE2;
   static_assert(TM >= 1 && TN >= 1 && BK % 32 == 0, "tile");
 
-  __shared__ __attribute__((aligned(16))) T smem[SMEM_ELEMS];
+  // The two pipeline buffers are separate objects so the compiler can move
+  // LDS writes of one past reads of the other.  Epilogue staging: the first
+  // half of the waves
+  // use buffer 0, the other half buffer 1.
+  __shared__ __attribute__((aligned(16))) T smem0[BUF_ELEMS];
+  __shared__ __attribute__((aligned(16))) T smem1[BUF_ELEMS];
+  auto sbuf = [&](int b) -> T* { return b ? smem1 : smem0; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
+  static_assert(WGM * WGN == 4 || WGM * WGN == 8, "4 or 8 waves");
 
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
   const int tile_m = logical % a.tiles_m, tile_n = logical / a.tiles_m;
@@ -78,7 +118,7 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   for (int i = 0; i < A_IT; ++i) {
     const int c = tid + i * NT;
     const int co = m0 + c / GPR;
-    a_ok[i] = (c < BM * GPR) && (co < a.Cout);
+    a_ok[i] = (A_FULL || c < BM * GPR) && (co < a.Cout);
     a_ptr[i] = w + (int64_t)(a_ok[i] ? co : 0) * a.K + (c % GPR) * 8;
   }
   int b_iy0[B_IT], b_ix0[B_IT];
@@ -88,7 +128,7 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   for (int i = 0; i < B_IT; ++i) {
     const int c = tid + i * NT;
     const int m = n0 + c / GPR;
-    b_ok[i] = (c < BN * GPR) && (m < a.M);
+    b_ok[i] = (B_FULL || c < BN * GPR) && (m < a.M);
     const int mm = b_ok[i] ? m : 0;
     int rr, ox;
     const int bb = fdivmod(mm, HWo, inv_hwo, rr);
@@ -155,101 +195,179 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   };
 
   auto store_tiles = [&](int buf) {
-    T* sA = smem + buf * TILE_ELEMS;
+    T* sA = sbuf(buf);
     T* sB = sA + BM * LDK;
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       const int c = tid + i * NT;
-      if (c < BM * GPR) E::store(&sA[(c / GPR) * LDK + (c % GPR) * 8], ra[i]);
+      if (A_FULL || c < BM * GPR) E::store(&sA[(c / GPR) * LDK + (c % GPR) * 8], ra[i]);
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
       const int c = tid + i * NT;
-      if (c < BN * GPR) E::store(&sB[(c / GPR) * LDK + (c % GPR) * 8], rb[i]);
+      if (B_FULL || c < BN * GPR) E::store(&sB[(c / GPR) * LDK + (c % GPR) * 8], rb[i]);
     }
   };
 
-  f32x4_t acc[TM][TN];
+  f32x16_t acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int nk = (a.K + BK - 1) / BK;
+  const int frag_row = lane & 31;
+  const int frag_k = (lane >> 5) * 8;
+
+  if constexpr (PIPE) {
+    // Step k: LDS buffer k&1 holds step k; register set (k+1)&1 holds step
+    // k+1 (loaded during step k-1) and is written to buffer (k+1)&1 while
+    // the MFMAs of step k run; set k&1 receives the loads of step k+2.  Loads
+    // at k0 >= K read zeros (out-of-range buffer offsets), so the body has no
+    // branches and an odd step count runs one all-zero step.
+    G ra0[A_IT], rb0[B_IT], ra1[A_IT], rb1[B_IT];
+    auto load_set = [&](int k0, G (&ra)[A_IT], G (&rb)[B_IT]) {
+      const uint32_t dead = k0 < a.K ? 0u : kOOB;
+#pragma unroll
+      for (int i = 0; i < A_IT; ++i) ra[i] = E::bload(rw, a_off[i] | dead, (uint32_t)k0 * sizeof(T));
+      const int ky = t_ky, kx = t_kx;
+      const uint32_t off = (uint32_t)((ky * a.W + kx) * a.x_pitch + t_ci) * sizeof(T);
+      t_ci += BK;
+      if (t_ci == a.Cin) {
+        t_ci = 0;
+        if (++t_kx == a.kw) { t_kx = 0; ++t_ky; }
+      }
+#pragma unroll
+      for (int i = 0; i < B_IT; ++i) {
+        const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
+        const bool ok = b_ok[i] && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+        rb[i] = E::bload(rx, (ok ? b_off[i] + off : kOOB) | dead, 0);
+      }
+    };
+    auto store_set = [&](int buf, const G (&ra)[A_IT], const G (&rb)[B_IT]) {
+      T* sA = sbuf(buf);
+      T* sB = sA + BM * LDK;
+#pragma unroll
+      for (int i = 0; i < A_IT; ++i) {
+        const int c = tid + i * NT;
+        E::store(&sA[(c / GPR) * LDK + (c % GPR) * 8], ra[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < B_IT; ++i) {
+        const int c = tid + i * NT;
+        E::store(&sB[(c / GPR) * LDK + (c % GPR) * 8], rb[i]);
+      }
+    };
+    auto step = [&](int cur, const G (&wa)[A_IT], const G (&wb)[B_IT], G (&la)[A_IT], G (&lb)[B_IT], int k_load) {
+      load_set(k_load, la, lb);
+      store_set(cur ^ 1, wa, wb);
+      const T* sA = sbuf(cur);
+      const T* sB = sA + BM * LDK;
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        G fa[TM], fb[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          fa[i] = E::load(&sA[(wm * WTM + i * 32 + frag_row) * LDK + kk * 16 + frag_k]);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          fb[j] = E::load(&sB[(wn * WTN + j * 32 + frag_row) * LDK + kk * 16 + frag_k]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32_k16(fa[i], fb[j], acc[i][j]);
+      }
+      pipe_schedule<BK / 16 * TM * TN, TM + TN, TM * TN, A_IT + B_IT>();
+      __syncthreads();
+    };
+    load_set(0, ra0, rb0);
+    load_set(BK, ra1, rb1);
+    store_set(0, ra0, rb0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+      step(0, ra1, rb1, ra0, rb0, (kt + 2) * BK);
+      step(1, ra0, rb0, ra1, rb1, (kt + 3) * BK);
+    }
+  } else {
   load_tiles(0);
   store_tiles(0);
   __syncthreads();
 
-  const int frag_row = lane & 15;
-  const int frag_k = (lane >> 4) * 8;
-
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < nk) load_tiles((kt + 1) * BK);
-    const T* sA = smem + cur * TILE_ELEMS;
+    const T* sA = sbuf(cur);
     const T* sB = sA + BM * LDK;
 #pragma unroll
-    for (int kk = 0; kk < BK / 32; ++kk) {
+    for (int kk = 0; kk < BK / 16; ++kk) {
       G fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
-        fa[i] = E::load(&sA[(wm * WTM + i * 16 + frag_row) * LDK + kk * 32 + frag_k]);
+        fa[i] = E::load(&sA[(wm * WTM + i * 32 + frag_row) * LDK + kk * 16 + frag_k]);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        fb[j] = E::load(&sB[(wn * WTN + j * 16 + frag_row) * LDK + kk * 32 + frag_k]);
+        fb[j] = E::load(&sB[(wn * WTN + j * 32 + frag_row) * LDK + kk * 16 + frag_k]);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_k32(fa[i], fb[j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32_k16(fa[i], fb[j], acc[i][j]);
     }
     if (kt + 1 < nk) store_tiles(cur ^ 1);
     __syncthreads();
   }
+  }
 
-  // Epilogue: folded BN, activation, residual.
-  const int q = lane >> 4;
+  // Epilogue: folded BN, activation, residual.  Accumulator register
+  // g*4 + r of MFMA tile (i, j) is channel i*32 + g*8 + hq*4 + r of pixel
+  // j*32 + (lane & 31), hq = lane >> 5.
+  const int hq = lane >> 5;
   if (a.stage) {
     // Staged store: every wave writes its (WTN pixel x WTM channel) tile to
     // LDS, then stores whole 16-byte channel chunks per lane, so consecutive
     // lanes write contiguous bytes of a pixel's NHWC row.
-    T* st = smem + wave * WTN * (WTM + SPAD);
+    constexpr int HW_ = WGM * WGN / 2;
+    T* st = sbuf(wave / HW_) + (wave % HW_) * WTN * (WTM + SPAD);
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int cl = i * 16 + q * 4;          // channel within the wave tile
-      const int co = m0 + wm * WTM + cl;
-      float sc[4], sh[4];
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int c = co + r < a.Cout ? co + r : a.Cout - 1;
-        sc[r] = a.scale[c];
-        sh[r] = a.shift[c];
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int pl = j * 16 + (lane & 15);
-        const int m = n0 + wn * WTN + pl;
-        float v[4];
+      for (int g = 0; g < 4; ++g) {
+        const int cl = i * 32 + g * 8 + hq * 4;   // channel within the wave tile
+        const int co = m0 + wm * WTM + cl;
+        float sc[4], sh[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float t = acc[i][j][r] * sc[r] + sh[r];
-          if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
-          v[r] = t;
+          const int c = co + r < a.Cout ? co + r : a.Cout - 1;
+          sc[r] = a.scale[c];
+          sh[r] = a.shift[c];
         }
-        if (a.res && m < a.M && co < a.Cout) {
-          int pp;
-          const int bb = fdivmod(m, HWo, inv_hwo, pp);
-          const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + co;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) v[r] += E::to_f(rp[r]);
-        }
-        T* sp = st + pl * (WTM + SPAD) + cl;
-        if (sizeof(T) == 2) {
-          *reinterpret_cast<u32x2_t*>(sp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        } else {
-          *reinterpret_cast<f32x4_t*>(sp) = (f32x4_t){v[0], v[1], v[2], v[3]};
+        for (int j = 0; j < TN; ++j) {
+          const int pl = j * 32 + (lane & 31);
+          const int m = n0 + wn * WTN + pl;
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = acc[i][j][g * 4 + r] * sc[r] + sh[r];
+            if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
+            v[r] = t;
+          }
+          if (a.res && m < a.M && co < a.Cout) {
+            int pp;
+            const int bb = fdivmod(m, HWo, inv_hwo, pp);
+            const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + co;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] += E::to_f(rp[r]);
+          }
+          T* sp = st + pl * (WTM + SPAD) + cl;
+          if constexpr (sizeof(T) == 2) {
+            *reinterpret_cast<u32x2_t*>(sp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          } else {
+            *reinterpret_cast<f32x4_t*>(sp) = (f32x4_t){v[0], v[1], v[2], v[3]};
+          }
         }
       }
-    }
     __syncthreads();
     constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
     constexpr int CPP = WTM / EPC;            // chunks per pixel row
@@ -267,69 +385,72 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
     return;
   }
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int co = m0 + wm * WTM + i * 16 + q * 4;
-    if (co >= a.Cout) continue;
-    float sc[4], sh[4];
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = co + r < a.Cout ? co + r : a.Cout - 1;
-      sc[r] = a.scale[c];
-      sh[r] = a.shift[c];
-    }
-    const bool full4 = (co + 3 < a.Cout);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int m = n0 + wn * WTN + j * 16 + (lane & 15);
-      if (m >= a.M) continue;
-      int pp;
-      const int bb = fdivmod(m, HWo, inv_hwo, pp);
-      float v[4];
+    for (int g = 0; g < 4; ++g) {
+      const int co = m0 + wm * WTM + i * 32 + g * 8 + hq * 4;
+      if (co >= a.Cout) continue;
+      float sc[4], sh[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float t = acc[i][j][r] * sc[r] + sh[r];
-        if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
-        v[r] = t;
+        const int c = co + r < a.Cout ? co + r : a.Cout - 1;
+        sc[r] = a.scale[c];
+        sh[r] = a.shift[c];
       }
-      if (a.res) {
-        const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + (int64_t)co * a.r_sc;
+      const bool full4 = (co + 3 < a.Cout);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (co + r < a.Cout) v[r] += E::to_f(rp[r * a.r_sc]);
-      }
-      const int64_t yo = bb * a.y_sb + pp * a.y_sp + (int64_t)co * a.y_sc;
-      if (a.y_f32) {
-        float* yp = reinterpret_cast<float*>(a.y) + yo;
-        if (a.y_sc == 1 && full4) {
-          *reinterpret_cast<f32x4_t*>(yp) = (f32x4_t){v[0], v[1], v[2], v[3]};
-        } else {
+      for (int j = 0; j < TN; ++j) {
+        const int m = n0 + wn * WTN + j * 32 + (lane & 31);
+        if (m >= a.M) continue;
+        int pp;
+        const int bb = fdivmod(m, HWo, inv_hwo, pp);
+        float v[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (co + r < a.Cout) yp[r * a.y_sc] = v[r];
+        for (int r = 0; r < 4; ++r) {
+          float t = acc[i][j][g * 4 + r] * sc[r] + sh[r];
+          if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
+          v[r] = t;
         }
-      } else {
-        T* yp = reinterpret_cast<T*>(a.y) + yo;
-        if (sizeof(T) == 2 && a.y_sc == 1 && full4) {
-          *reinterpret_cast<u32x2_t*>(yp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        } else {
+        if (a.res) {
+          const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + (int64_t)co * a.r_sc;
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            if (co + r < a.Cout) yp[r * a.y_sc] = E::from_f(v[r]);
+            if (co + r < a.Cout) v[r] += E::to_f(rp[r * a.r_sc]);
+        }
+        const int64_t yo = bb * a.y_sb + pp * a.y_sp + (int64_t)co * a.y_sc;
+        if (a.y_f32) {
+          float* yp = reinterpret_cast<float*>(a.y) + yo;
+          if (a.y_sc == 1 && full4) {
+            *reinterpret_cast<f32x4_t*>(yp) = (f32x4_t){v[0], v[1], v[2], v[3]};
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (co + r < a.Cout) yp[r * a.y_sc] = v[r];
+          }
+        } else {
+          T* yp = reinterpret_cast<T*>(a.y) + yo;
+          if (sizeof(T) == 2 && a.y_sc == 1 && full4) {
+            *reinterpret_cast<u32x2_t*>(yp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (co + r < a.Cout) yp[r * a.y_sc] = E::from_f(v[r]);
+          }
         }
       }
     }
-  }
 }
 
 }  // namespace
 
-#define VRS_CONV_KERNEL(NAME, T, BM, BN, BK, WGM, WGN, AL)                              \
-  extern "C" __global__ __launch_bounds__(256) void NAME(vrs_conv_args a) {            \
-    conv_body<T, BM, BN, BK, WGM, WGN, AL>(a);                                          \
+#define VRS_CONV_KERNEL(NAME, T, BM, BN, BK, WGM, WGN, AL)                                        \
+  extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void NAME(vrs_conv_args a) {           \
+    conv_body<T, BM, BN, BK, WGM, WGN, AL>(a);                                                    \
   }
 
 // Kernel names: vrs_conv_<type>_<BM>x<BN>_k<BK>_<a|g>.  Wave tiles: 128x128
-// and 64x256 -> 64x64, 256x128 -> 128x64, 128x256 -> 64x128, 32x256 -> 32x64.
+// and 64x256 -> 64x64, 256x128 -> 128x64, 128x256 -> 64x128, 32x256 -> 32x64
+// (in 32x32 MFMA tiles).
 VRS_CONV_KERNEL(vrs_conv_bf16_128x128_k32_a, bf16_t, 128, 128, 32, 2, 2, true)
 VRS_CONV_KERNEL(vrs_conv_bf16_128x128_k32_g, bf16_t, 128, 128, 32, 2, 2, false)
 VRS_CONV_KERNEL(vrs_conv_bf16_128x128_k64_a, bf16_t, 128, 128, 64, 2, 2, true)
@@ -342,6 +463,9 @@ VRS_CONV_KERNEL(vrs_conv_bf16_64x256_k32_g, bf16_t, 64, 256, 32, 1, 4, false)
 VRS_CONV_KERNEL(vrs_conv_bf16_64x256_k64_a, bf16_t, 64, 256, 64, 1, 4, true)
 VRS_CONV_KERNEL(vrs_conv_bf16_32x256_k32_a, bf16_t, 32, 256, 32, 1, 4, true)
 VRS_CONV_KERNEL(vrs_conv_bf16_32x256_k32_g, bf16_t, 32, 256, 32, 1, 4, false)
+// 8 waves (512 threads), wave tile 128x64: half the global loads per MFMA of
+// the 4-wave tiles, for the large layers with Cout >= 256 and Cin % 64 == 0.
+VRS_CONV_KERNEL(vrs_conv_bf16_256x256_k64_a, bf16_t, 256, 256, 64, 2, 4, true)
 // f32 (parity path, fp32 MFMA)
 VRS_CONV_KERNEL(vrs_conv_f32_128x128_k32_a, float, 128, 128, 32, 2, 2, true)
 VRS_CONV_KERNEL(vrs_conv_f32_128x128_k32_g, float, 128, 128, 32, 2, 2, false)
