@@ -289,21 +289,24 @@ def micro(ctx, emit):
               "mb": round((in_b + out_b + cout * cin * k * k * 2) / 1e6, 1), "buffer_sets": n_sets})
         del xs, ys
 
-    # (c) depthwise 3x3 512 @20x20, HBM-bound
-    C, hw = 512, 20
-    wdw = (rng.standard_normal((C, 1, 3, 3)) * np.sqrt(2.0 / 9)).astype(np.float32)
-    wp = torch.from_numpy(vrs.pack_conv_weight(wdw, C, 1, vrs.BF16)).to(dev)
-    sc = torch.full((C,), 1.0 / np.sqrt(1.001), device=dev)
-    sh = torch.zeros(C, device=dev)
-    nb = 2 * B * hw * hw * C * 2
-    n_sets = sets_for(nb)
-    xs = [torch.nn.functional.silu(torch.randn(B, hw, hw, C, device=dev)).to(torch.bfloat16) for _ in range(n_sets)]
-    ys = [torch.empty(B, hw, hw, C, dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
-    ms = _time_launches(lambda i: ctx.conv2d(vrs.nhwc(xs[i]), wp, sc, sh, vrs.nhwc(ys[i]), 3, 1, C, vrs.ACT_SILU,
-                                             None, vrs.BF16), n_sets, iters=60)
-    emit({"config": "c3c dw3x3 512 @20", "batch": B, "us": round(ms * 1e3, 2), "mb": round(nb / 1e6, 2),
-          "gbs": round(nb / ms / 1e6, 1), "frac_hbm": round(nb / ms / 1e6 / PEAK_HBM_GBS, 4), "buffer_sets": n_sets})
-    del xs, ys
+    # (c) depthwise 3x3 512 @20x20, HBM-bound; plus the YOLO26m head's largest
+    # depthwise shape (256 ch @80x80, batch 64) where launch latency matters less
+    for name, C, hw, bb in (("c3c dw3x3 512 @20", 512, 20, B), ("dw3x3 256 @80 (YOLO26m head, bs64)", 256, 80, 64)):
+        wdw = (rng.standard_normal((C, 1, 3, 3)) * np.sqrt(2.0 / 9)).astype(np.float32)
+        wp = torch.from_numpy(vrs.pack_conv_weight(wdw, C, 1, vrs.BF16)).to(dev)
+        sc = torch.full((C,), 1.0 / np.sqrt(1.001), device=dev)
+        sh = torch.zeros(C, device=dev)
+        nb = 2 * bb * hw * hw * C * 2
+        n_sets = sets_for(nb)
+        xs = [torch.nn.functional.silu(torch.randn(bb, hw, hw, C, device=dev)).to(torch.bfloat16)
+              for _ in range(n_sets)]
+        ys = [torch.empty(bb, hw, hw, C, dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
+        ms = _time_launches(lambda i: ctx.conv2d(vrs.nhwc(xs[i]), wp, sc, sh, vrs.nhwc(ys[i]), 3, 1, C,
+                                                 vrs.ACT_SILU, None, vrs.BF16), n_sets, iters=60)
+        emit({"config": name, "batch": bb, "us": round(ms * 1e3, 2), "mb": round(nb / 1e6, 2),
+              "gbs": round(nb / ms / 1e6, 1), "frac_hbm": round(nb / ms / 1e6 / PEAK_HBM_GBS, 4),
+              "buffer_sets": n_sets})
+        del xs, ys
 
     # ---- config 2: isolated PSA attention block, B=32, 256 ch @20x20, 4 heads --
     desc = vrs.block(vrs.BLOCK_PSA_ATTN, 256, 256, heads=4)

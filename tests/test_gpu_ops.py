@@ -119,26 +119,40 @@ def test_conv2d_tile_rejections():
                      tile=vrs.TILE_128x256)
 
 
+DW_SHAPES = [
+    # n, c, h, w, strides: band/patch/channel-block edges of the row-walking
+    # stride-1 kernel (bands of 10 rows below 64 rows, 16 above; 8-column
+    # patches; 64-channel blocks) and the generic stride-2 kernel
+    (2, 64, 11, 9, (1, 2)),
+    (1, 200, 70, 20, (1,)),
+    (2, 24, 3, 3, (1, 2)),
+    (1, 136, 21, 17, (1,)),
+]
+
+
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("act", [vrs.ACT_SILU, vrs.ACT_NONE])
-def test_dwconv(dtype, act):
+@pytest.mark.parametrize("shape", DW_SHAPES)
+def test_dwconv(dtype, act, shape):
     import torch
     rnd = rounder(dtype)
     rng = np.random.default_rng(7)
-    n, c, h, w = 2, 64, 11, 9
+    n, c, h, w, strides = shape
     x = rnd(rng.standard_normal((n, c, h, w)).astype(np.float32))
     wt = rnd((rng.standard_normal((c, 1, 3, 3)) * 0.4).astype(np.float32))
     scale = rng.uniform(0.5, 1.5, c).astype(np.float32)
     shift = rng.normal(0, 0.2, c).astype(np.float32)
     C = ctx()
-    xt = to_nhwc(x, dtype, 96, 8)
-    for s in (1, 2):
+    xt = to_nhwc(x, dtype, c + 32, 8)
+    for s in strides:
         ref = oracle.affine_act(oracle.conv2d(x, wt, s, 1, groups=c), scale, shift, act)
-        yt = torch.zeros((n, ref.shape[2], ref.shape[3], c), dtype=tdtype(dtype), device="cuda")
+        yt = torch.full((n, ref.shape[2], ref.shape[3], c + 16), 7.0, dtype=tdtype(dtype), device="cuda")
         C.conv2d(vrs.nhwc(xt, c, 8), dev(vrs.pack_conv_weight(wt, c, 1, dtype)), dev(scale), dev(shift),
-                 vrs.nhwc(yt), 3, s, c, act, None, dtype)
+                 vrs.nhwc(yt, c, 8), 3, s, c, act, None, dtype)
         torch.cuda.synchronize()
-        assert rel_err(from_nhwc(yt), ref, FLOOR[dtype]) < TOL[dtype], s
+        assert rel_err(from_nhwc(yt, c, 8), ref, FLOOR[dtype]) < TOL[dtype], s
+        rest = torch.cat([yt[..., :8], yt[..., 8 + c:]], -1).float()
+        assert torch.all(rest == 7.0)
 
 
 @pytest.mark.parametrize("dtype", DT)
@@ -254,7 +268,8 @@ def test_detect_postprocess_empty():
 
 
 @pytest.mark.parametrize("cfg", [
-    (2, 30, 4, [(16, 16), (8, 8), (4, 4), (2, 2)], 4),   # unrolled 4-level x 4-point kernel
+    (2, 30, 4, [(16, 16), (8, 8), (4, 4), (2, 2)], 4),   # level-split kernel (one wave per level)
+    (1, 6, 16, [(9, 9), (5, 5), (3, 3), (2, 2)], 4),     # unrolled 4x4 kernel (> 8 heads)
     (1, 7, 8, [(13, 11), (7, 6)], 3),                    # generic kernel
     (1, 5, 8, [(80, 80), (40, 40), (20, 20), (10, 10)], 4),  # BASELINE config 4 level shapes
 ])

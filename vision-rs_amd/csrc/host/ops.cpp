@@ -219,14 +219,19 @@ int vrs_msda(vrs_ctx* ctx, const vrs_msda_desc* d, const float* value, const flo
   if (reinterpret_cast<uintptr_t>(value) % 16 || reinterpret_cast<uintptr_t>(out) % 16 ||
       reinterpret_cast<uintptr_t>(off) % 8)
     return fail(VRS_EBADSHAPE, "vrs_msda: value/out must be 16-byte and off 8-byte aligned");
-  // 8 lanes per (query, head), each owning 4 of the 32 channels
-  const char* name = (d->levels == 4 && d->points == 4) ? "vrs_msda_l4p4_f32" : "vrs_msda_f32";
+  // 8 lanes per (query, head), each owning 4 of the 32 channels.  L = 4,
+  // P = 4 with <= 8 heads: one workgroup per query, one wave per level.
+  const bool split = d->levels == 4 && d->points == 4 && d->heads <= 8;
+  const char* name = split ? "vrs_msda_l4p4s_f32"
+                           : (d->levels == 4 && d->points == 4) ? "vrs_msda_l4p4_f32" : "vrs_msda_f32";
   hipFunction_t f;
   int rc = get_fn(ctx, name, &f);
   if (rc) return rc;
   const int64_t threads = (int64_t)d->n * d->q * d->heads * 8;
+  const int64_t blocks = split ? (int64_t)d->n * d->q : (threads + 255) / 256;
+  if (blocks >= (1ll << 31)) return fail(VRS_EBADSHAPE, "vrs_msda: grid too large");
   std::vector<Launch> ls;
-  ls.push_back(make_launch(name, f, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a));
+  ls.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(256), 0, a));
   return run_all(ls, stream);
 }
 

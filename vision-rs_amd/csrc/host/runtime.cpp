@@ -213,13 +213,28 @@ int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w
     a.N = x.n; a.H = x.h; a.W = x.w; a.C = x.c; a.x_pitch = x.pitch;
     a.Ho = y.h; a.Wo = y.w; a.y_pitch = y.pitch;
     a.kh = a.kw = cs.k; a.stride = cs.stride; a.pad = cs.k / 2; a.act = cs.act;
-    const int64_t per_img = (int64_t)((y.h + 3) / 4) * y.w * (x.c / 8);
-    if (per_img >= (1ll << 24)) return fail(VRS_EBADSHAPE, "dwconv: map too large for one grid row");
     char name[48];
-    snprintf(name, sizeof name, "vrs_dwconv3_s%d_%s", cs.stride, dsuffix(cs.dtype));
     hipFunction_t f;
-    if ((rc = get_fn(ctx, name, &f))) return rc;
-    out.push_back(make_launch(name, f, dim3((unsigned)((per_img + 255) / 256), (unsigned)x.n), dim3(256), 0, a));
+    const int64_t xb = ((int64_t)x.n * x.h * x.w * x.pitch - x.c_off) * (int64_t)elt_size(cs.dtype);
+    if (cs.stride == 1 && xb < (1ll << 31)) {
+      // row-walking kernel: bands of 16 output rows on large maps, 10 on small ones
+      const int rb = x.h >= 64 ? 16 : 10;
+      a.x_bytes = (int32_t)xb;
+      a.cblocks = (x.c + 63) / 64;
+      a.patches = (x.w + 7) / 8;
+      a.bands = (x.h + rb - 1) / rb;
+      const int64_t wgs = (int64_t)x.n * a.bands * a.cblocks * ((a.patches + 3) / 4);
+      if (wgs >= (1ll << 31)) return fail(VRS_EBADSHAPE, "dwconv: grid too large");
+      snprintf(name, sizeof name, "vrs_dwconv3_s1w%d_%s", rb, dsuffix(cs.dtype));
+      if ((rc = get_fn(ctx, name, &f))) return rc;
+      out.push_back(make_launch(name, f, dim3((unsigned)wgs), dim3(256), 0, a));
+    } else {
+      const int64_t per_img = (int64_t)((y.h + 3) / 4) * y.w * (x.c / 8);
+      if (per_img >= (1ll << 24)) return fail(VRS_EBADSHAPE, "dwconv: map too large for one grid row");
+      snprintf(name, sizeof name, "vrs_dwconv3_s%d_%s", cs.stride, dsuffix(cs.dtype));
+      if ((rc = get_fn(ctx, name, &f))) return rc;
+      out.push_back(make_launch(name, f, dim3((unsigned)((per_img + 255) / 256), (unsigned)x.n), dim3(256), 0, a));
+    }
     const double es = (double)elt_size(cs.dtype);
     out.back().flops = 2.0 * x.n * y.h * y.w * (double)x.c * cs.k * cs.k;
     out.back().bytes = (double)x.n * x.h * x.w * x.c * es + (double)y.n * y.h * y.w * y.c * es +

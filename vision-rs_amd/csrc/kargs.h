@@ -52,6 +52,9 @@ typedef struct {
   int32_t Ho, Wo, y_pitch;
   int32_t kh, kw, stride, pad;
   int32_t act;
+  /* row-walking stride-1 kernel: raw-buffer extent of x, 64-channel blocks,
+   * 8-column patches and row bands per image */
+  int32_t x_bytes, cblocks, patches, bands;
 } vrs_dw_args;
 
 /* SPPF pooling: reads channels [0,c) of a NHWC buffer (pitch) and writes the

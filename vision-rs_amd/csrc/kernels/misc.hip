@@ -95,6 +95,148 @@ __device__ __forceinline__ void dw_body(const vrs_dw_args& a) {
 }
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Stride-1 depthwise 3x3, row walking.  A wave owns 8 output columns x 64
+// channels (lane = channel group g + 8 * column cx) of one band of RB output
+// rows and walks down the band's RB + 2 input rows once: each lane loads its
+// own column (16 bytes per bf16 group), takes the left/right neighbours from
+// the lanes 8 below/above (ds_bpermute), and only the patch's edge lanes load
+// the halo column.  Every input row feeds the three output rows it touches
+// through a 3-slot accumulator ring, so an input pixel is read once per band
+// (plus the 2-row band halo) instead of once per tap; loads run two rows
+// ahead.  The four waves of a workgroup take adjacent column patches so
+// their edge columns meet in L1.
+template <typename T, int RB>
+__device__ __forceinline__ void dww_body(const vrs_dw_args& a) {
+  using E = Elt<T>;
+  using G = typename E::group;
+  constexpr int NW = (int)sizeof(G) / 4;          // dwords per group
+  static_assert((RB + 2) % 3 == 0, "rows per band: RB + 2 must be a multiple of 3");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int gl = lane & 7, cx = lane >> 3;
+  // workgroup -> (image, band, channel block, 4 adjacent patches)
+  const int pq = (a.patches + 3) >> 2;
+  int wgi = blockIdx.x;
+  const int pquad = wgi % pq; wgi /= pq;
+  const int cb = wgi % a.cblocks; wgi /= a.cblocks;
+  const int band = wgi % a.bands;
+  const int b = wgi / a.bands;
+  const int patch = pquad * 4 + wave;
+  const int ox = patch * 8 + cx;
+  const int c0 = cb * 64 + gl * 8;
+  const bool cok = c0 < a.C && patch < a.patches;
+  const bool colok = cok && ox < a.W;             // stride 1: Wo == W, Ho == H
+  const int oy0 = band * RB;
+
+  float wv[9][8];
+  {
+    const T* wp = reinterpret_cast<const T*>(a.w);
+    const int cw = cok ? c0 : 0;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      G gw = E::load(wp + (int64_t)k * a.C + cw);
+      const T* ew = reinterpret_cast<const T*>(&gw);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) wv[k][c] = E::to_f(ew[c]);
+    }
+  }
+  float sc[8], sh[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    sc[c] = a.scale[(cok ? c0 : 0) + c];
+    sh[c] = a.shift[(cok ? c0 : 0) + c];
+  }
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
+  const int img = b * a.H;
+  // halo column of the patch-edge lanes: left for cx == 0, right for cx == 7
+  const int hx = cx == 0 ? ox - 1 : (cx == 7 ? ox + 1 : -1);
+  const bool hok = cok && (cx == 0 || cx == 7) && (unsigned)hx < (unsigned)a.W;
+  auto row_off = [&](int iy, int xx, bool ok) -> uint32_t {
+    return (ok && (unsigned)iy < (unsigned)a.H)
+               ? (uint32_t)((((img + iy) * a.W + xx) * a.x_pitch + c0) * (int)sizeof(T))
+               : kOOB;
+  };
+  G own[3], halo[3];   // prefetch ring of input rows (own column, halo column)
+  auto fetch = [&](int slot, int iy) {
+    own[slot] = E::bload(rx, row_off(iy, ox, colok), 0);
+    halo[slot] = E::bload(rx, row_off(iy, hx, hok), 0);
+  };
+
+  float acc[3][8];
+#pragma unroll
+  for (int s = 0; s < 3; ++s)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[s][c] = 0.f;
+
+  T* y = reinterpret_cast<T*>(a.y);
+  const int iy0 = oy0 - 1;
+  // Input row u of the band (0..RB+1) sits in prefetch slot u % 3 and feeds
+  // output rows v = u - ky (ky = 0..2) through accumulator slot v % 3; after
+  // row u, output row u - 2 is complete (slot (u + 1) % 3).
+  auto process = [&](int p, int u) {
+    const uint32_t* ov = reinterpret_cast<const uint32_t*>(&own[p]);
+    const uint32_t* hv = reinterpret_cast<const uint32_t*>(&halo[p]);
+    uint32_t lw[NW], rw[NW];
+#pragma unroll
+    for (int d = 0; d < NW; ++d) {
+      const uint32_t fromleft = (uint32_t)__shfl((int)ov[d], cx == 0 ? lane : lane - 8);
+      const uint32_t fromright = (uint32_t)__shfl((int)ov[d], cx == 7 ? lane : lane + 8);
+      lw[d] = cx == 0 ? hv[d] : fromleft;
+      rw[d] = cx == 7 ? hv[d] : fromright;
+    }
+    const T* el = reinterpret_cast<const T*>(lw);
+    const T* eo = reinterpret_cast<const T*>(ov);
+    const T* er = reinterpret_cast<const T*>(rw);
+    float xv[3][8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      xv[0][c] = E::to_f(el[c]);
+      xv[1][c] = E::to_f(eo[c]);
+      xv[2][c] = E::to_f(er[c]);
+    }
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky) {
+      const int s = ((p - ky) % 3 + 3) % 3;   // accumulator slot of v = u - ky (static)
+#pragma unroll
+      for (int kx = 0; kx < 3; ++kx)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[s][c] += wv[ky * 3 + kx][c] * xv[kx][c];
+    }
+    const int sv = (p + 1) % 3;
+    const int oy = oy0 + u - 2;
+    if (u >= 2 && oy < a.H && colok) {
+      G out;
+      T* o = reinterpret_cast<T*>(&out);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float t = acc[sv][c] * sc[c] + sh[c];
+        if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
+        o[c] = E::from_f(t);
+      }
+      E::store(y + ((int64_t)(img + oy) * a.W + ox) * a.y_pitch + c0, out);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[sv][c] = 0.f;
+  };
+
+  fetch(0, iy0);
+  fetch(1, iy0 + 1);
+  for (int u = 0; u < RB + 2; u += 3) {
+    fetch(2, iy0 + u + 2);
+    process(0, u);
+    fetch(0, iy0 + u + 3);
+    process(1, u + 1);
+    fetch(1, iy0 + u + 4);
+    process(2, u + 2);
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w16_bf16(vrs_dw_args a) { dww_body<bf16_t, 16>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w10_bf16(vrs_dw_args a) { dww_body<bf16_t, 10>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w16_f32(vrs_dw_args a) { dww_body<float, 16>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w10_f32(vrs_dw_args a) { dww_body<float, 10>(a); }
+
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1_bf16(vrs_dw_args a) { dw_body<bf16_t, 1>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s2_bf16(vrs_dw_args a) { dw_body<bf16_t, 2>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1_f32(vrs_dw_args a) { dw_body<float, 1>(a); }

@@ -101,7 +101,55 @@ __device__ __forceinline__ void msda_any(const vrs_msda_args& a) {
   *reinterpret_cast<f32x4_t*>(a.out + bq * row + h * 32 + part * 4) = acc;
 }
 
+// L = 4, P = 4 split by level: workgroup = one (b, q), wave = one level, so a
+// query's 64 bilinear corner fetches per lane spread over four waves (4x the
+// waves in flight of one wave per query); the four partial sums meet in LDS.
+__device__ __forceinline__ void msda_split_body(const vrs_msda_args& a) {
+  constexpr int P = 4;
+  __shared__ f32x4_t part[4][64];
+  const int lane = threadIdx.x & 63, l = threadIdx.x >> 6;
+  const int64_t bq = blockIdx.x;
+  const int h = lane >> 3, pc = lane & 7;   // head, 4-channel part
+  const int b = (int)(bq / a.Q);
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if (h < a.heads) {
+    const float rx = a.ref[bq * 2 + 0], ry = a.ref[bq * 2 + 1];
+    const int64_t row = (int64_t)a.heads * 32;
+    const float* vl = a.value + ((int64_t)b * a.S + a.lstart[l]) * row + h * 32 + pc * 4;
+    const int Hl = a.lh[l], Wl = a.lw[l];
+    const int64_t obase = ((bq * a.heads + h) * 4 + l) * P;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t oi = obase + p;
+      const float2 off = *reinterpret_cast<const float2*>(a.off + 2 * oi);
+      const float w = a.attw[oi];
+      const float ix = (rx + off.x) * (float)Wl - 0.5f;
+      const float iy = (ry + off.y) * (float)Hl - 0.5f;
+      const float fx = floorf(ix), fy = floorf(iy);
+      const int x0 = (int)fx, y0 = (int)fy;
+      const float ax1 = ix - fx, ay1 = iy - fy;
+      const float ax0 = 1.f - ax1, ay0 = 1.f - ay1;
+      const bool xv0 = (unsigned)x0 < (unsigned)Wl, xv1 = (unsigned)(x0 + 1) < (unsigned)Wl;
+      const bool yv0 = (unsigned)y0 < (unsigned)Hl, yv1 = (unsigned)(y0 + 1) < (unsigned)Hl;
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      const f32x4_t v00 = (yv0 && xv0) ? *reinterpret_cast<const f32x4_t*>(vl + ((int64_t)y0 * Wl + x0) * row) : z;
+      const f32x4_t v01 = (yv0 && xv1) ? *reinterpret_cast<const f32x4_t*>(vl + ((int64_t)y0 * Wl + x0 + 1) * row) : z;
+      const f32x4_t v10 = (yv1 && xv0) ? *reinterpret_cast<const f32x4_t*>(vl + ((int64_t)(y0 + 1) * Wl + x0) * row) : z;
+      const f32x4_t v11 =
+          (yv1 && xv1) ? *reinterpret_cast<const f32x4_t*>(vl + ((int64_t)(y0 + 1) * Wl + x0 + 1) * row) : z;
+      acc += w * (ay0 * (ax0 * v00 + ax1 * v01) + ay1 * (ax0 * v10 + ax1 * v11));
+    }
+  }
+  part[l][lane] = acc;
+  __syncthreads();
+  if (l == 0 && h < a.heads) {
+    const f32x4_t sum = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+    *reinterpret_cast<f32x4_t*>(a.out + bq * (int64_t)a.heads * 32 + h * 32 + pc * 4) = sum;
+  }
+}
+
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(256) void vrs_msda_l4p4_f32(vrs_msda_args a) { msda_body<4, 4>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_msda_l4p4s_f32(vrs_msda_args a) { msda_split_body(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_msda_f32(vrs_msda_args a) { msda_any(a); }
