@@ -32,6 +32,7 @@ sys.path.insert(0, os.path.join(ROOT, "vision-rs_amd"))
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_F32_TFLOPS = 157.3
+PEAK_FP8_TFLOPS = 5000.0    # dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
@@ -361,7 +362,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--size", type=int, default=640)
     ap.add_argument("--variant", default="m")
-    ap.add_argument("--dtype", default="bf16", choices=["bf16", "f32"])
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "f32", "fp8"])
+    ap.add_argument("--no-fp8", action="store_true", help="skip the fp8 second run (BASELINE config 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--layers", action="store_true", help="also print the per-layer table to stderr")
     ap.add_argument("--micro", action="store_true",
@@ -393,34 +395,56 @@ def main() -> int:
     if a.traffic_pass:
         traffic_pass(a, ctx, a.traffic_pass)
         return 0
-    log(f"[bench] YOLO26{a.variant} {a.dtype} bs{a.batch} {a.size}x{a.size}: building")
-    dt = vrs.BF16 if a.dtype == "bf16" else vrs.F32
+    dt = {"bf16": vrs.BF16, "f32": vrs.F32, "fp8": vrs.FP8}[a.dtype]
     desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant=a.variant, one2one=True)
-    m = vrs.Model(ctx, desc, a.batch, a.size, a.size, dt, 1e-3)
-    P = seeded_params(m.params(), seed=0, bn="identity")
-    m.load(P)
     x = torch.from_numpy(images(a.batch, a.size, a.size, seed=0)).cuda()
-    outs = m.alloc_outputs()
     stream = torch.cuda.Stream()
-    with torch.cuda.stream(stream):
-        m.forward(x, outs, stream.cuda_stream)
-        torch.cuda.synchronize()
-        m.capture(x, outs, stream.cuda_stream)
-        log(f"[bench] captured {len(m.launch_names())} launches; warmup {a.warmup}")
-        for _ in range(a.warmup):
-            m.replay(stream.cuda_stream)
-        torch.cuda.synchronize()
-        log(f"[bench] timing {a.steps} steps")
-        t0 = time.perf_counter()
-        for _ in range(a.steps):
-            m.replay(stream.cuda_stream)
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-        log("[bench] per-kernel profile")
-        per_sym, layers = kernel_profile(m)
+
+    def run(dtype):
+        """Build, (calibrate,) capture and time one forward per step; returns
+        (model, elapsed seconds, per-kernel, per-layer)."""
+        log(f"[bench] YOLO26{a.variant} {['f32', 'bf16', 'fp8'][dtype]} bs{a.batch} {a.size}x{a.size}: building")
+        m = vrs.Model(ctx, desc, a.batch, a.size, a.size, dtype, 1e-3)
+        m.load(P)
+        outs = m.alloc_outputs()
+        with torch.cuda.stream(stream):
+            if dtype == vrs.FP8:
+                m.calibrate(x, stream.cuda_stream)   # activation scales from this batch (bf16 pass)
+            m.forward(x, outs, stream.cuda_stream)
+            torch.cuda.synchronize()
+            m.capture(x, outs, stream.cuda_stream)
+            log(f"[bench] captured {len(m.launch_names())} launches; warmup {a.warmup}")
+            for _ in range(a.warmup):
+                m.replay(stream.cuda_stream)
+            torch.cuda.synchronize()
+            log(f"[bench] timing {a.steps} steps")
+            t0 = time.perf_counter()
+            for _ in range(a.steps):
+                m.replay(stream.cuda_stream)
+            torch.cuda.synchronize()
+            el = time.perf_counter() - t0
+            log("[bench] per-kernel profile")
+            ps, ly = kernel_profile(m)
+        return m, el, ps, ly
+
+    P = seeded_params(vrs.Model(None, desc, a.batch, a.size, a.size).params(), seed=0, bn="identity")
+    m, elapsed, per_sym, layers = run(dt)
+    fp8_run = None
+    if dt == vrs.BF16 and not a.no_fp8:
+        m8, el8, ps8, _ = run(vrs.FP8)
+        top = sorted(ps8.items(), key=lambda kv: -kv[1]["ms"])[:4]
+        fp8_run = {"value": round(a.batch * a.steps / el8, 1), "unit": "images/s",
+                   "ms_per_step": round(el8 * 1e3 / a.steps, 3),
+                   "fp8_convs": sum(1 for _, f8, _ in m8.conv_info() if f8), "convs": len(m8.conv_info()),
+                   "note": "e4m3 weights (per-channel absmax/448) and e4m3 activations (per-tensor power-of-two "
+                           "step calibrated on this batch) on the fp8 MFMA for convs with Cin % 64 == 0; the "
+                           "rest bf16; activations stored bf16",
+                   "kernels": {s: {"launches": d["launches"], "ms": round(d["ms"], 4),
+                                   "tflops": round(d["flops"] / max(d["ms"], 1e-9) / 1e9, 2)} for s, d in top}}
+        m8.close()
     ms = elapsed * 1e3 / a.steps
     value = a.batch * a.steps / elapsed
-    peak = PEAK_BF16_TFLOPS if dt == vrs.BF16 else PEAK_F32_TFLOPS
+    peak = PEAK_BF16_TFLOPS if dt == vrs.BF16 else PEAK_FP8_TFLOPS if dt == vrs.FP8 else PEAK_F32_TFLOPS
     dom = max(per_sym.items(), key=lambda kv: kv[1]["ms"])
     roof = roofline_of(dom[0], dom[1], peak)
     if a.variant == "m" and a.batch == 64 and a.size == 640 and a.dtype == "bf16":
@@ -453,6 +477,7 @@ def main() -> int:
                    "achieved_tflops_e2e": round(total_flops / (ms / 1e3) / 1e12, 1)},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "fp8_run": fp8_run,
         "kernels": kern,
     }
     print(json.dumps(line), flush=True)

@@ -46,6 +46,11 @@ extern "C" {
 /* ---- enums -------------------------------------------------------------- */
 #define VRS_F32 0
 #define VRS_BF16 1
+/* Dense convs with e4m3 weights (per-output-channel scale absmax/448) and
+ * e4m3-quantised activations (a per-tensor power-of-two scale) on the fp8
+ * MFMA; activations stay bfloat16 in memory.  No reference function: BASELINE
+ * config 5's second run. */
+#define VRS_FP8 2
 
 #define VRS_ACT_NONE 0
 #define VRS_ACT_SILU 1
@@ -91,8 +96,11 @@ typedef struct {
   int32_t stride;
   int32_t groups;   /* 1 = dense (implicit GEMM on MFMA); == channels = depthwise */
   int32_t act;      /* VRS_ACT_NONE or VRS_ACT_SILU */
-  int32_t dtype;    /* VRS_BF16 or VRS_F32: element type of x, y, res */
+  int32_t dtype;    /* VRS_BF16 or VRS_F32: element type of x, y, res;
+                       VRS_FP8 (dense, Cin % 64 == 0): bf16 x/y/res, e4m3 weights */
   int32_t tile;     /* dense only: VRS_TILE_* (0 = automatic) */
+  float in_scale;   /* VRS_FP8: activation quantisation step, a power of two:
+                       x8 = rne(clamp(x, +-448*in_scale) / in_scale) */
 } vrs_conv_desc;
 
 /* Conv2d + folded BN (+SiLU) (+residual).  Replaces teeny-kernels
@@ -115,6 +123,14 @@ int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const vo
  * Returns the byte count needed when out == NULL. */
 int64_t vrs_pack_conv_weight(const float* w_oihw, int32_t cout, int32_t cin_per_group, int32_t k,
                              int32_t groups, int32_t cin_pad, int32_t dtype, void* out);
+
+/* fp8 weight pack (no reference function): per output channel c,
+ * s[c] = max|w[c]| / 448 (1 when all zero) and q = rne_e4m3(w / s[c]) into
+ * the dense layout [Cout][k][k][cin_pad] of bytes.  vrs_conv2d with VRS_FP8
+ * expects scale[c] to include s[c] * in_scale (times the BN scale).
+ * Returns the byte count needed when out == NULL. */
+int64_t vrs_pack_conv_weight_fp8(const float* w_oihw, int32_t cout, int32_t cin, int32_t k, int32_t cin_pad,
+                                 uint8_t* out, float* out_scale);
 
 /* BN fold, examples/yolo26.rs:3437-3495: scale = gamma/sqrt(var+eps),
  * shift = beta - scale*mean (host arithmetic, done once at load time).
@@ -257,6 +273,15 @@ int vrs_model_launch_work(const vrs_model* m, int32_t i, double* flops, double* 
 /* Run launches [first, first+count) of the prepared forward on `stream`
  * (per-kernel timing with events between launches). */
 int vrs_model_run_launches(vrs_model* m, int32_t first, int32_t count, void* stream);
+/* VRS_FP8 models: set the per-tensor activation scales of the fp8 convs from
+ * one bfloat16 forward of `x` (same layout as vrs_model_forward): in_scale =
+ * the smallest power of two >= max|input| / 448.  Required once before the
+ * first fp8 forward/capture; synchronises `stream`. */
+int vrs_model_calibrate(vrs_model* m, const float* x, void* stream);
+/* Convs in build order: parameter prefix (e.g. "model.3"), whether it runs on
+ * fp8 and its activation scale (0 before calibration). */
+int vrs_model_num_convs(const vrs_model* m);
+int vrs_model_conv_info(const vrs_model* m, int32_t i, const char** prefix, int32_t* fp8, float* in_scale);
 int vrs_model_destroy(vrs_model* m);
 
 #ifdef __cplusplus

@@ -61,14 +61,44 @@ class Params(dict):
     so a bfloat16 run can be compared against an oracle that stores its
     activations at the same precision and at the same points."""
 
-    def __init__(self, *a, eps=1e-3, act_q=None, **k):
+    def __init__(self, *a, eps=1e-3, act_q=None, fp8=None, **k):
         super().__init__(*a, **k)
         self.eps = eps
         self.act_q = act_q if act_q is not None else (lambda t: t)
+        # conv prefix -> activation step of the convs that run on e4m3
+        # (weights per output channel, inputs per tensor; see fp8_conv_inputs)
+        self.fp8 = fp8 or {}
+
+
+def e4m3_round(x):
+    """float32 -> nearest OCP e4m3 value (ties to even, saturating at +-448,
+    subnormal step 2^-9).  No reference function (BASELINE config 5's fp8
+    run); pinned against torch.float8_e4m3fn in tests/test_oracle_golden.py."""
+    x = np.asarray(x, np.float32)
+    a = np.minimum(np.abs(x), np.float32(448.0))
+    sub = np.rint(a * np.float32(512.0)) / np.float32(512.0)
+    f, e2 = np.frexp(np.maximum(a, np.float32(2.0 ** -6)))
+    mant = np.rint((f * 2.0 - 1.0) * 8.0).astype(np.float32)
+    norm = np.ldexp(np.float32(1.0) + mant / np.float32(8.0), e2 - 1).astype(np.float32)
+    return np.where(a < 2.0 ** -6, sub, norm).astype(np.float32) * np.sign(x).astype(np.float32)
+
+
+def fp8_conv_inputs(x, w, in_scale):
+    """The e4m3 operands of an fp8 conv, dequantised: x on the per-tensor step
+    in_scale (a power of two), w per output channel on step max|w|/448."""
+    wf = np.asarray(w, np.float32)
+    amax = np.abs(wf.reshape(wf.shape[0], -1)).max(axis=1).astype(np.float32)
+    sc = np.where(amax > 0, amax / np.float32(448.0), np.float32(1.0)).astype(np.float32)
+    scb = sc.reshape(-1, *([1] * (wf.ndim - 1)))
+    wq = e4m3_round(wf / scb) * scb
+    s = np.float32(in_scale)
+    return e4m3_round(np.asarray(x, np.float32) / s) * s, wq.astype(np.float32)
 
 
 def _conv_bn_act(P, pre, x, k, s, g, act, res=None):
     w = P[_j(pre, "conv.weight")]
+    if pre in P.fp8:
+        x, w = fp8_conv_inputs(x, w, P.fp8[pre])
     y = conv2d(x, w, stride=s, pad=k // 2, groups=g)
     scale, shift = bn_fold(P[_j(pre, "bn.weight")], P[_j(pre, "bn.bias")],
                            P[_j(pre, "bn.running_mean")], P[_j(pre, "bn.running_var")], P.eps)
@@ -91,8 +121,12 @@ def dwconv(c, k, s):  # conv.rs:75-85: depthwise -> BN -> SiLU
 
 
 def conv_plain(c_in, c_out, k, s):  # conv.rs:90-99: conv with bias
-    return lambda P, pre, x: conv2d(x, P[_j(pre, "weight")], stride=s, pad=k // 2,
-                                    bias=P[_j(pre, "bias")])
+    def f(P, pre, x):
+        w = P[_j(pre, "weight")]
+        if pre in P.fp8:
+            x, w = fp8_conv_inputs(x, w, P.fp8[pre])
+        return conv2d(x, w, stride=s, pad=k // 2, bias=P[_j(pre, "bias")])
+    return f
 
 
 def bottleneck_std(c, shortcut):  # bottleneck.rs:37-49: shortcut -> elem_add(x, y)

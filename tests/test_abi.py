@@ -83,3 +83,19 @@ def test_no_gpu_context_fails_cleanly():
     h = C.c_void_p()
     rc = vrs.lib().vrs_ctx_create(0, vrs.LIB_DIR.encode(), C.byref(h))
     assert rc in (-1, -5) and not h
+
+
+def test_pack_conv_weight_fp8_matches_torch():
+    """Host e4m3 packing: per-channel step max|w|/448, ties to even, zero pad."""
+    import torch
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((6, 5, 3, 3)) * np.exp(rng.uniform(-8, 3, (6, 5, 3, 3)))).astype(np.float32)
+    w[0].flat[:8] = [448, -448, 2 ** -9, 2 ** -10, 3 * 2 ** -10, 1.0625, 1.1875, 232]   # step 1.0 on row 0
+    q, sc = vrs.pack_conv_weight_fp8(w, cin_pad=8)
+    amax = np.abs(w.reshape(6, -1)).max(1)
+    assert np.array_equal(sc, (amax / np.float32(448)).astype(np.float32))
+    ref = torch.from_numpy(w / sc[:, None, None, None]).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    got = q.reshape(6, 3, 3, 8)
+    assert np.array_equal(got[..., :5].transpose(0, 3, 1, 2), ref.numpy())
+    assert np.all(got[..., 5:] == 0)
+

@@ -106,6 +106,60 @@ def test_conv2d_every_tile(dtype, tile, yview):
     assert torch.all(rest == 7.0)
 
 
+FP8_CASES = [
+    # n, cin, h, w, cout, k, s, residual, tile
+    (2, 64, 20, 20, 128, 3, 1, False, vrs.TILE_128x128),
+    (2, 128, 9, 11, 256, 3, 2, False, vrs.TILE_256x128),
+    (2, 192, 12, 12, 64, 1, 1, True, vrs.TILE_64x256),
+    (1, 256, 10, 10, 96, 3, 1, False, vrs.TILE_128x256),
+    (2, 64, 15, 7, 200, 1, 1, True, vrs.TILE_AUTO),
+]
+
+
+@pytest.mark.parametrize("case", FP8_CASES)
+def test_conv2d_fp8(case):
+    """e4m3 weights (per-channel absmax/448) and e4m3-quantised bf16 inputs
+    (power-of-two step) on the fp8 MFMA, against the oracle conv of the same
+    dequantised operands: only accumulation order and the bf16 output
+    rounding differ, so the bf16 bar applies."""
+    import torch
+    n, cin, h, w, cout, k, s, with_res, tile = case
+    rng = np.random.default_rng(31 + cin)
+    x = bf16_round(rng.standard_normal((n, cin, h, w)).astype(np.float32) * 3.0)
+    wt = (rng.standard_normal((cout, cin, k, k)) * np.sqrt(2.0 / (cin * k * k))).astype(np.float32)
+    bn_s = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    in_scale = float(2.0 ** np.ceil(np.log2(np.abs(x).max() / 448.0)))
+    q, ws = vrs.pack_conv_weight_fp8(wt)
+    from oracle.yolo26 import fp8_conv_inputs
+    xq, wq = fp8_conv_inputs(x, wt, in_scale)
+    ho, wo = (h + 2 * (k // 2) - k) // s + 1, (w + 2 * (k // 2) - k) // s + 1
+    res = bf16_round(rng.standard_normal((n, cout, ho, wo)).astype(np.float32)) if with_res else None
+    ref = oracle.affine_act(oracle.conv2d(xq, wq, s, k // 2), bn_s, shift, 1)
+    if with_res:
+        ref = ref + res
+    xt = to_nhwc(x, vrs.BF16)
+    yt = torch.full((n, ho, wo, cout), 7.0, dtype=torch.bfloat16, device="cuda")
+    rt = to_nhwc(res, vrs.BF16) if with_res else None
+    ctx().conv2d(vrs.nhwc(xt), dev(q), dev((bn_s * ws * in_scale).astype(np.float32)), dev(shift), vrs.nhwc(yt),
+                 k, s, 1, vrs.ACT_SILU, vrs.nhwc(rt) if with_res else None, vrs.FP8, tile=tile, in_scale=in_scale)
+    torch.cuda.synchronize()
+    assert rel_err(from_nhwc(yt), ref, FLOOR[vrs.BF16]) < TOL[vrs.BF16]
+
+
+def test_conv2d_fp8_rejections():
+    import torch
+    x = torch.zeros((1, 4, 4, 32), dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros((1, 4, 4, 64), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(64 * 32, dtype=torch.uint8, device="cuda")
+    sc = torch.ones(64, device="cuda")
+    with pytest.raises(vrs.VrsError):   # Cin % 64 != 0
+        ctx().conv2d(vrs.nhwc(x), w, sc, sc, vrs.nhwc(y), 1, 1, 1, vrs.ACT_NONE, None, vrs.FP8, in_scale=1.0)
+    x = torch.zeros((1, 4, 4, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(vrs.VrsError):   # step not a power of two
+        ctx().conv2d(vrs.nhwc(x), w, sc, sc, vrs.nhwc(y), 1, 1, 1, vrs.ACT_NONE, None, vrs.FP8, in_scale=0.3)
+
+
 def test_conv2d_tile_rejections():
     import torch
     x = torch.zeros((1, 4, 4, 48), dtype=torch.bfloat16, device="cuda")

@@ -17,6 +17,7 @@ class Recorder(dict):
         super().__init__(P)
         self.eps = eps
         self.act_q = lambda t: t
+        self.fp8 = {}
         self.used = set()
 
     def __getitem__(self, k):

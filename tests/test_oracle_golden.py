@@ -322,3 +322,20 @@ def test_msda_brute_tiny():
     assert oracle.msda(value, [(H, W)], ref, off, attw)[0, 0, 0] == value[0, 1 * W + 2, 0, 0]
     ref = np.array([[[0.0, (1 + 0.5) / H]]], np.float32)  # x = -0.5 px: half of column 0
     assert abs(oracle.msda(value, [(H, W)], ref, off, attw)[0, 0, 0] - 0.5 * value[0, W, 0, 0]) < 1e-6
+
+
+def test_e4m3_round_matches_torch():
+    """Pins oracle.yolo26.e4m3_round (the fp8 emulation) to torch's OCP e4m3
+    conversion: ties to even, subnormals, the 448 maximum; values beyond 448
+    saturate (the device clamps before converting)."""
+    import torch
+    from oracle.yolo26 import e4m3_round
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(100000) * np.exp(rng.uniform(-12, 7, 100000))
+    edges = [448, -448, 0.0, 2 ** -9, 2 ** -10, 3 * 2 ** -10, 2 ** -6, 1.0625, 1.1875, 232, 240, 464 - 1e-3]
+    x = np.concatenate([x, edges]).astype(np.float32)
+    x = x[np.abs(x) <= 448]
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(e4m3_round(x), ref)
+    assert np.array_equal(e4m3_round(np.array([500.0, -1e6, 449.0], np.float32)), np.array([448, -448, 448.0]))
+

@@ -53,6 +53,13 @@ struct ConvStep {
   void* w = nullptr;
   float* scale = nullptr;
   float* shift = nullptr;
+  // VRS_FP8 models: dense convs with Cin % 64 == 0 run on e4m3
+  bool f8 = false;
+  void* w8 = nullptr;               // e4m3 weights [Cout][k][k][Cin]
+  float* scale8 = nullptr;          // BN scale * weight scale * in_scale (after calibration)
+  std::vector<float> scale8_host;   // BN scale * weight scale
+  float in_scale = 0.f;             // activation step (power of two), 0 = not calibrated
+  int tile8 = VRS_TILE_AUTO;
 };
 
 struct Step {
@@ -86,11 +93,19 @@ struct vrs_model {
   std::vector<float*> prep_outs;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  // fp8: calibrated scales; calib_mode runs every conv on bf16 with an
+  // absmax reduction in front of each fp8 conv (slot = conv index)
+  bool calibrated = false;
+  bool calib_mode = false;
+  unsigned* absmax = nullptr;
 };
 
 namespace {
 
 std::string J(const std::string& pre, const std::string& n) { return pre.empty() ? n : pre + "." + n; }
+
+// element type of activations and of every non-fp8 kernel
+int act_dt(const vrs_model* m) { return m->dtype == VRS_FP8 ? VRS_BF16 : m->dtype; }
 
 class Builder {
  public:
@@ -479,45 +494,63 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
     std::string label;
     switch (st.type) {
       case Step::PACK:
-        rc = prep_pack_input(m->ctx, x, m->batch, m->in_c, m->in_h, m->in_w, view_of(m, st.b), m->dtype, ls);
+        rc = prep_pack_input(m->ctx, x, m->batch, m->in_c, m->in_h, m->in_w, view_of(m, st.b), act_dt(m), ls);
         label = "input";
         break;
       case Step::CONV: {
         const ConvStep& c = m->convs[st.conv];
         ConvSpec cs;
-        cs.k = c.k; cs.stride = c.s; cs.dtype = m->dtype; cs.depthwise = c.dw;
+        cs.k = c.k; cs.stride = c.s; cs.dtype = act_dt(m); cs.depthwise = c.dw;
         cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
         cs.cin_real = c.cin == m->bufs[c.x.buf].pitch && c.x.buf == 0 ? m->in_c : 0;
         cs.tile = c.tile;
+        const void* w = c.w;
+        const float* scale = c.scale;
         label = c.pre.empty() ? "conv" : c.pre;
+        if (c.f8 && m->calib_mode) {
+          const vrs_nhwc xv = view_of(m, c.x);
+          rc = prep_absmax(m->ctx, xv, m->absmax + st.conv, ls);
+          if (rc) return rc;
+          for (size_t i = before; i < ls.size(); ++i) labels.push_back(label + ".calib:" + ls[i].name);
+        } else if (c.f8) {
+          if (!m->calibrated) return fail(VRS_ESTATE, "fp8 model: call vrs_model_calibrate first");
+          cs.dtype = VRS_FP8;
+          cs.in_scale = c.in_scale;
+          cs.tile = c.tile8;
+          w = c.w8;
+          scale = c.scale8;
+        }
+        const size_t conv_first = ls.size();
         if (c.out_idx >= 0) {
-          rc = prep_conv_flat(m->ctx, cs, view_of(m, c.x), c.w, c.scale, c.shift, c.cout, o[c.out_idx] + c.out_off,
+          rc = prep_conv_flat(m->ctx, cs, view_of(m, c.x), w, scale, c.shift, c.cout, o[c.out_idx] + c.out_off,
                               c.sb, c.sp, c.sc, ls);
         } else {
           vrs_nhwc r;
           if (c.has_res) r = view_of(m, c.res);
-          rc = prep_conv(m->ctx, cs, view_of(m, c.x), c.w, c.scale, c.shift, c.has_res ? &r : nullptr,
+          rc = prep_conv(m->ctx, cs, view_of(m, c.x), w, scale, c.shift, c.has_res ? &r : nullptr,
                          view_of(m, c.y), ls);
         }
-        break;
+        if (rc) return rc;
+        for (size_t i = conv_first; i < ls.size(); ++i) labels.push_back(label + ":" + ls[i].name);
+        continue;
       }
       case Step::POOL:
-        rc = prep_pool(m->ctx, view_of(m, st.a), m->dtype, ls);
+        rc = prep_pool(m->ctx, view_of(m, st.a), act_dt(m), ls);
         label = "sppf.pool";
         break;
       case Step::UP:
-        rc = prep_up(m->ctx, view_of(m, st.a), view_of(m, st.b), m->dtype, ls);
+        rc = prep_up(m->ctx, view_of(m, st.a), view_of(m, st.b), act_dt(m), ls);
         label = "upsample";
         break;
       case Step::ATTN: {
         const ConvStep& pe = m->convs[st.conv];
-        rc = prep_attn(m->ctx, st.heads, m->dtype, view_of(m, st.a), pe.w, pe.scale,
+        rc = prep_attn(m->ctx, st.heads, act_dt(m), view_of(m, st.a), pe.w, pe.scale,
                        pe.shift, view_of(m, st.b), ls);
         label = pe.pre.substr(0, pe.pre.size() >= 3 ? pe.pre.size() - 3 : 0) + ".core";
         break;
       }
       case Step::UNPACK:
-        rc = prep_unpack(m->ctx, view_of(m, st.a), m->dtype, o[st.out_idx], ls);
+        rc = prep_unpack(m->ctx, view_of(m, st.a), act_dt(m), o[st.out_idx], ls);
         label = "output";
         break;
     }
@@ -551,12 +584,15 @@ int autotune_tiles(vrs_model* m) {
   VRS_HIP(hipEventCreate(&e0));
   VRS_HIP(hipEventCreate(&e1));
   int rc = VRS_OK;
-  for (ConvStep& c : m->convs) {
+  for (ConvStep& c : m->convs)
+   for (int pass = 0; pass < (c.f8 ? 2 : 1); ++pass) {
     if (c.dw || c.out_idx >= 0 || c.y.buf < 0) continue;
-    const std::vector<int> cand = conv_tile_candidates(c.cout, c.cin, m->dtype);
+    const int dt = pass ? VRS_FP8 : act_dt(m);
+    const std::vector<int> cand = conv_tile_candidates(c.cout, c.cin, dt);
     if (cand.size() < 2) continue;
     ConvSpec cs;
-    cs.k = c.k; cs.stride = c.s; cs.dtype = m->dtype; cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
+    cs.k = c.k; cs.stride = c.s; cs.dtype = dt; cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
+    cs.in_scale = 1.f;  // timing only: values do not matter
     vrs_nhwc r;
     if (c.has_res) r = view_of(m, c.res);
     float best = 1e30f;
@@ -564,8 +600,8 @@ int autotune_tiles(vrs_model* m) {
     for (int t : cand) {
       cs.tile = t;
       std::vector<Launch> ls;
-      if (prep_conv(m->ctx, cs, view_of(m, c.x), c.w, c.scale, c.shift, c.has_res ? &r : nullptr, view_of(m, c.y),
-                    ls) != VRS_OK)
+      if (prep_conv(m->ctx, cs, view_of(m, c.x), pass ? c.w8 : c.w, pass ? c.scale8 : c.scale, c.shift,
+                    c.has_res ? &r : nullptr, view_of(m, c.y), ls) != VRS_OK)
         continue;
       if ((rc = run(ls[0], s))) break;
       VRS_HIP(hipEventRecord(e0, s));
@@ -579,7 +615,7 @@ int autotune_tiles(vrs_model* m) {
       if (ms < best) { best = ms; best_tile = t; }
     }
     if (rc) break;
-    c.tile = best_tile;
+    (pass ? c.tile8 : c.tile) = best_tile;
   }
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
@@ -602,7 +638,8 @@ int vrs_model_create(vrs_ctx* ctx, const vrs_block_desc* d, int32_t batch, int32
   if (!d || !out) return fail(VRS_EINVAL, "vrs_model_create: null argument");
   *out = nullptr;
   if (batch <= 0 || h <= 0 || w <= 0) return fail(VRS_EBADSHAPE, "vrs_model_create: empty input");
-  if (dtype != VRS_BF16 && dtype != VRS_F32) return fail(VRS_EUNSUPPORTED, "vrs_model_create: dtype %d", dtype);
+  if (dtype != VRS_BF16 && dtype != VRS_F32 && dtype != VRS_FP8)
+    return fail(VRS_EUNSUPPORTED, "vrs_model_create: dtype %d", dtype);
   if (d->c_in <= 0 || (d->kind != VRS_BLOCK_YOLO26 && d->c_out <= 0 && d->kind != VRS_BLOCK_PSA_ATTN))
     return fail(VRS_EINVAL, "vrs_model_create: channels");
   std::unique_ptr<vrs_model> m(new vrs_model);
@@ -647,7 +684,7 @@ int vrs_model_finalize(vrs_model* m) {
   if (m->finalized) return VRS_OK;
   for (const Param& p : m->params)
     if (!p.loaded) return fail(VRS_ESTATE, "parameter '%s' not loaded", p.name.c_str());
-  const size_t es = elt_size(m->dtype);
+  const size_t es = elt_size(act_dt(m));
   for (Buf& b : m->bufs) {
     const size_t bytes = (size_t)m->batch * b.h * b.w * b.pitch * es;
     VRS_HIP(hipMalloc(&b.dev, bytes));
@@ -670,10 +707,11 @@ int vrs_model_finalize(vrs_model* m) {
     const int cin_g = w->dims[1];
     const int groups = c.dw ? c.cout : 1;
     const int cin_pad = c.dw ? 1 : c.cin;
-    const int64_t bytes = vrs_pack_conv_weight(nullptr, c.cout, cin_g, c.k, groups, cin_pad, m->dtype, nullptr);
+    const int pdt = act_dt(m);
+    const int64_t bytes = vrs_pack_conv_weight(nullptr, c.cout, cin_g, c.k, groups, cin_pad, pdt, nullptr);
     if (bytes < 0) return (int)bytes;
     std::vector<uint8_t> packed((size_t)bytes);
-    const int64_t r = vrs_pack_conv_weight(w->host.data(), c.cout, cin_g, c.k, groups, cin_pad, m->dtype, packed.data());
+    const int64_t r = vrs_pack_conv_weight(w->host.data(), c.cout, cin_g, c.k, groups, cin_pad, pdt, packed.data());
     if (r < 0) return (int)r;
     int rc;
     if ((rc = dev_upload(m, packed.data(), packed.size(), &c.w))) return rc;
@@ -682,6 +720,24 @@ int vrs_model_finalize(vrs_model* m) {
     c.scale = static_cast<float*>(p);
     if ((rc = dev_upload(m, shift.data(), shift.size() * 4, &p))) return rc;
     c.shift = static_cast<float*>(p);
+    c.f8 = m->dtype == VRS_FP8 && !c.dw && c.cin % 64 == 0 && cin_g == c.cin;
+    if (c.f8) {  // e4m3 copy of the weights; the bf16 one serves calibration
+      std::vector<uint8_t> q((size_t)vrs_pack_conv_weight_fp8(nullptr, c.cout, cin_g, c.k, c.cin, nullptr, nullptr));
+      std::vector<float> ws(c.cout);
+      const int64_t r8 = vrs_pack_conv_weight_fp8(w->host.data(), c.cout, cin_g, c.k, c.cin, q.data(), ws.data());
+      if (r8 < 0) return (int)r8;
+      if ((rc = dev_upload(m, q.data(), q.size(), &c.w8))) return rc;
+      c.scale8_host.resize(c.cout);
+      for (int i = 0; i < c.cout; ++i) c.scale8_host[i] = scale[i] * ws[i];
+      if ((rc = dev_upload(m, c.scale8_host.data(), c.cout * 4, &p))) return rc;  // times in_scale later
+      c.scale8 = static_cast<float*>(p);
+    }
+  }
+  if (m->dtype == VRS_FP8) {
+    void* p;
+    VRS_HIP(hipMalloc(&p, m->convs.size() * sizeof(unsigned)));
+    m->allocs.push_back(p);
+    m->absmax = static_cast<unsigned*>(p);
   }
   for (Param& p : m->params) std::vector<float>().swap(p.host);
   if (m->autotune) {
@@ -776,6 +832,74 @@ int vrs_model_run_launches(vrs_model* m, int32_t first, int32_t count, void* str
     int rc = run(m->launches[i], static_cast<hipStream_t>(stream));
     if (rc) return rc;
   }
+  return VRS_OK;
+}
+
+int vrs_model_calibrate(vrs_model* m, const float* x, void* stream) {
+  if (!m || !x) return fail(VRS_EINVAL, "vrs_model_calibrate: null argument");
+  if (m->dtype != VRS_FP8) return fail(VRS_ESTATE, "vrs_model_calibrate: not an fp8 model");
+  if (!m->finalized) return fail(VRS_ESTATE, "vrs_model_calibrate: call vrs_model_finalize first");
+  // scratch outputs for the bf16 pass (this is set-up, not the launch path)
+  std::vector<float*> outs;
+  int rc = VRS_OK;
+  for (const auto& d : m->out_dims) {
+    int64_t n = 1;
+    for (int v : d) n *= v;
+    void* p = nullptr;
+    if (hipMalloc(&p, (size_t)n * 4) != hipSuccess) { rc = fail(VRS_EHIP, "vrs_model_calibrate: hipMalloc"); break; }
+    outs.push_back(static_cast<float*>(p));
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!rc) {
+    m->calib_mode = true;
+    m->launches.clear();
+    m->prep_x = nullptr;
+    rc = prepare(m, x, outs.data());
+    if (!rc && hipMemsetAsync(m->absmax, 0, m->convs.size() * sizeof(unsigned), s) != hipSuccess)
+      rc = fail(VRS_EHIP, "vrs_model_calibrate: memset");
+    for (size_t i = 0; !rc && i < m->launches.size(); ++i) rc = run(m->launches[i], s);
+    if (!rc && hipStreamSynchronize(s) != hipSuccess) rc = fail(VRS_EHIP, "vrs_model_calibrate: sync");
+  }
+  std::vector<unsigned> amax(m->convs.size());
+  if (!rc && hipMemcpy(amax.data(), m->absmax, amax.size() * sizeof(unsigned), hipMemcpyDeviceToHost) != hipSuccess)
+    rc = fail(VRS_EHIP, "vrs_model_calibrate: readback");
+  for (float* p : outs) (void)hipFree(p);
+  m->calib_mode = false;
+  m->launches.clear();
+  m->prep_x = nullptr;
+  if (rc) return rc;
+  for (size_t i = 0; i < m->convs.size(); ++i) {
+    ConvStep& c = m->convs[i];
+    if (!c.f8) continue;
+    float a;
+    memcpy(&a, &amax[i], 4);
+    // smallest power of two >= a / 448 (1 for an all-zero input)
+    float sc = 1.f;
+    if (a > 0.f && std::isfinite(a)) {
+      int e;
+      const float f = std::frexp(a / 448.f, &e);
+      sc = std::ldexp(1.f, f == 0.5f ? e - 1 : e);
+    }
+    c.in_scale = sc;
+    std::vector<float> s8(c.scale8_host);
+    for (float& v : s8) v *= sc;
+    VRS_HIP(hipMemcpy(c.scale8, s8.data(), s8.size() * 4, hipMemcpyHostToDevice));
+  }
+  if (m->exec) { (void)hipGraphExecDestroy(m->exec); m->exec = nullptr; }
+  if (m->graph) { (void)hipGraphDestroy(m->graph); m->graph = nullptr; }
+  m->calibrated = true;
+  return VRS_OK;
+}
+
+int vrs_model_num_convs(const vrs_model* m) { return m ? (int)m->convs.size() : fail(VRS_EINVAL, "null model"); }
+
+int vrs_model_conv_info(const vrs_model* m, int32_t i, const char** prefix, int32_t* fp8, float* in_scale) {
+  if (!m || !prefix || !fp8 || !in_scale) return fail(VRS_EINVAL, "vrs_model_conv_info: null argument");
+  if (i < 0 || i >= (int)m->convs.size()) return fail(VRS_EINVAL, "vrs_model_conv_info: index %d", i);
+  const ConvStep& c = m->convs[i];
+  *prefix = c.pre.c_str();
+  *fp8 = c.f8 ? 1 : 0;
+  *in_scale = c.in_scale;
   return VRS_OK;
 }
 

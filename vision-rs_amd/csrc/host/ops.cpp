@@ -4,6 +4,7 @@
 #include <cstring>
 
 #include "vrs_internal.h"
+#include <algorithm>
 
 using namespace vrs;
 
@@ -27,6 +28,27 @@ uint16_t host_f2bf(float f) {
 
 }  // namespace
 
+namespace vrs {
+uint8_t f32_to_e4m3(float v) {
+  uint32_t u;
+  memcpy(&u, &v, 4);
+  const uint8_t sign = (uint8_t)((u >> 24) & 0x80);
+  if (std::isnan(v)) return (uint8_t)(sign | 0x7f);
+  float a = std::fabs(v);
+  if (a >= 448.f) return (uint8_t)(sign | 0x7e);               // saturate at 448 = 1.75 * 2^8
+  if (a < 0.015625f) {                                          // below 2^-6: subnormal, step 2^-9
+    const int q = (int)std::nearbyint(a * 512.f);               // 0..8; 8 is the smallest normal
+    return (uint8_t)(sign | q);
+  }
+  int e2;
+  const float f = std::frexp(a, &e2);                           // a = f * 2^e2, f in [0.5, 1)
+  int e = e2 - 1;                                               // a = (1 + m) * 2^e
+  int q = (int)std::nearbyint((f * 2.f - 1.f) * 8.f);           // 3 mantissa bits, ties to even
+  if (q == 8) { q = 0; ++e; }
+  return (uint8_t)(sign | ((e + 7) << 3) | q);
+}
+}  // namespace vrs
+
 extern "C" {
 
 int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const void* w, const float* scale,
@@ -34,6 +56,7 @@ int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const vo
   if (!ctx || !d || !x || !y) return fail(VRS_EINVAL, "vrs_conv2d: null argument");
   ConvSpec cs;
   cs.k = d->k; cs.stride = d->stride; cs.act = d->act; cs.dtype = d->dtype; cs.tile = d->tile;
+  cs.in_scale = d->in_scale;
   if (d->groups == 1) cs.depthwise = false;
   else if (d->groups == x->c && d->groups == y->c) cs.depthwise = true;
   else return fail(VRS_EUNSUPPORTED, "vrs_conv2d: groups=%d (only 1 or depthwise)", d->groups);
@@ -76,6 +99,28 @@ int64_t vrs_pack_conv_weight(const float* w, int32_t cout, int32_t cin_g, int32_
           if (dtype == VRS_F32) static_cast<float*>(out)[o] = v;
           else static_cast<uint16_t*>(out)[o] = host_f2bf(v);
         }
+  return bytes;
+}
+
+int64_t vrs_pack_conv_weight_fp8(const float* w, int32_t cout, int32_t cin, int32_t k, int32_t cin_pad,
+                                 uint8_t* out, float* out_scale) {
+  if (cout <= 0 || cin <= 0 || k <= 0 || cin_pad < cin) return fail(VRS_EINVAL, "pack_conv_weight_fp8: shape");
+  const int64_t bytes = (int64_t)cout * k * k * cin_pad;
+  if (!out) return bytes;
+  if (!w || !out_scale) return fail(VRS_EINVAL, "pack_conv_weight_fp8: null argument");
+  const int64_t per = (int64_t)cin * k * k;
+  for (int co = 0; co < cout; ++co) {
+    float amax = 0.f;
+    for (int64_t i = 0; i < per; ++i) amax = std::max(amax, std::fabs(w[co * per + i]));
+    const float sc = amax > 0.f ? amax / 448.f : 1.f;
+    out_scale[co] = sc;
+    for (int ky = 0; ky < k; ++ky)
+      for (int kx = 0; kx < k; ++kx)
+        for (int ci = 0; ci < cin_pad; ++ci) {
+          const int64_t o = (((int64_t)co * k + ky) * k + kx) * cin_pad + ci;
+          out[o] = ci < cin ? f32_to_e4m3(w[((int64_t)(co * cin + ci) * k + ky) * k + kx] / sc) : 0;
+        }
+  }
   return bytes;
 }
 

@@ -3,6 +3,7 @@
 // failures through status codes (include/vrs.h conventions).
 #include <dirent.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -94,6 +95,16 @@ static const TileInfo* tile_info(int code) {
 static int tile_kernel(int code, int cin, int dtype, char* name, size_t n, int* bm, int* bn, int* threads) {
   const TileInfo* t = tile_info(code);
   if (!t) return fail(VRS_EINVAL, "conv: unknown tile code %d", code);
+  if (dtype == VRS_FP8) {
+    if (cin % 64 != 0) return fail(VRS_EUNSUPPORTED, "conv fp8: needs Cin %% 64 == 0 (Cin=%d)", cin);
+    if (t->code == VRS_TILE_32x256 || t->code == VRS_TILE_256x256)
+      return fail(VRS_EUNSUPPORTED, "conv fp8: tile %s not built", t->tag);
+    snprintf(name, n, "vrs_conv_fp8_%s_k64_a", t->tag);
+    *bm = t->bm;
+    *bn = t->bn;
+    *threads = t->threads;
+    return VRS_OK;
+  }
   if (dtype == VRS_F32 && !t->f32) return fail(VRS_EUNSUPPORTED, "conv: tile %s has no float32 build", t->tag);
   const bool g = cin % 32 != 0;
   bool k64 = !(code & VRS_TILE_K32) && dtype == VRS_BF16 && cin % 64 == 0 && t->code != VRS_TILE_32x256;
@@ -124,6 +135,14 @@ static int auto_tile(int cout, int cin, int64_t M, int dtype, int num_cu) {
 
 std::vector<int> conv_tile_candidates(int cout, int cin, int dtype) {
   std::vector<int> c;
+  if (dtype == VRS_FP8) {
+    if (cin % 64) return c;
+    c.push_back(VRS_TILE_128x128);
+    c.push_back(VRS_TILE_64x256);
+    if (cout > 128) c.push_back(VRS_TILE_256x128);
+    if (cout <= 128) c.push_back(VRS_TILE_128x256);
+    return c;
+  }
   const bool g = cin % 32 != 0;
   for (const auto& t : kTiles) {
     if (dtype == VRS_F32 && !t.f32) continue;
@@ -143,7 +162,21 @@ std::vector<int> conv_tile_candidates(int cout, int cin, int dtype) {
 static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
                       const float* shift, int cout, int ho, int wo, vrs_conv_args& a, std::vector<Launch>& out) {
   int rc;
-  if ((rc = check_dtype(cs.dtype))) return rc;
+  const bool f8 = cs.dtype == VRS_FP8;
+  if (!f8 && (rc = check_dtype(cs.dtype))) return rc;
+  if (f8) {
+    int e = 0;
+    const float m = frexpf(cs.in_scale, &e);
+    if (!(cs.in_scale > 0.f) || m != 0.5f || cs.in_scale < 1e-30f || cs.in_scale > 1e30f)
+      return fail(VRS_EINVAL, "conv fp8: in_scale %g must be a positive power of two", (double)cs.in_scale);
+    a.in_scale = cs.in_scale;
+    // bfloat16 bits of 448 * in_scale (exact: 448 has 3 significant bits)
+    uint32_t fb;
+    const float lim = 448.f * cs.in_scale;
+    memcpy(&fb, &lim, 4);
+    const uint32_t hb = fb >> 16;
+    a.clamp_bits = hb | (hb << 16);
+  }
   if ((rc = check_view(x, "conv input", 8))) return rc;
   if (!w || !scale || !shift) return fail(VRS_EINVAL, "conv: null weight/scale/shift");
   if (cs.k < 1 || cs.k > 7 || cs.k % 2 == 0 || cs.stride < 1) return fail(VRS_EBADSHAPE, "conv: k=%d s=%d", cs.k, cs.stride);
@@ -156,7 +189,7 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   a.shift = shift;
   {  // raw-buffer extents (the kernels use 32-bit byte offsets)
     const int64_t xb = ((int64_t)x.n * x.h * x.w * x.pitch - x.c_off) * (int64_t)elt_size(cs.dtype);
-    const int64_t wb = (int64_t)cout * cs.k * cs.k * x.c * (int64_t)elt_size(cs.dtype);
+    const int64_t wb = (int64_t)cout * cs.k * cs.k * x.c * (f8 ? 1 : (int64_t)elt_size(cs.dtype));
     if (xb >= (1ll << 31) || wb >= (1ll << 31))
       return fail(VRS_EBADSHAPE, "conv: input buffer (%lld B) or weights (%lld B) exceed 2 GiB", (long long)xb,
                   (long long)wb);
@@ -174,7 +207,9 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   a.act = cs.act;
   char name[64];
   int bm, bn, threads;
-  const int tile = cs.tile ? cs.tile : auto_tile(cout, x.c, M, cs.dtype, ctx->num_cu);
+  const int tile = cs.tile ? cs.tile
+                            : f8 ? (cout <= 64 ? VRS_TILE_64x256 : VRS_TILE_128x128)
+                                 : auto_tile(cout, x.c, M, cs.dtype, ctx->num_cu);
   if ((rc = tile_kernel(tile, x.c, cs.dtype, name, sizeof name, &bm, &bn, &threads))) return rc;
   a.tiles_m = (cout + bm - 1) / bm;
   a.tiles_n = (int32_t)((M + bn - 1) / bn);
@@ -187,7 +222,7 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   const double cin = cs.cin_real > 0 ? cs.cin_real : x.c;
   const double kk = (double)cs.k * cs.k;
   out.back().flops = 2.0 * (double)M * cout * kk * cin;
-  out.back().bytes = (double)x.n * x.h * x.w * cin * es + (double)cout * kk * cin * es +
+  out.back().bytes = (double)x.n * x.h * x.w * cin * es + (double)cout * kk * cin * (f8 ? 1.0 : es) +
                      (double)M * cout * (a.y_f32 ? 4.0 : es) + (a.res ? (double)M * cout * es : 0.0) + 8.0 * cout;
   return VRS_OK;
 }
@@ -370,6 +405,25 @@ int prep_attn(vrs_ctx* ctx, int heads, int dtype, const vrs_nhwc& qkv, const voi
   const double N = (double)qkv.h * qkv.w;
   out.back().flops = 2.0 * a.B * heads * N * N * (32 + 64) + 2.0 * a.B * N * o.c * 9;
   out.back().bytes = (double)a.B * N * (qkv.c + o.c) * elt_size(dtype) + (double)o.c * (9 * elt_size(dtype) + 8);
+  return VRS_OK;
+}
+
+int prep_absmax(vrs_ctx* ctx, const vrs_nhwc& x, unsigned* out, std::vector<Launch>& ls) {
+  int rc;
+  if ((rc = check_view(x, "absmax input", 8))) return rc;
+  vrs_absmax_args a{};
+  a.x = at(x, VRS_BF16);
+  a.out = out;
+  a.npix = (int64_t)x.n * x.h * x.w;
+  a.c = x.c;
+  a.pitch = x.pitch;
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, "vrs_absmax_bf16", &f))) return rc;
+  const int64_t items = a.npix * (x.c / 8);
+  const int64_t cap = 8ll * (ctx->num_cu > 0 ? ctx->num_cu : 256);
+  const int64_t blocks = std::min<int64_t>(cap, (items + 255) / 256);
+  ls.push_back(make_launch("vrs_absmax_bf16", f, dim3((unsigned)std::max<int64_t>(1, blocks)), dim3(256), 0, a));
+  ls.back().bytes = (double)items * 16.0;
   return VRS_OK;
 }
 

@@ -70,7 +70,12 @@ struct ConvSpec {
   bool depthwise = false;
   int cin_real = 0;  // unpadded input channels for work accounting (0: the view's)
   int tile = VRS_TILE_AUTO;  // dense conv tile (VRS_TILE_*)
+  float in_scale = 1.f;      // VRS_FP8: activation quantisation step (power of two)
 };
+// max |x| of a bfloat16 NHWC view into *out (float bits; caller zeroes it)
+int prep_absmax(vrs_ctx* ctx, const vrs_nhwc& x, unsigned* out, std::vector<Launch>& ls);
+// float -> e4m3 (OCP, max 448) with round-to-nearest-even; |v| > 448 saturates
+uint8_t f32_to_e4m3(float v);
 // Dense conv tiles worth trying for a layer (autotuning candidates).
 std::vector<int> conv_tile_candidates(int cout, int cin, int dtype);
 int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,

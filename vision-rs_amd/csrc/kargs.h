@@ -38,6 +38,11 @@ typedef struct {
                      aligned channel offset and pitch) */
   int32_t x_bytes;  /* readable bytes from x to the end of its buffer (< 2^31) */
   int32_t w_bytes;  /* bytes of the packed weights (< 2^31) */
+  /* fp8 kernels: activations are quantised to e4m3 as x / in_scale (a power
+   * of two) after clamping |x| to 448 * in_scale, whose bfloat16 bits are
+   * clamp_bits (in both halves) */
+  float in_scale;
+  uint32_t clamp_bits;
 } vrs_conv_args;
 
 /* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the
@@ -145,5 +150,15 @@ typedef struct {
   int32_t B, S, Q, heads, L, P;
   int32_t lh[8], lw[8], lstart[8];
 } vrs_msda_args;
+
+
+/* max |x| over an NHWC view (npix pixels x c channels, channel pitch) into
+ * *out as float bits (atomic max on the non-negative float's bit pattern) */
+typedef struct {
+  const void* x;
+  unsigned* out;
+  int64_t npix;
+  int32_t c, pitch;
+} vrs_absmax_args;
 
 #endif

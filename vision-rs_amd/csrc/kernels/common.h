@@ -150,3 +150,25 @@ __device__ __forceinline__ f32x16_t mfma32_k16(const Elt<float>::group& a, const
   for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[j], bv1[j], acc, 0, 0, 0);
   return acc;
 }
+
+// 32x32x64 fp8 step: lane l supplies 32 e4m3 bytes of A[row l%32][k (l/32)*32 ..]
+// and of B[k ..][col l%32]; block scales fixed at 1.0 (E8M0 0x7f); same
+// accumulator layout as the 32x32 bf16 step.
+typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8_t;
+__device__ __forceinline__ f32x16_t mfma32_fp8_k64(const i32x8_t& a, const i32x8_t& b, f32x16_t acc) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+}
+
+// Two bfloat16 (one dword) -> two e4m3 bytes: |x| clamped to the bf16 bits
+// `lim` (448 * scale), then rne(x / scale) with scale a power of two.
+typedef __attribute__((__vector_size__(2 * sizeof(short)))) short i16x2_t;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_to_fp8x2(uint32_t v, uint32_t lim, float scale) {
+  typedef __attribute__((__vector_size__(2 * sizeof(unsigned short)))) unsigned short u16x2_t;
+  const u16x2_t mag = __builtin_bit_cast(u16x2_t, v & 0x7fff7fffu);
+  const u16x2_t l = __builtin_bit_cast(u16x2_t, lim);
+  const u16x2_t m = mag < l ? mag : l;   // v_pk_min_u16
+  const uint32_t c = __builtin_bit_cast(uint32_t, m) | (v & 0x80008000u);
+  const i16x2_t r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16((i16x2_t){0, 0}, __builtin_bit_cast(bf16x2_t, c), scale, false);
+  return (uint32_t)(uint16_t)r[0];
+}

@@ -56,32 +56,40 @@ __device__ __forceinline__ void pipe_schedule() {
 // BM output channels x BN pixels per workgroup, BK reduction elements per
 // pipeline step, WGM x WGN waves (wave tile (BM/WGM) x (BN/WGN)).
 // ALIGNED: Cin % BK == 0, so a K step never straddles two filter taps.
-template <typename T, int BM, int BN, int BK, int WGM, int WGN, bool ALIGNED>
+// F8: weights are e4m3 bytes (A operand, 16-byte chunks of 16 k), the bf16
+// activations are quantised to e4m3 while staged into LDS (8 k per 16-byte
+// group -> 8 bytes), and the 32x32x64 fp8 MFMA consumes 64-byte LDS rows.
+template <typename T, int BM, int BN, int BK, int WGM, int WGN, bool ALIGNED, bool F8 = false>
 __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   using E = Elt<T>;
   using G = typename E::group;
+  static_assert(!F8 || (sizeof(T) == 2 && BK == 64 && ALIGNED), "fp8: bf16 activations, 64-deep steps");
   // LDS rows of BK + 8 elements: the 32 rows a half-wave reads with
   // ds_read_b128 (row stride 144 B for BK=64 bf16) start on distinct 4-bank
   // groups of the 64 banks (measured: 4% conflict cycles vs 34% at +16).
   constexpr int PAD = 8;
   constexpr int LDK = BK + PAD;              // LDS row stride in elements
-  constexpr int GPR = BK / 8;                // 8-element groups per tile row
+  constexpr int GPR = BK / 8;                // 8-element groups per tile row (B, and A when !F8)
+  constexpr int GPRA = F8 ? BK / 16 : GPR;   // 16-byte weight chunks per row
+  constexpr int AEL = F8 ? 16 : 8;           // weight elements per chunk
+  constexpr int LDKB = BK + 16;              // F8: LDS row stride in bytes (80: conflict-free)
   constexpr int NT = 64 * WGM * WGN;         // threads per workgroup
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int TM = WTM / 32, TN = WTN / 32;   // 32x32 MFMA tiles per wave
-  constexpr int A_IT = (BM * GPR + NT - 1) / NT;
+  constexpr int A_IT = (BM * GPRA + NT - 1) / NT;
   constexpr int B_IT = (BN * GPR + NT - 1) / NT;
-  constexpr bool A_FULL = (BM * GPR) % NT == 0;   // every thread owns A_IT chunks
+  constexpr bool A_FULL = (BM * GPRA) % NT == 0;   // every thread owns A_IT chunks
   constexpr bool B_FULL = (BN * GPR) % NT == 0;
   // Branch-free software pipeline (two register sets, interleaved schedule)
   // when every thread loads whole chunks; otherwise the plain loop.
   constexpr bool PIPE = ALIGNED && A_FULL && B_FULL;
-  constexpr int TILE_ELEMS = (BM + BN) * LDK;            // one pipeline stage
+  constexpr int TILE_ELEMS = F8 ? (BM + BN) * LDKB / 2 : (BM + BN) * LDK;   // one pipeline stage
   // epilogue staging: per wave WTN pixels x (WTM + SPAD) channels
   constexpr int SPAD = 16 / (int)sizeof(T);
   constexpr int STAGE2 = (WGM * WGN / 2) * WTN * (WTM + SPAD);   // half the waves' staging
   constexpr int BUF_ELEMS = TILE_ELEMS > STAGE2 ? TILE_ELEMS : STAGE2;
   static_assert(TM >= 1 && TN >= 1 && BK % 32 == 0, "tile");
+  static_assert(!F8 || PIPE, "fp8 needs whole-chunk loads (the pipelined loop)");
 
   // The two pipeline buffers are separate objects so the compiler can move
   // LDS writes of one past reads of the other.  Epilogue staging: the first
@@ -117,9 +125,9 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
 #pragma unroll
   for (int i = 0; i < A_IT; ++i) {
     const int c = tid + i * NT;
-    const int co = m0 + c / GPR;
-    a_ok[i] = (A_FULL || c < BM * GPR) && (co < a.Cout);
-    a_ptr[i] = w + (int64_t)(a_ok[i] ? co : 0) * a.K + (c % GPR) * 8;
+    const int co = m0 + c / GPRA;
+    a_ok[i] = (A_FULL || c < BM * GPRA) && (co < a.Cout);
+    a_ptr[i] = w + (int64_t)(a_ok[i] ? co : 0) * a.K + (c % GPRA) * 8;
   }
   int b_iy0[B_IT], b_ix0[B_IT];
   const T* b_ptr[B_IT];
@@ -149,8 +157,14 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   uint32_t a_off[A_IT], b_off[B_IT];
   if (ALIGNED) {
 #pragma unroll
-    for (int i = 0; i < A_IT; ++i)
-      a_off[i] = a_ok[i] ? (uint32_t)((a_ptr[i] - w) * (int)sizeof(T)) : kOOB;
+    for (int i = 0; i < A_IT; ++i) {
+      if constexpr (F8) {   // weights are bytes: row co * K, chunk * 16
+        const int c = tid + i * NT;
+        a_off[i] = a_ok[i] ? (uint32_t)((m0 + c / GPRA) * a.K + (c % GPRA) * AEL) : kOOB;
+      } else {
+        a_off[i] = a_ok[i] ? (uint32_t)((a_ptr[i] - w) * (int)sizeof(T)) : kOOB;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) b_off[i] = (uint32_t)((b_ptr[i] - x) * (int64_t)sizeof(T));
   }
@@ -231,7 +245,7 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
     auto load_set = [&](int k0, G (&ra)[A_IT], G (&rb)[B_IT]) {
       const uint32_t dead = k0 < a.K ? 0u : kOOB;
 #pragma unroll
-      for (int i = 0; i < A_IT; ++i) ra[i] = E::bload(rw, a_off[i] | dead, (uint32_t)k0 * sizeof(T));
+      for (int i = 0; i < A_IT; ++i) ra[i] = E::bload(rw, a_off[i] | dead, (uint32_t)k0 * (F8 ? 1u : (uint32_t)sizeof(T)));
       const int ky = t_ky, kx = t_kx;
       const uint32_t off = (uint32_t)((ky * a.W + kx) * a.x_pitch + t_ci) * sizeof(T);
       t_ci += BK;
@@ -247,22 +261,65 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
       }
     };
     auto store_set = [&](int buf, const G (&ra)[A_IT], const G (&rb)[B_IT]) {
-      T* sA = sbuf(buf);
-      T* sB = sA + BM * LDK;
+      if constexpr (F8) {
+        unsigned char* sA = reinterpret_cast<unsigned char*>(sbuf(buf));
+        unsigned char* sB = sA + BM * LDKB;
 #pragma unroll
-      for (int i = 0; i < A_IT; ++i) {
-        const int c = tid + i * NT;
-        E::store(&sA[(c / GPR) * LDK + (c % GPR) * 8], ra[i]);
-      }
+        for (int i = 0; i < A_IT; ++i) {
+          const int c = tid + i * NT;
+          *reinterpret_cast<u32x4_t*>(sA + (c / GPRA) * LDKB + (c % GPRA) * 16) =
+              *reinterpret_cast<const u32x4_t*>(&ra[i]);
+        }
 #pragma unroll
-      for (int i = 0; i < B_IT; ++i) {
-        const int c = tid + i * NT;
-        E::store(&sB[(c / GPR) * LDK + (c % GPR) * 8], rb[i]);
+        for (int i = 0; i < B_IT; ++i) {
+          const int c = tid + i * NT;
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&rb[i]);
+          const u32x2_t q = {bf16x2_to_fp8x2(v[0], a.clamp_bits, a.in_scale) |
+                                 (bf16x2_to_fp8x2(v[1], a.clamp_bits, a.in_scale) << 16),
+                             bf16x2_to_fp8x2(v[2], a.clamp_bits, a.in_scale) |
+                                 (bf16x2_to_fp8x2(v[3], a.clamp_bits, a.in_scale) << 16)};
+          *reinterpret_cast<u32x2_t*>(sB + (c / GPR) * LDKB + (c % GPR) * 8) = q;
+        }
+      } else {
+        T* sA = sbuf(buf);
+        T* sB = sA + BM * LDK;
+#pragma unroll
+        for (int i = 0; i < A_IT; ++i) {
+          const int c = tid + i * NT;
+          E::store(&sA[(c / GPR) * LDK + (c % GPR) * 8], ra[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < B_IT; ++i) {
+          const int c = tid + i * NT;
+          E::store(&sB[(c / GPR) * LDK + (c % GPR) * 8], rb[i]);
+        }
       }
     };
     auto step = [&](int cur, const G (&wa)[A_IT], const G (&wb)[B_IT], G (&la)[A_IT], G (&lb)[B_IT], int k_load) {
       load_set(k_load, la, lb);
       store_set(cur ^ 1, wa, wb);
+      if constexpr (F8) {
+        const unsigned char* sA = reinterpret_cast<const unsigned char*>(sbuf(cur));
+        const unsigned char* sB = sA + BM * LDKB;
+        const int fk = (lane >> 5) * 32;
+        i32x8_t fa[TM], fb[TN];
+        auto ld32 = [&](const unsigned char* p) {
+          const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(p);
+          const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(p + 16);
+          return (i32x8_t){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        };
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[i] = ld32(sA + (wm * WTM + i * 32 + frag_row) * LDKB + fk);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[j] = ld32(sB + (wn * WTN + j * 32 + frag_row) * LDKB + fk);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32_fp8_k64(fa[i], fb[j], acc[i][j]);
+        pipe_schedule<TM * TN, 2 * (TM + TN), TM * TN, A_IT + B_IT>();
+        __syncthreads();
+        return;
+      }
       const T* sA = sbuf(cur);
       const T* sB = sA + BM * LDK;
 #pragma unroll
@@ -466,6 +523,16 @@ VRS_CONV_KERNEL(vrs_conv_bf16_32x256_k32_g, bf16_t, 32, 256, 32, 1, 4, false)
 // 8 waves (512 threads), wave tile 128x64: half the global loads per MFMA of
 // the 4-wave tiles, for the large layers with Cout >= 256 and Cin % 64 == 0.
 VRS_CONV_KERNEL(vrs_conv_bf16_256x256_k64_a, bf16_t, 256, 256, 64, 2, 4, true)
+// fp8 e4m3 weights + e4m3-quantised bf16 activations (32x32x64 fp8 MFMA),
+// 64-deep steps (Cin % 64 == 0), bf16 outputs
+#define VRS_CONV_F8(NAME, BM, BN, WGM, WGN)                                                       \
+  extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void NAME(vrs_conv_args a) {          \
+    conv_body<bf16_t, BM, BN, 64, WGM, WGN, true, true>(a);                                      \
+  }
+VRS_CONV_F8(vrs_conv_fp8_128x128_k64_a, 128, 128, 2, 2)
+VRS_CONV_F8(vrs_conv_fp8_256x128_k64_a, 256, 128, 2, 2)
+VRS_CONV_F8(vrs_conv_fp8_128x256_k64_a, 128, 256, 2, 2)
+VRS_CONV_F8(vrs_conv_fp8_64x256_k64_a, 64, 256, 1, 4)
 // f32 (parity path, fp32 MFMA)
 VRS_CONV_KERNEL(vrs_conv_f32_128x128_k32_a, float, 128, 128, 32, 2, 2, true)
 VRS_CONV_KERNEL(vrs_conv_f32_128x128_k32_g, float, 128, 128, 32, 2, 2, false)

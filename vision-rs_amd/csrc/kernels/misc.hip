@@ -347,3 +347,27 @@ __device__ __forceinline__ void up_body(const vrs_up_args& a) {
 
 extern "C" __global__ __launch_bounds__(256) void vrs_upsample2x_bf16(vrs_up_args a) { up_body<bf16_t>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_upsample2x_f32(vrs_up_args a) { up_body<float>(a); }
+
+// ---------------------------------------------------------------------------
+// Calibration reduction for the fp8 path: max |x| of a bfloat16 NHWC view.
+// Lanes take 8-channel groups (16 bytes) in a grid-stride loop; the wave
+// maximum goes out with one atomic max on the float bits (non-negative
+// floats order like their bit patterns).
+extern "C" __global__ __launch_bounds__(256) void vrs_absmax_bf16(vrs_absmax_args a) {
+  const int cg = a.c >> 3;
+  const int64_t n = a.npix * cg;
+  float m = 0.f;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t p = i / cg;
+    const int g = (int)(i - p * cg);
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const bf16_t*>(a.x) + p * a.pitch + g * 8);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      m = fmaxf(m, fabsf(__uint_as_float(v[d] << 16)));
+      m = fmaxf(m, fabsf(__uint_as_float(v[d] & 0xffff0000u)));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if ((threadIdx.x & 63) == 0) atomicMax(a.out, __float_as_uint(m));
+}

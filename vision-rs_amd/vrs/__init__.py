@@ -21,7 +21,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 SO = os.path.join(LIB_DIR, "libvrs.so")
 
 VRS_OK = 0
-F32, BF16 = 0, 1
+F32, BF16, FP8 = 0, 1, 2
 ACT_NONE, ACT_SILU = 0, 1
 BLOCK_CONV, BLOCK_C3K2, BLOCK_C3K2_PSA, BLOCK_C2PSA, BLOCK_SPPF, BLOCK_PSA_ATTN, BLOCK_DETECT_BOX, BLOCK_YOLO26 = \
     1, 2, 3, 4, 5, 6, 7, 8
@@ -46,7 +46,7 @@ class Nhwc(C.Structure):
 
 class ConvDesc(C.Structure):
     _fields_ = [("k", C.c_int32), ("stride", C.c_int32), ("groups", C.c_int32), ("act", C.c_int32),
-                ("dtype", C.c_int32), ("tile", C.c_int32)]
+                ("dtype", C.c_int32), ("tile", C.c_int32), ("in_scale", C.c_float)]
 
 
 class PsaDesc(C.Structure):
@@ -81,6 +81,7 @@ SIGNATURES = {
     "vrs_ctx_destroy": (C.c_int, [_vp]),
     "vrs_conv2d": (C.c_int, [_vp, _P(ConvDesc), _P(Nhwc), _vp, _vp, _vp, _P(Nhwc), _P(Nhwc), _vp]),
     "vrs_pack_conv_weight": (_i64, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "vrs_pack_conv_weight_fp8": (_i64, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "vrs_bn_fold": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _i32, _vp, _vp]),
     "vrs_pack_input": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _P(Nhwc), _i32, _vp]),
     "vrs_unpack_output": (C.c_int, [_vp, _P(Nhwc), _i32, _vp, _vp]),
@@ -106,6 +107,9 @@ SIGNATURES = {
     "vrs_model_launch_name": (C.c_char_p, [_vp, _i32]),
     "vrs_model_launch_work": (C.c_int, [_vp, _i32, _P(C.c_double), _P(C.c_double)]),
     "vrs_model_run_launches": (C.c_int, [_vp, _i32, _i32, _vp]),
+    "vrs_model_calibrate": (C.c_int, [_vp, _vp, _vp]),
+    "vrs_model_num_convs": (C.c_int, [_vp]),
+    "vrs_model_conv_info": (C.c_int, [_vp, _i32, _P(C.c_char_p), _P(_i32), _P(_f32)]),
     "vrs_model_destroy": (C.c_int, [_vp]),
 }
 
@@ -181,9 +185,10 @@ class Context:
 
     # ---- single ops --------------------------------------------------------
     def conv2d(self, x, w, scale, shift, y, k, stride=1, groups=1, act=ACT_SILU, res=None, dtype=BF16,
-               stream=None, tile=TILE_AUTO):
-        """x, y, res: Nhwc views; w/scale/shift: device tensors."""
-        d = ConvDesc(k, stride, groups, act, dtype, tile)
+               stream=None, tile=TILE_AUTO, in_scale=1.0):
+        """x, y, res: Nhwc views; w/scale/shift: device tensors.  FP8: w from
+        pack_conv_weight_fp8, scale including weight scale * in_scale."""
+        d = ConvDesc(k, stride, groups, act, dtype, tile, in_scale)
         check(lib().vrs_conv2d(self.handle, C.byref(d), C.byref(x), _ptr(w), _ptr(scale), _ptr(shift),
                                C.byref(res) if res is not None else None, C.byref(y), _stream(stream)))
 
@@ -252,6 +257,20 @@ def pack_conv_weight(w_oihw, groups=1, cin_pad=None, dtype=BF16):
     out = np.empty(n, np.uint8)
     check(lib().vrs_pack_conv_weight(w.ctypes.data, cout, cin_g, k, groups, cin_pad, dtype, out.ctypes.data))
     return out
+
+
+def pack_conv_weight_fp8(w_oihw, cin_pad=None):
+    """Host e4m3 pack (dense only): (bytes [Cout][k][k][cin_pad], per-channel
+    weight scales absmax/448)."""
+    import numpy as np
+    w = np.ascontiguousarray(w_oihw, dtype=np.float32)
+    cout, cin, k, _ = w.shape
+    cin_pad = cin if cin_pad is None else cin_pad
+    n = check(lib().vrs_pack_conv_weight_fp8(None, cout, cin, k, cin_pad, None, None))
+    out = np.empty(n, np.uint8)
+    sc = np.empty(cout, np.float32)
+    check(lib().vrs_pack_conv_weight_fp8(w.ctypes.data, cout, cin, k, cin_pad, out.ctypes.data, sc.ctypes.data))
+    return out, sc
 
 
 def bn_fold(gamma, beta, mean, var, eps):
@@ -339,6 +358,19 @@ class Model:
             f, b = C.c_double(), C.c_double()
             check(lib().vrs_model_launch_work(self.handle, i, C.byref(f), C.byref(b)))
             out.append((f.value, b.value))
+        return out
+
+    def calibrate(self, x, stream=None):
+        """FP8 models: activation scales from one bf16 forward of x."""
+        check(lib().vrs_model_calibrate(self.handle, _ptr(x), _stream(stream)))
+
+    def conv_info(self):
+        """[(prefix, runs_on_fp8, in_scale)] per conv in build order."""
+        out = []
+        for i in range(check(lib().vrs_model_num_convs(self.handle))):
+            pre, f8, sc = C.c_char_p(), C.c_int32(), C.c_float()
+            check(lib().vrs_model_conv_info(self.handle, i, C.byref(pre), C.byref(f8), C.byref(sc)))
+            out.append((pre.value.decode(), bool(f8.value), sc.value))
         return out
 
     def run_launches(self, first, count, stream=None):
