@@ -605,14 +605,16 @@ int autotune_tiles(vrs_model* m) {
         continue;
       if ((rc = run(ls[0], s))) break;
       VRS_HIP(hipEventRecord(e0, s));
-      for (int it = 0; it < 3; ++it)
+      for (int it = 0; it < 5; ++it)
         if ((rc = run(ls[0], s))) break;
       if (rc) break;
       VRS_HIP(hipEventRecord(e1, s));
       VRS_HIP(hipEventSynchronize(e1));
       float ms = 0.f;
       VRS_HIP(hipEventElapsedTime(&ms, e0, e1));
-      if (ms < best) { best = ms; best_tile = t; }
+      // a later candidate must win by 2%: near-ties keep the earlier one, so
+      // the choice does not flip with timing noise from run to run
+      if (ms < 0.98f * best) { best = ms; best_tile = t; }
     }
     if (rc) break;
     (pass ? c.tile8 : c.tile) = best_tile;
