@@ -138,6 +138,16 @@ int64_t vrs_pack_conv_weight_fp8(const float* w_oihw, int32_t cout, int32_t cin,
 int vrs_bn_fold(const float* gamma, const float* beta, const float* mean, const float* var,
                 float eps, int32_t c, float* scale, float* shift);
 
+/* The stem layer model.0 = conv(3, c, 3, 2) (yolo26/mod.rs:126-195, blocks/
+ * conv.rs:31-46) straight from the NCHW float32 image, replacing
+ * vrs_pack_input + vrs_conv2d for the first layer: y (NHWC view of Cout <= 128
+ * channels, dtype) = act(scale * conv3x3s2(x) + shift).  Weights from
+ * vrs_pack_stem_weight: [ceil32(Cout)][32] with k = c*9 + ky*3 + kx (27 used). */
+int64_t vrs_pack_stem_weight(const float* w_oihw, int32_t cout, int32_t dtype, void* out);
+int vrs_conv_stem(vrs_ctx* ctx, const vrs_conv_desc* d, const float* x_nchw, int32_t n, int32_t c, int32_t h,
+                  int32_t w, const void* w_packed, const float* scale, const float* shift, const vrs_nhwc* y,
+                  void* stream);
+
 /* NCHW float32 -> NHWC dtype, zero-padding channels C..y->c-1 (C <= y->c < C+8). */
 int vrs_pack_input(vrs_ctx* ctx, const float* x_nchw, int32_t n, int32_t c, int32_t h, int32_t w,
                    const vrs_nhwc* y, int32_t dtype, void* stream);

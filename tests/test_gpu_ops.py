@@ -160,6 +160,30 @@ def test_conv2d_fp8_rejections():
         ctx().conv2d(vrs.nhwc(x), w, sc, sc, vrs.nhwc(y), 1, 1, 1, vrs.ACT_NONE, None, vrs.FP8, in_scale=0.3)
 
 
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("shape", [(2, 64, 40, 66), (1, 16, 18, 30), (1, 96, 10, 128), (1, 64, 640, 640),
+                                   (1, 32, 7, 9)])
+def test_conv_stem(dtype, shape):
+    """Fused stem (NCHW float32 image -> NHWC, 3x3 s2) against the oracle conv."""
+    import torch
+    n, cout, h, w = shape
+    rnd = rounder(dtype)
+    rng = np.random.default_rng(11 + cout)
+    x = rnd(rng.uniform(0, 1, (n, 3, h, w)).astype(np.float32))
+    wt = rnd((rng.standard_normal((cout, 3, 3, 3)) * np.sqrt(2.0 / 27)).astype(np.float32))
+    scale = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    ref = oracle.affine_act(oracle.conv2d(x, wt, 2, 1), scale, shift, 1)
+    ho, wo = ref.shape[2], ref.shape[3]
+    yt = torch.full((n, ho, wo, cout + 16), 7.0, dtype=tdtype(dtype), device="cuda")
+    ctx().conv_stem(dev(x), dev(vrs.pack_stem_weight(wt, dtype)), dev(scale), dev(shift), vrs.nhwc(yt, cout, 8),
+                    vrs.ACT_SILU, dtype)
+    torch.cuda.synchronize()
+    assert rel_err(from_nhwc(yt, cout, 8), ref, FLOOR[dtype]) < TOL[dtype]
+    rest = torch.cat([yt[..., :8], yt[..., 8 + cout:]], -1).float()
+    assert torch.all(rest == 7.0)
+
+
 def test_conv2d_tile_rejections():
     import torch
     x = torch.zeros((1, 4, 4, 48), dtype=torch.bfloat16, device="cuda")

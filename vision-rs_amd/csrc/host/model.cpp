@@ -49,6 +49,7 @@ struct ConvStep {
   int out_idx = -1;
   int64_t out_off = 0, sb = 0, sp = 0, sc = 0;
   int tile = VRS_TILE_AUTO;  // chosen at finalize (autotune) for dense NHWC convs
+  bool stem = false;         // fused input conv: reads the NCHW float32 image (no x buffer)
   // device parameters (finalize)
   void* w = nullptr;
   float* scale = nullptr;
@@ -63,7 +64,7 @@ struct ConvStep {
 };
 
 struct Step {
-  enum Type { PACK, CONV, POOL, UP, ATTN, UNPACK } type;
+  enum Type { PACK, CONV, POOL, UP, ATTN, UNPACK, STEM } type;
   int conv = -1;      // CONV / ATTN (the PE conv's parameters)
   V a, b;             // PACK: b = dest; POOL: a; UP: a -> b; ATTN: a = qkv, b = out; UNPACK: a
   int heads = 0;
@@ -303,6 +304,16 @@ class Builder {
     m_->out_dims = {{m_->batch, (int32_t)(4 * A)}, {m_->batch, (int32_t)(nc * A)}};
   }
 
+  // model.0 straight from the NCHW float32 image (no packed input buffer)
+  void stem(const std::string& pre, V y) {
+    const int i = conv_common(pre, V{-1, 0, 3}, y.c, 3, 2, CK_BN_SILU, false);
+    m_->convs[i].y = y;
+    m_->convs[i].stem = true;
+    Step st;
+    st.type = Step::STEM; st.conv = i;
+    m_->steps.push_back(st);
+  }
+
   V input(int c_real) {
     V in = alloc(m_->in_h, m_->in_w, (c_real + 7) / 8 * 8);
     real_c_[in.buf] = c_real;
@@ -320,6 +331,7 @@ class Builder {
   }
 
   int real_cin(V x) const {
+    if (x.buf < 0) return x.c;
     auto it = real_c_.find(x.buf);
     return (it != real_c_.end() && x.c_off == 0 && x.c == m_->bufs[x.buf].pitch) ? it->second : x.c;
   }
@@ -426,9 +438,8 @@ int build(vrs_model* m) {
       const int c0 = ch(64), c1 = ch(128), c2 = ch(256), c3 = ch(512), c4 = ch(1024);
       const int n = round_half_away(std::max(2 * dep, 1.0f));  // rep(2, d), mod.rs:111-117
       const int H = m->in_h, W = m->in_w;
-      V in = b.input(3);
       V x0 = b.alloc(H / 2, W / 2, c0);
-      b.conv("model.0", in, x0, 3, 2, CK_BN_SILU);
+      b.stem("model.0", x0);
       V x1 = b.alloc(H / 4, W / 4, c1);
       b.conv("model.1", x0, x1, 3, 2, CK_BN_SILU);
       V x2 = b.alloc(H / 4, W / 4, c2);
@@ -534,6 +545,13 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         for (size_t i = conv_first; i < ls.size(); ++i) labels.push_back(label + ":" + ls[i].name);
         continue;
       }
+      case Step::STEM: {
+        const ConvStep& c = m->convs[st.conv];
+        rc = prep_stem(m->ctx, VRS_ACT_SILU, act_dt(m), x, m->batch, m->in_h, m->in_w, c.w, c.scale, c.shift,
+                       c.cout, view_of(m, c.y), ls);
+        label = c.pre;
+        break;
+      }
       case Step::POOL:
         rc = prep_pool(m->ctx, view_of(m, st.a), act_dt(m), ls);
         label = "sppf.pool";
@@ -586,7 +604,7 @@ int autotune_tiles(vrs_model* m) {
   int rc = VRS_OK;
   for (ConvStep& c : m->convs)
    for (int pass = 0; pass < (c.f8 ? 2 : 1); ++pass) {
-    if (c.dw || c.out_idx >= 0 || c.y.buf < 0) continue;
+    if (c.dw || c.stem || c.out_idx >= 0 || c.y.buf < 0) continue;
     const int dt = pass ? VRS_FP8 : act_dt(m);
     const std::vector<int> cand = conv_tile_candidates(c.cout, c.cin, dt);
     if (cand.size() < 2) continue;
@@ -710,10 +728,13 @@ int vrs_model_finalize(vrs_model* m) {
     const int groups = c.dw ? c.cout : 1;
     const int cin_pad = c.dw ? 1 : c.cin;
     const int pdt = act_dt(m);
-    const int64_t bytes = vrs_pack_conv_weight(nullptr, c.cout, cin_g, c.k, groups, cin_pad, pdt, nullptr);
+    const int64_t bytes = c.stem ? vrs_pack_stem_weight(nullptr, c.cout, pdt, nullptr)
+                                 : vrs_pack_conv_weight(nullptr, c.cout, cin_g, c.k, groups, cin_pad, pdt, nullptr);
     if (bytes < 0) return (int)bytes;
     std::vector<uint8_t> packed((size_t)bytes);
-    const int64_t r = vrs_pack_conv_weight(w->host.data(), c.cout, cin_g, c.k, groups, cin_pad, pdt, packed.data());
+    const int64_t r =
+        c.stem ? vrs_pack_stem_weight(w->host.data(), c.cout, pdt, packed.data())
+               : vrs_pack_conv_weight(w->host.data(), c.cout, cin_g, c.k, groups, cin_pad, pdt, packed.data());
     if (r < 0) return (int)r;
     int rc;
     if ((rc = dev_upload(m, packed.data(), packed.size(), &c.w))) return rc;
@@ -722,7 +743,7 @@ int vrs_model_finalize(vrs_model* m) {
     c.scale = static_cast<float*>(p);
     if ((rc = dev_upload(m, shift.data(), shift.size() * 4, &p))) return rc;
     c.shift = static_cast<float*>(p);
-    c.f8 = m->dtype == VRS_FP8 && !c.dw && c.cin % 64 == 0 && cin_g == c.cin;
+    c.f8 = m->dtype == VRS_FP8 && !c.dw && !c.stem && c.cin % 64 == 0 && cin_g == c.cin;
     if (c.f8) {  // e4m3 copy of the weights; the bf16 one serves calibration
       std::vector<uint8_t> q((size_t)vrs_pack_conv_weight_fp8(nullptr, c.cout, cin_g, c.k, c.cin, nullptr, nullptr));
       std::vector<float> ws(c.cout);

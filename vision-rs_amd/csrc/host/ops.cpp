@@ -124,6 +124,35 @@ int64_t vrs_pack_conv_weight_fp8(const float* w, int32_t cout, int32_t cin, int3
   return bytes;
 }
 
+int64_t vrs_pack_stem_weight(const float* w, int32_t cout, int32_t dtype, void* out) {
+  if (cout < 1 || cout > 128) return fail(VRS_EINVAL, "pack_stem_weight: cout %d (1..128)", cout);
+  if (dtype != VRS_BF16 && dtype != VRS_F32) return fail(VRS_EUNSUPPORTED, "pack_stem_weight: dtype");
+  const int cpad = (cout + 31) / 32 * 32;
+  const int64_t bytes = (int64_t)cpad * 32 * (int64_t)elt_size(dtype);
+  if (!out) return bytes;
+  if (!w) return fail(VRS_EINVAL, "pack_stem_weight: null weights");
+  for (int co = 0; co < cpad; ++co)
+    for (int k = 0; k < 32; ++k) {
+      // k = c*9 + ky*3 + kx is exactly the OIHW offset within one output channel
+      const float v = (co < cout && k < 27) ? w[co * 27 + k] : 0.f;
+      const int64_t o = (int64_t)co * 32 + k;
+      if (dtype == VRS_F32) static_cast<float*>(out)[o] = v;
+      else static_cast<uint16_t*>(out)[o] = host_f2bf(v);
+    }
+  return bytes;
+}
+
+int vrs_conv_stem(vrs_ctx* ctx, const vrs_conv_desc* d, const float* x, int32_t n, int32_t c, int32_t h, int32_t w,
+                  const void* wp, const float* scale, const float* shift, const vrs_nhwc* y, void* stream) {
+  if (!ctx || !d || !x || !y) return fail(VRS_EINVAL, "vrs_conv_stem: null argument");
+  if (c != 3 || d->k != 3 || d->stride != 2 || d->groups != 1)
+    return fail(VRS_EUNSUPPORTED, "vrs_conv_stem: 3 channels, 3x3, stride 2 only");
+  if (d->act != VRS_ACT_NONE && d->act != VRS_ACT_SILU) return fail(VRS_EINVAL, "vrs_conv_stem: act %d", d->act);
+  std::vector<Launch> ls;
+  int rc = prep_stem(ctx, d->act, d->dtype, x, n, h, w, wp, scale, shift, y->c, *y, ls);
+  return rc ? rc : run_all(ls, stream);
+}
+
 int vrs_bn_fold(const float* gamma, const float* beta, const float* mean, const float* var, float eps, int32_t c,
                 float* scale, float* shift) {
   if (!gamma || !beta || !mean || !var || !scale || !shift || c <= 0) return fail(VRS_EINVAL, "vrs_bn_fold: bad args");

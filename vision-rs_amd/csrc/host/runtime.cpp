@@ -427,6 +427,37 @@ int prep_absmax(vrs_ctx* ctx, const vrs_nhwc& x, unsigned* out, std::vector<Laun
   return VRS_OK;
 }
 
+int prep_stem(vrs_ctx* ctx, int act, int dtype, const float* x, int n, int h, int w, const void* wp,
+              const float* scale, const float* shift, int cout, const vrs_nhwc& y, std::vector<Launch>& ls) {
+  int rc;
+  if ((rc = check_dtype(dtype))) return rc;
+  if (!x || !wp || !scale || !shift) return fail(VRS_EINVAL, "stem: null argument");
+  if (reinterpret_cast<uintptr_t>(x) % 16) return fail(VRS_EBADSHAPE, "stem: image not 16-byte aligned");
+  if ((rc = check_view(y, "stem output", 4))) return rc;
+  const int ho = out_size(h, 3, 2), wo = out_size(w, 3, 2);
+  if (y.n != n || y.h != ho || y.w != wo || y.c != cout)
+    return fail(VRS_EBADSHAPE, "stem: output view %dx%dx%dx%d for input %dx3x%dx%d, cout %d", y.n, y.h, y.w, y.c, n,
+                h, w, cout);
+  if (cout < 8 || cout > 128 || cout % 8) return fail(VRS_EUNSUPPORTED, "stem: cout %d (8..128, multiple of 8)", cout);
+  if (y.pitch % 8 || y.c_off % 8) return fail(VRS_EBADSHAPE, "stem: output pitch/offset must be multiples of 8");
+  vrs_stem_args a{};
+  a.x = x; a.w = wp; a.scale = scale; a.shift = shift; a.y = const_cast<void*>(at(y, dtype));
+  a.N = n; a.H = h; a.W = w; a.Ho = ho; a.Wo = wo; a.cout = cout; a.cout_pad = (cout + 31) / 32 * 32;
+  a.y_pitch = y.pitch; a.act = act;
+  a.segs = (wo + 63) / 64;
+  const int64_t wgs = (int64_t)n * ((ho + 1) / 2) * a.segs;   // 2 output rows x 64 pixels each
+  if (wgs >= (1ll << 31)) return fail(VRS_EBADSHAPE, "stem: grid too large");
+  char name[32];
+  snprintf(name, sizeof name, "vrs_stem_%s", dsuffix(dtype));
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  ls.push_back(make_launch(name, f, dim3((unsigned)wgs), dim3(256), 0, a));
+  const double es = (double)elt_size(dtype);
+  ls.back().flops = 2.0 * n * ho * wo * (double)cout * 27;
+  ls.back().bytes = (double)n * 3 * h * w * 4 + (double)n * ho * wo * cout * es + (double)cout * 27 * es + 8.0 * cout;
+  return VRS_OK;
+}
+
 }  // namespace vrs
 
 using namespace vrs;

@@ -72,6 +72,10 @@ struct ConvSpec {
   int tile = VRS_TILE_AUTO;  // dense conv tile (VRS_TILE_*)
   float in_scale = 1.f;      // VRS_FP8: activation quantisation step (power of two)
 };
+// stem conv (3x3 s2, Cin 3) straight from the NCHW float32 image; weights
+// packed by vrs_pack_stem_weight
+int prep_stem(vrs_ctx* ctx, int act, int dtype, const float* x, int n, int h, int w, const void* wp,
+              const float* scale, const float* shift, int cout, const vrs_nhwc& y, std::vector<Launch>& ls);
 // max |x| of a bfloat16 NHWC view into *out (float bits; caller zeroes it)
 int prep_absmax(vrs_ctx* ctx, const vrs_nhwc& x, unsigned* out, std::vector<Launch>& ls);
 // float -> e4m3 (OCP, max 448) with round-to-nearest-even; |v| > 448 saturates

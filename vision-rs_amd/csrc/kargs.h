@@ -161,4 +161,18 @@ typedef struct {
   int32_t c, pitch;
 } vrs_absmax_args;
 
+
+/* Stem conv straight from the NCHW float32 image: 3x3, stride 2, pad 1,
+ * Cin = 3 (K = 27 padded to 32, k = c*9 + ky*3 + kx), Cout <= 128, folded BN
+ * + SiLU, NHWC output of the element type. */
+typedef struct {
+  const float* x;
+  const void* w;       /* [cout_pad][32] element type */
+  const float* scale;
+  const float* shift;
+  void* y;             /* view base (pixel 0, first channel of the view) */
+  int32_t N, H, W, Ho, Wo, cout, cout_pad, y_pitch, act;
+  int32_t segs;        /* 64-pixel segments per output row */
+} vrs_stem_args;
+
 #endif

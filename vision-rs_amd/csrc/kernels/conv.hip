@@ -576,3 +576,134 @@ __device__ __forceinline__ void unpack_body(const vrs_pack_args& a) {
 
 extern "C" __global__ __launch_bounds__(256) void vrs_unpack_nchw_bf16(vrs_pack_args a) { unpack_body<bf16_t>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_unpack_nchw_f32(vrs_pack_args a) { unpack_body<float>(a); }
+
+// ---------------------------------------------------------------------------
+// Stem (model.0 = conv(3, c, 3, 2), yolo26/mod.rs:126-195) fused with the
+// input layout change.  A workgroup owns 2 output rows x 64 output pixels of
+// one image: it stages the 5 input rows x 132 columns x 3 channels it needs
+// (NCHW f32: each channel row is a contiguous run, loaded as float4 from a
+// 16-byte aligned start), builds the 128 x 32 im2col tile (k = c*9 + ky*3 +
+// kx, 27 real + 5 zero) in LDS, runs it through the 32x32x16 MFMA against the
+// [cout_pad][32] weights, and stages the NHWC result in LDS so every lane
+// stores whole 16-byte channel chunks.  Replaces the separate NCHW->NHWC pack
+// (which padded 3 channels to 8 and wrote 2.7x the input bytes) and the
+// padded-Cin conv.
+template <typename T>
+__device__ __forceinline__ void stem_body(const vrs_stem_args& a) {
+  using E = Elt<T>;
+  using G = typename E::group;
+  constexpr int PX = 64, RO = 2, RI = 2 * RO + 1;      // pixels per row, output rows, input rows
+  constexpr int CW = 2 * PX + 4, NQ = CW / 4;           // staged columns (float4 aligned)
+  constexpr int KP = 32 + 8;                            // im2col row (+pad)
+  constexpr int OP = 128 + 16 / (int)sizeof(T);         // output staging row (channels + pad)
+  // the output staging reuses the input and im2col space (both dead by then)
+  constexpr int IN_BYTES = 3 * RI * CW * 4, SB_BYTES = RO * PX * KP * (int)sizeof(T);
+  constexpr int SO_BYTES = RO * PX * OP * (int)sizeof(T);
+  constexpr int LDS_BYTES = IN_BYTES + SB_BYTES > SO_BYTES ? IN_BYTES + SB_BYTES : SO_BYTES;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
+  float (*sin_)[RI][CW] = reinterpret_cast<float (*)[RI][CW]>(lds);
+  T* sb = reinterpret_cast<T*>(lds + IN_BYTES);
+  T* so = reinterpret_cast<T*>(lds);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int wg = blockIdx.x;
+  const int seg = wg % a.segs; wg /= a.segs;
+  const int rp = (a.Ho + RO - 1) / RO;
+  const int oyp = wg % rp;
+  const int b = wg / rp;
+  const int ox0 = seg * PX, oy0 = oyp * RO;
+  const int64_t plane = (int64_t)a.H * a.W;
+  const float* xb = a.x + (int64_t)b * 3 * plane;
+  const int x0 = 2 * ox0 - 4;                           // staged column 0 (multiple of 4)
+  const bool vec = (a.W & 3) == 0;                      // rows 16-byte aligned
+  for (int i = tid; i < 3 * RI * NQ; i += 256) {
+    const int c = i / (RI * NQ), r = (i / NQ) % RI, q = i % NQ;
+    const int iy = 2 * oy0 - 1 + r, ix = x0 + 4 * q;
+    f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+    if ((unsigned)iy < (unsigned)a.H) {
+      const float* row = xb + c * plane + (int64_t)iy * a.W;
+      if (vec && ix >= 0 && ix + 3 < a.W) {
+        v = *reinterpret_cast<const f32x4_t*>(row + ix);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((unsigned)(ix + e) < (unsigned)a.W) v[e] = row[ix + e];
+      }
+    }
+    *reinterpret_cast<f32x4_t*>(&sin_[c][r][4 * q]) = v;
+  }
+  __syncthreads();
+  {
+    // a thread keeps one k (256 % 32 == 0): its (c, ky, kx) offset is fixed
+    const int k = tid & 31;
+    const int c = k / 9, t = k - c * 9, ky = t / 3, kx = t - ky * 3;
+    const float* src = &sin_[k < 27 ? c : 0][k < 27 ? ky : 0][k < 27 ? kx + 3 : 0];
+#pragma unroll 4
+    for (int px = tid >> 5; px < RO * PX; px += 256 / 32) {   // px: row-major over (output row, pixel)
+      const int ro = px / PX, p = px - ro * PX;
+      // column 2*(ox0+p) - 1 + kx relative to x0; input row 2*(oy0+ro) - 1 + ky
+      const float v = k < 27 ? src[2 * ro * CW + 2 * p] : 0.f;
+      sb[px * KP + k] = E::from_f(v);
+    }
+  }
+  __syncthreads();
+  const T* w = reinterpret_cast<const T*>(a.w);
+  const int pt_n = RO * PX / 32;
+  const int tiles = (a.cout_pad / 32) * pt_n;
+  const int hq = lane >> 5;
+  constexpr int MAXT = (128 / 32) * (RO * PX / 32) / 4;   // tiles per wave at cout_pad = 128
+  f32x16_t acc[MAXT];
+#pragma unroll
+  for (int j = 0; j < MAXT; ++j) {   // all MFMAs first: the staging below overwrites sb
+    const int t = wave + 4 * j;
+    if (t >= tiles) break;
+    const int ct = t / pt_n, pt = t % pt_n;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const G fa = E::load(w + (int64_t)(ct * 32 + (lane & 31)) * 32 + ks * 16 + hq * 8);
+      const G fb = E::load(&sb[(pt * 32 + (lane & 31)) * KP + ks * 16 + hq * 8]);
+      acc[j] = mfma32_k16(fa, fb, acc[j]);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < MAXT; ++j) {
+    const int t = wave + 4 * j;
+    if (t >= tiles) break;
+    const int ct = t / pt_n, pt = t % pt_n;
+    const int px = pt * 32 + (lane & 31);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int co = ct * 32 + g * 8 + hq * 4;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int c = co + r < a.cout ? co + r : a.cout - 1;
+        float u = acc[j][g * 4 + r] * a.scale[c] + a.shift[c];
+        if (a.act == VRS_ACT_SILU) u = silu_t<T>(u);
+        v[r] = u;
+      }
+      T* sp = so + px * OP + co;
+      if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<u32x2_t*>(sp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      } else {
+        *reinterpret_cast<f32x4_t*>(sp) = (f32x4_t){v[0], v[1], v[2], v[3]};
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int EPC = 16 / (int)sizeof(T);              // elements per 16-byte chunk
+  const int cpp = a.cout / EPC;                         // chunks per pixel (cout % 8 == 0, checked)
+  for (int i = tid; i < RO * PX * cpp; i += 256) {
+    const int px = i / cpp, part = i - px * cpp;
+    const int ro = px / PX, p = px % PX;
+    const int oy = oy0 + ro, ox = ox0 + p;
+    if (oy >= a.Ho || ox >= a.Wo) continue;
+    T* yp = reinterpret_cast<T*>(a.y) + (((int64_t)b * a.Ho + oy) * a.Wo + ox) * a.y_pitch + part * EPC;
+    *reinterpret_cast<u32x4_t*>(yp) = *reinterpret_cast<const u32x4_t*>(so + px * OP + part * EPC);
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void vrs_stem_bf16(vrs_stem_args a) { stem_body<bf16_t>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_stem_f32(vrs_stem_args a) { stem_body<float>(a); }

@@ -82,6 +82,8 @@ SIGNATURES = {
     "vrs_conv2d": (C.c_int, [_vp, _P(ConvDesc), _P(Nhwc), _vp, _vp, _vp, _P(Nhwc), _P(Nhwc), _vp]),
     "vrs_pack_conv_weight": (_i64, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "vrs_pack_conv_weight_fp8": (_i64, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "vrs_pack_stem_weight": (_i64, [_vp, _i32, _i32, _vp]),
+    "vrs_conv_stem": (C.c_int, [_vp, _P(ConvDesc), _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _P(Nhwc), _vp]),
     "vrs_bn_fold": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _i32, _vp, _vp]),
     "vrs_pack_input": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _P(Nhwc), _i32, _vp]),
     "vrs_unpack_output": (C.c_int, [_vp, _P(Nhwc), _i32, _vp, _vp]),
@@ -192,6 +194,13 @@ class Context:
         check(lib().vrs_conv2d(self.handle, C.byref(d), C.byref(x), _ptr(w), _ptr(scale), _ptr(shift),
                                C.byref(res) if res is not None else None, C.byref(y), _stream(stream)))
 
+    def conv_stem(self, x_nchw, w, scale, shift, y, act=ACT_SILU, dtype=BF16, stream=None):
+        """model.0 (3x3 s2, 3 channels) from the NCHW float32 image into NHWC view y."""
+        n, c, h, w_ = x_nchw.shape
+        d = ConvDesc(3, 2, 1, act, dtype, TILE_AUTO, 1.0)
+        check(lib().vrs_conv_stem(self.handle, C.byref(d), _ptr(x_nchw), n, c, h, w_, _ptr(w), _ptr(scale),
+                                  _ptr(shift), C.byref(y), _stream(stream)))
+
     def pack_input(self, x_nchw, y, dtype, stream=None):
         n, c, h, w = x_nchw.shape
         check(lib().vrs_pack_input(self.handle, _ptr(x_nchw), n, c, h, w, C.byref(y), dtype, _stream(stream)))
@@ -256,6 +265,16 @@ def pack_conv_weight(w_oihw, groups=1, cin_pad=None, dtype=BF16):
     n = check(lib().vrs_pack_conv_weight(None, cout, cin_g, k, groups, cin_pad, dtype, None))
     out = np.empty(n, np.uint8)
     check(lib().vrs_pack_conv_weight(w.ctypes.data, cout, cin_g, k, groups, cin_pad, dtype, out.ctypes.data))
+    return out
+
+
+def pack_stem_weight(w_oihw, dtype=BF16):
+    """Host pack of the stem weights [Cout][3][3][3] -> [ceil32(Cout)][32] (k = c*9 + ky*3 + kx)."""
+    import numpy as np
+    w = np.ascontiguousarray(w_oihw, dtype=np.float32)
+    n = check(lib().vrs_pack_stem_weight(None, w.shape[0], dtype, None))
+    out = np.empty(n, np.uint8)
+    check(lib().vrs_pack_stem_weight(w.ctypes.data, w.shape[0], dtype, out.ctypes.data))
     return out
 
 
