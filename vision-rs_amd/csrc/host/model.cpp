@@ -50,6 +50,7 @@ struct ConvStep {
   int64_t out_off = 0, sb = 0, sp = 0, sc = 0;
   int tile = VRS_TILE_AUTO;  // chosen at finalize (autotune) for dense NHWC convs
   bool stem = false;         // fused input conv: reads the NCHW float32 image (no x buffer)
+  int cin_real = 0;          // unpadded input channels (work accounting)
   // device parameters (finalize)
   void* w = nullptr;
   float* scale = nullptr;
@@ -135,6 +136,7 @@ class Builder {
     ConvStep c;
     c.pre = pre; c.kind = kind; c.dw = dw; c.k = k; c.s = s; c.cin = x.c; c.cout = cout; c.x = x;
     const int cin_g = dw ? 1 : real_cin(x);
+    c.cin_real = real_cin(x);
     if (kind == CK_PLAIN) {
       add_param(J(pre, "weight"), {cout, cin_g, k, k});
       add_param(J(pre, "bias"), {cout});
@@ -513,7 +515,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         ConvSpec cs;
         cs.k = c.k; cs.stride = c.s; cs.dtype = act_dt(m); cs.depthwise = c.dw;
         cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
-        cs.cin_real = c.cin == m->bufs[c.x.buf].pitch && c.x.buf == 0 ? m->in_c : 0;
+        cs.cin_real = c.cin_real != c.cin ? c.cin_real : 0;
         cs.tile = c.tile;
         const void* w = c.w;
         const float* scale = c.scale;
