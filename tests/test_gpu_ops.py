@@ -162,7 +162,7 @@ def test_conv2d_fp8_rejections():
 
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("shape", [(2, 64, 40, 66), (1, 16, 18, 30), (1, 96, 10, 128), (1, 64, 640, 640),
-                                   (1, 32, 7, 9)])
+                                   (1, 32, 7, 9), (1, 128, 12, 20), (3, 40, 130, 132)])
 def test_conv_stem(dtype, shape):
     """Fused stem (NCHW float32 image -> NHWC, 3x3 s2) against the oracle conv."""
     import torch

@@ -427,6 +427,18 @@ int prep_absmax(vrs_ctx* ctx, const vrs_nhwc& x, unsigned* out, std::vector<Laun
   return VRS_OK;
 }
 
+// Resident workgroups per CU of a 256-thread kernel, from its register and
+// LDS use (CDNA4: 4 SIMDs x 512 registers per lane, 160 KB LDS per CU).
+static int resident_wgs(hipFunction_t f) {
+  int vgpr = 0, lds = 0;
+  hipFuncGetAttribute(&lds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, f);
+  hipFuncGetAttribute(&vgpr, HIP_FUNC_ATTRIBUTE_NUM_REGS, f);
+  int by_reg = vgpr > 0 ? 512 / ((vgpr + 7) / 8 * 8) : 1;   // waves per SIMD = groups per CU
+  int by_lds = lds > 0 ? (160 * 1024) / lds : 8;
+  int n = std::min(std::min(by_reg, by_lds), 8);
+  return n < 1 ? 1 : n;
+}
+
 int prep_stem(vrs_ctx* ctx, int act, int dtype, const float* x, int n, int h, int w, const void* wp,
               const float* scale, const float* shift, int cout, const vrs_nhwc& y, std::vector<Launch>& ls) {
   int rc;
@@ -445,12 +457,17 @@ int prep_stem(vrs_ctx* ctx, int act, int dtype, const float* x, int n, int h, in
   a.N = n; a.H = h; a.W = w; a.Ho = ho; a.Wo = wo; a.cout = cout; a.cout_pad = (cout + 31) / 32 * 32;
   a.y_pitch = y.pitch; a.act = act;
   a.segs = (wo + 63) / 64;
-  const int64_t wgs = (int64_t)n * ((ho + 1) / 2) * a.segs;   // 2 output rows x 64 pixels each
-  if (wgs >= (1ll << 31)) return fail(VRS_EBADSHAPE, "stem: grid too large");
+  const int64_t items = (int64_t)n * ((ho + 1) / 2) * a.segs;   // 2 output rows x 64 pixels each
+  if (items >= (1ll << 31)) return fail(VRS_EBADSHAPE, "stem: grid too large");
+  // persistent grid: the resident workgroups loop over the items
+  if ((int64_t)3 * h * w * 4 >= (1ll << 31) || (int64_t)ho * wo * y.pitch * (int64_t)elt_size(dtype) >= (1ll << 31))
+    return fail(VRS_EBADSHAPE, "stem: one image (in or out) must be under 2 GiB");
   char name[32];
-  snprintf(name, sizeof name, "vrs_stem_%s", dsuffix(dtype));
+  snprintf(name, sizeof name, "vrs_stem_%s_c%d%s", dsuffix(dtype), a.cout_pad / 32, w % 4 ? "_u" : "");
   hipFunction_t f;
   if ((rc = get_fn(ctx, name, &f))) return rc;
+  // persistent grid: the resident workgroups loop over the items
+  const int64_t wgs = std::min<int64_t>(items, (int64_t)resident_wgs(f) * (ctx->num_cu > 0 ? ctx->num_cu : 256));
   ls.push_back(make_launch(name, f, dim3((unsigned)wgs), dim3(256), 0, a));
   const double es = (double)elt_size(dtype);
   ls.back().flops = 2.0 * n * ho * wo * (double)cout * 27;

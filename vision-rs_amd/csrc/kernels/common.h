@@ -56,6 +56,42 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 }
 constexpr uint32_t kOOB = 0x80000000u;  // an offset every resource here rejects
 
+// Scalar (SMEM) buffer load of 8 dwords at a wave-uniform byte offset; dwords
+// at or past the resource's byte size read 0.
+typedef float f32x8_hw __attribute__((ext_vector_type(8)));
+typedef int i32x4_hw __attribute__((ext_vector_type(4)));
+__device__ f32x8_hw vrs_s_buffer_load_x8(i32x4_hw rsrc, int offset, int aux) __asm("llvm.amdgcn.s.buffer.load.v8f32");
+
+// Per-channel epilogue constants (folded BN scale or shift, n channels) read
+// through the scalar cache: one wave-uniform 8-channel group cb..cb+7 per
+// load, of which lanes 0-31 keep cb..cb+3 and lanes 32-63 cb+4..cb+7 -- the
+// channels of a 32x32 MFMA accumulator quad (hq = lane >> 5).  Channels past
+// n read 0.  Per-lane vector loads of the same values cost one vector memory
+// instruction per value and made the epilogue the busiest part of the
+// memory pipeline.
+struct ChanConst {
+  i32x4_hw r;
+  __device__ __forceinline__ ChanConst(const float* p, int n) {
+    const uint64_t b = reinterpret_cast<uint64_t>(p);
+    r = (i32x4_hw){(int)(uint32_t)b, (int)(uint32_t)(b >> 32), n * 4, 0x00020000};
+  }
+  // hi_mask: all ones on lanes 32-63, zero on lanes 0-31 (see upper_half_mask)
+  __device__ __forceinline__ void quad(int cb, uint32_t hi_mask, float (&out)[4]) const {
+    const f32x8_hw s = vrs_s_buffer_load_x8(r, __builtin_amdgcn_readfirstlane(cb) * 4, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)   // one v_bfi_b32 per value
+      out[e] = __uint_as_float((__float_as_uint(s[4 + e]) & hi_mask) | (__float_as_uint(s[e]) & ~hi_mask));
+  }
+};
+// Lane mask for ChanConst::quad, opaque to the optimiser so the per-lane
+// choice stays a bit select (as a known 0/1 choice it is rewritten into a
+// dynamic vector index: a compare/select chain per value).
+__device__ __forceinline__ uint32_t upper_half_mask() {
+  uint32_t m = (threadIdx.x & 32) ? 0xffffffffu : 0u;
+  asm volatile("" : "+v"(m));
+  return m;
+}
+
 // ---- element traits --------------------------------------------------------
 // A "group" is 8 consecutive elements along K: the unit one lane feeds into
 // the 16x16x32 MFMA step (bf16: one 16-byte register quad; f32: two quads).
@@ -75,6 +111,11 @@ template <> struct Elt<bf16_t> {
   }
   static __device__ __forceinline__ float to_f(bf16_t v) { return bf2f(v); }
   static __device__ __forceinline__ bf16_t from_f(float v) { return f2bf(v); }
+  static __device__ __forceinline__ group from_f8(const float (&v)[8]) {
+    group g;
+    g.v = (u32x4_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+    return g;
+  }
 };
 
 template <> struct Elt<float> {
@@ -93,6 +134,12 @@ template <> struct Elt<float> {
   }
   static __device__ __forceinline__ group zero() {
     group g; g.lo = (u32x4_t){0, 0, 0, 0}; g.hi = g.lo; return g;
+  }
+  static __device__ __forceinline__ group from_f8(const float (&v)[8]) {
+    group g;
+    g.lo = (u32x4_t){__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+    g.hi = (u32x4_t){__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])};
+    return g;
   }
   static __device__ __forceinline__ void store(float* p, const group& g) {
     *reinterpret_cast<u32x4_t*>(p) = g.lo;

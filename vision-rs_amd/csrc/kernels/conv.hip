@@ -240,7 +240,9 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
     // k+1 (loaded during step k-1) and is written to buffer (k+1)&1 while
     // the MFMAs of step k run; set k&1 receives the loads of step k+2.  Loads
     // at k0 >= K read zeros (out-of-range buffer offsets), so the body has no
-    // branches and an odd step count runs one all-zero step.
+    // branches; an odd step count ends with one more copy of the step (the
+    // 8-wave tile, which has no registers to spare for it, runs one all-zero
+    // step instead).
     G ra0[A_IT], rb0[B_IT], ra1[A_IT], rb1[B_IT];
     auto load_set = [&](int k0, G (&ra)[A_IT], G (&rb)[B_IT]) {
       const uint32_t dead = k0 < a.K ? 0u : kOOB;
@@ -343,10 +345,12 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
     load_set(BK, ra1, rb1);
     store_set(0, ra0, rb0);
     __syncthreads();
-    for (int kt = 0; kt < nk; kt += 2) {
+    constexpr bool TAIL = WGM * WGN == 4;
+    for (int kt = 0; TAIL ? kt + 1 < nk : kt < nk; kt += 2) {
       step(0, ra1, rb1, ra0, rb0, (kt + 2) * BK);
       step(1, ra0, rb0, ra1, rb1, (kt + 3) * BK);
     }
+    if (TAIL && (nk & 1)) step(0, ra1, rb1, ra0, rb0, (nk + 1) * BK);
   } else {
   load_tiles(0);
   store_tiles(0);
@@ -380,6 +384,8 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   // g*4 + r of MFMA tile (i, j) is channel i*32 + g*8 + hq*4 + r of pixel
   // j*32 + (lane & 31), hq = lane >> 5.
   const int hq = lane >> 5;
+  const ChanConst c_scale(a.scale, a.Cout), c_shift(a.shift, a.Cout);
+  const uint32_t hmask = upper_half_mask();
   if (a.stage) {
     // Staged store: every wave writes its (WTN pixel x WTM channel) tile to
     // LDS, then stores whole 16-byte channel chunks per lane, so consecutive
@@ -393,12 +399,8 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
         const int cl = i * 32 + g * 8 + hq * 4;   // channel within the wave tile
         const int co = m0 + wm * WTM + cl;
         float sc[4], sh[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int c = co + r < a.Cout ? co + r : a.Cout - 1;
-          sc[r] = a.scale[c];
-          sh[r] = a.shift[c];
-        }
+        c_scale.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sc);
+        c_shift.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sh);
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           const int pl = j * 32 + (lane & 31);
@@ -446,14 +448,10 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int co = m0 + wm * WTM + i * 32 + g * 8 + hq * 4;
-      if (co >= a.Cout) continue;
       float sc[4], sh[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int c = co + r < a.Cout ? co + r : a.Cout - 1;
-        sc[r] = a.scale[c];
-        sh[r] = a.shift[c];
-      }
+      c_scale.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sc);
+      c_shift.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sh);
+      if (co >= a.Cout) continue;
       const bool full4 = (co + 3 < a.Cout);
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
@@ -579,131 +577,182 @@ extern "C" __global__ __launch_bounds__(256) void vrs_unpack_nchw_f32(vrs_pack_a
 
 // ---------------------------------------------------------------------------
 // Stem (model.0 = conv(3, c, 3, 2), yolo26/mod.rs:126-195) fused with the
-// input layout change.  A workgroup owns 2 output rows x 64 output pixels of
-// one image: it stages the 5 input rows x 132 columns x 3 channels it needs
-// (NCHW f32: each channel row is a contiguous run, loaded as float4 from a
-// 16-byte aligned start), builds the 128 x 32 im2col tile (k = c*9 + ky*3 +
-// kx, 27 real + 5 zero) in LDS, runs it through the 32x32x16 MFMA against the
-// [cout_pad][32] weights, and stages the NHWC result in LDS so every lane
-// stores whole 16-byte channel chunks.  Replaces the separate NCHW->NHWC pack
-// (which padded 3 channels to 8 and wrote 2.7x the input bytes) and the
-// padded-Cin conv.
-template <typename T>
+// input layout change: 3x3 stride-2 pad-1 conv straight from the NCHW float32
+// image, folded BN + activation, NHWC output of the element type.
+//
+// Work item: 2 output rows x 64 output pixels of one image.  The grid is
+// persistent (a few workgroups per CU, each taking items blockIdx.x,
+// +gridDim.x, ...), and an item's 3 channels x 5 input rows x 132 columns are
+// loaded into registers while the previous item is computed and stored.
+// Per item: the rows go to LDS; each wave takes one 32-pixel tile and builds
+// its MFMA operand straight from those rows (k = c*9 + ky*3 + kx, 27 taps + 5
+// zero); the [CT*32][32] weights sit in LDS for the whole kernel; results are
+// staged in LDS (aliasing the input rows) and written as 16-byte channel
+// chunks.  Every global load and store is a raw buffer access with a fixed
+// count per item (out-of-range chunks use out-of-range offsets), so the only
+// wait on vector memory -- for the prefetched rows -- leaves the previous
+// item's stores in flight.  VEC: image width a multiple of 4 (float4 rows).
+template <typename T, int CT, bool VEC>
 __device__ __forceinline__ void stem_body(const vrs_stem_args& a) {
   using E = Elt<T>;
   using G = typename E::group;
   constexpr int PX = 64, RO = 2, RI = 2 * RO + 1;      // pixels per row, output rows, input rows
   constexpr int CW = 2 * PX + 4, NQ = CW / 4;           // staged columns (float4 aligned)
-  constexpr int KP = 32 + 8;                            // im2col row (+pad)
-  constexpr int OP = 128 + 16 / (int)sizeof(T);         // output staging row (channels + pad)
-  // the output staging reuses the input and im2col space (both dead by then)
-  constexpr int IN_BYTES = 3 * RI * CW * 4, SB_BYTES = RO * PX * KP * (int)sizeof(T);
+  constexpr int CP = CT * 32;                           // padded output channels
+  constexpr int EPC = 16 / (int)sizeof(T);              // elements per 16-byte chunk
+  constexpr int OP = CP + EPC;                          // output staging row (channels + pad)
+  constexpr int WP = 32 + EPC;                          // weight row in LDS (k + pad)
+  constexpr int IN_BYTES = 3 * RI * CW * 4;
   constexpr int SO_BYTES = RO * PX * OP * (int)sizeof(T);
-  constexpr int LDS_BYTES = IN_BYTES + SB_BYTES > SO_BYTES ? IN_BYTES + SB_BYTES : SO_BYTES;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
+  constexpr int A_BYTES = IN_BYTES > SO_BYTES ? IN_BYTES : SO_BYTES;   // input and output staging alias
+  constexpr int W_BYTES = CP * WP * (int)sizeof(T);
+  __shared__ __attribute__((aligned(16))) unsigned char lds[A_BYTES + W_BYTES];
   float (*sin_)[RI][CW] = reinterpret_cast<float (*)[RI][CW]>(lds);
-  T* sb = reinterpret_cast<T*>(lds + IN_BYTES);
   T* so = reinterpret_cast<T*>(lds);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int wg = blockIdx.x;
-  const int seg = wg % a.segs; wg /= a.segs;
+  T* sw = reinterpret_cast<T*>(lds + A_BYTES);
+  const int tid = threadIdx.x, lane = tid & 63, hq = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // weights -> LDS, once
+  for (int i = tid; i < CP * 32 / EPC; i += 256) {
+    const int row = i / (32 / EPC), part = i % (32 / EPC);
+    *reinterpret_cast<u32x4_t*>(sw + row * WP + part * EPC) =
+        reinterpret_cast<const u32x4_t*>(a.w)[i];
+  }
+  // accumulator lane l holds channel j*32 + (l & 31) of tile j
+  float sc[CT], sh[CT];
+#pragma unroll
+  for (int j = 0; j < CT; ++j) {
+    const int c = j * 32 + (lane & 31), cc = c < a.cout ? c : a.cout - 1;
+    sc[j] = a.scale[cc];
+    sh[j] = a.shift[cc];
+  }
+
   const int rp = (a.Ho + RO - 1) / RO;
-  const int oyp = wg % rp;
-  const int b = wg / rp;
-  const int ox0 = seg * PX, oy0 = oyp * RO;
-  const int64_t plane = (int64_t)a.H * a.W;
-  const float* xb = a.x + (int64_t)b * 3 * plane;
-  const int x0 = 2 * ox0 - 4;                           // staged column 0 (multiple of 4)
-  const bool vec = (a.W & 3) == 0;                      // rows 16-byte aligned
-  for (int i = tid; i < 3 * RI * NQ; i += 256) {
-    const int c = i / (RI * NQ), r = (i / NQ) % RI, q = i % NQ;
-    const int iy = 2 * oy0 - 1 + r, ix = x0 + 4 * q;
-    f32x4_t v = {0.f, 0.f, 0.f, 0.f};
-    if ((unsigned)iy < (unsigned)a.H) {
-      const float* row = xb + c * plane + (int64_t)iy * a.W;
-      if (vec && ix >= 0 && ix + 3 < a.W) {
-        v = *reinterpret_cast<const f32x4_t*>(row + ix);
+  const int total = a.N * rp * a.segs;                  // work items (< 2^31, checked on the host)
+  const int plane = a.H * a.W;                          // 3 * plane * 4 < 2^31 (host)
+  constexpr int NIN = 3 * RI * NQ, NPT = (NIN + 255) / 256;   // float4 chunks of one item's input
+  f32x4_t pre[NPT];
+  auto fetch = [&](int item) {
+    const int seg = item % a.segs, rest = item / a.segs;
+    const int oy0 = (rest % rp) * RO, b = rest / rp;
+    const int x0 = 2 * seg * PX - 4;                    // staged column 0 (multiple of 4)
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (int64_t)b * 3 * plane, 3 * plane * 4);
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int i = tid + j * 256;
+      const int c = i / (RI * NQ), r = (i / NQ) % RI, q = i % NQ;
+      const int iy = 2 * oy0 - 1 + r, ix = x0 + 4 * q;
+      const bool row_ok = i < NIN && (unsigned)iy < (unsigned)a.H;
+      const uint32_t base = (uint32_t)((c * a.H + iy) * a.W + ix) * 4u;
+      if constexpr (VEC) {   // a chunk is wholly inside or wholly outside the row
+        pre[j] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rx, row_ok && ix >= 0 && ix < a.W ? base : kOOB, 0, 0));
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if ((unsigned)(ix + e) < (unsigned)a.W) v[e] = row[ix + e];
+          pre[j][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                    rx, row_ok && (unsigned)(ix + e) < (unsigned)a.W ? base + 4u * e : kOOB, 0, 0));
       }
     }
-    *reinterpret_cast<f32x4_t*>(&sin_[c][r][4 * q]) = v;
-  }
-  __syncthreads();
-  {
-    // a thread keeps one k (256 % 32 == 0): its (c, ky, kx) offset is fixed
-    const int k = tid & 31;
-    const int c = k / 9, t = k - c * 9, ky = t / 3, kx = t - ky * 3;
-    const float* src = &sin_[k < 27 ? c : 0][k < 27 ? ky : 0][k < 27 ? kx + 3 : 0];
-#pragma unroll 4
-    for (int px = tid >> 5; px < RO * PX; px += 256 / 32) {   // px: row-major over (output row, pixel)
-      const int ro = px / PX, p = px - ro * PX;
-      // column 2*(ox0+p) - 1 + kx relative to x0; input row 2*(oy0+ro) - 1 + ky
-      const float v = k < 27 ? src[2 * ro * CW + 2 * p] : 0.f;
-      sb[px * KP + k] = E::from_f(v);
-    }
-  }
-  __syncthreads();
-  const T* w = reinterpret_cast<const T*>(a.w);
-  const int pt_n = RO * PX / 32;
-  const int tiles = (a.cout_pad / 32) * pt_n;
-  const int hq = lane >> 5;
-  constexpr int MAXT = (128 / 32) * (RO * PX / 32) / 4;   // tiles per wave at cout_pad = 128
-  f32x16_t acc[MAXT];
-#pragma unroll
-  for (int j = 0; j < MAXT; ++j) {   // all MFMAs first: the staging below overwrites sb
-    const int t = wave + 4 * j;
-    if (t >= tiles) break;
-    const int ct = t / pt_n, pt = t % pt_n;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const G fa = E::load(w + (int64_t)(ct * 32 + (lane & 31)) * 32 + ks * 16 + hq * 8);
-      const G fb = E::load(&sb[(pt * 32 + (lane & 31)) * KP + ks * 16 + hq * 8]);
-      acc[j] = mfma32_k16(fa, fb, acc[j]);
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < MAXT; ++j) {
-    const int t = wave + 4 * j;
-    if (t >= tiles) break;
-    const int ct = t / pt_n, pt = t % pt_n;
-    const int px = pt * 32 + (lane & 31);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int co = ct * 32 + g * 8 + hq * 4;
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int c = co + r < a.cout ? co + r : a.cout - 1;
-        float u = acc[j][g * 4 + r] * a.scale[c] + a.shift[c];
-        if (a.act == VRS_ACT_SILU) u = silu_t<T>(u);
-        v[r] = u;
-      }
-      T* sp = so + px * OP + co;
-      if constexpr (sizeof(T) == 2) {
-        *reinterpret_cast<u32x2_t*>(sp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-      } else {
-        *reinterpret_cast<f32x4_t*>(sp) = (f32x4_t){v[0], v[1], v[2], v[3]};
-      }
-    }
-  }
-  __syncthreads();
-  constexpr int EPC = 16 / (int)sizeof(T);              // elements per 16-byte chunk
+  };
+
+  // MFMA B operand: lane l feeds pixel (l & 31) of its wave's tile and
+  // k = ks*16 + hq*8 + e; tap_off(k) is the tap's float offset from the
+  // pixel's window origin (k >= 27, zero weights: offset 0, zeroed after).
+  constexpr auto tap_off = [](int k) { return k < 27 ? (k / 9 * RI + k % 9 / 3) * CW + k % 3 : 0; };
+  // window origin of this lane's pixel (ro, p): input row 2*(oy0+ro) - 1 is
+  // staged row 2*ro, column 2*(ox0+p) - 1 is staged column 2*p + 3
+  const int mpx = wave * 32 + (lane & 31);
+  const float* org = &sin_[0][2 * (mpx / PX)][2 * (mpx % PX) + 3];
+
+  constexpr int CPPM = CP / EPC, NST = RO * PX * CPPM / 256;   // store chunks per pixel, per thread
+  static_assert(RO * PX * CPPM % 256 == 0, "whole store rounds");
   const int cpp = a.cout / EPC;                         // chunks per pixel (cout % 8 == 0, checked)
-  for (int i = tid; i < RO * PX * cpp; i += 256) {
-    const int px = i / cpp, part = i - px * cpp;
-    const int ro = px / PX, p = px % PX;
-    const int oy = oy0 + ro, ox = ox0 + p;
-    if (oy >= a.Ho || ox >= a.Wo) continue;
-    T* yp = reinterpret_cast<T*>(a.y) + (((int64_t)b * a.Ho + oy) * a.Wo + ox) * a.y_pitch + part * EPC;
-    *reinterpret_cast<u32x4_t*>(yp) = *reinterpret_cast<const u32x4_t*>(so + px * OP + part * EPC);
+
+  int item = blockIdx.x;
+  if (item >= total) return;
+  fetch(item);
+  for (; item < total; item += gridDim.x) {
+    const int seg = item % a.segs, rest = item / a.segs;
+    const int oy0 = (rest % rp) * RO, b = rest / rp;
+    __syncthreads();   // the previous item's staged output has been read
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int i = tid + j * 256;
+      if (i < NIN) {
+        const int c = i / (RI * NQ), r = (i / NQ) % RI, q = i % NQ;
+        *reinterpret_cast<f32x4_t*>(&sin_[c][r][4 * q]) = pre[j];
+      }
+    }
+    if (item + (int)gridDim.x < total) fetch(item + gridDim.x);
+    __syncthreads();
+    f32x16_t acc[CT];
+    {
+      G fb[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = org[hq ? tap_off(ks * 16 + 8 + e) : tap_off(ks * 16 + e)];
+        if (ks == 1 && hq) {
+#pragma unroll
+          for (int e = 3; e < 8; ++e) v[e] = 0.f;   // k = 27..31
+        }
+        fb[ks] = E::from_f8(v);
+      }
+#pragma unroll
+      for (int j = 0; j < CT; ++j) {   // pixels as the A operand: a lane's accumulators share one channel
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          acc[j] = mfma32_k16(fb[ks], E::load(sw + (j * 32 + (lane & 31)) * WP + ks * 16 + hq * 8), acc[j]);
+      }
+    }
+    __syncthreads();   // every wave is done with the input rows (the staging overwrites them)
+    // accumulator register r of tile j: channel j*32 + (lane & 31), pixel
+    // wave*32 + (r/4)*8 + hq*4 + r%4
+    auto epilogue = [&](auto silu_on) {
+#pragma unroll
+      for (int j = 0; j < CT; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float u = acc[j][r] * sc[j] + sh[j];
+          if constexpr (decltype(silu_on)::value) u = silu_t<T>(u);
+          so[(wave * 32 + (r >> 2) * 8 + hq * 4 + (r & 3)) * OP + j * 32 + (lane & 31)] = E::from_f(u);
+        }
+    };
+    if (a.act == VRS_ACT_SILU) epilogue(std::true_type{});
+    else epilogue(std::false_type{});
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc(reinterpret_cast<T*>(a.y) + (int64_t)b * a.Ho * a.Wo * a.y_pitch, a.Ho * a.Wo * a.y_pitch * (int)sizeof(T));
+#pragma unroll
+    for (int s = 0; s < NST; ++s) {
+      const int i = tid + s * 256;
+      const int px = i / CPPM, part = i % CPPM;
+      const int oy = oy0 + px / PX, ox = seg * PX + px % PX;
+      const bool ok = part < cpp && oy < a.Ho && ox < a.Wo;
+      const uint32_t off = ok ? (uint32_t)(((oy * a.Wo + ox) * a.y_pitch + part * EPC) * (int)sizeof(T)) : kOOB;
+      __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4_t*>(so + px * OP + part * EPC), ry, off, 0, 0);
+    }
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void vrs_stem_bf16(vrs_stem_args a) { stem_body<bf16_t>(a); }
-extern "C" __global__ __launch_bounds__(256) void vrs_stem_f32(vrs_stem_args a) { stem_body<float>(a); }
+#define VRS_STEM(DT, T, CT, LB)                                                                          \
+  extern "C" __global__ __launch_bounds__(256, LB) void vrs_stem_##DT##_c##CT(vrs_stem_args a) {        \
+    stem_body<T, CT, true>(a);                                                                           \
+  }                                                                                                      \
+  extern "C" __global__ __launch_bounds__(256, LB) void vrs_stem_##DT##_c##CT##_u(vrs_stem_args a) {    \
+    stem_body<T, CT, false>(a);                                                                          \
+  }
+// kernel names: vrs_stem_<type>_c<cout_pad/32>[_u: image width not a multiple of 4]
+VRS_STEM(bf16, bf16_t, 1, 4)
+VRS_STEM(bf16, bf16_t, 2, 4)
+VRS_STEM(bf16, bf16_t, 3, 4)
+VRS_STEM(bf16, bf16_t, 4, 4)
+VRS_STEM(f32, float, 1, 2)
+VRS_STEM(f32, float, 2, 2)
+VRS_STEM(f32, float, 3, 2)
+VRS_STEM(f32, float, 4, 2)
