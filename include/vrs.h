@@ -90,6 +90,11 @@ typedef struct {
 #define VRS_TILE_32x256 5
 #define VRS_TILE_256x256 6   /* 512 threads; bf16, Cin % 64 == 0 */
 #define VRS_TILE_K32 0x100
+/* OR VRS_TILE_PERSIST: persistent grid (resident workgroups loop over the
+ * tiles with one continuous load stream) for memory-bound shapes; bf16,
+ * 128x128 or 64x256, Cin % step == 0, an even number of K steps, no residual,
+ * output channel offset/pitch/count multiples of 8. */
+#define VRS_TILE_PERSIST 0x200
 
 typedef struct {
   int32_t k;        /* square kernel size; padding = k/2 (blocks/conv.rs:36) */

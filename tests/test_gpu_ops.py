@@ -106,6 +106,69 @@ def test_conv2d_every_tile(dtype, tile, yview):
     assert torch.all(rest == 7.0)
 
 
+PERSIST_CASES = [
+    # n, cin, h, w, cout, k, s, tile: several tiles per workgroup, ragged pixel
+    # and channel tiles, padding taps, stride 2, both step depths
+    (8, 128, 96, 96, 256, 1, 1, vrs.TILE_128x128 | vrs.TILE_K32 | vrs.TILE_PERSIST),
+    (8, 128, 96, 96, 256, 1, 1, vrs.TILE_128x128 | vrs.TILE_PERSIST),
+    (3, 192, 50, 70, 80, 1, 1, vrs.TILE_128x128 | vrs.TILE_K32 | vrs.TILE_PERSIST),
+    (4, 64, 60, 60, 64, 3, 1, vrs.TILE_64x256 | vrs.TILE_K32 | vrs.TILE_PERSIST),
+    (2, 64, 41, 37, 32, 3, 2, vrs.TILE_64x256 | vrs.TILE_K32 | vrs.TILE_PERSIST),
+    (2, 128, 30, 22, 128, 3, 1, vrs.TILE_128x128 | vrs.TILE_PERSIST),
+]
+
+
+@pytest.mark.parametrize("case", PERSIST_CASES)
+def test_conv2d_persistent(case):
+    """Persistent-grid conv (one load stream across a workgroup's tiles) into a
+    channel view, against the oracle; bytes outside the view stay untouched."""
+    import torch
+    n, cin, h, w, cout, k, s, tile = case
+    dtype = vrs.BF16
+    rnd = rounder(dtype)
+    rng = np.random.default_rng(cin + cout + k)
+    x = rnd(rng.standard_normal((n, cin, h, w)).astype(np.float32))
+    wt = rnd((rng.standard_normal((cout, cin, k, k)) * np.sqrt(2.0 / (cin * k * k))).astype(np.float32))
+    scale = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    xt = to_nhwc(x, dtype)
+    ho, wo = (h + 2 * (k // 2) - k) // s + 1, (w + 2 * (k // 2) - k) // s + 1
+    yp, yo = cout + 16, 8
+    yt = torch.full((n, ho, wo, yp), 7.0, dtype=tdtype(dtype), device="cuda")
+    wp = dev(vrs.pack_conv_weight(wt, 1, cin, dtype))
+    ctx().conv2d(vrs.nhwc(xt), wp, dev(scale), dev(shift), vrs.nhwc(yt, cout, yo), k, s, 1, vrs.ACT_SILU, None,
+                 dtype, tile=tile)
+    torch.cuda.synchronize()
+    # the oracle on a sample of images keeps the check fast at these sizes
+    ns = min(n, 2)
+    ref = oracle.affine_act(oracle.conv2d(x[:ns], wt, s, k // 2), scale, shift, 1)
+    assert rel_err(from_nhwc(yt[:ns], cout, yo), ref, FLOOR[dtype]) < TOL[dtype]
+    # every image: same result as the non-persistent kernel of the same tile
+    y2 = torch.full_like(yt, 7.0)
+    ctx().conv2d(vrs.nhwc(xt), wp, dev(scale), dev(shift), vrs.nhwc(y2, cout, yo), k, s, 1, vrs.ACT_SILU, None,
+                 dtype, tile=tile & ~vrs.TILE_PERSIST)
+    torch.cuda.synchronize()
+    assert torch.equal(yt, y2)
+
+
+def test_conv2d_persistent_rejections():
+    import torch
+    t = vrs.TILE_128x128 | vrs.TILE_K32 | vrs.TILE_PERSIST
+    x = torch.zeros((1, 8, 8, 96), dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros((1, 8, 8, 128), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(128 * 96, dtype=torch.bfloat16, device="cuda")
+    s = torch.ones(128, device="cuda")
+    with pytest.raises(vrs.VrsError):   # 3 K steps: odd
+        ctx().conv2d(vrs.nhwc(x), w, s, s, vrs.nhwc(y), 1, 1, 1, vrs.ACT_SILU, None, vrs.BF16, tile=t)
+    x = torch.zeros((1, 8, 8, 128), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(128 * 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(vrs.VrsError):   # residual
+        ctx().conv2d(vrs.nhwc(x), w, s, s, vrs.nhwc(y), 1, 1, 1, vrs.ACT_SILU, vrs.nhwc(y), vrs.BF16, tile=t)
+    with pytest.raises(vrs.VrsError):   # float32
+        ctx().conv2d(vrs.nhwc(x.float()), w, s, s, vrs.nhwc(y.float()), 1, 1, 1, vrs.ACT_SILU, None, vrs.F32,
+                     tile=t)
+
+
 FP8_CASES = [
     # n, cin, h, w, cout, k, s, residual, tile
     (2, 64, 20, 20, 128, 3, 1, False, vrs.TILE_128x128),

@@ -75,6 +75,17 @@ static int check_dtype(int dtype) {
 
 static inline int out_size(int in, int k, int s) { return (in + 2 * (k / 2) - k) / s + 1; }
 
+// Resident workgroups per CU of a kernel (registers, AGPRs and LDS as the
+// runtime's occupancy calculator sees them), 1..8.
+static int resident_wgs(hipFunction_t f, int threads = 256) {
+  int n = 0;
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, threads, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    n = 1;
+  }
+  return n < 1 ? 1 : n > 8 ? 8 : n;
+}
+
 // Dense-conv tiles.  bf16 has every tile with 32- and (when Cin % 64 == 0)
 // 64-deep K steps; the float32 parity path has 128x128, 64x256 and 32x256.
 struct TileInfo { int code, bm, bn; const char* tag; bool f32; bool k32; int threads; };
@@ -108,6 +119,17 @@ static int tile_kernel(int code, int cin, int dtype, char* name, size_t n, int* 
   if (dtype == VRS_F32 && !t->f32) return fail(VRS_EUNSUPPORTED, "conv: tile %s has no float32 build", t->tag);
   const bool g = cin % 32 != 0;
   bool k64 = !(code & VRS_TILE_K32) && dtype == VRS_BF16 && cin % 64 == 0 && t->code != VRS_TILE_32x256;
+  if (code & VRS_TILE_PERSIST) {
+    if (dtype != VRS_BF16 || g || (t->code != VRS_TILE_128x128 && t->code != VRS_TILE_64x256) ||
+        (t->code == VRS_TILE_64x256 && k64))
+      return fail(VRS_EUNSUPPORTED, "conv: persistent tile %s%s not built for this dtype/Cin", t->tag,
+                  k64 ? " k64" : "");
+    snprintf(name, n, "vrs_conv_bf16_%s_k%d_p", t->tag, k64 ? 64 : 32);
+    *bm = t->bm;
+    *bn = t->bn;
+    *threads = t->threads;
+    return VRS_OK;
+  }
   if (!t->k32 && (!k64 || g))
     return fail(VRS_EUNSUPPORTED, "conv: tile %s needs Cin %% 64 == 0 and 64-deep steps (Cin=%d)", t->tag, cin);
   if (g && t->code != VRS_TILE_128x128 && t->code != VRS_TILE_64x256 && t->code != VRS_TILE_32x256)
@@ -155,6 +177,10 @@ std::vector<int> conv_tile_candidates(int cout, int cin, int dtype) {
     }
     c.push_back(t.code);
     if (dtype == VRS_BF16 && cin % 64 == 0 && t.code != VRS_TILE_32x256) c.push_back(t.code | VRS_TILE_K32);
+    if (dtype == VRS_BF16 && !g && (t.code == VRS_TILE_128x128 || t.code == VRS_TILE_64x256)) {
+      c.push_back(t.code | VRS_TILE_K32 | VRS_TILE_PERSIST);
+      if (t.code == VRS_TILE_128x128 && cin % 64 == 0) c.push_back(t.code | VRS_TILE_PERSIST);
+    }
   }
   return c;
 }
@@ -213,10 +239,20 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   if ((rc = tile_kernel(tile, x.c, cs.dtype, name, sizeof name, &bm, &bn, &threads))) return rc;
   a.tiles_m = (cout + bm - 1) / bm;
   a.tiles_n = (int32_t)((M + bn - 1) / bn);
-  const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
+  int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
   if (blocks >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: grid too large");
   hipFunction_t f;
   if ((rc = get_fn(ctx, name, &f))) return rc;
+  if (tile & VRS_TILE_PERSIST) {
+    const int bk = strstr(name, "_k64_") ? 64 : 32;
+    if (a.res || !a.stage || a.y_f32 || a.K % (2 * bk) != 0)
+      return fail(VRS_EUNSUPPORTED, "conv: persistent tile needs no residual, a staged bf16 output and an even "
+                  "number of %d-deep K steps (K=%d)", bk, a.K);
+    const int64_t yb = ((int64_t)(a.N - 1) * a.y_sb + (int64_t)ho * wo * a.y_sp) * 2;
+    if (yb >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: persistent tile: output view exceeds 2 GiB");
+    a.y_bytes = (int32_t)yb;
+    blocks = std::min<int64_t>(blocks, (int64_t)resident_wgs(f, threads) * (ctx->num_cu > 0 ? ctx->num_cu : 256));
+  }
   out.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(threads), 0, a));
   const double es = (double)elt_size(cs.dtype);
   const double cin = cs.cin_real > 0 ? cs.cin_real : x.c;
@@ -427,17 +463,6 @@ int prep_absmax(vrs_ctx* ctx, const vrs_nhwc& x, unsigned* out, std::vector<Laun
   return VRS_OK;
 }
 
-// Resident workgroups per CU of a 256-thread kernel, from its register and
-// LDS use (CDNA4: 4 SIMDs x 512 registers per lane, 160 KB LDS per CU).
-static int resident_wgs(hipFunction_t f) {
-  int vgpr = 0, lds = 0;
-  hipFuncGetAttribute(&lds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, f);
-  hipFuncGetAttribute(&vgpr, HIP_FUNC_ATTRIBUTE_NUM_REGS, f);
-  int by_reg = vgpr > 0 ? 512 / ((vgpr + 7) / 8 * 8) : 1;   // waves per SIMD = groups per CU
-  int by_lds = lds > 0 ? (160 * 1024) / lds : 8;
-  int n = std::min(std::min(by_reg, by_lds), 8);
-  return n < 1 ? 1 : n;
-}
 
 int prep_stem(vrs_ctx* ctx, int act, int dtype, const float* x, int n, int h, int w, const void* wp,
               const float* scale, const float* shift, int cout, const vrs_nhwc& y, std::vector<Launch>& ls) {

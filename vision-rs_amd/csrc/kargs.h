@@ -43,6 +43,9 @@ typedef struct {
    * clamp_bits (in both halves) */
   float in_scale;
   uint32_t clamp_bits;
+  /* persistent kernels: bytes from y to the end of the output view's last
+   * pixel (< 2^31) */
+  int32_t y_bytes;
 } vrs_conv_args;
 
 /* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the

@@ -496,10 +496,204 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
     }
 }
 
+
+// Persistent variant for the memory-bound shapes (bf16, Cin % BK == 0, even
+// K-step count, no residual, staged 16-byte stores).  A workgroup takes tiles
+// xcd_remap(blockIdx.x) + i*gridDim.x and runs one continuous load stream
+// over its (tile, K step) sequence: the two steps in flight at the end of a
+// tile are the next tile's first two, so the epilogue -- which stages through
+// its own LDS area, not the pipeline buffers -- runs while they land.  Stores
+// are raw buffer stores with a fixed count per lane (out-of-range chunks use
+// out-of-range offsets), so waiting for the next loads never waits for them.
+template <int BM, int BN, int BK, int WGM, int WGN>
+__device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
+  using T = bf16_t;
+  using E = Elt<T>;
+  using G = E::group;
+  constexpr int PAD = 8, LDK = BK + PAD, GPR = BK / 8;
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int A_IT = BM * GPR / NT, B_IT = BN * GPR / NT;
+  static_assert(BM * GPR % NT == 0 && BN * GPR % NT == 0, "whole chunks per thread");
+  constexpr int TILE_ELEMS = (BM + BN) * LDK;
+  constexpr int SPAD = 8, SROW = WTM + SPAD;           // staging row: WTM channels + pad
+  constexpr int EPC = 8, CPP = WTM / EPC;               // 16-byte chunks per staged pixel
+  constexpr int NST = WTN * CPP / 64;                   // stores per lane per tile
+  static_assert(WTN * CPP % 64 == 0, "whole store rounds");
+  __shared__ __attribute__((aligned(16))) T smem0[TILE_ELEMS];
+  __shared__ __attribute__((aligned(16))) T smem1[TILE_ELEMS];
+  __shared__ __attribute__((aligned(16))) T sstage[WGM * WGN * WTN * SROW];
+  auto sbuf = [&](int b) -> T* { return b ? smem1 : smem0; };
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN, hq = lane >> 5;
+  const int HWo = a.Ho * a.Wo;
+  const float inv_hwo = 1.0f / (float)HWo, inv_wo = 1.0f / (float)a.Wo;
+  const int total = a.tiles_m * a.tiles_n;
+  const int nk = a.K / BK;                              // even, >= 2 (host)
+  int tile = xcd_remap(blockIdx.x, gridDim.x);
+  if (tile >= total) return;
+
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, a.w_bytes);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, a.y_bytes);
+
+  // load stream state: tile being loaded, its next K step, chunk geometry
+  int ld_tile = tile, ld_k = 0, t_ky = 0, t_kx = 0, t_ci = 0;
+  uint32_t a_off[A_IT], b_off[B_IT];
+  int b_iy0[B_IT], b_ix0[B_IT];
+  bool b_ok[B_IT];
+  auto geometry = [&](int t) {
+    const int m0 = (t % a.tiles_m) * BM, n0 = (t / a.tiles_m) * BN;
+#pragma unroll
+    for (int i = 0; i < A_IT; ++i) {
+      const int c = tid + i * NT, co = m0 + c / GPR;
+      a_off[i] = co < a.Cout ? (uint32_t)((co * a.K + (c % GPR) * 8) * 2) : kOOB;
+    }
+#pragma unroll
+    for (int i = 0; i < B_IT; ++i) {
+      const int c = tid + i * NT, m = n0 + c / GPR;
+      b_ok[i] = m < a.M;
+      int rr, ox;
+      const int bb = fdivmod(b_ok[i] ? m : 0, HWo, inv_hwo, rr);
+      const int oy = fdivmod(rr, a.Wo, inv_wo, ox);
+      b_iy0[i] = oy * a.stride - a.pad;
+      b_ix0[i] = ox * a.stride - a.pad;
+      b_off[i] = (uint32_t)((((int64_t)bb * a.H + b_iy0[i]) * a.W + b_ix0[i]) * a.x_pitch + (c % GPR) * 8) * 2u;
+    }
+  };
+  geometry(ld_tile);
+  auto load_set = [&](G (&ra)[A_IT], G (&rb)[B_IT]) {
+    if (ld_k == nk) {   // the stream moves on to the next tile
+      ld_tile += gridDim.x;
+      ld_k = 0;
+      t_ky = t_kx = t_ci = 0;
+      if (ld_tile < total) geometry(ld_tile);
+    }
+    const uint32_t dead = ld_tile < total ? 0u : kOOB;
+#pragma unroll
+    for (int i = 0; i < A_IT; ++i) ra[i] = E::bload(rw, a_off[i] | dead, (uint32_t)ld_k * BK * 2u);
+    const int ky = t_ky, kx = t_kx;
+    const uint32_t off = (uint32_t)((ky * a.W + kx) * a.x_pitch + t_ci) * 2u;
+    t_ci += BK;
+    if (t_ci == a.Cin) {
+      t_ci = 0;
+      if (++t_kx == a.kw) { t_kx = 0; ++t_ky; }
+    }
+#pragma unroll
+    for (int i = 0; i < B_IT; ++i) {
+      const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
+      const bool ok = b_ok[i] && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+      rb[i] = E::bload(rx, (ok ? b_off[i] + off : kOOB) | dead, 0);
+    }
+    ++ld_k;
+  };
+  auto store_set = [&](int buf, const G (&ra)[A_IT], const G (&rb)[B_IT]) {
+    T* sA = sbuf(buf);
+    T* sB = sA + BM * LDK;
+#pragma unroll
+    for (int i = 0; i < A_IT; ++i) {
+      const int c = tid + i * NT;
+      E::store(&sA[(c / GPR) * LDK + (c % GPR) * 8], ra[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < B_IT; ++i) {
+      const int c = tid + i * NT;
+      E::store(&sB[(c / GPR) * LDK + (c % GPR) * 8], rb[i]);
+    }
+  };
+
+  f32x16_t acc[TM][TN];
+  const int frag_row = lane & 31, frag_k = hq * 8;
+  auto step = [&](int cur, const G (&wa)[A_IT], const G (&wb)[B_IT], G (&la)[A_IT], G (&lb)[B_IT]) {
+    load_set(la, lb);
+    store_set(cur ^ 1, wa, wb);
+    const T* sA = sbuf(cur);
+    const T* sB = sA + BM * LDK;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      G fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = E::load(&sA[(wm * WTM + i * 32 + frag_row) * LDK + kk * 16 + frag_k]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = E::load(&sB[(wn * WTN + j * 32 + frag_row) * LDK + kk * 16 + frag_k]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32_k16(fa[i], fb[j], acc[i][j]);
+    }
+    pipe_schedule<BK / 16 * TM * TN, TM + TN, TM * TN, A_IT + B_IT>();
+    __syncthreads();
+  };
+
+  G ra0[A_IT], rb0[B_IT], ra1[A_IT], rb1[B_IT];
+  load_set(ra0, rb0);
+  load_set(ra1, rb1);
+  store_set(0, ra0, rb0);
+  __syncthreads();
+  const ChanConst c_scale(a.scale, a.Cout), c_shift(a.shift, a.Cout);
+  const uint32_t hmask = upper_half_mask();
+  T* st = sstage + wave * WTN * SROW;
+  for (; tile < total; tile += gridDim.x) {
+    const int m0 = (tile % a.tiles_m) * BM, n0 = (tile / a.tiles_m) * BN;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    for (int kt = 0; kt < nk; kt += 2) {
+      step(0, ra1, rb1, ra0, rb0);
+      step(1, ra0, rb0, ra1, rb1);
+    }
+    // epilogue: this wave's (WTN pixel x WTM channel) tile -> its staging
+    // area -> 16-byte NHWC chunks.  Register g*4 + r of MFMA tile (i, j) is
+    // channel i*32 + g*8 + hq*4 + r of pixel j*32 + (lane & 31).
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int cl = i * 32 + g * 8 + hq * 4;
+        float sc[4], sh[4];
+        c_scale.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sc);
+        c_shift.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sh);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = acc[i][j][g * 4 + r] * sc[r] + sh[r];
+            if (a.act == VRS_ACT_SILU) t = silu_fast(t);
+            v[r] = t;
+          }
+          *reinterpret_cast<u32x2_t*>(st + (j * 32 + (lane & 31)) * SROW + cl) =
+              (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        }
+      }
+    __builtin_amdgcn_wave_barrier();   // the staging is read back by this wave only
+#pragma unroll
+    for (int s = 0; s < NST; ++s) {
+      const int c = lane + s * 64;
+      const int pl = c / CPP, part = c % CPP;
+      const int m = n0 + wn * WTN + pl;
+      const int co = m0 + wm * WTM + part * EPC;
+      int pp;
+      const int bb = fdivmod(m < a.M ? m : 0, HWo, inv_hwo, pp);
+      const uint32_t off = m < a.M && co < a.Cout ? (uint32_t)((bb * a.y_sb + pp * a.y_sp + co) * 2) : kOOB;
+      __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4_t*>(st + pl * SROW + part * EPC), ry, off,
+                                             0, 0);
+    }
+    __builtin_amdgcn_wave_barrier();   // staging reads done before the next tile's writes
+  }
+}
 }  // namespace
 
+// Two workgroups' worth of waves per SIMD: the 256x128 and 128x256 tiles then
+// keep their accumulators in VGPRs and fit two groups per CU (measured 10-30%
+// faster on memory-bound shapes, neutral elsewhere).
 #define VRS_CONV_KERNEL(NAME, T, BM, BN, BK, WGM, WGN, AL)                                        \
-  extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void NAME(vrs_conv_args a) {           \
+  extern "C" __global__ __launch_bounds__(64 * WGM * WGN, 2) void NAME(vrs_conv_args a) {        \
     conv_body<T, BM, BN, BK, WGM, WGN, AL>(a);                                                    \
   }
 
@@ -527,6 +721,15 @@ VRS_CONV_KERNEL(vrs_conv_bf16_256x256_k64_a, bf16_t, 256, 256, 64, 2, 4, true)
   extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void NAME(vrs_conv_args a) {          \
     conv_body<bf16_t, BM, BN, 64, WGM, WGN, true, true>(a);                                      \
   }
+#define VRS_CONV_P(NAME, BM, BN, BK, WGM, WGN)                                                   \
+  extern "C" __global__ __launch_bounds__(64 * WGM * WGN, 2) void NAME(vrs_conv_args a) {        \
+    conv_persist_body<BM, BN, BK, WGM, WGN>(a);                                                   \
+  }
+// persistent (memory-bound shapes): vrs_conv_bf16_<BM>x<BN>_k<BK>_p
+VRS_CONV_P(vrs_conv_bf16_128x128_k32_p, 128, 128, 32, 2, 2)
+VRS_CONV_P(vrs_conv_bf16_64x256_k32_p, 64, 256, 32, 1, 4)
+VRS_CONV_P(vrs_conv_bf16_128x128_k64_p, 128, 128, 64, 2, 2)
+
 VRS_CONV_F8(vrs_conv_fp8_128x128_k64_a, 128, 128, 2, 2)
 VRS_CONV_F8(vrs_conv_fp8_256x128_k64_a, 256, 128, 2, 2)
 VRS_CONV_F8(vrs_conv_fp8_128x256_k64_a, 128, 256, 2, 2)
