@@ -8,6 +8,7 @@
 // channel slice of the buffer its consumer reads, so concat and chunk are
 // free, residual adds run in the producing conv's epilogue, and only convs,
 // the SPPF pool, upsample and PSA attention launch kernels.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -624,14 +625,21 @@ int autotune_tiles(vrs_model* m) {
                     c.has_res ? &r : nullptr, view_of(m, c.y), ls) != VRS_OK)
         continue;
       if ((rc = run(ls[0], s))) break;
-      VRS_HIP(hipEventRecord(e0, s));
-      for (int it = 0; it < 5; ++it)
-        if ((rc = run(ls[0], s))) break;
+      // best of three rounds of five launches: one slow round (a clock
+      // dip, another process) does not decide the tile
+      float ms = 1e30f;
+      for (int round = 0; round < 3 && !rc; ++round) {
+        VRS_HIP(hipEventRecord(e0, s));
+        for (int it = 0; it < 5; ++it)
+          if ((rc = run(ls[0], s))) break;
+        if (rc) break;
+        VRS_HIP(hipEventRecord(e1, s));
+        VRS_HIP(hipEventSynchronize(e1));
+        float r = 0.f;
+        VRS_HIP(hipEventElapsedTime(&r, e0, e1));
+        ms = std::min(ms, r);
+      }
       if (rc) break;
-      VRS_HIP(hipEventRecord(e1, s));
-      VRS_HIP(hipEventSynchronize(e1));
-      float ms = 0.f;
-      VRS_HIP(hipEventElapsedTime(&ms, e0, e1));
       // a later candidate must win by 2%: near-ties keep the earlier one, so
       // the choice does not flip with timing noise from run to run
       if (ms < 0.98f * best) { best = ms; best_tile = t; }
