@@ -203,6 +203,15 @@ int vrs_detect_postprocess(vrs_ctx* ctx, const vrs_detect_desc* d, const float* 
                            int32_t* count, float* score, int32_t* cls, int32_t* anchor, float* xywh,
                            void* stream);
 
+/* Un-letterbox (examples/yolo26.rs:1531-1547): the post-processed xywh in
+ * letterbox pixels ([n][max_det][4], vrs_detect_postprocess) -> [cx, cy, w, h]
+ * normalised to each original image, i.e. Detection::bbox
+ * (src/detect/mod.rs:52-60).  orig_wh [n][2] int32 (device): width and
+ * height before the letterbox to img_size.  Slots past count[b] get zeros. */
+int vrs_detect_unletterbox(vrs_ctx* ctx, int32_t n, int32_t max_det, int32_t img_size,
+                           const int32_t* orig_wh, const int32_t* count, const float* xywh,
+                           float* out, void* stream);
+
 /* DetectDecodeOp / detect_decode_forward (kernels/detect_decode.rs:36-217):
  * grid-unit anchors, [n][4][A] in and out. */
 int vrs_detect_decode_grid(vrs_ctx* ctx, const float* boxes, const float* anchor_x,
@@ -265,6 +274,15 @@ int vrs_model_num_params(const vrs_model* m);
 int vrs_model_param_info(const vrs_model* m, int32_t i, const char** name, int32_t* dims, int32_t* ndim);
 /* LoadedModel::load_param_f32 analogue: float32 host data, reference layout. */
 int vrs_model_load_param(vrs_model* m, const char* name, const float* data, int64_t numel);
+/* load_weights_from_safetensors (examples/yolo26.rs:3403-3550): every model
+ * parameter is looked up by name in a local .safetensors file (raw BN
+ * tensors; the fold happens at finalize, as vrs_model_load_param); "X.weight"
+ * and "X.conv.weight" stand in for each other as in the reference's
+ * fallback.  F32, F16, BF16 and F64 tensors are accepted (converted to f32);
+ * an element-count mismatch is an error.  Parameters absent from the file
+ * are counted in *n_missing, not an error (the reference warns and goes on);
+ * they must still be loaded before vrs_model_finalize. */
+int vrs_model_load_safetensors(vrs_model* m, const char* path, int32_t* n_loaded, int32_t* n_missing);
 /* Fold BN, repack/upload weights and allocate activations.  All params must be loaded. */
 int vrs_model_finalize(vrs_model* m);
 int vrs_model_num_outputs(const vrs_model* m);

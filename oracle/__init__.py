@@ -46,6 +46,7 @@ def lib():
         _lib.orc_detect_decode_grid.argtypes = [f32p, f32p, f32p, f32p, C.c_int, C.c_int, f32p]
         _lib.orc_detect_postprocess.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int, i32p,
                                                 C.c_int, C.c_float, C.c_int, i32p, f32p, i32p, i32p, f32p]
+        _lib.orc_detect_unletterbox.argtypes = [C.c_int, C.c_int, C.c_int, i32p, i32p, f32p, f32p]
         _lib.orc_msda.argtypes = [f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, i32p, i32p,
                                   f32p, f32p, f32p, C.c_int, C.c_int, f32p]
         _lib.orc_add.argtypes = [f32p, f32p, f32p, C.c_long]
@@ -165,6 +166,18 @@ def detect_postprocess(boxes, scores, nc, img_h, img_w, strides=(8, 16, 32), thr
     lib().orc_detect_postprocess(_f(boxes), _f(scores), B, nc, img_h, img_w, _i(st), len(strides),
                                  thr, max_det, _i(count), _f(sc), _i(cl), _i(an), _f(xy))
     return count, sc, cl, an, xy
+
+
+def detect_unletterbox(count, xywh, orig_wh, img_size):
+    """xywh [B,max_det,4] letterbox pixels -> normalised original-image boxes
+    (examples/yolo26.rs:1531-1547)."""
+    xywh = _c32(xywh)
+    B, max_det, _ = xywh.shape
+    count = np.ascontiguousarray(count, np.int32)
+    wh = np.ascontiguousarray(orig_wh, np.int32).reshape(B, 2)
+    out = np.empty_like(xywh)
+    lib().orc_detect_unletterbox(B, max_det, img_size, _i(wh), _i(count), _f(xywh), _f(out))
+    return out
 
 
 def msda(value, shapes, ref, off, attw):

@@ -20,6 +20,8 @@
  *   orc_psa_attention     c2psa fixture + torch softmax(QK^T)V restatement
  *   orc_detect_decode_grid detect_decode fixture (A13 layout)
  *   orc_detect_postprocess closed-form decode + brute-force argmax/sort checks
+ *   orc_detect_unletterbox closed forms (square image: divide by the size;
+ *                         2:1 image: known scale and padding)
  *   orc_msda              torch F.grid_sample (bilinear, zeros, align_corners=False)
  *                         + brute-force tiny cases
  */
@@ -438,4 +440,33 @@ void orc_msda(const float* value, int B, int S, int heads, int Dh, int L, const 
 void orc_add(const float* a, const float* b, float* y, long n) {
 #pragma omp parallel for schedule(static)
   for (long i = 0; i < n; ++i) y[i] = a[i] + b[i];
+}
+
+/* Un-letterbox (examples/yolo26.rs:1531-1547), float32 throughout:
+ * lb_scale = img / max(w, h); new = round(o * lb_scale) (f32::round: half away
+ * from zero); pad = (img - new) / 2 in integers; scale_o = o * lb_scale;
+ * cx_n = (cx - pad_x) / scale_x, cy_n likewise, w_n = w / scale_x,
+ * h_n = h / scale_y.  Slots past count[b] are zero. */
+void orc_detect_unletterbox(int B, int max_det, int img_size, const int* orig_wh, const int* count,
+                            const float* xywh, float* out) {
+  for (int b = 0; b < B; ++b) {
+    const int ow = orig_wh[2 * b], oh = orig_wh[2 * b + 1];
+    const float s = (float)img_size / (float)(ow > oh ? ow : oh);
+    const int nw = (int)roundf((float)ow * s), nh = (int)roundf((float)oh * s);
+    const float px = (float)(img_size > nw ? (img_size - nw) / 2 : 0);
+    const float py = (float)(img_size > nh ? (img_size - nh) / 2 : 0);
+    const float sx = (float)ow * s, sy = (float)oh * s;
+    for (int k = 0; k < max_det; ++k) {
+      const float* d = xywh + ((size_t)b * max_det + k) * 4;
+      float* o = out + ((size_t)b * max_det + k) * 4;
+      if (k >= count[b]) {
+        o[0] = o[1] = o[2] = o[3] = 0.f;
+        continue;
+      }
+      o[0] = (d[0] - px) / sx;
+      o[1] = (d[1] - py) / sy;
+      o[2] = d[2] / sx;
+      o[3] = d[3] / sy;
+    }
+  }
 }

@@ -136,6 +136,32 @@ def _yolo_params(m, seed=0, bn="identity", bf16=False):
     return P
 
 
+@pytest.mark.parametrize("dtype", [vrs.F32, vrs.BF16])
+def test_yolo26_weights_from_safetensors(dtype, tmp_path):
+    """A model loaded from a local .safetensors file (load_weights_from_safetensors,
+    examples/yolo26.rs:3403-3550) computes bit for bit what the same model loaded
+    tensor by tensor computes; for bf16 the file holds bfloat16 conv weights,
+    against tensors rounded to bfloat16."""
+    import torch
+    from safetensors.torch import save_file
+    x = np.random.default_rng(3).uniform(0, 1, (2, 3, 96, 128)).astype(np.float32)
+    desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="n", one2one=True)
+    m1 = vrs.Model(ctx(), desc, 2, 96, 128, dtype, 1e-3)
+    P = _yolo_params(m1, bn="random", bf16=dtype == vrs.BF16)
+    m1.load(P)
+    T = {k: torch.from_numpy(v) for k, v in P.items()}
+    if dtype == vrs.BF16:
+        T = {k: (v.to(torch.bfloat16) if v.ndim == 4 else v) for k, v in T.items()}
+    save_file(T, str(tmp_path / "m.safetensors"))
+    m2 = vrs.Model(ctx(), desc, 2, 96, 128, dtype, 1e-3)
+    assert m2.load_safetensors(tmp_path / "m.safetensors") == (len(P), 0)
+    o1 = [o.cpu().numpy() for o in m1.forward(dev(x))]
+    o2 = [o.cpu().numpy() for o in m2.forward(dev(x))]
+    torch.cuda.synchronize()
+    for a, b in zip(o1, o2):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_yolo26n_f32_640_vs_oracle():
     """YOLO26n, 1x3x640x640 U[0,1), Kaiming-normal seed 0, identity BN (eps 1e-3)."""
     x = np.random.default_rng(0).uniform(0, 1, (1, 3, 640, 640)).astype(np.float32)

@@ -408,6 +408,25 @@ def test_detect_postprocess_empty():
     assert np.all(an.cpu().numpy() == -1)
 
 
+def test_detect_unletterbox():
+    """Letterbox pixels -> boxes normalised to the original image, bit-exact
+    against the oracle's float32 restatement; slots past count are zero.  The
+    original sizes cover landscape, portrait, square, sizes whose scaled side
+    rounds, and an image smaller than the letterbox."""
+    import torch
+    rng = np.random.default_rng(5)
+    wh = np.array([[1920, 1080], [480, 640], [640, 640], [333, 777], [1001, 999], [37, 100]], np.int32)
+    B, max_det = len(wh), 300
+    xywh = rng.uniform(0, 640, (B, max_det, 4)).astype(np.float32)
+    count = np.array([300, 17, 0, 1, 250, 300], np.int32)
+    got = ctx().detect_unletterbox(dev(count), dev(xywh), dev(wh), 640)
+    torch.cuda.synchronize()
+    ref = oracle.detect_unletterbox(count, xywh, wh, 640)
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    with pytest.raises(vrs.VrsError):
+        ctx().detect_unletterbox(dev(count), dev(xywh), dev(wh), 0)
+
+
 @pytest.mark.parametrize("cfg", [
     (2, 30, 4, [(16, 16), (8, 8), (4, 4), (2, 2)], 4),   # level-split kernel (one wave per level)
     (1, 6, 16, [(9, 9), (5, 5), (3, 3), (2, 2)], 4),     # unrolled 4x4 kernel (> 8 heads)

@@ -303,6 +303,30 @@ def msda_inputs(B, Q, heads, Dh, shapes, P, seed=5):
     return value, ref, off, attw
 
 
+def test_detect_unletterbox_closed_forms():
+    """Un-letterbox (examples/yolo26.rs:1531-1547) pinned by cases whose
+    scale and padding are known exactly: a square image (divide by its side),
+    2:1 landscape / portrait (scale 1/2, 140-pixel bars), a size whose scaled
+    side rounds (333x777 -> 274 wide, 183-pixel bars), and zeroed slots."""
+    xywh = np.zeros((5, 3, 4), np.float32)
+    xywh[0, 0] = (160, 480, 320, 64)      # 640x640 -> divide by 640
+    xywh[1, 0] = (320, 320, 640, 360)     # 1280x720 letterboxed: the whole image
+    xywh[1, 1] = (0, 140, 64, 36)         # its top-left corner
+    xywh[2, 0] = (320, 320, 360, 640)     # 720x1280
+    xywh[3, 0] = (183, 320, 0, 640)       # 333x777: left bar ends at x = 183
+    xywh[4, 0] = (1, 2, 3, 4)             # count 0: zeroed
+    wh = np.array([[640, 640], [1280, 720], [720, 1280], [333, 777], [10, 10]], np.int32)
+    count = np.array([1, 2, 1, 1, 0], np.int32)
+    out = oracle.detect_unletterbox(count, xywh, wh, 640)
+    assert out[0, 0].tolist() == [0.25, 0.75, 0.5, np.float32(0.1)]
+    assert out[1, 0].tolist() == [0.5, 0.5, 1.0, 1.0]
+    assert out[1, 1].tolist() == [0.0, 0.0, np.float32(0.1), np.float32(0.1)]
+    assert out[2, 0].tolist() == [0.5, 0.5, 1.0, 1.0]
+    assert out[3, 0][0] == 0.0 and out[3, 0][2] == 0.0   # pad_x = (640 - 274) // 2 = 183
+    assert out[3, 0][3] == np.float32(640) / np.float32(np.float32(777) * (np.float32(640) / np.float32(777)))
+    assert not out[0, 1:].any() and not out[1, 2:].any() and not out[4].any()
+
+
 def test_msda_matches_grid_sample():
     pytest.importorskip("torch")
     shapes = [(16, 16), (8, 8), (4, 4), (2, 2)]

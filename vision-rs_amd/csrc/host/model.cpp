@@ -708,6 +708,45 @@ int vrs_model_load_param(vrs_model* m, const char* name, const float* data, int6
   return VRS_OK;
 }
 
+int vrs_model_load_safetensors(vrs_model* m, const char* path, int32_t* n_loaded, int32_t* n_missing) {
+  if (!m || !path) return fail(VRS_EINVAL, "vrs_model_load_safetensors: null argument");
+  if (m->finalized) return fail(VRS_ESTATE, "vrs_model_load_safetensors: model already finalized");
+  StFile f;
+  int rc = st_open(path, f);
+  if (rc) return rc;
+  int32_t loaded = 0, missing = 0;
+  std::vector<float> data;
+  auto ends = [](const std::string& s, const char* suf) {
+    const size_t n = strlen(suf);
+    return s.size() >= n && s.compare(s.size() - n, n, suf) == 0;
+  };
+  for (const Param& p : m->params) {
+    // direct name, then the reference's fallback between a fused node's
+    // "X.weight" and the checkpoint's "X.conv.weight" (examples/yolo26.rs:3499-3507),
+    // in both directions
+    const StTensor* t = st_find(f, p.name);
+    if (!t && ends(p.name, ".conv.weight"))
+      t = st_find(f, p.name.substr(0, p.name.size() - strlen(".conv.weight")) + ".weight");
+    else if (!t && ends(p.name, ".weight"))
+      t = st_find(f, p.name.substr(0, p.name.size() - strlen(".weight")) + ".conv.weight");
+    if (!t) {
+      ++missing;
+      continue;
+    }
+    int64_t n = 1;
+    for (int d : p.dims) n *= d;
+    if (t->numel != n)
+      return fail(VRS_EBADSHAPE, "safetensors: '%s' has %lld values, parameter expects %lld", p.name.c_str(),
+                  (long long)t->numel, (long long)n);
+    if ((rc = st_to_f32(f, p.name, *t, data))) return rc;
+    if ((rc = vrs_model_load_param(m, p.name.c_str(), data.data(), n))) return rc;
+    ++loaded;
+  }
+  if (n_loaded) *n_loaded = loaded;
+  if (n_missing) *n_missing = missing;
+  return VRS_OK;
+}
+
 int vrs_model_finalize(vrs_model* m) {
   if (!m) return fail(VRS_EINVAL, "null model");
   if (!m->ctx) return fail(VRS_ESTATE, "model was created without a context (record-only)");

@@ -259,6 +259,21 @@ int vrs_detect_postprocess(vrs_ctx* ctx, const vrs_detect_desc* d, const float* 
   return run_all(ls, stream);
 }
 
+int vrs_detect_unletterbox(vrs_ctx* ctx, int32_t n, int32_t max_det, int32_t img_size, const int32_t* orig_wh,
+                           const int32_t* count, const float* xywh, float* out, void* stream) {
+  if (!ctx || !orig_wh || !count || !xywh || !out) return fail(VRS_EINVAL, "vrs_detect_unletterbox: null argument");
+  if (n <= 0 || max_det <= 0 || img_size <= 0) return fail(VRS_EBADSHAPE, "vrs_detect_unletterbox: empty shape");
+  if ((int64_t)n * max_det >= (1ll << 31)) return fail(VRS_EBADSHAPE, "vrs_detect_unletterbox: too many slots");
+  hipFunction_t f;
+  int rc = get_fn(ctx, "vrs_detect_unletterbox", &f);
+  if (rc) return rc;
+  vrs_unlb_args a{orig_wh, count, xywh, out, n, max_det, img_size};
+  std::vector<Launch> ls;
+  ls.push_back(make_launch("vrs_detect_unletterbox", f, dim3((unsigned)(((int64_t)n * max_det + 255) / 256)),
+                           dim3(256), 0, a));
+  return run_all(ls, stream);
+}
+
 int vrs_detect_decode_grid(vrs_ctx* ctx, const float* boxes, const float* ax, const float* ay, const float* st,
                            int32_t n, int32_t a, float* out, void* stream) {
   if (!ctx || !boxes || !ax || !ay || !st || !out) return fail(VRS_EINVAL, "vrs_detect_decode_grid: null argument");

@@ -30,6 +30,22 @@ int hip_check(hipError_t e, const char* what);
     if (e_ != hipSuccess) return ::vrs::hip_check(e_, #call); \
   } while (0)
 
+// safetensors file in memory (safetensors.cpp): tensor table and raw bytes.
+struct StTensor {
+  std::string dtype;
+  std::vector<int64_t> shape;
+  size_t begin = 0, end = 0;   // byte range relative to the data section
+  int64_t numel = 0;
+};
+struct StFile {
+  std::vector<char> bytes;
+  size_t data_begin = 0;
+  std::unordered_map<std::string, StTensor> tensors;
+};
+int st_open(const char* path, StFile& f);
+const StTensor* st_find(const StFile& f, const std::string& name);
+int st_to_f32(const StFile& f, const std::string& name, const StTensor& t, std::vector<float>& out);
+
 // Resolve a kernel by name from the loaded code objects.
 int get_fn(vrs_ctx* ctx, const char* name, hipFunction_t* out);
 

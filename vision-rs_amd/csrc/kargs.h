@@ -131,6 +131,15 @@ typedef struct {
   int32_t B, A, max_det;
 } vrs_det2_args;
 
+/* Un-letterbox of post-processed detections (examples/yolo26.rs:1531-1547). */
+typedef struct {
+  const int32_t* orig_wh;  /* [B][2] original width, height */
+  const int32_t* count;    /* [B] */
+  const float* xywh;       /* [B][max_det][4] letterbox pixels */
+  float* out;              /* [B][max_det][4] normalised to the original image */
+  int32_t B, max_det, img_size;
+} vrs_unlb_args;
+
 /* Grid-unit decode on [B,4,A] (kernels/detect_decode.rs:36-86). */
 typedef struct {
   const float* boxes;

@@ -142,6 +142,33 @@ extern "C" __global__ __launch_bounds__(1024) void vrs_detect_stage2(vrs_det2_ar
   }
 }
 
+// Letterbox pixels -> [cx, cy, w, h] normalised to the original image, the
+// reference's un-letterbox (examples/yolo26.rs:1531-1547) in the same float32
+// operations: s = img / max(ow, oh); new = round(o * s) (half away from
+// zero); pad = (img - new) / 2 in integers; divide by o * s.  One thread per
+// detection slot; slots past count[b] are zeroed.
+extern "C" __global__ __launch_bounds__(256) void vrs_detect_unletterbox(vrs_unlb_args a) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.B * a.max_det) return;
+  const int b = (int)(i / a.max_det), k = (int)(i - (int64_t)b * a.max_det);
+  float* o = a.out + i * 4;
+  if (k >= a.count[b]) {
+    o[0] = o[1] = o[2] = o[3] = 0.f;
+    return;
+  }
+  const int ow = a.orig_wh[2 * b], oh = a.orig_wh[2 * b + 1];
+  const float s = (float)a.img_size / (float)(ow > oh ? ow : oh);
+  const int nw = (int)roundf((float)ow * s), nh = (int)roundf((float)oh * s);
+  const float px = (float)(a.img_size > nw ? (a.img_size - nw) / 2 : 0);
+  const float py = (float)(a.img_size > nh ? (a.img_size - nh) / 2 : 0);
+  const float sx = (float)ow * s, sy = (float)oh * s;
+  const float* d = a.xywh + i * 4;
+  o[0] = (d[0] - px) / sx;
+  o[1] = (d[1] - py) / sy;
+  o[2] = d[2] / sx;
+  o[3] = d[3] / sy;
+}
+
 // Grid-unit decode on [B,4,A] rows l,t,r,b (kernels/detect_decode.rs:36-86):
 // cx = (ax - l + ax + r) * 0.5 * s, cy likewise, w = (r + l) * s, h = (b + t) * s.
 extern "C" __global__ __launch_bounds__(256) void vrs_detect_decode_grid(vrs_dec_args a) {

@@ -94,12 +94,14 @@ SIGNATURES = {
     "vrs_detect_workspace_size": (_sz, [_P(DetectDesc)]),
     "vrs_detect_postprocess": (C.c_int, [_vp, _P(DetectDesc), _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vrs_detect_decode_grid": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
+    "vrs_detect_unletterbox": (C.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "vrs_msda": (C.c_int, [_vp, _P(MsdaDesc), _vp, _vp, _vp, _vp, _vp, _vp]),
     "vrs_model_create": (C.c_int, [_vp, _P(BlockDesc), _i32, _i32, _i32, _i32, _f32, _P(_vp)]),
     "vrs_model_set_autotune": (C.c_int, [_vp, _i32]),
     "vrs_model_num_params": (C.c_int, [_vp]),
     "vrs_model_param_info": (C.c_int, [_vp, _i32, _P(C.c_char_p), _P(_i32), _P(_i32)]),
     "vrs_model_load_param": (C.c_int, [_vp, C.c_char_p, _vp, _i64]),
+    "vrs_model_load_safetensors": (C.c_int, [_vp, C.c_char_p, _P(_i32), _P(_i32)]),
     "vrs_model_finalize": (C.c_int, [_vp]),
     "vrs_model_num_outputs": (C.c_int, [_vp]),
     "vrs_model_output_info": (C.c_int, [_vp, _i32, _P(_i64), _P(_i32), _P(_i32)]),
@@ -241,6 +243,16 @@ class Context:
                                            _stream(stream)))
         return count, score, cls, anchor, xywh
 
+    def detect_unletterbox(self, count, xywh, orig_wh, img_size, stream=None):
+        """Letterbox-pixel xywh [n][max_det][4] (detect_postprocess) -> boxes
+        normalised to each original image; orig_wh [n][2] int32 on the device."""
+        import torch
+        n, max_det, _ = xywh.shape
+        out = torch.empty_like(xywh)
+        check(lib().vrs_detect_unletterbox(self.handle, n, max_det, img_size, _ptr(orig_wh), _ptr(count),
+                                           _ptr(xywh), _ptr(out), _stream(stream)))
+        return out
+
     def detect_decode_grid(self, boxes, ax, ay, strides, out, stream=None):
         n, _, a = boxes.shape
         check(lib().vrs_detect_decode_grid(self.handle, _ptr(boxes), _ptr(ax), _ptr(ay), _ptr(strides), n, a,
@@ -338,6 +350,17 @@ class Model:
             check(lib().vrs_model_load_param(self.handle, name.encode(), a.ctypes.data, a.size))
         check(lib().vrs_model_finalize(self.handle))
         return self
+
+    def load_safetensors(self, path, finalize=True):
+        """load_weights_from_safetensors: parameters by name from a local file;
+        returns (loaded, missing) counts.  finalize=True folds BN and uploads
+        (every parameter must then have been found)."""
+        n_loaded, n_missing = C.c_int32(), C.c_int32()
+        check(lib().vrs_model_load_safetensors(self.handle, os.fsencode(path), C.byref(n_loaded),
+                                               C.byref(n_missing)))
+        if finalize:
+            check(lib().vrs_model_finalize(self.handle))
+        return n_loaded.value, n_missing.value
 
     def output_shapes(self):
         out = []
