@@ -68,7 +68,15 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   // ds_read_b128 (row stride 144 B for BK=64 bf16) start on distinct 4-bank
   // groups of the 64 banks (measured: 4% conflict cycles vs 34% at +16).
   constexpr int PAD = 8;
-  constexpr int LDK = BK + PAD;              // LDS row stride in elements
+  // bf16 with 32-deep steps: 64-byte rows, no padding, 16-byte chunk j of
+  // row r stored at chunk j ^ ((r >> 2) & 3): the 16 rows a quarter-wave
+  // reads (one chunk each) and the 4 rows x 4 chunks it writes both cover
+  // the 64 banks once (padded rows left the writes 2-way conflicted: 39 %
+  // conflict cycles on the 32x256 tile).
+  // (Wave tiles above 64x64 keep the padded rows: their register budget
+  // has no room for the swizzled addressing.)
+  constexpr bool SWZ = !F8 && sizeof(T) == 2 && BK == 32 && (BM / WGM) * (BN / WGN) <= 64 * 64;
+  constexpr int LDK = BK + (SWZ ? 0 : PAD);  // LDS row stride in elements
   constexpr int GPR = BK / 8;                // 8-element groups per tile row (B, and A when !F8)
   constexpr int GPRA = F8 ? BK / 16 : GPR;   // 16-byte weight chunks per row
   constexpr int AEL = F8 ? 16 : 8;           // weight elements per chunk
@@ -98,8 +106,13 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   __shared__ __attribute__((aligned(16))) T smem0[BUF_ELEMS];
   __shared__ __attribute__((aligned(16))) T smem1[BUF_ELEMS];
   auto sbuf = [&](int b) -> T* { return b ? smem1 : smem0; };
-
+  // element offset of 8-element chunk `chunk` of LDS row `row`
   const int tid = threadIdx.x;
+  // LDS slot of this thread's staged chunks: chunk i of the thread is row
+  // tid / GPR + i * NT / GPR (a multiple of 4 further down: same swizzle)
+  static_assert(!SWZ || (NT / GPR) % 4 == 0, "swizzle period");
+  const int st_row = tid / GPR, st_chunk = tid % GPR;
+  const int st_off = st_row * LDK + (SWZ ? st_chunk ^ ((st_row >> 2) & 3) : st_chunk) * 8;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
   static_assert(WGM * WGN == 4 || WGM * WGN == 8, "4 or 8 waves");
@@ -214,12 +227,12 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       const int c = tid + i * NT;
-      if (A_FULL || c < BM * GPR) E::store(&sA[(c / GPR) * LDK + (c % GPR) * 8], ra[i]);
+      if (A_FULL || c < BM * GPR) E::store(&sA[st_off + i * (NT / GPR) * LDK], ra[i]);
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
       const int c = tid + i * NT;
-      if (B_FULL || c < BN * GPR) E::store(&sB[(c / GPR) * LDK + (c % GPR) * 8], rb[i]);
+      if (B_FULL || c < BN * GPR) E::store(&sB[st_off + i * (NT / GPR) * LDK], rb[i]);
     }
   };
 
@@ -233,7 +246,10 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
 
   const int nk = (a.K + BK - 1) / BK;
   const int frag_row = lane & 31;
-  const int frag_k = (lane >> 5) * 8;
+  // fragment rows are frag_row plus multiples of 32, so their swizzle term is
+  // (frag_row >> 2) & 3 for every tile row
+  const int frag_swz = SWZ ? (frag_row >> 2) & 3 : 0;
+  auto frag_off = [&](int kk) { return ((kk * 2 + (lane >> 5)) ^ frag_swz) * 8; };
 
   if constexpr (PIPE) {
     // Step k: LDS buffer k&1 holds step k; register set (k+1)&1 holds step
@@ -288,12 +304,12 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
 #pragma unroll
         for (int i = 0; i < A_IT; ++i) {
           const int c = tid + i * NT;
-          E::store(&sA[(c / GPR) * LDK + (c % GPR) * 8], ra[i]);
+          E::store(&sA[st_off + i * (NT / GPR) * LDK], ra[i]);
         }
 #pragma unroll
         for (int i = 0; i < B_IT; ++i) {
           const int c = tid + i * NT;
-          E::store(&sB[(c / GPR) * LDK + (c % GPR) * 8], rb[i]);
+          E::store(&sB[st_off + i * (NT / GPR) * LDK], rb[i]);
         }
       }
     };
@@ -329,10 +345,10 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
         G fa[TM], fb[TN];
 #pragma unroll
         for (int i = 0; i < TM; ++i)
-          fa[i] = E::load(&sA[(wm * WTM + i * 32 + frag_row) * LDK + kk * 16 + frag_k]);
+          fa[i] = E::load(&sA[(wm * WTM + i * 32 + frag_row) * LDK + frag_off(kk)]);
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          fb[j] = E::load(&sB[(wn * WTN + j * 32 + frag_row) * LDK + kk * 16 + frag_k]);
+          fb[j] = E::load(&sB[(wn * WTN + j * 32 + frag_row) * LDK + frag_off(kk)]);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -366,10 +382,10 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
       G fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
-        fa[i] = E::load(&sA[(wm * WTM + i * 32 + frag_row) * LDK + kk * 16 + frag_k]);
+        fa[i] = E::load(&sA[(wm * WTM + i * 32 + frag_row) * LDK + frag_off(kk)]);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        fb[j] = E::load(&sB[(wn * WTN + j * 32 + frag_row) * LDK + kk * 16 + frag_k]);
+        fb[j] = E::load(&sB[(wn * WTN + j * 32 + frag_row) * LDK + frag_off(kk)]);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -510,7 +526,8 @@ __device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
   using T = bf16_t;
   using E = Elt<T>;
   using G = E::group;
-  constexpr int PAD = 8, LDK = BK + PAD, GPR = BK / 8;
+  constexpr bool SWZ = BK == 32;                        // same LDS layout as conv_body
+  constexpr int PAD = 8, LDK = BK + (SWZ ? 0 : PAD), GPR = BK / 8;
   constexpr int NT = 64 * WGM * WGN;
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -525,8 +542,10 @@ __device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
   __shared__ __attribute__((aligned(16))) T smem1[TILE_ELEMS];
   __shared__ __attribute__((aligned(16))) T sstage[WGM * WGN * WTN * SROW];
   auto sbuf = [&](int b) -> T* { return b ? smem1 : smem0; };
-
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  static_assert(!SWZ || (NT / GPR) % 4 == 0, "swizzle period");
+  const int st_row = tid / GPR, st_chunk = tid % GPR;
+  const int st_off = st_row * LDK + (SWZ ? st_chunk ^ ((st_row >> 2) & 3) : st_chunk) * 8;
   const int wm = wave / WGN, wn = wave % WGN, hq = lane >> 5;
   const int HWo = a.Ho * a.Wo;
   const float inv_hwo = 1.0f / (float)HWo, inv_wo = 1.0f / (float)a.Wo;
@@ -595,17 +614,19 @@ __device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       const int c = tid + i * NT;
-      E::store(&sA[(c / GPR) * LDK + (c % GPR) * 8], ra[i]);
+      E::store(&sA[st_off + i * (NT / GPR) * LDK], ra[i]);
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
       const int c = tid + i * NT;
-      E::store(&sB[(c / GPR) * LDK + (c % GPR) * 8], rb[i]);
+      E::store(&sB[st_off + i * (NT / GPR) * LDK], rb[i]);
     }
   };
 
   f32x16_t acc[TM][TN];
-  const int frag_row = lane & 31, frag_k = hq * 8;
+  const int frag_row = lane & 31;
+  const int frag_swz = SWZ ? (frag_row >> 2) & 3 : 0;
+  auto frag_off = [&](int kk) { return ((kk * 2 + hq) ^ frag_swz) * 8; };
   auto step = [&](int cur, const G (&wa)[A_IT], const G (&wb)[B_IT], G (&la)[A_IT], G (&lb)[B_IT]) {
     load_set(la, lb);
     store_set(cur ^ 1, wa, wb);
@@ -615,9 +636,9 @@ __device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
     for (int kk = 0; kk < BK / 16; ++kk) {
       G fa[TM], fb[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = E::load(&sA[(wm * WTM + i * 32 + frag_row) * LDK + kk * 16 + frag_k]);
+      for (int i = 0; i < TM; ++i) fa[i] = E::load(&sA[(wm * WTM + i * 32 + frag_row) * LDK + frag_off(kk)]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = E::load(&sB[(wn * WTN + j * 32 + frag_row) * LDK + kk * 16 + frag_k]);
+      for (int j = 0; j < TN; ++j) fb[j] = E::load(&sB[(wn * WTN + j * 32 + frag_row) * LDK + frag_off(kk)]);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
