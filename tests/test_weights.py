@@ -98,3 +98,34 @@ def test_errors(tmp_path):
             _model().load_safetensors(tmp_path / f"{f}.safetensors", finalize=False)
     with pytest.raises(vrs.VrsError):
         _model().load_safetensors(tmp_path / "absent.safetensors", finalize=False)
+
+
+def test_corrupted_files_fail_cleanly(tmp_path):
+    """Random byte and length corruptions of a valid file either load or
+    raise VrsError (no crash, no hang)."""
+    m0 = _model()
+    P = seeded_params(m0.params())
+    small = dict(sorted(P.items())[:6])
+    _write(tmp_path / "w.safetensors", {k: ("F32", v) for k, v in small.items()})
+    raw = bytearray((tmp_path / "w.safetensors").read_bytes())
+    hlen = struct.unpack("<Q", raw[:8])[0]
+    rng = np.random.default_rng(0)
+    outcomes = {"ok": 0, "err": 0}
+    for trial in range(300):
+        b = bytearray(raw)
+        kind = trial % 3
+        if kind == 0:      # flip bytes inside the JSON header
+            for _ in range(int(rng.integers(1, 4))):
+                b[8 + int(rng.integers(0, hlen))] = int(rng.integers(0, 256))
+        elif kind == 1:    # truncate anywhere
+            b = b[: int(rng.integers(0, len(b)))]
+        else:              # corrupt the header length
+            b[:8] = struct.pack("<Q", int(rng.integers(0, 2 * len(raw))))
+        f = tmp_path / f"c{trial}.safetensors"
+        f.write_bytes(bytes(b))
+        try:
+            _model().load_safetensors(f, finalize=False)
+            outcomes["ok"] += 1
+        except vrs.VrsError:
+            outcomes["err"] += 1
+    assert outcomes["err"] > 100

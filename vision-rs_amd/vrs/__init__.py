@@ -138,7 +138,7 @@ def lib():
 
 def check(rc: int) -> int:
     if rc < 0:
-        raise VrsError(rc, lib().vrs_last_error().decode())
+        raise VrsError(rc, lib().vrs_last_error().decode(errors="replace"))
     return rc
 
 
@@ -230,7 +230,7 @@ class Context:
         d = DetectDesc(n, nc, img_h, img_w, len(strides), st, thr, max_det)
         ws_bytes = lib().vrs_detect_workspace_size(C.byref(d))
         if ws_bytes == 0:
-            raise VrsError(-1, lib().vrs_last_error().decode())
+            raise VrsError(-1, lib().vrs_last_error().decode(errors="replace"))
         dev = boxes.device
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         count = torch.empty(n, dtype=torch.int32, device=dev)
