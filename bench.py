@@ -365,6 +365,8 @@ def main() -> int:
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "f32", "fp8"])
     ap.add_argument("--no-fp8", action="store_true", help="skip the fp8 second run (BASELINE config 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--streams", type=int, default=4,
+                    help="streams the graph capture spreads independent launches over (1 = serial)")
     ap.add_argument("--layers", action="store_true", help="also print the per-layer table to stderr")
     ap.add_argument("--micro", action="store_true",
                     help="instead: BASELINE configs 2-4 as isolated kernels, one JSON line each")
@@ -406,6 +408,7 @@ def main() -> int:
         log(f"[bench] YOLO26{a.variant} {['f32', 'bf16', 'fp8'][dtype]} bs{a.batch} {a.size}x{a.size}: building")
         m = vrs.Model(ctx, desc, a.batch, a.size, a.size, dtype, 1e-3)
         m.load(P)
+        m.set_streams(a.streams)
         outs = m.alloc_outputs()
         with torch.cuda.stream(stream):
             if dtype == vrs.FP8:
@@ -472,7 +475,7 @@ def main() -> int:
         "dtype": a.dtype, "data": "synthetic",
         "config": {"workload": f"YOLO26{a.variant} end-to-end forward {a.size}x{a.size} batch {a.batch}",
                    "batch": a.batch, "size": a.size, "variant": a.variant, "classes": 80,
-                   "weights": "seeded Kaiming-normal, identity BN folded", "graph": "hipGraph replay",
+                   "weights": "seeded Kaiming-normal, identity BN folded", "graph": f"hipGraph replay, {a.streams} capture streams",
                    "forward_tflop": round(total_flops / 1e12, 3),
                    "achieved_tflops_e2e": round(total_flops / (ms / 1e3) / 1e12, 1)},
         "roofline": roof,

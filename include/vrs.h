@@ -296,6 +296,12 @@ int vrs_model_forward(vrs_model* m, const float* x, float* const* outputs, void*
  * these buffers into a hipGraph; vrs_model_replay launches it (run_inplace). */
 int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void* stream);
 int vrs_model_replay(vrs_model* m, void* stream);
+/* Capture concurrency (no counterpart in the reference, whose graphs run on
+ * one stream): vrs_model_capture spreads the launches over this many streams
+ * (1..8, default 4), each launch waiting only for earlier launches that touch
+ * overlapping buffer channels, so independent branches run concurrently in
+ * the replayed graph.  1 = one serial chain. */
+int vrs_model_set_streams(vrs_model* m, int32_t streams);
 /* Number of kernel launches in one forward and their "layer:kernel" names
  * (valid after the first vrs_model_forward / vrs_model_capture). */
 int vrs_model_num_launches(const vrs_model* m);

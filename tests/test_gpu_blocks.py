@@ -162,6 +162,37 @@ def test_yolo26_weights_from_safetensors(dtype, tmp_path):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+@pytest.mark.parametrize("streams", [1, 4])
+def test_yolo26m_graph_replay_matches_eager(streams):
+    """The captured graph (launches spread over `streams` streams with
+    buffer-conflict dependencies) replayed three times, with eager work and
+    synchronisation between the replays, gives bit for bit the eager forward
+    on every replay."""
+    import torch
+    x = np.random.default_rng(4).uniform(0, 1, (2, 3, 320, 320)).astype(np.float32)
+    desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="m", one2one=True)
+    m = vrs.Model(ctx(), desc, 2, 320, 320, vrs.BF16, 1e-3)
+    m.load(_yolo_params(m, bn="random", bf16=True))
+    m.set_streams(streams)
+    xd = dev(x)
+    ref = [o.clone() for o in m.forward(xd)]
+    torch.cuda.synchronize()
+    outs = m.alloc_outputs()
+    st = torch.cuda.Stream()
+    m.capture(xd, outs, st.cuda_stream)
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        m.replay(st.cuda_stream)
+        st.synchronize()
+        for a, b in zip(outs, ref):
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32)), (rep, streams)
+        junk = torch.randn(1 << 20, device="cuda") * 2   # eager work between replays
+        torch.cuda.synchronize()
+        del junk
+
+
 def test_yolo26n_f32_640_vs_oracle():
     """YOLO26n, 1x3x640x640 U[0,1), Kaiming-normal seed 0, identity BN (eps 1e-3)."""
     x = np.random.default_rng(0).uniform(0, 1, (1, 3, 640, 640)).astype(np.float32)

@@ -65,6 +65,17 @@ struct ConvStep {
   int tile8 = VRS_TILE_AUTO;
 };
 
+// A launch's memory accesses, for the dependency graph of a capture:
+// resource (>= 0 an activation buffer, kResInput the input image, kResOut - i
+// output i) and a channel range [c0, c1).
+struct Access {
+  int res, c0, c1;
+};
+struct LaunchIO {
+  std::vector<Access> rd, wr;
+};
+constexpr int kResInput = -1, kResOut = -2;
+
 struct Step {
   enum Type { PACK, CONV, POOL, UP, ATTN, UNPACK, STEM } type;
   int conv = -1;      // CONV / ATTN (the PE conv's parameters)
@@ -92,6 +103,10 @@ struct vrs_model {
   // prepared launches for the last (x, outputs) pointers
   std::vector<Launch> launches;
   std::vector<std::string> labels;
+  std::vector<LaunchIO> io;      // per launch: what it reads and writes
+  int streams = 4;               // capture concurrency (1 = one serial chain)
+  std::vector<hipStream_t> side; // extra capture streams (default priority)
+  std::vector<hipEvent_t> evs;   // capture-time dependency events
   const float* prep_x = nullptr;
   std::vector<float*> prep_outs;
   hipGraph_t graph = nullptr;
@@ -502,10 +517,30 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
   if (!m->launches.empty() && m->prep_x == x && m->prep_outs == o) return VRS_OK;
   std::vector<Launch> ls;
   std::vector<std::string> labels;
+  std::vector<LaunchIO> io;
   int rc = VRS_OK;
+  auto acc = [](V v) { return Access{v.buf, v.c_off, v.c_off + v.c}; };
+  constexpr int kAll = 1 << 30;
   for (const Step& st : m->steps) {
     const size_t before = ls.size();
     std::string label;
+    LaunchIO sio;   // this step's accesses (every launch of the step gets them)
+    switch (st.type) {
+      case Step::PACK: sio.rd = {{kResInput, 0, kAll}}; sio.wr = {acc(st.b)}; break;
+      case Step::CONV: {
+        const ConvStep& c = m->convs[st.conv];
+        sio.rd = {acc(c.x)};
+        if (c.has_res) sio.rd.push_back(acc(c.res));
+        if (c.out_idx >= 0) sio.wr = {{kResOut - c.out_idx, 0, kAll}};
+        else sio.wr = {acc(c.y)};
+        break;
+      }
+      case Step::STEM: sio.rd = {{kResInput, 0, kAll}}; sio.wr = {acc(m->convs[st.conv].y)}; break;
+      case Step::POOL: sio.rd = {acc(st.a)}; sio.wr = {acc(st.a)}; break;
+      case Step::UP: case Step::ATTN: sio.rd = {acc(st.a)}; sio.wr = {acc(st.b)}; break;
+      case Step::UNPACK: sio.rd = {acc(st.a)}; sio.wr = {{kResOut - st.out_idx, 0, kAll}}; break;
+    }
+    auto flush_io = [&]() { while (io.size() < ls.size()) io.push_back(sio); };
     switch (st.type) {
       case Step::PACK:
         rc = prep_pack_input(m->ctx, x, m->batch, m->in_c, m->in_h, m->in_w, view_of(m, st.b), act_dt(m), ls);
@@ -546,6 +581,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         }
         if (rc) return rc;
         for (size_t i = conv_first; i < ls.size(); ++i) labels.push_back(label + ":" + ls[i].name);
+        flush_io();
         continue;
       }
       case Step::STEM: {
@@ -577,9 +613,11 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
     }
     if (rc) return rc;
     for (size_t i = before; i < ls.size(); ++i) labels.push_back(label + ":" + ls[i].name);
+    flush_io();
   }
   m->launches = std::move(ls);
   m->labels = std::move(labels);
+  m->io = std::move(io);
   m->prep_x = x;
   m->prep_outs = o;
   return VRS_OK;
@@ -860,17 +898,84 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
   if (m->exec) { (void)hipGraphExecDestroy(m->exec); m->exec = nullptr; }
   if (m->graph) { (void)hipGraphDestroy(m->graph); m->graph = nullptr; }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  VRS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-  for (const Launch& l : m->launches) {
-    if ((rc = run(l, s))) {
-      hipGraph_t g;
-      (void)hipStreamEndCapture(s, &g);
-      if (g) (void)hipGraphDestroy(g);
-      return rc;
+  // Concurrency: the launches go to up to m->streams streams of the capture,
+  // each waiting (through events) only for the earlier launches whose
+  // accesses conflict with its own -- a write against any overlapping read
+  // or write of the same buffer and channel range.  Independent branches
+  // (the Detect head's six chains, slices of one concat buffer) then become
+  // parallel graph branches.
+  const int n = (int)m->launches.size();
+  const int K = std::max(1, std::min(m->streams, 8));
+  while ((int)m->side.size() < K - 1) {
+    hipStream_t t;
+    VRS_HIP(hipStreamCreateWithFlags(&t, hipStreamNonBlocking));
+    m->side.push_back(t);
+  }
+  while ((int)m->evs.size() < n + K) {
+    hipEvent_t e;
+    VRS_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    m->evs.push_back(e);
+  }
+  std::vector<hipStream_t> ss(1, s);
+  for (int k = 0; k < K - 1; ++k) ss.push_back(m->side[k]);
+  auto conflict = [](const LaunchIO& a, const LaunchIO& b) {   // a after b
+    auto ov = [](const Access& x, const Access& y) { return x.res == y.res && x.c0 < y.c1 && y.c0 < x.c1; };
+    for (const Access& w : a.wr) {
+      for (const Access& r : b.rd) if (ov(w, r)) return true;
+      for (const Access& r : b.wr) if (ov(w, r)) return true;
     }
+    for (const Access& r : a.rd)
+      for (const Access& w : b.wr) if (ov(r, w)) return true;
+    return false;
+  };
+  VRS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  auto abort_capture = [&](int code) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(s, &g);
+    if (g) (void)hipGraphDestroy(g);
+    return code;
+  };
+  hipEvent_t fork = m->evs[n];
+  if (hipEventRecord(fork, s) != hipSuccess) return abort_capture(fail(VRS_EHIP, "capture: fork event"));
+  for (int k = 1; k < K; ++k)
+    if (hipStreamWaitEvent(ss[k], fork, 0) != hipSuccess) return abort_capture(fail(VRS_EHIP, "capture: fork wait"));
+  std::vector<int> stream_of(n, 0), last(K, -1);
+  std::vector<std::vector<int>> waited(K, std::vector<int>(K, -1));   // [s][t]: launches of t that s has waited for
+  for (int i = 0; i < n; ++i) {
+    std::vector<int> deps;
+    for (int j = 0; j < i; ++j)
+      if (conflict(m->io[i], m->io[j])) deps.push_back(j);
+    int st = 0;
+    if (!deps.empty()) {
+      st = stream_of[deps.back()];
+    } else {
+      for (int k = 1; k < K; ++k) if (last[k] < last[st]) st = k;
+    }
+    for (int j : deps) {
+      const int t = stream_of[j];
+      if (t == st || waited[st][t] >= j) continue;
+      if (hipStreamWaitEvent(ss[st], m->evs[j], 0) != hipSuccess)
+        return abort_capture(fail(VRS_EHIP, "capture: dependency wait"));
+      waited[st][t] = j;
+    }
+    if ((rc = run(m->launches[i], ss[st]))) return abort_capture(rc);
+    if (hipEventRecord(m->evs[i], ss[st]) != hipSuccess) return abort_capture(fail(VRS_EHIP, "capture: event"));
+    stream_of[i] = st;
+    last[st] = i;
+  }
+  for (int k = 1; k < K; ++k) {   // join every side stream back into the origin
+    if (hipEventRecord(m->evs[n + k], ss[k]) != hipSuccess || hipStreamWaitEvent(s, m->evs[n + k], 0) != hipSuccess)
+      return abort_capture(fail(VRS_EHIP, "capture: join"));
   }
   VRS_HIP(hipStreamEndCapture(s, &m->graph));
   VRS_HIP(hipGraphInstantiate(&m->exec, m->graph, nullptr, nullptr, 0));
+  return VRS_OK;
+}
+
+int vrs_model_set_streams(vrs_model* m, int32_t streams) {
+  if (!m) return fail(VRS_EINVAL, "null model");
+  if (streams < 1 || streams > 8) return fail(VRS_EINVAL, "vrs_model_set_streams: %d (1..8)", streams);
+  m->streams = streams;
   return VRS_OK;
 }
 
@@ -979,6 +1084,8 @@ int vrs_model_destroy(vrs_model* m) {
   if (!m) return VRS_OK;
   if (m->exec) (void)hipGraphExecDestroy(m->exec);
   if (m->graph) (void)hipGraphDestroy(m->graph);
+  for (hipEvent_t e : m->evs) (void)hipEventDestroy(e);
+  for (hipStream_t t : m->side) (void)hipStreamDestroy(t);
   for (void* p : m->allocs) (void)hipFree(p);
   delete m;
   return VRS_OK;

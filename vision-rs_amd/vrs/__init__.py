@@ -108,6 +108,7 @@ SIGNATURES = {
     "vrs_model_forward": (C.c_int, [_vp, _vp, _P(_vp), _vp]),
     "vrs_model_capture": (C.c_int, [_vp, _vp, _P(_vp), _vp]),
     "vrs_model_replay": (C.c_int, [_vp, _vp]),
+    "vrs_model_set_streams": (C.c_int, [_vp, _i32]),
     "vrs_model_num_launches": (C.c_int, [_vp]),
     "vrs_model_launch_name": (C.c_char_p, [_vp, _i32]),
     "vrs_model_launch_work": (C.c_int, [_vp, _i32, _P(C.c_double), _P(C.c_double)]),
@@ -389,6 +390,9 @@ class Model:
 
     def replay(self, stream):
         check(lib().vrs_model_replay(self.handle, C.c_void_p(stream)))
+
+    def set_streams(self, n):
+        check(lib().vrs_model_set_streams(self.handle, n))
 
     def launch_names(self):
         n = lib().vrs_model_num_launches(self.handle)
