@@ -353,6 +353,19 @@ def micro(ctx, emit):
           "frac_hbm": round(comp / ms / 1e6 / PEAK_HBM_GBS, 4), "issued_gather_mb": round(issued / 1e6, 1),
           "buffer_sets": n_sets})
 
+    # ---- letterbox preprocessing: 64 RGB8 1280x720 frames -> [64,3,640,640] f32 ----
+    nimg, (lw, lh), S = 64, (1280, 720), 640
+    src_b = nimg * lw * lh * 3
+    out_b = nimg * 3 * S * S * 4
+    n_sets = sets_for(src_b + out_b)
+    srcs = [torch.randint(0, 256, (src_b,), dtype=torch.uint8, device=dev) for _ in range(n_sets)]
+    outs_lb = [torch.empty(nimg, 3, S, S, device=dev) for _ in range(n_sets)]
+    offs = [i * lw * lh * 3 for i in range(nimg)]
+    ms = _time_launches(lambda i: ctx.letterbox(srcs[i], offs, [(lw, lh)] * nimg, S, out=outs_lb[i]), n_sets, iters=30)
+    emit({"config": "letterbox 64x 1280x720 RGB8 -> 640 f32 NCHW", "us": round(ms * 1e3, 2),
+          "mb": round((src_b + out_b) / 1e6, 1), "gbs": round((src_b + out_b) / ms / 1e6, 1),
+          "frac_hbm": round((src_b + out_b) / ms / 1e6 / PEAK_HBM_GBS, 4), "buffer_sets": n_sets})
+
 
 def main() -> int:
     ap = argparse.ArgumentParser()

@@ -212,6 +212,19 @@ int vrs_detect_unletterbox(vrs_ctx* ctx, int32_t n, int32_t max_det, int32_t img
                            const int32_t* orig_wh, const int32_t* count, const float* xywh,
                            float* out, void* stream);
 
+/* Letterbox preprocessing, preprocess_image_raw (examples/yolo26.rs:1229-1253):
+ * n RGB8 images in device memory (image i: wh[2i] x wh[2i+1] pixels, rows of
+ * 3*w bytes with no padding, starting at byte offsets[i] of rgb; offsets and
+ * wh are HOST arrays, every image must lie inside rgb_bytes) -> the model input
+ * [n][3][img_size][img_size] float32 (device).  scale = img_size / max(w, h)
+ * in f64, new = round(dim * scale); the image crate's Triangle resize (image
+ * 0.25.10 imageops::resize: vertical then horizontal pass, float32, rounded
+ * half away from zero to u8); centred with integer padding (img_size - new)/2
+ * on a 114/255 canvas; values u8 / 255.  Images shrunk by more than 62x per
+ * axis are rejected (VRS_EUNSUPPORTED). */
+int vrs_letterbox(vrs_ctx* ctx, int32_t n, int32_t img_size, const uint8_t* rgb, int64_t rgb_bytes,
+                  const int64_t* offsets, const int32_t* wh, float* out, void* stream);
+
 /* DetectDecodeOp / detect_decode_forward (kernels/detect_decode.rs:36-217):
  * grid-unit anchors, [n][4][A] in and out. */
 int vrs_detect_decode_grid(vrs_ctx* ctx, const float* boxes, const float* anchor_x,

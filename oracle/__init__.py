@@ -47,6 +47,7 @@ def lib():
         _lib.orc_detect_postprocess.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int, i32p,
                                                 C.c_int, C.c_float, C.c_int, i32p, f32p, i32p, i32p, f32p]
         _lib.orc_detect_unletterbox.argtypes = [C.c_int, C.c_int, C.c_int, i32p, i32p, f32p, f32p]
+        _lib.orc_letterbox.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, f32p, f32p, i32p]
         _lib.orc_msda.argtypes = [f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, i32p, i32p,
                                   f32p, f32p, f32p, C.c_int, C.c_int, f32p]
         _lib.orc_add.argtypes = [f32p, f32p, f32p, C.c_long]
@@ -178,6 +179,25 @@ def detect_unletterbox(count, xywh, orig_wh, img_size):
     out = np.empty_like(xywh)
     lib().orc_detect_unletterbox(B, max_det, img_size, _i(wh), _i(count), _f(xywh), _f(out))
     return out
+
+
+def letterbox(img, img_size, resized=False):
+    """RGB8 image [h, w, 3] (uint8) -> model input [3, img_size, img_size]
+    float32 (preprocess_image_raw, examples/yolo26.rs:1229-1253).  With
+    resized=True also returns the Triangle-resized [new_h, new_w, 3] float32
+    values before rounding to u8."""
+    img = np.ascontiguousarray(img, np.uint8)
+    h, w, _ = img.shape
+    out = np.empty((3, img_size, img_size), np.float32)
+    nwh = np.zeros(2, np.int32)
+    scale = img_size / max(w, h)
+    cap = 3 * (int(w * scale + 1)) * (int(h * scale + 1)) + 3
+    res = np.empty(cap, np.float32)
+    lib().orc_letterbox(img.ctypes.data, w, h, img_size, _f(out), _f(res), _i(nwh))
+    if not resized:
+        return out
+    nw, nh = int(nwh[0]), int(nwh[1])
+    return out, res[: 3 * nw * nh].reshape(nh, nw, 3).copy()
 
 
 def msda(value, shapes, ref, off, attw):

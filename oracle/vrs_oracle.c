@@ -22,6 +22,10 @@
  *   orc_detect_postprocess closed-form decode + brute-force argmax/sort checks
  *   orc_detect_unletterbox closed forms (square image: divide by the size;
  *                         2:1 image: known scale and padding)
+ *   orc_letterbox         torch F.interpolate(bilinear, antialias=True) on the
+ *                         float stage (same triangle filter, PIL formulation),
+ *                         closed forms (identity, 2x [1,3,3,1]/8, a half-way
+ *                         rounding case), geometry of the reference
  *   orc_msda              torch F.grid_sample (bilinear, zeros, align_corners=False)
  *                         + brute-force tiny cases
  */
@@ -469,4 +473,95 @@ void orc_detect_unletterbox(int B, int max_det, int img_size, const int* orig_wh
       o[3] = d[3] / sy;
     }
   }
+}
+
+/* Letterbox, preprocess_image_raw (examples/yolo26.rs:1229-1253): scale =
+ * img / max(w, h) in f64, new = round(dim * scale) (half away from zero),
+ * image::imageops::resize(img, new_w, new_h, FilterType::Triangle), centred at
+ * ((img - new_w) / 2, (img - new_h) / 2) on a 114/255 canvas, NCHW u8 / 255.
+ * The resize is the image crate's (0.25.10, Cargo.lock:2807-2810; the crate is
+ * not vendored), restated from its published imageops::sample:
+ *   resize: same size -> copy; else tmp = vertical_sample(img, new_h) (float32
+ *     buffer [new_h][w]), out = horizontal_sample(tmp, new_w);
+ *   each pass, per output index o: ratio = src / dst (f32), sratio = max(ratio,
+ *     1), support = 1 * sratio (triangle support 1), centre = (o + 0.5) *
+ *     ratio, left = clamp(floor(centre - support), 0, src - 1), right =
+ *     clamp(ceil(centre + support), left + 1, src), weights w_i =
+ *     tri((i - (centre - 0.5)) / sratio) for i in [left, right), each divided
+ *     by their running float32 sum; t = sum_i p_i * w_i in order;
+ *   horizontal_sample clamps t to [0, 255] and rounds half away from zero.
+ * Separate multiplies and adds (no FMA), as Rust evaluates them.
+ * resized (optional): the [new_h][new_w][3] float32 values before rounding. */
+static float orc_tri(float x) {
+  const float a = fabsf(x);
+  return a < 1.0f ? 1.0f - a : 0.0f;
+}
+static int orc_resample_weights(int o, int src, int dst, float* w, int* first) {
+  const float ratio = (float)src / (float)dst;
+  const float sratio = ratio < 1.0f ? 1.0f : ratio;
+  const float support = 1.0f * sratio;
+  const float centre = ((float)o + 0.5f) * ratio;
+  long left = (long)floorf(centre - support);
+  left = left < 0 ? 0 : (left > src - 1 ? src - 1 : left);
+  long right = (long)ceilf(centre + support);
+  right = right < left + 1 ? left + 1 : (right > src ? src : right);
+  const float c = centre - 0.5f;
+  float sum = 0.0f;
+  for (long i = left; i < right; ++i) {
+    w[i - left] = orc_tri(((float)i - c) / sratio);
+    sum += w[i - left];
+  }
+  for (long i = left; i < right; ++i) w[i - left] /= sum;
+  *first = (int)left;
+  return (int)(right - left);
+}
+void orc_letterbox(const uint8_t* rgb, int w, int h, int img_size, float* out, float* resized, int* new_wh) {
+  const double scale = (double)img_size / (double)(w > h ? w : h);
+  const int nw = (int)round((double)w * scale), nh = (int)round((double)h * scale);
+  const int pad_x = (img_size - nw) / 2, pad_y = (img_size - nh) / 2;
+  new_wh[0] = nw;
+  new_wh[1] = nh;
+  float* res = (float*)malloc(sizeof(float) * 3 * ((size_t)nw * nh + 1));
+  if (nw == w && nh == h) {
+    for (long i = 0; i < (long)w * h * 3; ++i) res[i] = (float)rgb[i];
+  } else {
+    const int maxt = 2 * (w > h ? w : h) + 4;
+    float* wts = (float*)malloc(sizeof(float) * maxt);
+    float* tmp = (float*)malloc(sizeof(float) * 3 * ((size_t)nh * w + 1));
+    for (int oy = 0; oy < nh; ++oy) {  /* vertical_sample */
+      int top;
+      const int n = orc_resample_weights(oy, h, nh, wts, &top);
+      for (int x = 0; x < w; ++x) {
+        float t[3] = {0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < n; ++j)
+          for (int c = 0; c < 3; ++c) t[c] += (float)rgb[((size_t)(top + j) * w + x) * 3 + c] * wts[j];
+        for (int c = 0; c < 3; ++c) tmp[((size_t)oy * w + x) * 3 + c] = t[c];
+      }
+    }
+    for (int ox = 0; ox < nw; ++ox) {  /* horizontal_sample */
+      int left;
+      const int n = orc_resample_weights(ox, w, nw, wts, &left);
+      for (int y = 0; y < nh; ++y) {
+        float t[3] = {0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < n; ++i)
+          for (int c = 0; c < 3; ++c) t[c] += tmp[((size_t)y * w + left + i) * 3 + c] * wts[i];
+        for (int c = 0; c < 3; ++c) res[((size_t)y * nw + ox) * 3 + c] = t[c];
+      }
+    }
+    free(tmp);
+    free(wts);
+  }
+  if (resized) memcpy(resized, res, sizeof(float) * 3 * (size_t)nw * nh);
+  const float pad = 114.0f / 255.0f;
+  const size_t plane = (size_t)img_size * img_size;
+  for (size_t i = 0; i < 3 * plane; ++i) out[i] = pad;
+  for (int y = 0; y < nh; ++y)
+    for (int x = 0; x < nw; ++x)
+      for (int c = 0; c < 3; ++c) {
+        float v = res[((size_t)y * nw + x) * 3 + c];
+        v = v < 0.0f ? 0.0f : (v > 255.0f ? 255.0f : v);
+        const uint8_t u = (uint8_t)roundf(v);
+        out[c * plane + (size_t)(pad_y + y) * img_size + pad_x + x] = (float)u / 255.0f;
+      }
+  free(res);
 }

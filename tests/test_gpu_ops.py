@@ -427,6 +427,55 @@ def test_detect_unletterbox():
         ctx().detect_unletterbox(dev(count), dev(xywh), dev(wh), 0)
 
 
+LB_SIZES = [(1280, 720), (640, 640), (517, 333), (333, 517), (1000, 37), (5, 3), (1, 1), (17, 2000), (4000, 100),
+            (1920, 1080), (639, 641), (2, 1), (100, 100), (64, 48), (3000, 3000), (701, 299), (8, 8), (1279, 719),
+            (333, 333), (50, 2000)]
+
+
+def test_letterbox():
+    """Letterbox preprocessing of 20 images of mixed sizes (two launches),
+    bit-exact against the oracle's two-pass restatement of the Triangle
+    resize: enlargements, shrinks up to 6.25x, the identity, 1x1, thin strips,
+    saturated regions, images starting at odd byte offsets."""
+    import torch
+    rng = np.random.default_rng(9)
+    imgs = []
+    for i, (w, h) in enumerate(LB_SIZES):
+        im = rng.integers(0, 256, (h, w, 3), dtype=np.uint8)
+        if i % 4 == 1:   # saturated blocks exercise the clamp
+            im[: h // 2, : w // 2] = 255
+            im[h // 2:, w // 2:] = 0
+        imgs.append(im)
+    offs, parts, pos = [], [], 0
+    for im in imgs:
+        parts.append(np.zeros(1 + pos % 3, np.uint8))   # odd starting offsets
+        pos += parts[-1].size
+        offs.append(pos)
+        parts.append(im.reshape(-1))
+        pos += im.size
+    flat = dev(np.concatenate(parts))
+    got = ctx().letterbox(flat, offs, LB_SIZES, 640)
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    for i, im in enumerate(imgs):
+        ref = oracle.letterbox(im, 640)
+        assert np.array_equal(got[i].view(np.uint32), ref.view(np.uint32)), (i, LB_SIZES[i])
+
+
+def test_letterbox_rejections():
+    """Host-side checks, no launch: empty images, images past the buffer, and
+    shrinks beyond 62x per axis (bounded filter windows)."""
+    import torch
+    flat = torch.zeros(4000 * 100 * 3, dtype=torch.uint8, device="cuda")
+    out = torch.empty(1, 3, 64, 64, device="cuda")
+    for offs, wh, S in [([0], [(0, 10)], 64), ([1], [(4000, 100)], 640), ([-1], [(10, 10)], 64),
+                        ([0], [(4000, 100)], 64)]:
+        with pytest.raises(vrs.VrsError):
+            ctx().letterbox(flat, offs, wh, S, out=out)
+    ctx().letterbox(flat, [0], [(4000, 100)], 65, out=torch.empty(1, 3, 65, 65, device="cuda"))   # 61.5x: accepted
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("cfg", [
     (2, 30, 4, [(16, 16), (8, 8), (4, 4), (2, 2)], 4),   # level-split kernel (one wave per level)
     (1, 6, 16, [(9, 9), (5, 5), (3, 3), (2, 2)], 4),     # unrolled 4x4 kernel (> 8 heads)

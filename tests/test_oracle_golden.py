@@ -327,6 +327,66 @@ def test_detect_unletterbox_closed_forms():
     assert not out[0, 1:].any() and not out[1, 2:].any() and not out[4].any()
 
 
+LETTERBOX_SIZES = [(1280, 720, 640), (517, 333, 640), (333, 517, 640), (1000, 37, 640), (5, 3, 640),
+                   (4000, 100, 64), (17, 2000, 640), (8, 8, 4), (2, 1, 4), (640, 640, 640), (1, 1, 32)]
+
+
+@pytest.mark.parametrize("w,h,S", LETTERBOX_SIZES)
+def test_letterbox_resize_matches_torch_antialias(w, h, S):
+    """The Triangle resize (image 0.25.10, restated in orc_letterbox) against
+    torch's antialiased bilinear interpolation, an independent implementation
+    (PIL's formulation) of the same filter: tent of support max(ratio, 1)
+    centred at (o + 0.5) * ratio, weights normalised over the clamped window.
+    Compared on the float stage before u8 rounding."""
+    torch = pytest.importorskip("torch")
+    img = np.random.default_rng(w * 7 + h).integers(0, 256, (h, w, 3), dtype=np.uint8)
+    out, res = oracle.letterbox(img, S, resized=True)
+    nh, nw, _ = res.shape
+    ref = torch.nn.functional.interpolate(torch.from_numpy(img).permute(2, 0, 1)[None].float(), size=(nh, nw),
+                                          mode="bilinear", antialias=True, align_corners=False)
+    ref = ref[0].permute(1, 2, 0).numpy()
+    assert np.abs(ref - res).max() < 2e-4
+    # the canvas holds round-half-away(clamp(res)) / 255 at the centred offset
+    px, py = (S - nw) // 2, (S - nh) // 2
+    q = (np.floor(np.clip(res, 0, 255) + 0.5) / np.float32(255)).astype(np.float32)
+    assert np.array_equal(out[:, py:py + nh, px:px + nw], q.transpose(2, 0, 1))
+    pad = np.ones((S, S), bool)
+    pad[py:py + nh, px:px + nw] = False
+    assert (out[:, pad] == np.float32(114) / np.float32(255)).all()
+
+
+def test_letterbox_closed_forms():
+    """Geometry of preprocess_image_raw (examples/yolo26.rs:1229-1253) and the
+    Triangle filter's exact cases: same size is the identity, a 2x shrink
+    weights interior taps [1, 3, 3, 1] / 8 per axis, and a 2x enlargement
+    interpolates at 1/4 and 3/4 with half-way values rounded away from zero."""
+    rng = np.random.default_rng(5)
+    # geometry: new size rounds in f64, padding is integer-halved
+    for (w, h, nw, nh) in [(1280, 720, 640, 360), (333, 517, 412, 640), (1000, 37, 640, 24), (17, 2000, 5, 640)]:
+        _, res = oracle.letterbox(np.zeros((h, w, 3), np.uint8), 640, resized=True)
+        assert res.shape == (nh, nw, 3)
+    # identity
+    img = rng.integers(0, 256, (640, 640, 3), dtype=np.uint8)
+    out = oracle.letterbox(img, 640)
+    assert np.array_equal(out, (img.astype(np.float32) / np.float32(255)).transpose(2, 0, 1))
+    # 2x shrink: 8x8 -> 4x4, output (1, 1) reads rows/cols 1..4 with [1,3,3,1]/8
+    img = rng.integers(0, 256, (8, 8, 3), dtype=np.uint8)
+    _, res = oracle.letterbox(img, 4, resized=True)
+    k = np.array([1, 3, 3, 1], np.float64) / 8
+    for c in range(3):
+        for oy, ox in [(1, 1), (1, 2), (2, 1), (2, 2)]:
+            win = img[2 * oy - 1:2 * oy + 3, 2 * ox - 1:2 * ox + 3, c].astype(np.float64)
+            assert abs(res[oy, ox, c] - k @ win @ k) < 1e-4
+    # 2x enlargement of the 2x1 row [0, 2]: [0, 0.5, 1.5, 2] -> u8 [0, 1, 2, 2]
+    img = np.zeros((1, 2, 3), np.uint8)
+    img[0, 1] = 2
+    out, res = oracle.letterbox(img, 4, resized=True)
+    assert res[:, :, 0].tolist() == [[0, 0.5, 1.5, 2]] * 2
+    pad = np.float32(114) / np.float32(255)
+    assert out[0].tolist() == [[pad] * 4, [0, np.float32(1) / 255, np.float32(2) / 255, np.float32(2) / 255],
+                               [0, np.float32(1) / 255, np.float32(2) / 255, np.float32(2) / 255], [pad] * 4]
+
+
 def test_msda_matches_grid_sample():
     pytest.importorskip("torch")
     shapes = [(16, 16), (8, 8), (4, 4), (2, 2)]

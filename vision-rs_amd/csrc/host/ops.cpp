@@ -274,6 +274,47 @@ int vrs_detect_unletterbox(vrs_ctx* ctx, int32_t n, int32_t max_det, int32_t img
   return run_all(ls, stream);
 }
 
+int vrs_letterbox(vrs_ctx* ctx, int32_t n, int32_t img_size, const uint8_t* rgb, int64_t rgb_bytes,
+                  const int64_t* offsets, const int32_t* wh, float* out, void* stream) {
+  if (!ctx || !rgb || !offsets || !wh || !out) return fail(VRS_EINVAL, "vrs_letterbox: null argument");
+  if (n <= 0 || img_size <= 0 || rgb_bytes <= 0) return fail(VRS_EBADSHAPE, "vrs_letterbox: empty shape");
+  if (img_size > 16384) return fail(VRS_EBADSHAPE, "vrs_letterbox: img_size %d > 16384", img_size);
+  std::vector<vrs_lb_image> ims((size_t)n);
+  for (int i = 0; i < n; ++i) {
+    const int32_t w = wh[2 * i], h = wh[2 * i + 1];
+    const int64_t off = offsets[i];
+    if (w <= 0 || h <= 0) return fail(VRS_EBADSHAPE, "vrs_letterbox: image %d is %dx%d", i, w, h);
+    if (off < 0 || off > rgb_bytes || (rgb_bytes - off) / 3 / w < h)
+      return fail(VRS_EBADSHAPE, "vrs_letterbox: image %d (%dx%d at byte %lld) runs past rgb_bytes", i, w, h,
+                  (long long)off);
+    // preprocess_image_raw: scale and new size in f64, round half away from
+    // zero, integer centring
+    const double scale = (double)img_size / (double)(w > h ? w : h);
+    const int32_t nw = (int32_t)std::round((double)w * scale), nh = (int32_t)std::round((double)h * scale);
+    // bounded filter windows: ratio <= 62 gives at most 2*62 + 2 taps
+    if ((nw > 0 && (float)w / (float)nw > 62.0f) || (nh > 0 && (float)h / (float)nh > 62.0f))
+      return fail(VRS_EUNSUPPORTED, "vrs_letterbox: image %d (%dx%d) shrinks by more than 62x", i, w, h);
+    ims[(size_t)i] = vrs_lb_image{off, w, h, nw, nh, (img_size - nw) / 2, (img_size - nh) / 2};
+  }
+  hipFunction_t f;
+  int rc = get_fn(ctx, "vrs_letterbox_f32", &f);
+  if (rc) return rc;
+  const int64_t per_image = 3ll * img_size * img_size;
+  const unsigned tiles = (unsigned)(((img_size + 63) / 64) * ((img_size + 3) / 4));
+  std::vector<Launch> ls;
+  for (int b0 = 0; b0 < n; b0 += VRS_LB_MAX_IMAGES) {
+    vrs_lb_args a{};
+    a.rgb = rgb;
+    a.out = out + (int64_t)b0 * per_image;
+    a.pad = 114.0f / 255.0f;
+    a.S = img_size;
+    a.count = std::min(VRS_LB_MAX_IMAGES, n - b0);
+    for (int k = 0; k < a.count; ++k) a.img[k] = ims[(size_t)(b0 + k)];
+    ls.push_back(make_launch("vrs_letterbox_f32", f, dim3(tiles, (unsigned)a.count), dim3(256), 0, a));
+  }
+  return run_all(ls, stream);
+}
+
 int vrs_detect_decode_grid(vrs_ctx* ctx, const float* boxes, const float* ax, const float* ay, const float* st,
                            int32_t n, int32_t a, float* out, void* stream) {
   if (!ctx || !boxes || !ax || !ay || !st || !out) return fail(VRS_EINVAL, "vrs_detect_decode_grid: null argument");

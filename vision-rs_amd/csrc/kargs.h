@@ -140,6 +140,23 @@ typedef struct {
   int32_t B, max_det, img_size;
 } vrs_unlb_args;
 
+/* Letterbox preprocessing, up to VRS_LB_MAX_IMAGES images per launch (grid.y
+ * = image).  Per image: RGB8 rows of w*3 bytes at rgb + off, the resized size
+ * (nw, nh) and the canvas offset (px, py), all computed on the host. */
+#define VRS_LB_MAX_IMAGES 16
+#define VRS_LB_MAX_TAPS 128 /* filter taps per output row/column (ratio <= 63) */
+typedef struct {
+  int64_t off;
+  int32_t w, h, nw, nh, px, py;
+} vrs_lb_image;
+typedef struct {
+  const uint8_t* rgb;
+  float* out;           /* [count][3][S][S] for these images */
+  float pad;            /* 114 / 255 in float32 */
+  int32_t S, count;
+  vrs_lb_image img[VRS_LB_MAX_IMAGES];
+} vrs_lb_args;
+
 /* Grid-unit decode on [B,4,A] (kernels/detect_decode.rs:36-86). */
 typedef struct {
   const float* boxes;

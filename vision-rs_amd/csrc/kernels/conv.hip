@@ -183,19 +183,38 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   }
 
   // (ky, kx, ci0) of the next step to load, advanced incrementally (ALIGNED:
-  // a step never crosses a tap, so ci0 wraps exactly at Cin).
+  // a step never crosses a tap).  Steps run channel-chunk-outer, tap-inner:
+  // the kh*kw taps of one BK-channel chunk are consecutive steps, so the
+  // input rows a tile reads stay in L1/L2 across its taps instead of being
+  // fetched again per tap; the weight offset of a step is
+  // (ky*kw + kx)*Cin + ci0 in the [Cout][kh][kw][Cin] packing.
+  // float32 kernels (the 1e-4 parity path) keep the tap-outer order, whose
+  // float32 summation order the network-level tolerance was set against.
+  constexpr bool TAP_INNER = sizeof(T) == 2;
   int t_ky = 0, t_kx = 0, t_ci = 0;
-  auto load_tiles = [&](int k0) {
-    if (ALIGNED) {
-#pragma unroll
-      for (int i = 0; i < A_IT; ++i) ra[i] = E::bload(rw, a_off[i], (uint32_t)k0 * sizeof(T));
-      const int ky = t_ky, kx = t_kx;
-      const uint32_t off = (uint32_t)((ky * a.W + kx) * a.x_pitch + t_ci) * sizeof(T);
+  auto advance = [&]() {
+    if constexpr (TAP_INNER) {
+      if (++t_kx == a.kw) {
+        t_kx = 0;
+        if (++t_ky == a.kh) { t_ky = 0; t_ci += BK; }
+      }
+    } else {
       t_ci += BK;
       if (t_ci == a.Cin) {
         t_ci = 0;
         if (++t_kx == a.kw) { t_kx = 0; ++t_ky; }
       }
+    }
+  };
+  auto load_tiles = [&](int k0) {
+    if (ALIGNED) {
+#pragma unroll
+      for (int i = 0; i < A_IT; ++i)
+        ra[i] = E::bload(rw, a_off[i], (TAP_INNER ? (uint32_t)((t_ky * a.kw + t_kx) * a.Cin + t_ci) : (uint32_t)k0) *
+                                           sizeof(T));
+      const int ky = t_ky, kx = t_kx;
+      const uint32_t off = (uint32_t)((ky * a.W + kx) * a.x_pitch + t_ci) * sizeof(T);
+      advance();
 #pragma unroll
       for (int i = 0; i < B_IT; ++i) {
         const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
@@ -263,14 +282,13 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
     auto load_set = [&](int k0, G (&ra)[A_IT], G (&rb)[B_IT]) {
       const uint32_t dead = k0 < a.K ? 0u : kOOB;
 #pragma unroll
-      for (int i = 0; i < A_IT; ++i) ra[i] = E::bload(rw, a_off[i] | dead, (uint32_t)k0 * (F8 ? 1u : (uint32_t)sizeof(T)));
+      for (int i = 0; i < A_IT; ++i)
+        ra[i] = E::bload(rw, a_off[i] | dead,
+                         (TAP_INNER ? (uint32_t)((t_ky * a.kw + t_kx) * a.Cin + t_ci) : (uint32_t)k0) *
+                             (F8 ? 1u : (uint32_t)sizeof(T)));
       const int ky = t_ky, kx = t_kx;
       const uint32_t off = (uint32_t)((ky * a.W + kx) * a.x_pitch + t_ci) * sizeof(T);
-      t_ci += BK;
-      if (t_ci == a.Cin) {
-        t_ci = 0;
-        if (++t_kx == a.kw) { t_kx = 0; ++t_ky; }
-      }
+      advance();
 #pragma unroll
       for (int i = 0; i < B_IT; ++i) {
         const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
@@ -592,13 +610,13 @@ __device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
     }
     const uint32_t dead = ld_tile < total ? 0u : kOOB;
 #pragma unroll
-    for (int i = 0; i < A_IT; ++i) ra[i] = E::bload(rw, a_off[i] | dead, (uint32_t)ld_k * BK * 2u);
+    for (int i = 0; i < A_IT; ++i)
+      ra[i] = E::bload(rw, a_off[i] | dead, (uint32_t)((t_ky * a.kw + t_kx) * a.Cin + t_ci) * 2u);
     const int ky = t_ky, kx = t_kx;
     const uint32_t off = (uint32_t)((ky * a.W + kx) * a.x_pitch + t_ci) * 2u;
-    t_ci += BK;
-    if (t_ci == a.Cin) {
-      t_ci = 0;
-      if (++t_kx == a.kw) { t_kx = 0; ++t_ky; }
+    if (++t_kx == a.kw) {
+      t_kx = 0;
+      if (++t_ky == a.kh) { t_ky = 0; t_ci += BK; }
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {

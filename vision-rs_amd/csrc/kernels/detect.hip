@@ -169,6 +169,128 @@ extern "C" __global__ __launch_bounds__(256) void vrs_detect_unletterbox(vrs_unl
   o[3] = d[3] / sy;
 }
 
+// ---- letterbox preprocessing (examples/yolo26.rs:1229-1253) ---------------
+// preprocess_image_raw resizes with image 0.25.10 imageops::resize(...,
+// FilterType::Triangle): a vertical pass over the source columns into float32
+// (weights normalised per output row), then a horizontal pass over that
+// buffer (normalised per output column), clamped to [0, 255] and rounded half
+// away from zero to u8; the canvas holds u8 / 255 inside the resized region
+// and 114 / 255 elsewhere.  Per axis, output index o of a dst-long axis from a
+// src-long one: ratio = src / dst, sr = max(ratio, 1), centre = (o + 0.5) *
+// ratio, taps i in [clamp(floor(centre - sr), 0, src - 1), clamp(ceil(centre
+// + sr), lo + 1, src)), weight tri((i - (centre - 0.5)) / sr) / sum, tri(x) =
+// max(0, 1 - |x|).  The kernel fuses both passes per output pixel with the
+// same float32 operations in the same order (vertical sum over a column's
+// taps, then the horizontal sum over columns), so it reproduces the two-pass
+// result bit for bit; contraction into FMA is off as in the reference.
+namespace {
+__device__ inline float lb_tri(float x) {
+  const float a = fabsf(x);
+  return a < 1.0f ? 1.0f - a : 0.0f;
+}
+struct LbAxis {
+  int lo, hi;
+  float c, sr, sum;
+};
+__device__ inline LbAxis lb_axis(int o, int src, int dst) {
+#pragma clang fp contract(off)
+  LbAxis ax;
+  const float ratio = (float)src / (float)dst;
+  ax.sr = ratio < 1.0f ? 1.0f : ratio;  // support 1 x sratio
+  const float centre = ((float)o + 0.5f) * ratio;
+  int lo = (int)floorf(centre - ax.sr);
+  lo = lo < 0 ? 0 : (lo > src - 1 ? src - 1 : lo);
+  int hi = (int)ceilf(centre + ax.sr);
+  hi = hi < lo + 1 ? lo + 1 : (hi > src ? src : hi);
+  // the host bounds ratio so that a window has at most VRS_LB_MAX_TAPS taps
+  if (hi - lo > VRS_LB_MAX_TAPS) hi = lo + VRS_LB_MAX_TAPS;
+  ax.lo = lo;
+  ax.hi = hi;
+  ax.c = centre - 0.5f;
+  float sum = 0.0f;
+  for (int i = lo; i < hi; ++i) sum += lb_tri(((float)i - ax.c) / ax.sr);
+  ax.sum = sum;
+  return ax;
+}
+__device__ inline float lb_quant(float v) {  // clamp, round half away from zero, / 255
+  v = v < 0.0f ? 0.0f : (v > 255.0f ? 255.0f : v);
+  return roundf(v) / 255.0f;
+}
+constexpr int LB_TW = 64, LB_TH = 4, LB_LD = VRS_LB_MAX_TAPS + 1;  // odd row pitch: no bank conflicts
+}  // namespace
+
+// One workgroup per 64 x 4 tile of one image's canvas (grid.y = image).  The
+// 64 column and 4 row windows of the tile are computed once into LDS; each
+// thread then sums its pixel's window from the RGB8 source (all three
+// channels per tap) and writes the three NCHW planes.
+extern "C" __global__ __launch_bounds__(256) void vrs_letterbox_f32(vrs_lb_args a) {
+#pragma clang fp contract(off)
+  __shared__ float wcol[LB_TW * LB_LD];
+  __shared__ float wrow[LB_TH * LB_LD];
+  __shared__ int gcol[LB_TW][2], grow[LB_TH][2];
+  const vrs_lb_image im = a.img[blockIdx.y];
+  const int tiles_x = (a.S + LB_TW - 1) / LB_TW;
+  const int x0 = (int)(blockIdx.x % tiles_x) * LB_TW, y0 = (int)(blockIdx.x / tiles_x) * LB_TH;
+  const int tx = threadIdx.x % LB_TW, ty = threadIdx.x / LB_TW;
+  // does the tile meet the resized region? (uniform over the workgroup)
+  const bool inside = x0 < im.px + im.nw && x0 + LB_TW > im.px && y0 < im.py + im.nh && y0 + LB_TH > im.py;
+  if (inside) {
+    const int t = threadIdx.x;
+    if (t < LB_TW) {
+      const int p = x0 + t - im.px;
+      if (p >= 0 && p < im.nw) {
+        const LbAxis ax = lb_axis(p, im.w, im.nw);
+        gcol[t][0] = ax.lo;
+        gcol[t][1] = ax.hi;
+        for (int i = ax.lo; i < ax.hi; ++i) wcol[t * LB_LD + i - ax.lo] = lb_tri(((float)i - ax.c) / ax.sr) / ax.sum;
+      }
+    } else if (t < LB_TW + LB_TH) {
+      const int r = t - LB_TW, p = y0 + r - im.py;
+      if (p >= 0 && p < im.nh) {
+        const LbAxis ax = lb_axis(p, im.h, im.nh);
+        grow[r][0] = ax.lo;
+        grow[r][1] = ax.hi;
+        for (int i = ax.lo; i < ax.hi; ++i) wrow[r * LB_LD + i - ax.lo] = lb_tri(((float)i - ax.c) / ax.sr) / ax.sum;
+      }
+    }
+    __syncthreads();
+  }
+  const int ox = x0 + tx, oy = y0 + ty;
+  if (ox >= a.S || oy >= a.S) return;
+  const int64_t plane = (int64_t)a.S * a.S;
+  float* o = a.out + (int64_t)blockIdx.y * 3 * plane + (int64_t)oy * a.S + ox;
+  const int px = ox - im.px, py = oy - im.py;
+  if (!inside || px < 0 || px >= im.nw || py < 0 || py >= im.nh) {
+    o[0] = a.pad;
+    o[plane] = a.pad;
+    o[2 * plane] = a.pad;
+    return;
+  }
+  const int lo = gcol[tx][0], hi = gcol[tx][1], top = grow[ty][0], bot = grow[ty][1];
+  const int64_t row = (int64_t)im.w * 3;
+  const uint8_t* src = a.rgb + im.off + (int64_t)top * row;
+  const float* wy = wrow + ty * LB_LD;
+  const float* wx = wcol + tx * LB_LD;
+  float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+  for (int i = lo; i < hi; ++i) {
+    const uint8_t* p = src + (int64_t)i * 3;
+    float t0 = 0.0f, t1 = 0.0f, t2 = 0.0f;
+    for (int j = 0; j < bot - top; ++j, p += row) {
+      const float w = wy[j];
+      t0 += (float)p[0] * w;
+      t1 += (float)p[1] * w;
+      t2 += (float)p[2] * w;
+    }
+    const float w = wx[i - lo];
+    s0 += t0 * w;
+    s1 += t1 * w;
+    s2 += t2 * w;
+  }
+  o[0] = lb_quant(s0);
+  o[plane] = lb_quant(s1);
+  o[2 * plane] = lb_quant(s2);
+}
+
 // Grid-unit decode on [B,4,A] rows l,t,r,b (kernels/detect_decode.rs:36-86):
 // cx = (ax - l + ax + r) * 0.5 * s, cy likewise, w = (r + l) * s, h = (b + t) * s.
 extern "C" __global__ __launch_bounds__(256) void vrs_detect_decode_grid(vrs_dec_args a) {

@@ -95,6 +95,7 @@ SIGNATURES = {
     "vrs_detect_postprocess": (C.c_int, [_vp, _P(DetectDesc), _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vrs_detect_decode_grid": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "vrs_detect_unletterbox": (C.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "vrs_letterbox": (C.c_int, [_vp, _i32, _i32, _vp, _i64, _P(_i64), _P(_i32), _vp, _vp]),
     "vrs_msda": (C.c_int, [_vp, _P(MsdaDesc), _vp, _vp, _vp, _vp, _vp, _vp]),
     "vrs_model_create": (C.c_int, [_vp, _P(BlockDesc), _i32, _i32, _i32, _i32, _f32, _P(_vp)]),
     "vrs_model_set_autotune": (C.c_int, [_vp, _i32]),
@@ -252,6 +253,20 @@ class Context:
         out = torch.empty_like(xywh)
         check(lib().vrs_detect_unletterbox(self.handle, n, max_det, img_size, _ptr(orig_wh), _ptr(count),
                                            _ptr(xywh), _ptr(out), _stream(stream)))
+        return out
+
+    def letterbox(self, rgb, offsets, wh, img_size, out=None, stream=None):
+        """Letterbox n RGB8 images held in one flat uint8 device tensor (image
+        i: wh[i] = (w, h) pixels at byte offsets[i]) into the model input
+        [n][3][img_size][img_size] float32 (preprocess_image_raw)."""
+        import torch
+        n = len(wh)
+        if out is None:
+            out = torch.empty(n, 3, img_size, img_size, dtype=torch.float32, device=rgb.device)
+        offs = (C.c_int64 * n)(*[int(o) for o in offsets])
+        dims = (C.c_int32 * (2 * n))(*[int(v) for w_h in wh for v in w_h])
+        check(lib().vrs_letterbox(self.handle, n, img_size, _ptr(rgb), rgb.numel() * rgb.element_size(), offs, dims,
+                                  _ptr(out), _stream(stream)))
         return out
 
     def detect_decode_grid(self, boxes, ax, ay, strides, out, stream=None):
