@@ -429,14 +429,16 @@ def test_detect_unletterbox():
 
 LB_SIZES = [(1280, 720), (640, 640), (517, 333), (333, 517), (1000, 37), (5, 3), (1, 1), (17, 2000), (4000, 100),
             (1920, 1080), (639, 641), (2, 1), (100, 100), (64, 48), (3000, 3000), (701, 299), (8, 8), (1279, 719),
-            (333, 333), (50, 2000)]
+            (333, 333), (50, 2000), (2560, 1440), (2600, 100), (5120, 300), (6000, 200)]
 
 
 def test_letterbox():
-    """Letterbox preprocessing of 20 images of mixed sizes (two launches),
-    bit-exact against the oracle's two-pass restatement of the Triangle
-    resize: enlargements, shrinks up to 6.25x, the identity, 1x1, thin strips,
-    saturated regions, images starting at odd byte offsets."""
+    """Letterbox preprocessing of 24 images of mixed sizes, bit-exact against
+    the oracle's two-pass restatement of the Triangle resize, through every
+    kernel: enlargements and shrinks up to 2x (staged, 64-wide tiles), up to 4x
+    (1920 and exactly 4x at 2560 wide), up to 8x (2600, 4000, exactly 8x at
+    5120 wide: 32-wide tiles) and beyond (6000 wide: direct kernel); the
+    identity, 1x1, thin strips, saturated regions, odd byte offsets."""
     import torch
     rng = np.random.default_rng(9)
     imgs = []

@@ -294,23 +294,41 @@ int vrs_letterbox(vrs_ctx* ctx, int32_t n, int32_t img_size, const uint8_t* rgb,
     // bounded filter windows: ratio <= 62 gives at most 2*62 + 2 taps
     if ((nw > 0 && (float)w / (float)nw > 62.0f) || (nh > 0 && (float)h / (float)nh > 62.0f))
       return fail(VRS_EUNSUPPORTED, "vrs_letterbox: image %d (%dx%d) shrinks by more than 62x", i, w, h);
-    ims[(size_t)i] = vrs_lb_image{off, w, h, nw, nh, (img_size - nw) / 2, (img_size - nh) / 2};
+    ims[(size_t)i] = vrs_lb_image{off, w, h, nw, nh, (img_size - nw) / 2, (img_size - nh) / 2, i, 0};
   }
-  hipFunction_t f;
-  int rc = get_fn(ctx, "vrs_letterbox_f32", &f);
-  if (rc) return rc;
-  const int64_t per_image = 3ll * img_size * img_size;
-  const unsigned tiles = (unsigned)(((img_size + 63) / 64) * ((img_size + 3) / 4));
+  // per image the staged kernel for shrinks up to 2x, 4x, then
+  // VRS_LB_STAGED_RATIO x per axis (the kernels' own float32 ratio), else the
+  // direct kernel
+  auto kind = [](const vrs_lb_image& im) {
+    auto within = [&](float r) {
+      return (im.nw == 0 || (float)im.w / (float)im.nw <= r) && (im.nh == 0 || (float)im.h / (float)im.nh <= r);
+    };
+    return within(2.0f) ? 0 : within(4.0f) ? 1 : within((float)VRS_LB_STAGED_RATIO) ? 2 : 3;
+  };
+  static const char* names[4] = {"vrs_letterbox_f32_s2", "vrs_letterbox_f32_s4", "vrs_letterbox_f32_s8",
+                                 "vrs_letterbox_f32"};
   std::vector<Launch> ls;
-  for (int b0 = 0; b0 < n; b0 += VRS_LB_MAX_IMAGES) {
-    vrs_lb_args a{};
-    a.rgb = rgb;
-    a.out = out + (int64_t)b0 * per_image;
-    a.pad = 114.0f / 255.0f;
-    a.S = img_size;
-    a.count = std::min(VRS_LB_MAX_IMAGES, n - b0);
-    for (int k = 0; k < a.count; ++k) a.img[k] = ims[(size_t)(b0 + k)];
-    ls.push_back(make_launch("vrs_letterbox_f32", f, dim3(tiles, (unsigned)a.count), dim3(256), 0, a));
+  for (int pass = 0; pass < 4; ++pass) {
+    std::vector<vrs_lb_image> sel;
+    for (const auto& im : ims)
+      if (kind(im) == pass) sel.push_back(im);
+    if (sel.empty()) continue;
+    const char* name = names[pass];
+    hipFunction_t f;
+    int rc = get_fn(ctx, name, &f);
+    if (rc) return rc;
+    const int tw = pass == 2 ? 32 : 64;   // tile width; 4 rows
+    const unsigned tiles = (unsigned)(((img_size + tw - 1) / tw) * ((img_size + 3) / 4));
+    for (size_t b0 = 0; b0 < sel.size(); b0 += VRS_LB_MAX_IMAGES) {
+      vrs_lb_args a{};
+      a.rgb = rgb;
+      a.out = out;
+      a.pad = 114.0f / 255.0f;
+      a.S = img_size;
+      a.count = (int32_t)std::min<size_t>(VRS_LB_MAX_IMAGES, sel.size() - b0);
+      for (int k = 0; k < a.count; ++k) a.img[k] = sel[b0 + (size_t)k];
+      ls.push_back(make_launch(name, f, dim3(tiles, (unsigned)a.count), dim3(pass == 2 ? 128 : 256), 0, a));
+    }
   }
   return run_all(ls, stream);
 }

@@ -142,16 +142,18 @@ typedef struct {
 
 /* Letterbox preprocessing, up to VRS_LB_MAX_IMAGES images per launch (grid.y
  * = image).  Per image: RGB8 rows of w*3 bytes at rgb + off, the resized size
- * (nw, nh) and the canvas offset (px, py), all computed on the host. */
+ * (nw, nh), the canvas offset (px, py) and the output slot, all computed on
+ * the host. */
 #define VRS_LB_MAX_IMAGES 16
-#define VRS_LB_MAX_TAPS 128 /* filter taps per output row/column (ratio <= 63) */
+#define VRS_LB_MAX_TAPS 128   /* direct kernel: taps per output row/column (ratio <= 62) */
+#define VRS_LB_STAGED_RATIO 8 /* staged kernels: images shrunk at most 8x per axis */
 typedef struct {
   int64_t off;
-  int32_t w, h, nw, nh, px, py;
+  int32_t w, h, nw, nh, px, py, slot, pad_;
 } vrs_lb_image;
 typedef struct {
   const uint8_t* rgb;
-  float* out;           /* [count][3][S][S] for these images */
+  float* out;           /* [slots][3][S][S] */
   float pad;            /* 114 / 255 in float32 */
   int32_t S, count;
   vrs_lb_image img[VRS_LB_MAX_IMAGES];

@@ -188,29 +188,30 @@ __device__ inline float lb_tri(float x) {
   const float a = fabsf(x);
   return a < 1.0f ? 1.0f - a : 0.0f;
 }
-struct LbAxis {
-  int lo, hi;
-  float c, sr, sum;
-};
-__device__ inline LbAxis lb_axis(int o, int src, int dst) {
+// Window [lo, lo + n) of output index o along a dst-long axis from a
+// src-long one, with its normalised weights written to w[0..n) (n <= cap; the
+// host's ratio bounds keep the true window within cap).  One division per tap
+// for the weight and one for the normalisation, as the reference does them.
+__device__ inline int lb_window(int o, int src, int dst, int cap, float* w, int& lo) {
 #pragma clang fp contract(off)
-  LbAxis ax;
   const float ratio = (float)src / (float)dst;
-  ax.sr = ratio < 1.0f ? 1.0f : ratio;  // support 1 x sratio
+  const float sr = ratio < 1.0f ? 1.0f : ratio;  // support 1 x sratio
   const float centre = ((float)o + 0.5f) * ratio;
-  int lo = (int)floorf(centre - ax.sr);
-  lo = lo < 0 ? 0 : (lo > src - 1 ? src - 1 : lo);
-  int hi = (int)ceilf(centre + ax.sr);
-  hi = hi < lo + 1 ? lo + 1 : (hi > src ? src : hi);
-  // the host bounds ratio so that a window has at most VRS_LB_MAX_TAPS taps
-  if (hi - lo > VRS_LB_MAX_TAPS) hi = lo + VRS_LB_MAX_TAPS;
-  ax.lo = lo;
-  ax.hi = hi;
-  ax.c = centre - 0.5f;
+  int l = (int)floorf(centre - sr);
+  l = l < 0 ? 0 : (l > src - 1 ? src - 1 : l);
+  int h = (int)ceilf(centre + sr);
+  h = h < l + 1 ? l + 1 : (h > src ? src : h);
+  if (h - l > cap) h = l + cap;
+  const float c = centre - 0.5f;
   float sum = 0.0f;
-  for (int i = lo; i < hi; ++i) sum += lb_tri(((float)i - ax.c) / ax.sr);
-  ax.sum = sum;
-  return ax;
+  for (int i = l; i < h; ++i) {
+    const float v = lb_tri(((float)i - c) / sr);
+    w[i - l] = v;
+    sum += v;
+  }
+  for (int i = 0; i < h - l; ++i) w[i] = w[i] / sum;
+  lo = l;
+  return h - l;
 }
 __device__ inline float lb_quant(float v) {  // clamp, round half away from zero, / 255
   v = v < 0.0f ? 0.0f : (v > 255.0f ? 255.0f : v);
@@ -239,18 +240,18 @@ extern "C" __global__ __launch_bounds__(256) void vrs_letterbox_f32(vrs_lb_args 
     if (t < LB_TW) {
       const int p = x0 + t - im.px;
       if (p >= 0 && p < im.nw) {
-        const LbAxis ax = lb_axis(p, im.w, im.nw);
-        gcol[t][0] = ax.lo;
-        gcol[t][1] = ax.hi;
-        for (int i = ax.lo; i < ax.hi; ++i) wcol[t * LB_LD + i - ax.lo] = lb_tri(((float)i - ax.c) / ax.sr) / ax.sum;
+        int lo;
+        const int n = lb_window(p, im.w, im.nw, VRS_LB_MAX_TAPS, wcol + t * LB_LD, lo);
+        gcol[t][0] = lo;
+        gcol[t][1] = lo + n;
       }
     } else if (t < LB_TW + LB_TH) {
       const int r = t - LB_TW, p = y0 + r - im.py;
       if (p >= 0 && p < im.nh) {
-        const LbAxis ax = lb_axis(p, im.h, im.nh);
-        grow[r][0] = ax.lo;
-        grow[r][1] = ax.hi;
-        for (int i = ax.lo; i < ax.hi; ++i) wrow[r * LB_LD + i - ax.lo] = lb_tri(((float)i - ax.c) / ax.sr) / ax.sum;
+        int lo;
+        const int n = lb_window(p, im.h, im.nh, VRS_LB_MAX_TAPS, wrow + r * LB_LD, lo);
+        grow[r][0] = lo;
+        grow[r][1] = lo + n;
       }
     }
     __syncthreads();
@@ -258,7 +259,7 @@ extern "C" __global__ __launch_bounds__(256) void vrs_letterbox_f32(vrs_lb_args 
   const int ox = x0 + tx, oy = y0 + ty;
   if (ox >= a.S || oy >= a.S) return;
   const int64_t plane = (int64_t)a.S * a.S;
-  float* o = a.out + (int64_t)blockIdx.y * 3 * plane + (int64_t)oy * a.S + ox;
+  float* o = a.out + (int64_t)im.slot * 3 * plane + (int64_t)oy * a.S + ox;
   const int px = ox - im.px, py = oy - im.py;
   if (!inside || px < 0 || px >= im.nw || py < 0 || py >= im.nh) {
     o[0] = a.pad;
@@ -272,14 +273,28 @@ extern "C" __global__ __launch_bounds__(256) void vrs_letterbox_f32(vrs_lb_args 
   const float* wy = wrow + ty * LB_LD;
   const float* wx = wcol + tx * LB_LD;
   float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+  const int n = bot - top;
   for (int i = lo; i < hi; ++i) {
     const uint8_t* p = src + (int64_t)i * 3;
     float t0 = 0.0f, t1 = 0.0f, t2 = 0.0f;
-    for (int j = 0; j < bot - top; ++j, p += row) {
-      const float w = wy[j];
-      t0 += (float)p[0] * w;
-      t1 += (float)p[1] * w;
-      t2 += (float)p[2] * w;
+    for (int j0 = 0; j0 < n; j0 += 8) {   // 8 taps' bytes in flight, then the sums in order
+      uint8_t q[8][3];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j0 + j < n) {
+          const uint8_t* pj = p + (int64_t)(j0 + j) * row;
+          q[j][0] = pj[0];
+          q[j][1] = pj[1];
+          q[j][2] = pj[2];
+        }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j0 + j < n) {
+          const float w = wy[j0 + j];
+          t0 += (float)q[j][0] * w;
+          t1 += (float)q[j][1] * w;
+          t2 += (float)q[j][2] * w;
+        }
     }
     const float w = wx[i - lo];
     s0 += t0 * w;
@@ -289,6 +304,172 @@ extern "C" __global__ __launch_bounds__(256) void vrs_letterbox_f32(vrs_lb_args 
   o[0] = lb_quant(s0);
   o[plane] = lb_quant(s1);
   o[2 * plane] = lb_quant(s2);
+}
+
+// Staged variants for images shrunk at most 2x (vrs_letterbox_f32_s2), 4x
+// (_s4) or VRS_LB_STAGED_RATIO = 8x (_s8) per axis: one workgroup per 64 x 4
+// tile (32 x 4 for _s8).  After the
+// windows, the source patch the tile reads (rows spanned by its 4 row windows
+// x columns spanned by its 64 column windows) is copied into LDS with aligned
+// dword loads, all in flight together; the vertical pass then runs once per
+// (tile row, source column) from LDS into a float32 buffer, and the
+// horizontal pass reads that buffer -- the same float32 operations in the same
+// order as the direct kernel and the two-pass reference.  The patch is copied
+// in 16-byte loads so that a workgroup keeps its whole patch in flight at
+// once (the kernel is bound by loads in flight, not by bandwidth).
+namespace {
+// R: the largest shrink factor per axis the instance accepts; LDS is sized
+// for it, so the small-ratio instance fits twice as many workgroups per CU
+template <int R, int LBS_TW>
+__device__ __forceinline__ void lb_staged(const vrs_lb_args& a) {
+#pragma clang fp contract(off)
+  constexpr int LBS_TH = 4, NT = LBS_TW * LBS_TH, LBS_TAPS = 2 * R + 2, LBS_LD = LBS_TAPS + 1;
+  // source columns / rows a tile touches: (n - 1) * ratio + 2 * ratio + 2, +2 slack
+  constexpr int LBS_CMAX = (LBS_TW - 1) * R + 2 * R + 4;
+  constexpr int LBS_RMAX = (LBS_TH - 1) * R + 2 * R + 4;
+  constexpr int LBS_PW = (LBS_CMAX * 3 + 15 + 15) / 16;   // 16-byte chunks per patch row (15-byte lead-in)
+  constexpr int LBS_VREG = 4;                               // chunks in flight per thread and round
+  __shared__ float wcol[LBS_TW * LBS_LD];
+  __shared__ float wrow[LBS_TH * LBS_LD];
+  __shared__ int gcol[LBS_TW][2], grow[LBS_TH][2];
+  __shared__ u32x4_t patch[LBS_RMAX * LBS_PW];
+  __shared__ int plead[LBS_RMAX];
+  __shared__ float vbuf[LBS_TH * LBS_CMAX * 3];
+  const vrs_lb_image im = a.img[blockIdx.y];
+  const int tiles_x = (a.S + LBS_TW - 1) / LBS_TW;
+  const int x0 = (int)(blockIdx.x % tiles_x) * LBS_TW, y0 = (int)(blockIdx.x / tiles_x) * LBS_TH;
+  const int64_t plane = (int64_t)a.S * a.S;
+  float* ob = a.out + (int64_t)im.slot * 3 * plane;
+  const int t = threadIdx.x;
+  const int tx = t % LBS_TW, ty = t / LBS_TW;
+  const int ox = x0 + tx, oy = y0 + ty;
+  // in-image columns [cf, cl] and rows [rf, rl] of the tile (uniform)
+  const int cf = max(im.px - x0, 0), cl = min(im.px + im.nw - x0, LBS_TW) - 1;
+  const int rf = max(im.py - y0, 0), rl = min(im.py + im.nh - y0, LBS_TH) - 1;
+  if (cf > cl || rf > rl) {   // all padding
+    if (ox < a.S && oy < a.S) {
+      float* o = ob + (int64_t)oy * a.S + ox;
+      o[0] = a.pad;
+      o[plane] = a.pad;
+      o[2 * plane] = a.pad;
+    }
+    return;
+  }
+  if (t < LBS_TW) {
+    if (t >= cf && t <= cl) {
+      int lo;
+      const int n = lb_window(x0 + t - im.px, im.w, im.nw, LBS_TAPS, wcol + t * LBS_LD, lo);
+      gcol[t][0] = lo;
+      gcol[t][1] = lo + n;
+    }
+  } else if (t < LBS_TW + LBS_TH) {
+    const int r = t - LBS_TW;
+    if (r >= rf && r <= rl) {
+      int lo;
+      const int n = lb_window(y0 + r - im.py, im.h, im.nh, LBS_TAPS, wrow + r * LBS_LD, lo);
+      grow[r][0] = lo;
+      grow[r][1] = lo + n;
+    }
+  }
+  __syncthreads();
+  // window bounds are non-decreasing along an axis: the patch is source rows
+  // [top of the first row window, bottom of the last) x columns [lo of the
+  // first column window, hi of the last)
+  const int c_lo = gcol[cf][0];
+  const int ncol = min(gcol[cl][1] - c_lo, LBS_CMAX);   // <= LBS_CMAX and LBS_RMAX by the ratio bound
+  const int ytop = grow[rf][0];
+  const int nrow = min(grow[rl][1] - ytop, LBS_RMAX);
+  // patch row i holds the source bytes [s_i, s_i + 3*ncol) of image row
+  // ytop + i (s_i = off + ((ytop + i)*w + c_lo)*3), copied as the 16-byte
+  // aligned chunks that cover them; the bytes start at plead[i] = address of
+  // s_i mod 16.  Chunks straddling the image's first or last byte (only
+  // those) are assembled from byte loads.
+  const unsigned char* img0 = a.rgb + im.off;
+  const unsigned char* img1 = img0 + (int64_t)im.w * im.h * 3;
+  const int nq = (3 * ncol + 15 + 15) / 16;   // chunks per row copy (<= LBS_PW)
+  const int total = nrow * nq;
+  if (t < nrow)
+    plead[t] = (int)(reinterpret_cast<uintptr_t>(img0 + ((int64_t)(ytop + t) * im.w + c_lo) * 3) & 15);
+  for (int base = t; base < total; base += NT * LBS_VREG) {
+    u32x4_t v[LBS_VREG];
+#pragma unroll
+    for (int u = 0; u < LBS_VREG; ++u) {
+      const int idx = base + u * NT;
+      if (idx < total) {
+        const int i = idx / nq, d = idx - (idx / nq) * nq;
+        const unsigned char* row_p = img0 + ((int64_t)(ytop + i) * im.w + c_lo) * 3;
+        const unsigned char* q = reinterpret_cast<const unsigned char*>(
+            (reinterpret_cast<uintptr_t>(row_p) & ~(uintptr_t)15) + 16 * (uintptr_t)d);
+        if (q >= img0 && q + 16 <= img1) {
+          v[u] = *reinterpret_cast<const u32x4_t*>(q);
+        } else {
+          uint32_t wv[4] = {0, 0, 0, 0};
+          for (int k = 0; k < 16; ++k)
+            if (q + k >= img0 && q + k < img1) wv[k / 4] |= (uint32_t)q[k] << (8 * (k % 4));
+          v[u] = (u32x4_t){wv[0], wv[1], wv[2], wv[3]};
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < LBS_VREG; ++u) {
+      const int idx = base + u * NT;
+      if (idx < total) patch[(idx / nq) * LBS_PW + idx % nq] = v[u];
+    }
+  }
+  __syncthreads();
+  // vertical pass: one (tile row, patch column) per thread and step; the row
+  // loop is uniform over the workgroup
+  const unsigned char* pb = reinterpret_cast<const unsigned char*>(patch);
+  for (int r = rf; r <= rl; ++r) {
+    const int top = grow[r][0], n = grow[r][1] - top;
+    const float* wy = wrow + r * LBS_LD;
+    for (int x = t; x < ncol; x += NT) {
+      float t0 = 0.0f, t1 = 0.0f, t2 = 0.0f;
+      for (int j = 0; j < n; ++j) {
+        const int i = top - ytop + j;
+        const unsigned char* q = pb + i * LBS_PW * 16 + plead[i] + x * 3;
+        const float w = wy[j];
+        t0 += (float)q[0] * w;
+        t1 += (float)q[1] * w;
+        t2 += (float)q[2] * w;
+      }
+      float* vv = vbuf + (r * LBS_CMAX + x) * 3;
+      vv[0] = t0;
+      vv[1] = t1;
+      vv[2] = t2;
+    }
+  }
+  __syncthreads();
+  // horizontal pass, one pixel per thread
+  if (ox >= a.S || oy >= a.S) return;
+  float* o = ob + (int64_t)oy * a.S + ox;
+  if (tx < cf || tx > cl || ty < rf || ty > rl) {
+    o[0] = a.pad;
+    o[plane] = a.pad;
+    o[2 * plane] = a.pad;
+    return;
+  }
+  const int lo = gcol[tx][0], n = min(gcol[tx][1], c_lo + ncol) - lo;
+  const float* vv = vbuf + (ty * LBS_CMAX + lo - c_lo) * 3;
+  const float* wx = wcol + tx * LBS_LD;
+  float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    const float w = wx[i];
+    s0 += vv[3 * i] * w;
+    s1 += vv[3 * i + 1] * w;
+    s2 += vv[3 * i + 2] * w;
+  }
+  o[0] = lb_quant(s0);
+  o[plane] = lb_quant(s1);
+  o[2 * plane] = lb_quant(s2);
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void vrs_letterbox_f32_s2(vrs_lb_args a) { lb_staged<2, 64>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_letterbox_f32_s4(vrs_lb_args a) { lb_staged<4, 64>(a); }
+// 32 x 4 tiles (128 threads) keep the patch of an 8x shrink within 40 KB of LDS
+extern "C" __global__ __launch_bounds__(128) void vrs_letterbox_f32_s8(vrs_lb_args a) {
+  lb_staged<VRS_LB_STAGED_RATIO, 32>(a);
 }
 
 // Grid-unit decode on [B,4,A] rows l,t,r,b (kernels/detect_decode.rs:36-86):
