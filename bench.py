@@ -453,8 +453,9 @@ def main() -> int:
                    "ms_per_step": round(el8 * 1e3 / a.steps, 3),
                    "fp8_convs": sum(1 for _, f8, _ in m8.conv_info() if f8), "convs": len(m8.conv_info()),
                    "note": "e4m3 weights (per-channel absmax/448) and e4m3 activations (per-tensor power-of-two "
-                           "step calibrated on this batch) on the fp8 MFMA for convs with Cin % 64 == 0; the "
-                           "rest bf16; activations stored bf16",
+                           "step calibrated on this batch) on the fp8 MFMA for convs with Cin % 64 == 0 whose "
+                           "fastest fp8 tile beats their fastest bf16 tile (autotuned per layer); the rest bf16; "
+                           "activations stored bf16",
                    "kernels": {s: {"launches": d["launches"], "ms": round(d["ms"], 4),
                                    "tflops": round(d["flops"] / max(d["ms"], 1e-9) / 1e9, 2)} for s, d in top}}
         m8.close()

@@ -176,6 +176,8 @@ FP8_CASES = [
     (2, 192, 12, 12, 64, 1, 1, True, vrs.TILE_64x256),
     (1, 256, 10, 10, 96, 3, 1, False, vrs.TILE_128x256),
     (2, 64, 15, 7, 200, 1, 1, True, vrs.TILE_AUTO),
+    (2, 128, 14, 10, 256, 3, 1, True, vrs.TILE_256x256),
+    (1, 256, 9, 13, 320, 3, 2, False, vrs.TILE_256x256),
 ]
 
 

@@ -63,6 +63,9 @@ struct ConvStep {
   std::vector<float> scale8_host;   // BN scale * weight scale
   float in_scale = 0.f;             // activation step (power of two), 0 = not calibrated
   int tile8 = VRS_TILE_AUTO;
+  // autotune: false when this layer's best bf16 tile beat its best fp8 tile
+  // (the layer then runs bf16 in the fp8 model)
+  bool run_f8 = true;
 };
 
 // A launch's memory accesses, for the dependency graph of a capture:
@@ -561,7 +564,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
           rc = prep_absmax(m->ctx, xv, m->absmax + st.conv, ls);
           if (rc) return rc;
           for (size_t i = before; i < ls.size(); ++i) labels.push_back(label + ".calib:" + ls[i].name);
-        } else if (c.f8) {
+        } else if (c.f8 && c.run_f8) {
           if (!m->calibrated) return fail(VRS_ESTATE, "fp8 model: call vrs_model_calibrate first");
           cs.dtype = VRS_FP8;
           cs.in_scale = c.in_scale;
@@ -643,7 +646,8 @@ int autotune_tiles(vrs_model* m) {
   VRS_HIP(hipEventCreate(&e0));
   VRS_HIP(hipEventCreate(&e1));
   int rc = VRS_OK;
-  for (ConvStep& c : m->convs)
+  for (ConvStep& c : m->convs) {
+   float best_of[2] = {1e30f, 1e30f};   // fastest bf16 / fp8 tile of this layer
    for (int pass = 0; pass < (c.f8 ? 2 : 1); ++pass) {
     if (c.dw || c.stem || c.out_idx >= 0 || c.y.buf < 0) continue;
     const int dt = pass ? VRS_FP8 : act_dt(m);
@@ -684,6 +688,11 @@ int autotune_tiles(vrs_model* m) {
     }
     if (rc) break;
     (pass ? c.tile8 : c.tile) = best_tile;
+    best_of[pass] = best;
+   }
+   if (rc) break;
+   // fp8 models: a layer whose bf16 tile is faster by 2% stays on bf16
+   if (c.f8) c.run_f8 = !(best_of[0] < 0.98f * best_of[1]);
   }
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
@@ -1075,7 +1084,7 @@ int vrs_model_conv_info(const vrs_model* m, int32_t i, const char** prefix, int3
   if (i < 0 || i >= (int)m->convs.size()) return fail(VRS_EINVAL, "vrs_model_conv_info: index %d", i);
   const ConvStep& c = m->convs[i];
   *prefix = c.pre.c_str();
-  *fp8 = c.f8 ? 1 : 0;
+  *fp8 = c.f8 && c.run_f8 ? 1 : 0;
   *in_scale = c.in_scale;
   return VRS_OK;
 }

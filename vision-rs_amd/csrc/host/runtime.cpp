@@ -108,8 +108,7 @@ static int tile_kernel(int code, int cin, int dtype, char* name, size_t n, int* 
   if (!t) return fail(VRS_EINVAL, "conv: unknown tile code %d", code);
   if (dtype == VRS_FP8) {
     if (cin % 64 != 0) return fail(VRS_EUNSUPPORTED, "conv fp8: needs Cin %% 64 == 0 (Cin=%d)", cin);
-    if (t->code == VRS_TILE_32x256 || t->code == VRS_TILE_256x256)
-      return fail(VRS_EUNSUPPORTED, "conv fp8: tile %s not built", t->tag);
+    if (t->code == VRS_TILE_32x256) return fail(VRS_EUNSUPPORTED, "conv fp8: tile %s not built", t->tag);
     snprintf(name, n, "vrs_conv_fp8_%s_k64_a", t->tag);
     *bm = t->bm;
     *bn = t->bn;
@@ -163,6 +162,7 @@ std::vector<int> conv_tile_candidates(int cout, int cin, int dtype) {
     c.push_back(VRS_TILE_64x256);
     if (cout > 128) c.push_back(VRS_TILE_256x128);
     if (cout <= 128) c.push_back(VRS_TILE_128x256);
+    if (cout >= 256) c.push_back(VRS_TILE_256x256);
     return c;
   }
   const bool g = cin % 32 != 0;

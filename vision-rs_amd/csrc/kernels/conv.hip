@@ -773,6 +773,8 @@ VRS_CONV_F8(vrs_conv_fp8_128x128_k64_a, 128, 128, 2, 2)
 VRS_CONV_F8(vrs_conv_fp8_256x128_k64_a, 256, 128, 2, 2)
 VRS_CONV_F8(vrs_conv_fp8_128x256_k64_a, 128, 256, 2, 2)
 VRS_CONV_F8(vrs_conv_fp8_64x256_k64_a, 64, 256, 1, 4)
+// 8 waves (512 threads) of 128x64, as the bf16 256x256 tile
+VRS_CONV_F8(vrs_conv_fp8_256x256_k64_a, 256, 256, 2, 4)
 // f32 (parity path, fp32 MFMA)
 VRS_CONV_KERNEL(vrs_conv_f32_128x128_k32_a, float, 128, 128, 32, 2, 2, true)
 VRS_CONV_KERNEL(vrs_conv_f32_128x128_k32_g, float, 128, 128, 32, 2, 2, false)
