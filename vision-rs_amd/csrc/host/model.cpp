@@ -66,6 +66,10 @@ struct ConvStep {
   // autotune: false when this layer's best bf16 tile beat its best fp8 tile
   // (the layer then runs bf16 in the fp8 model)
   bool run_f8 = true;
+  // fused nearest-2x upsample: input channels [0, up.c) come from this
+  // half-resolution view (the upsample step feeding them was dropped)
+  bool has_up = false;
+  V up;
 };
 
 // A launch's memory accesses, for the dependency graph of a capture:
@@ -534,6 +538,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         const ConvStep& c = m->convs[st.conv];
         sio.rd = {acc(c.x)};
         if (c.has_res) sio.rd.push_back(acc(c.res));
+        if (c.has_up) sio.rd.push_back(acc(c.up));
         if (c.out_idx >= 0) sio.wr = {{kResOut - c.out_idx, 0, kAll}};
         else sio.wr = {acc(c.y)};
         break;
@@ -556,11 +561,22 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
         cs.cin_real = c.cin_real != c.cin ? c.cin_real : 0;
         cs.tile = c.tile;
+        vrs_nhwc upv;
+        if (c.has_up) {
+          upv = view_of(m, c.up);
+          cs.up = &upv;
+        }
         const void* w = c.w;
         const float* scale = c.scale;
         label = c.pre.empty() ? "conv" : c.pre;
         if (c.f8 && m->calib_mode) {
-          const vrs_nhwc xv = view_of(m, c.x);
+          vrs_nhwc xv = view_of(m, c.x);
+          if (c.has_up) {  // max |x| over the upsample source and the rest of the channels
+            rc = prep_absmax(m->ctx, upv, m->absmax + st.conv, ls);
+            if (rc) return rc;
+            xv.c_off += c.up.c;
+            xv.c -= c.up.c;
+          }
           rc = prep_absmax(m->ctx, xv, m->absmax + st.conv, ls);
           if (rc) return rc;
           for (size_t i = before; i < ls.size(); ++i) labels.push_back(label + ".calib:" + ls[i].name);
@@ -656,6 +672,11 @@ int autotune_tiles(vrs_model* m) {
     ConvSpec cs;
     cs.k = c.k; cs.stride = c.s; cs.dtype = dt; cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
     cs.in_scale = 1.f;  // timing only: values do not matter
+    vrs_nhwc upv;
+    if (c.has_up) {
+      upv = view_of(m, c.up);
+      cs.up = &upv;
+    }
     vrs_nhwc r;
     if (c.has_res) r = view_of(m, c.res);
     float best = 1e30f;
@@ -701,6 +722,54 @@ int autotune_tiles(vrs_model* m) {
   return rc;
 }
 
+// A nearest-2x upsample into a concat slice whose only reader is a 1x1
+// stride-1 dense conv taking that slice as its first channels (the neck's
+// Upsample -> Concat -> C3k2 cv1, yolo26/mod.rs:126-195) is folded into the
+// conv: it reads those channels from the half-resolution source at (y/2,
+// x/2), and the upsample step is dropped.
+void fuse_upsamples(vrs_model* m) {
+  auto overlaps = [](V a, V b) { return a.buf == b.buf && a.c_off < b.c_off + b.c && b.c_off < a.c_off + a.c; };
+  for (size_t i = 0; i < m->steps.size();) {
+    const Step up = m->steps[i];
+    if (up.type != Step::UP) {
+      ++i;
+      continue;
+    }
+    int reader = -1, nreaders = 0;
+    for (size_t j = 0; j < m->steps.size(); ++j) {
+      if (j == i) continue;
+      const Step& st = m->steps[j];
+      std::vector<V> rd;
+      if (st.type == Step::CONV) {
+        const ConvStep& c = m->convs[st.conv];
+        rd.push_back(c.x);
+        if (c.has_res) rd.push_back(c.res);
+        if (c.has_up) rd.push_back(c.up);
+      } else if (st.type == Step::POOL || st.type == Step::UP || st.type == Step::ATTN || st.type == Step::UNPACK) {
+        rd.push_back(st.a);
+      }
+      for (const V& v : rd)
+        if (overlaps(v, up.b)) {
+          ++nreaders;
+          reader = (int)j;
+          break;
+        }
+    }
+    bool fuse = nreaders == 1 && m->steps[reader].type == Step::CONV;
+    if (fuse) {
+      ConvStep& c = m->convs[m->steps[reader].conv];
+      fuse = !c.dw && !c.stem && c.k == 1 && c.s == 1 && c.out_idx < 0 && c.x.buf == up.b.buf &&
+             c.x.c_off == up.b.c_off && c.x.c > up.b.c && up.b.c % 64 == 0 && up.a.c == up.b.c;
+      if (fuse) {
+        c.up = up.a;
+        c.has_up = true;
+      }
+    }
+    if (fuse) m->steps.erase(m->steps.begin() + (ptrdiff_t)i);
+    else ++i;
+  }
+}
+
 const Param* P(const vrs_model* m, const std::string& name) {
   auto it = m->pidx.find(name);
   return it == m->pidx.end() ? nullptr : &m->params[it->second];
@@ -724,6 +793,7 @@ int vrs_model_create(vrs_ctx* ctx, const vrs_block_desc* d, int32_t batch, int32
   m->eps = bn_eps;
   int rc = build(m.get());
   if (rc) return rc;
+  fuse_upsamples(m.get());
   *out = m.release();
   return VRS_OK;
 }
@@ -839,7 +909,8 @@ int vrs_model_finalize(vrs_model* m) {
     c.scale = static_cast<float*>(p);
     if ((rc = dev_upload(m, shift.data(), shift.size() * 4, &p))) return rc;
     c.shift = static_cast<float*>(p);
-    c.f8 = m->dtype == VRS_FP8 && !c.dw && !c.stem && c.cin % 64 == 0 && cin_g == c.cin;
+    // (a fused-upsample conv stays bfloat16: its kernels have no fp8 instance)
+    c.f8 = m->dtype == VRS_FP8 && !c.dw && !c.stem && !c.has_up && c.cin % 64 == 0 && cin_g == c.cin;
     if (c.f8) {  // e4m3 copy of the weights; the bf16 one serves calibration
       std::vector<uint8_t> q((size_t)vrs_pack_conv_weight_fp8(nullptr, c.cout, cin_g, c.k, c.cin, nullptr, nullptr));
       std::vector<float> ws(c.cout);

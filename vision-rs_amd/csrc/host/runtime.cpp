@@ -103,9 +103,18 @@ static const TileInfo* tile_info(int code) {
 }
 
 // Kernel name for a tile, or an error when the combination is not built.
-static int tile_kernel(int code, int cin, int dtype, char* name, size_t n, int* bm, int* bn, int* threads) {
+// up: the fused-upsample instance (_u), built for 128x128, 256x128 and
+// 128x256 in bf16 and 128x128 and 64x256 in float32, aligned and not persistent
+static int tile_kernel(int code, int cin, int dtype, bool up, char* name, size_t n, int* bm, int* bn, int* threads) {
   const TileInfo* t = tile_info(code);
   if (!t) return fail(VRS_EINVAL, "conv: unknown tile code %d", code);
+  if (up) {
+    const bool built = dtype == VRS_BF16 ? (t->code == VRS_TILE_128x128 || t->code == VRS_TILE_256x128 ||
+                                            t->code == VRS_TILE_128x256)
+                                         : dtype == VRS_F32 && (t->code == VRS_TILE_128x128 || t->code == VRS_TILE_64x256);
+    if (!built || (code & VRS_TILE_PERSIST) || cin % 32 != 0)
+      return fail(VRS_EUNSUPPORTED, "conv: no fused-upsample kernel for tile %s (dtype %d, Cin %d)", t->tag, dtype, cin);
+  }
   if (dtype == VRS_FP8) {
     if (cin % 64 != 0) return fail(VRS_EUNSUPPORTED, "conv fp8: needs Cin %% 64 == 0 (Cin=%d)", cin);
     if (t->code == VRS_TILE_32x256) return fail(VRS_EUNSUPPORTED, "conv fp8: tile %s not built", t->tag);
@@ -133,7 +142,7 @@ static int tile_kernel(int code, int cin, int dtype, char* name, size_t n, int* 
     return fail(VRS_EUNSUPPORTED, "conv: tile %s needs Cin %% 64 == 0 and 64-deep steps (Cin=%d)", t->tag, cin);
   if (g && t->code != VRS_TILE_128x128 && t->code != VRS_TILE_64x256 && t->code != VRS_TILE_32x256)
     return fail(VRS_EUNSUPPORTED, "conv: tile %s needs Cin %% 32 == 0 (Cin=%d)", t->tag, cin);
-  snprintf(name, n, "vrs_conv_%s_%s_k%d_%c", dsuffix(dtype), t->tag, k64 ? 64 : 32, g ? 'g' : 'a');
+  snprintf(name, n, "vrs_conv_%s_%s_k%d_%c", dsuffix(dtype), t->tag, k64 ? 64 : 32, up ? 'u' : g ? 'g' : 'a');
   *bm = t->bm;
   *bn = t->bn;
   *threads = t->threads;
@@ -222,6 +231,22 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
     a.x_bytes = (int32_t)xb;
     a.w_bytes = (int32_t)wb;
   }
+  if (cs.up) {  // channels [0, up->c) of the input are up(*cs.up), nearest 2x
+    const vrs_nhwc& u = *cs.up;
+    if ((rc = check_view(u, "conv upsample source", 8))) return rc;
+    if (cs.k != 1 || cs.stride != 1 || u.n != x.n || 2 * u.h != x.h || 2 * u.w != x.w || u.c >= x.c || u.c % 64)
+      return fail(VRS_EBADSHAPE, "conv: a fused upsample needs a 1x1 stride-1 conv, a half-size source and a "
+                  "split at a multiple of 64 channels below Cin (source %dx%dx%d, input %dx%dx%d)", u.h, u.w, u.c,
+                  x.h, x.w, x.c);
+    const int64_t ub = ((int64_t)u.n * u.h * u.w * u.pitch - u.c_off) * (int64_t)elt_size(cs.dtype);
+    if (ub >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: upsample source exceeds 2 GiB");
+    a.x2 = at(u, cs.dtype);
+    a.x2_bytes = (int32_t)ub;
+    a.c_split = u.c;
+    a.H2 = u.h;
+    a.W2 = u.w;
+    a.x2_pitch = u.pitch;
+  }
   a.N = x.n; a.H = x.h; a.W = x.w; a.Cin = x.c; a.x_pitch = x.pitch;
   a.Ho = ho; a.Wo = wo; a.Cout = cout;
   a.kh = a.kw = cs.k; a.stride = cs.stride; a.pad = cs.k / 2;
@@ -235,8 +260,9 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   int bm, bn, threads;
   const int tile = cs.tile ? cs.tile
                             : f8 ? (cout <= 64 ? VRS_TILE_64x256 : VRS_TILE_128x128)
-                                 : auto_tile(cout, x.c, M, cs.dtype, ctx->num_cu);
-  if ((rc = tile_kernel(tile, x.c, cs.dtype, name, sizeof name, &bm, &bn, &threads))) return rc;
+                                 : cs.up ? VRS_TILE_128x128   // built in every fused-upsample dtype
+                                         : auto_tile(cout, x.c, M, cs.dtype, ctx->num_cu);
+  if ((rc = tile_kernel(tile, x.c, cs.dtype, cs.up != nullptr, name, sizeof name, &bm, &bn, &threads))) return rc;
   a.tiles_m = (cout + bm - 1) / bm;
   a.tiles_n = (int32_t)((M + bn - 1) / bn);
   int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
@@ -258,7 +284,8 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   const double cin = cs.cin_real > 0 ? cs.cin_real : x.c;
   const double kk = (double)cs.k * cs.k;
   out.back().flops = 2.0 * (double)M * cout * kk * cin;
-  out.back().bytes = (double)x.n * x.h * x.w * cin * es + (double)cout * kk * cin * (f8 ? 1.0 : es) +
+  const double cin_up = cs.up ? (double)cs.up->c : 0.0;   // read at a quarter of the pixels
+  out.back().bytes = (double)x.n * x.h * x.w * (cin - 0.75 * cin_up) * es + (double)cout * kk * cin * (f8 ? 1.0 : es) +
                      (double)M * cout * (a.y_f32 ? 4.0 : es) + (a.res ? (double)M * cout * es : 0.0) + 8.0 * cout;
   return VRS_OK;
 }

@@ -87,6 +87,9 @@ struct ConvSpec {
   int cin_real = 0;  // unpadded input channels for work accounting (0: the view's)
   int tile = VRS_TILE_AUTO;  // dense conv tile (VRS_TILE_*)
   float in_scale = 1.f;      // VRS_FP8: activation quantisation step (power of two)
+  // fused nearest-2x upsample (1x1 stride-1 dense convs): input channels
+  // [0, up->c) are read from this half-resolution view instead of x
+  const vrs_nhwc* up = nullptr;
 };
 // stem conv (3x3 s2, Cin 3) straight from the NCHW float32 image; weights
 // packed by vrs_pack_stem_weight

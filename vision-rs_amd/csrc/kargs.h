@@ -46,6 +46,13 @@ typedef struct {
   /* persistent kernels: bytes from y to the end of the output view's last
    * pixel (< 2^31) */
   int32_t y_bytes;
+  /* fused nearest-2x upsample (1x1 stride-1 convs, 32-deep-step aligned
+   * kernels): input channels [0, c_split) are read from x2, an NHWC buffer of
+   * H2 x W2 = (H/2) x (W/2) pixels with pitch x2_pitch (pointer at its first
+   * channel, x2_bytes readable), at pixel (y/2, x/2); channels [c_split, Cin)
+   * from x as usual.  c_split = 0: no fusion. */
+  const void* x2;
+  int32_t x2_bytes, c_split, H2, W2, x2_pitch;
 } vrs_conv_args;
 
 /* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the

@@ -59,7 +59,10 @@ __device__ __forceinline__ void pipe_schedule() {
 // F8: weights are e4m3 bytes (A operand, 16-byte chunks of 16 k), the bf16
 // activations are quantised to e4m3 while staged into LDS (8 k per 16-byte
 // group -> 8 bytes), and the 32x32x64 fp8 MFMA consumes 64-byte LDS rows.
-template <typename T, int BM, int BN, int BK, int WGM, int WGN, bool ALIGNED, bool F8 = false>
+// UP: input channels [0, a.c_split) come from the half-resolution a.x2 at
+// (y/2, x/2) (fused nearest-2x upsample; 1x1 stride-1 convs, checked on the
+// host); the K steps of those channels come first and switch the B source.
+template <typename T, int BM, int BN, int BK, int WGM, int WGN, bool ALIGNED, bool F8 = false, bool UP = false>
 __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   using E = Elt<T>;
   using G = typename E::group;
@@ -145,6 +148,7 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   int b_iy0[B_IT], b_ix0[B_IT];
   const T* b_ptr[B_IT];
   bool b_ok[B_IT];
+  uint32_t b_off2[B_IT];   // fused upsample: byte offset of the pixel's source in x2
 #pragma unroll
   for (int i = 0; i < B_IT; ++i) {
     const int c = tid + i * NT;
@@ -157,6 +161,10 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
     b_iy0[i] = oy * a.stride - a.pad;
     b_ix0[i] = ox * a.stride - a.pad;
     b_ptr[i] = x + (((int64_t)bb * a.H + b_iy0[i]) * a.W + b_ix0[i]) * a.x_pitch + (c % GPR) * 8;
+    if constexpr (UP)
+      b_off2[i] = b_ok[i] ? (uint32_t)((((int64_t)bb * a.H2 + (oy >> 1)) * a.W2 + (ox >> 1)) * a.x2_pitch + (c % GPR) * 8) *
+                                (uint32_t)sizeof(T)
+                          : kOOB;
   }
 
   G ra[A_IT], rb[B_IT];
@@ -167,6 +175,7 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   // in the zero padding (or past the last pixel/row) use kOOB and read zeros.
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, a.w_bytes);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t rx2 = UP ? make_rsrc(a.x2, a.x2_bytes) : rx;
   uint32_t a_off[A_IT], b_off[B_IT];
   if (ALIGNED) {
 #pragma unroll
@@ -214,12 +223,17 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
                                            sizeof(T));
       const int ky = t_ky, kx = t_kx;
       const uint32_t off = (uint32_t)((ky * a.W + kx) * a.x_pitch + t_ci) * sizeof(T);
+      const bool lo = UP && t_ci < a.c_split;   // fused upsample: this chunk comes from x2 (uniform)
+      const uint32_t off2 = (uint32_t)t_ci * sizeof(T);
       advance();
 #pragma unroll
       for (int i = 0; i < B_IT; ++i) {
         const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
         const bool ok = b_ok[i] && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
-        rb[i] = E::bload(rx, ok ? b_off[i] + off : kOOB, 0);
+        if constexpr (UP)
+          rb[i] = E::bload(lo ? rx2 : rx, lo ? b_off2[i] + off2 : (ok ? b_off[i] + off : kOOB), 0);
+        else
+          rb[i] = E::bload(rx, ok ? b_off[i] + off : kOOB, 0);
       }
     } else {
 #pragma unroll
@@ -288,12 +302,17 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
                              (F8 ? 1u : (uint32_t)sizeof(T)));
       const int ky = t_ky, kx = t_kx;
       const uint32_t off = (uint32_t)((ky * a.W + kx) * a.x_pitch + t_ci) * sizeof(T);
+      const bool lo = UP && t_ci < a.c_split;   // fused upsample: this chunk comes from x2 (uniform)
+      const uint32_t off2 = (uint32_t)t_ci * sizeof(T);
       advance();
 #pragma unroll
       for (int i = 0; i < B_IT; ++i) {
         const int iy = b_iy0[i] + ky, ix = b_ix0[i] + kx;
         const bool ok = b_ok[i] && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
-        rb[i] = E::bload(rx, (ok ? b_off[i] + off : kOOB) | dead, 0);
+        if constexpr (UP)
+          rb[i] = E::bload(lo ? rx2 : rx, (lo ? b_off2[i] + off2 : (ok ? b_off[i] + off : kOOB)) | dead, 0);
+        else
+          rb[i] = E::bload(rx, (ok ? b_off[i] + off : kOOB) | dead, 0);
       }
     };
     auto store_set = [&](int buf, const G (&ra)[A_IT], const G (&rb)[B_IT]) {
@@ -754,6 +773,19 @@ VRS_CONV_KERNEL(vrs_conv_bf16_32x256_k32_g, bf16_t, 32, 256, 32, 1, 4, false)
 // 8 waves (512 threads), wave tile 128x64: half the global loads per MFMA of
 // the 4-wave tiles, for the large layers with Cout >= 256 and Cin % 64 == 0.
 VRS_CONV_KERNEL(vrs_conv_bf16_256x256_k64_a, bf16_t, 256, 256, 64, 2, 4, true)
+// Fused nearest-2x upsample (_u): the 1x1 convs that read an upsampled concat
+#define VRS_CONV_KERNEL_U(NAME, T, BM, BN, BK, WGM, WGN)                                          \
+  extern "C" __global__ __launch_bounds__(64 * WGM * WGN, 2) void NAME(vrs_conv_args a) {        \
+    conv_body<T, BM, BN, BK, WGM, WGN, true, false, true>(a);                                     \
+  }
+VRS_CONV_KERNEL_U(vrs_conv_bf16_128x128_k32_u, bf16_t, 128, 128, 32, 2, 2)
+VRS_CONV_KERNEL_U(vrs_conv_bf16_128x128_k64_u, bf16_t, 128, 128, 64, 2, 2)
+VRS_CONV_KERNEL_U(vrs_conv_bf16_256x128_k32_u, bf16_t, 256, 128, 32, 2, 2)
+VRS_CONV_KERNEL_U(vrs_conv_bf16_256x128_k64_u, bf16_t, 256, 128, 64, 2, 2)
+VRS_CONV_KERNEL_U(vrs_conv_bf16_128x256_k32_u, bf16_t, 128, 256, 32, 2, 2)
+VRS_CONV_KERNEL_U(vrs_conv_bf16_128x256_k64_u, bf16_t, 128, 256, 64, 2, 2)
+VRS_CONV_KERNEL_U(vrs_conv_f32_128x128_k32_u, float, 128, 128, 32, 2, 2)
+VRS_CONV_KERNEL_U(vrs_conv_f32_64x256_k32_u, float, 64, 256, 32, 1, 4)
 // fp8 e4m3 weights + e4m3-quantised bf16 activations (32x32x64 fp8 MFMA),
 // 64-deep steps (Cin % 64 == 0), bf16 outputs
 #define VRS_CONV_F8(NAME, BM, BN, WGM, WGN)                                                       \
