@@ -179,28 +179,31 @@ __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
   for (int dt = 0; dt < 4; ++dt) {
     const int d0 = dt * 16 + lg * 4;
     const int c0 = h * VD + d0;
+    // the nine taps' V and weight loads all go out before the sums (taps
+    // outside the map load the query's own V and are masked), then the sums
+    // run in tap order over the taps inside the map
+    using L = typename std::conditional<sizeof(T) == 2, u32x2_t, f32x4_t>::type;
+    L vv[9], ww[9];
+    bool ok[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+      const int yy = qy + t / 3 - 1, xx = qx + t % 3 - 1;
+      ok[t] = (unsigned)yy < (unsigned)a.H && (unsigned)xx < (unsigned)a.W;
+      const int pix = ok[t] ? yy * a.W + xx : qn;
+      vv[t] = *reinterpret_cast<const L*>(qkv + (img + pix) * a.qkv_pitch + hc + 2 * KD + d0);
+      ww[t] = *reinterpret_cast<const L*>(wpe + t * C + c0);
+    }
     float pe[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ky = 0; ky < 3; ++ky) {
-      const int yy = qy + ky - 1;
-      if ((unsigned)yy >= (unsigned)a.H) continue;
+    for (int t = 0; t < 9; ++t) {
+      if (!ok[t]) continue;
 #pragma unroll
-      for (int kx = 0; kx < 3; ++kx) {
-        const int xx = qx + kx - 1;
-        if ((unsigned)xx >= (unsigned)a.W) continue;
-        const T* vp = qkv + (img + yy * a.W + xx) * a.qkv_pitch + hc + 2 * KD + d0;
-        const T* wk = wpe + (ky * 3 + kx) * C + c0;
+      for (int r = 0; r < 4; ++r) {
         if constexpr (sizeof(T) == 2) {
-          const u32x2_t vv = *reinterpret_cast<const u32x2_t*>(vp);
-          const u32x2_t ww = *reinterpret_cast<const u32x2_t*>(wk);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint32_t vw = vv[r >> 1] >> (16 * (r & 1)), wwv = ww[r >> 1] >> (16 * (r & 1));
-            pe[r] += bf2f((bf16_t)wwv) * bf2f((bf16_t)vw);
-          }
+          const uint32_t vw = vv[t][r >> 1] >> (16 * (r & 1)), wwv = ww[t][r >> 1] >> (16 * (r & 1));
+          pe[r] += bf2f((bf16_t)wwv) * bf2f((bf16_t)vw);
         } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) pe[r] += E::to_f(wk[r]) * E::to_f(vp[r]);
+          pe[r] += ww[t][r] * vv[t][r];
         }
       }
     }
