@@ -236,12 +236,28 @@ def _time_launches(fn, n_sets, iters=20, warmup=3):
     return sum(e0.elapsed_time(e1) for e0, e1 in evs) / iters  # ms
 
 
-def micro(ctx, emit):
-    """BASELINE configs 2-4 as isolated kernels (bf16 unless stated)."""
+def _cpu_ms(fn, reps=1):
+    """Wall time of fn() on the CPU oracle (float32 restatement, OpenMP over
+    the host's cores), after one warm call: the reference has no CPU path, so
+    this is the CPU baseline timed beside each GPU config."""
+    fn()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
+def micro(ctx, emit, cpu=True):
+    """BASELINE configs 2-4 as isolated kernels (bf16 unless stated), each with
+    the CPU oracle's time for the same config beside it (cpu_ms; cpu=False
+    skips it)."""
     import numpy as np
     import torch
     import vrs
     from vrs.synth import seeded_params
+    if cpu:
+        import oracle
+        cores = oracle.num_threads()
     dev = "cuda"
     MALL = 256 * 2 ** 20  # Infinity Cache: rotate buffer sets beyond it for HBM-bound kernels
 
@@ -284,10 +300,17 @@ def micro(ctx, emit):
             if best is None or ms < best[1]:
                 best = (tile, ms)
         tile, ms = best
-        emit({"config": name, "batch": B, "us": round(ms * 1e3, 2), "tile": tile,
-              "gflop": round(flops / 1e9, 2), "tflops": round(flops / ms / 1e9, 1),
-              "frac_mfma": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
-              "mb": round((in_b + out_b + cout * cin * k * k * 2) / 1e6, 1), "buffer_sets": n_sets})
+        line = {"config": name, "batch": B, "us": round(ms * 1e3, 2), "tile": tile,
+                "gflop": round(flops / 1e9, 2), "tflops": round(flops / ms / 1e9, 1),
+                "frac_mfma": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+                "mb": round((in_b + out_b + cout * cin * k * k * 2) / 1e6, 1), "buffer_sets": n_sets}
+        if cpu:
+            xc = rng.standard_normal((B, cin, hw, hw)).astype(np.float32)
+            scc = np.full(cout, 1.0 / np.sqrt(1.001), np.float32)
+            line["cpu_ms"] = round(_cpu_ms(lambda: oracle.affine_act(oracle.conv2d(xc, wt, s, k // 2), scc,
+                                                                       np.zeros(cout, np.float32), 1)), 1)
+            line["cpu_cores"] = cores
+        emit(line)
         del xs, ys
 
     # (c) depthwise 3x3 512 @20x20, HBM-bound; plus the YOLO26m head's largest
@@ -304,9 +327,16 @@ def micro(ctx, emit):
         ys = [torch.empty(bb, hw, hw, C, dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
         ms = _time_launches(lambda i: ctx.conv2d(vrs.nhwc(xs[i]), wp, sc, sh, vrs.nhwc(ys[i]), 3, 1, C,
                                                  vrs.ACT_SILU, None, vrs.BF16), n_sets, iters=60)
-        emit({"config": name, "batch": bb, "us": round(ms * 1e3, 2), "mb": round(nb / 1e6, 2),
-              "gbs": round(nb / ms / 1e6, 1), "frac_hbm": round(nb / ms / 1e6 / PEAK_HBM_GBS, 4),
-              "buffer_sets": n_sets})
+        line = {"config": name, "batch": bb, "us": round(ms * 1e3, 2), "mb": round(nb / 1e6, 2),
+                "gbs": round(nb / ms / 1e6, 1), "frac_hbm": round(nb / ms / 1e6 / PEAK_HBM_GBS, 4),
+                "buffer_sets": n_sets}
+        if cpu:
+            xc = rng.standard_normal((bb, C, hw, hw)).astype(np.float32)
+            scc = np.full(C, 1.0 / np.sqrt(1.001), np.float32)
+            line["cpu_ms"] = round(_cpu_ms(lambda: oracle.affine_act(oracle.conv2d(xc, wdw, 1, 1, groups=C), scc,
+                                                                       np.zeros(C, np.float32), 1)), 1)
+            line["cpu_cores"] = cores
+        emit(line)
         del xs, ys
 
     # ---- config 2: isolated PSA attention block, B=32, 256 ch @20x20, 4 heads --
@@ -327,11 +357,16 @@ def micro(ctx, emit):
     ms_blk = _time_launches(lambda i: m.run_launches(1, len(names) - 2), 1, iters=20)  # qkv..proj, no pack/unpack
     core_fl = work[ai][0]
     blk_fl = sum(w[0] for w in work[1:len(names) - 1])
-    emit({"config": "c2 psa attention B32 256ch 20x20 4 heads", "core_us": round(ms_core * 1e3, 2),
-          "core_gflop": round(core_fl / 1e9, 3), "core_tflops": round(core_fl / ms_core / 1e9, 1),
-          "core_frac_mfma": round(core_fl / ms_core / 1e9 / PEAK_BF16_TFLOPS, 4),
-          "block_us": round(ms_blk * 1e3, 2), "block_gflop": round(blk_fl / 1e9, 3),
-          "block_tflops": round(blk_fl / ms_blk / 1e9, 1)})
+    line = {"config": "c2 psa attention B32 256ch 20x20 4 heads", "core_us": round(ms_core * 1e3, 2),
+            "core_gflop": round(core_fl / 1e9, 3), "core_tflops": round(core_fl / ms_core / 1e9, 1),
+            "core_frac_mfma": round(core_fl / ms_core / 1e9 / PEAK_BF16_TFLOPS, 4),
+            "block_us": round(ms_blk * 1e3, 2), "block_gflop": round(blk_fl / 1e9, 3),
+            "block_tflops": round(blk_fl / ms_blk / 1e9, 1)}
+    if cpu:  # the attention core (softmax(q k^T * kd^-0.5) v) on the oracle
+        qkvc = np.random.default_rng(2).standard_normal((32, 4 * 128, 20, 20)).astype(np.float32)
+        line["cpu_core_ms"] = round(_cpu_ms(lambda: oracle.psa_attention(qkvc, 4, 32, 64)), 1)
+        line["cpu_cores"] = cores
+    emit(line)
     m.close()
 
     # ---- config 4: MSDA, fp32 value, B=8, Q=300, 8 heads, 4 levels x 4 points ----
@@ -348,10 +383,15 @@ def micro(ctx, emit):
     ms = _time_launches(lambda i: ctx.msda(vals[i], shapes, ref, off, attw, out), n_sets, iters=60)
     comp = vbytes + ref.numel() * 4 + off.numel() * 4 + attw.numel() * 4 + out.numel() * 4
     issued = Bq * Q * Hh * L * Pp * 4 * 32 * 4
-    emit({"config": "c4 msda B8 Q300 8h 4L 4P fp32", "us": round(ms * 1e3, 2),
-          "compulsory_mb": round(comp / 1e6, 2), "gbs_compulsory": round(comp / ms / 1e6, 1),
-          "frac_hbm": round(comp / ms / 1e6 / PEAK_HBM_GBS, 4), "issued_gather_mb": round(issued / 1e6, 1),
-          "buffer_sets": n_sets})
+    line = {"config": "c4 msda B8 Q300 8h 4L 4P fp32", "us": round(ms * 1e3, 2),
+            "compulsory_mb": round(comp / 1e6, 2), "gbs_compulsory": round(comp / ms / 1e6, 1),
+            "frac_hbm": round(comp / ms / 1e6 / PEAK_HBM_GBS, 4), "issued_gather_mb": round(issued / 1e6, 1),
+            "buffer_sets": n_sets}
+    if cpu:
+        vc, rc_, oc, ac = (t.cpu().numpy() for t in (vals[0], ref, off, attw))
+        line["cpu_ms"] = round(_cpu_ms(lambda: oracle.msda(vc, shapes, rc_, oc, ac), reps=3), 2)
+        line["cpu_cores"] = cores
+    emit(line)
 
     # ---- letterbox preprocessing: 64 RGB8 1280x720 frames -> [64,3,640,640] f32 ----
     nimg, (lw, lh), S = 64, (1280, 720), 640
@@ -362,9 +402,16 @@ def micro(ctx, emit):
     outs_lb = [torch.empty(nimg, 3, S, S, device=dev) for _ in range(n_sets)]
     offs = [i * lw * lh * 3 for i in range(nimg)]
     ms = _time_launches(lambda i: ctx.letterbox(srcs[i], offs, [(lw, lh)] * nimg, S, out=outs_lb[i]), n_sets, iters=30)
-    emit({"config": "letterbox 64x 1280x720 RGB8 -> 640 f32 NCHW", "us": round(ms * 1e3, 2),
-          "mb": round((src_b + out_b) / 1e6, 1), "gbs": round((src_b + out_b) / ms / 1e6, 1),
-          "frac_hbm": round((src_b + out_b) / ms / 1e6 / PEAK_HBM_GBS, 4), "buffer_sets": n_sets})
+    line = {"config": "letterbox 64x 1280x720 RGB8 -> 640 f32 NCHW", "us": round(ms * 1e3, 2),
+            "mb": round((src_b + out_b) / 1e6, 1), "gbs": round((src_b + out_b) / ms / 1e6, 1),
+            "frac_hbm": round((src_b + out_b) / ms / 1e6 / PEAK_HBM_GBS, 4), "buffer_sets": n_sets}
+    if cpu:  # the oracle is single-threaded per frame: 4 frames timed, scaled to 64
+        frame = srcs[0][: lw * lh * 3].cpu().numpy().reshape(lh, lw, 3)
+        per = _cpu_ms(lambda: oracle.letterbox(frame, S), reps=4)
+        line["cpu_ms"] = round(per * nimg, 1)
+        line["cpu_sample"] = "4 frames timed one at a time (1 thread), x64"
+        line["cpu_cores"] = 1
+    emit(line)
 
 
 def main() -> int:
@@ -405,7 +452,7 @@ def main() -> int:
     torch.cuda.init()
     ctx = vrs.Context(0)
     if a.micro:
-        micro(ctx, lambda d: print(json.dumps(d), flush=True))
+        micro(ctx, lambda d: print(json.dumps(d), flush=True), cpu=not a.no_cpu)
         return 0
     if a.traffic_pass:
         traffic_pass(a, ctx, a.traffic_pass)
