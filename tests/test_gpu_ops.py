@@ -74,6 +74,66 @@ def test_conv2d(case, dtype):
         assert torch.all(rest == 7.0)
 
 
+def _random_conv_cases(n_cases, seed):
+    """Seeded random dense-conv shapes: ragged pixel and channel counts, both
+    kernel sizes and strides, residual on or off, channel-slice input/output
+    views, and a tile drawn from those built for the dtype."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n_cases):
+        k = int(rng.choice([1, 3]))
+        s = int(rng.choice([1, 2])) if k == 3 else 1
+        cin = int(rng.choice([8, 16, 24, 32, 40, 64, 96, 128, 192, 256]))
+        cout = int(rng.integers(1, 40)) * 8
+        n = int(rng.integers(1, 4))
+        h, w = int(rng.integers(3, 23)), int(rng.integers(3, 23))
+        res = bool(rng.integers(0, 2))
+        xo = int(rng.choice([0, 8]))
+        yo = int(rng.choice([0, 8, 16]))
+        cases.append((n, cin, h, w, cout, k, s, res, xo, yo, int(rng.integers(0, 1 << 30))))
+    return cases
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("case", _random_conv_cases(24, 2026))
+def test_conv2d_random(case, dtype):
+    """24 seeded random shapes per dtype, each on one tile drawn from the
+    tiles built for the dtype (the 64-deep step whenever Cin allows it),
+    against the oracle; bytes outside the output view stay untouched."""
+    import torch
+    n, cin, h, w, cout, k, s, with_res, xo, yo, tseed = case
+    trng = np.random.default_rng(tseed)
+    tiles = TILES_BF16 + [vrs.TILE_256x256] if dtype == vrs.BF16 else TILES_F32
+    tile = int(trng.choice(tiles))
+    if tile == vrs.TILE_256x256 and cin % 64:
+        tile = vrs.TILE_128x128
+    if cin % 32 and tile not in (vrs.TILE_128x128, vrs.TILE_64x256, vrs.TILE_32x256):
+        tile = vrs.TILE_64x256    # unaligned Cin: the generic-load kernels
+    if dtype == vrs.BF16 and trng.integers(0, 2) and tile != vrs.TILE_256x256:
+        tile |= vrs.TILE_K32
+    rnd = rounder(dtype)
+    x = rnd(trng.standard_normal((n, cin, h, w)).astype(np.float32))
+    wt = rnd((trng.standard_normal((cout, cin, k, k)) * np.sqrt(2.0 / (cin * k * k))).astype(np.float32))
+    scale = trng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = trng.normal(0, 0.2, cout).astype(np.float32)
+    ho, wo = (h + 2 * (k // 2) - k) // s + 1, (w + 2 * (k // 2) - k) // s + 1
+    ref = oracle.affine_act(oracle.conv2d(x, wt, s, k // 2), scale, shift, 1)
+    res = rnd(trng.standard_normal((n, cout, ho, wo)).astype(np.float32)) if with_res else None
+    if with_res:
+        ref = ref + res
+    xp, yp = cin + xo + 8 * (xo > 0), cout + yo + 8
+    xt = to_nhwc(x, dtype, xp, xo)
+    yt = torch.full((n, ho, wo, yp), 7.0, dtype=tdtype(dtype), device="cuda")
+    rt = to_nhwc(res, dtype, yp, yo) if with_res else None
+    ctx().conv2d(vrs.nhwc(xt, cin, xo), dev(vrs.pack_conv_weight(wt, 1, cin, dtype)), dev(scale), dev(shift),
+                 vrs.nhwc(yt, cout, yo), k, s, 1, vrs.ACT_SILU, vrs.nhwc(rt, cout, yo) if with_res else None, dtype,
+                 tile=tile)
+    torch.cuda.synchronize()
+    assert rel_err(from_nhwc(yt, cout, yo), ref, FLOOR[dtype]) < TOL[dtype], (case, tile)
+    rest = torch.cat([yt[..., :yo], yt[..., yo + cout:]], -1).float()
+    assert torch.all(rest == 7.0)
+
+
 TILES_BF16 = [vrs.TILE_128x128, vrs.TILE_256x128, vrs.TILE_128x256, vrs.TILE_64x256, vrs.TILE_32x256]
 TILES_F32 = [vrs.TILE_128x128, vrs.TILE_64x256, vrs.TILE_32x256]
 
