@@ -176,6 +176,95 @@ def traffic_summary(fetch_dir, write_dir):
     return "\n".join(out)
 
 
+def mfma_summary(pmc_dir, xcds=8, simds=1024):
+    """Markdown table of MFMA busy per launch of the last forward, from one
+    --pmc pass of GRBM_GUI_ACTIVE and SQ_VALU_MFMA_BUSY_CYCLES over the
+    --traffic-pass workload.  GRBM_GUI_ACTIVE is summed over the XCDs and
+    SQ_VALU_MFMA_BUSY_CYCLES over every SIMD (one cycle per 1024 bf16 flops
+    of MFMA issue), so busy = MFMA_BUSY / (GRBM_GUI_ACTIVE / xcds * simds)."""
+    import csv
+    import glob
+    with open(os.path.join(pmc_dir, "labels.json")) as f:
+        meta = json.load(f)
+    labels, work = meta["labels"], meta["work"]
+    disp = {}
+    for fn in glob.glob(os.path.join(pmc_dir, "**", "*counter_collection.csv"), recursive=True):
+        with open(fn) as f:
+            for r in csv.DictReader(f):
+                d = disp.setdefault(int(r["Dispatch_Id"]), {"k": r["Kernel_Name"],
+                                                             "ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+                d[r["Counter_Name"]] = float(r["Counter_Value"])
+    mine = [d for _, d in sorted(disp.items()) if d["k"].startswith("vrs_")][-len(labels):]
+    if [d["k"] for d in mine] != [lab.split(":")[-1] for lab in labels]:
+        raise SystemExit(f"the last {len(labels)} vrs_ dispatches do not match the forward's launches")
+    out = [f"busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcds} x {simds} SIMDs); "
+           "clock = GRBM_GUI_ACTIVE / XCDs / duration; TFLOP/s = algorithmic flops / duration.", "",
+           "| launch | kernel | us | clock MHz | MFMA busy % | algorithmic TFLOP/s |",
+           "|---|---|---|---|---|---|"]
+    sym_tot = {}
+    for lab, d, (fl, _) in zip(labels, mine, work):
+        if fl <= 0:
+            continue
+        cyc = d["GRBM_GUI_ACTIVE"] / xcds
+        busy = d["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * simds)
+        us = d["ns"] / 1e3
+        sym = lab.split(":")[-1]
+        t = sym_tot.setdefault(sym, [0, 0.0, 0.0, 0.0, 0.0])
+        t[0] += 1
+        t[1] += us
+        t[2] += fl
+        t[3] += d["SQ_VALU_MFMA_BUSY_CYCLES"] / simds
+        t[4] += cyc
+        out.append(f"| {lab.rsplit(':', 1)[0]} | {sym} | {us:.1f} | {cyc / us:.0f} | {100 * busy:.1f} | "
+                   f"{fl / us / 1e6:.1f} |")
+    out += ["", "| kernel | launches | total us | MFMA busy % (over its cycles) | algorithmic TFLOP/s |",
+            "|---|---|---|---|---|"]
+    for sym, (n, us, fl, bc, cyc) in sorted(sym_tot.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"| {sym} | {n} | {us:.0f} | {100 * bc / cyc:.1f} | {fl / us / 1e6:.1f} |")
+    return "\n".join(out)
+
+
+def pmc_table(dirs, copy_bytes=2 ** 30):
+    """Per (kernel, grid) medians of every counter in the given --pmc passes
+    (typically over `bench.py --micro --no-cpu`), with the FETCH_SIZE and
+    WRITE_SIZE passes scaled to HBM bytes by the 1 GiB calibration copy and
+    MFMA busy as in mfma_summary."""
+    import csv
+    import glob
+    import statistics
+    per = {}
+    for d in dirs:
+        for fn in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(fn) as f:
+                for r in csv.DictReader(f):
+                    k = (r["Kernel_Name"], int(r["Grid_Size"]))
+                    e = per.setdefault(k, {})
+                    e.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+                    e.setdefault("ns:" + r["Counter_Name"], []).append(
+                        int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    med = {k: {c: statistics.median(v) for c, v in e.items()} for k, e in per.items()}
+    cal = {c: max(e.get(c, 0.0) for (n, _), e in med.items() if "copybuffer" in n.lower())
+           for c in ("FETCH_SIZE", "WRITE_SIZE")}
+    fac = {c: copy_bytes / 1024.0 / v if v else None for c, v in cal.items()}
+    out = [f"Calibration (1 GiB device copy): FETCH_SIZE factor {fac['FETCH_SIZE'] or 0:.4f}, "
+           f"WRITE_SIZE factor {fac['WRITE_SIZE'] or 0:.4f}.", "",
+           "| kernel | grid | us | MFMA busy % | HBM read MB | HBM write MB | HBM GB/s |", "|---|---|---|---|---|---|---|"]
+    for (name, grid), e in sorted(med.items()):
+        if not name.startswith("vrs_"):
+            continue
+        us = [e[c] / 1e3 for c in e if c.startswith("ns:")]
+        us = statistics.median(us) if us else 0.0
+        busy = ""
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in e and e.get("GRBM_GUI_ACTIVE"):
+            busy = f"{100 * e['SQ_VALU_MFMA_BUSY_CYCLES'] / (e['GRBM_GUI_ACTIVE'] / 8 * 1024):.1f}"
+        rd = e["FETCH_SIZE"] * fac["FETCH_SIZE"] * 1024 / 1e6 if "FETCH_SIZE" in e and fac["FETCH_SIZE"] else None
+        wr = e["WRITE_SIZE"] * fac["WRITE_SIZE"] * 1024 / 1e6 if "WRITE_SIZE" in e and fac["WRITE_SIZE"] else None
+        gbs = f"{(rd + wr) / us * 1e3:.0f}" if rd is not None and wr is not None and us else ""
+        out.append(f"| {name} | {grid} | {us:.1f} | {busy} | {'' if rd is None else f'{rd:.2f}'} | "
+                   f"{'' if wr is None else f'{wr:.2f}'} | {gbs} |")
+    return "\n".join(out)
+
+
 def traffic_lookup(sym, names):
     """HBM bytes per launch of `sym` in this forward, from the committed
     per-launch table (launches whose layer ran the same kernel there)."""
@@ -434,9 +523,20 @@ def main() -> int:
                     help="instead: the workload profiled by the rocprofv3 --pmc traffic passes")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="instead (no GPU): print the per-launch HBM traffic table from the two passes")
+    ap.add_argument("--mfma-summary", metavar="PMC_DIR",
+                    help="instead (no GPU): print the per-launch MFMA busy table from a GRBM_GUI_ACTIVE + "
+                         "SQ_VALU_MFMA_BUSY_CYCLES pass over the --traffic-pass workload")
+    ap.add_argument("--pmc-table", nargs="+", metavar="PMC_DIR",
+                    help="instead (no GPU): per-kernel medians of the counters in these --pmc passes")
     a = ap.parse_args()
+    if a.pmc_table:
+        print(pmc_table(a.pmc_table))
+        return 0
     if a.traffic_summary:
         print(traffic_summary(*a.traffic_summary))
+        return 0
+    if a.mfma_summary:
+        print(mfma_summary(a.mfma_summary))
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
