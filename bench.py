@@ -502,6 +502,29 @@ def micro(ctx, emit, cpu=True):
         line["cpu_cores"] = 1
     emit(line)
 
+    # ---- Detect post-process (decode, score, stable top-k) on the bs64 640 outputs ----
+    B, nc, A, max_det = 64, 80, 8400, 300
+    g = torch.Generator(device=dev).manual_seed(0)
+    boxes = torch.rand(B, 4 * A, device=dev, generator=g) * 8.0
+    # class logits ~ N(-6, 1.5): about 4 % of the anchors have a class above the
+    # 0.25 threshold, a few hundred candidates per image for the top 300
+    scores = torch.randn(B, nc * A, device=dev, generator=g) * 1.5 - 6.0
+    ws = torch.empty(64 * 2 ** 20, dtype=torch.uint8, device=dev)
+    pp = ctx.detect_postprocess(boxes, scores, nc, 640, 640, (8, 16, 32), 0.25, max_det, workspace=ws)
+    ms = _time_launches(lambda i: ctx.detect_postprocess(boxes, scores, nc, 640, 640, (8, 16, 32), 0.25, max_det,
+                                                         outs=pp, workspace=ws), 1, iters=30)
+    in_b = (boxes.numel() + scores.numel()) * 4
+    line = {"config": "detect post-process bs64 640 (8400 anchors, 80 classes, thr 0.25, top 300)",
+            "us": round(ms * 1e3, 2), "mb": round(in_b / 1e6, 1), "gbs": round(in_b / ms / 1e6, 1),
+            "frac_hbm": round(in_b / ms / 1e6 / PEAK_HBM_GBS, 4),
+            "detections_per_image": round(float(pp[0].float().mean()), 1)}
+    if cpu:
+        bc, scc = boxes.cpu().numpy(), scores.cpu().numpy()
+        line["cpu_ms"] = round(_cpu_ms(lambda: oracle.detect_postprocess(bc, scc, nc, 640, 640, (8, 16, 32), 0.25,
+                                                                          max_det), reps=3), 2)
+        line["cpu_cores"] = cores
+    emit(line)
+
 
 def main() -> int:
     ap = argparse.ArgumentParser()

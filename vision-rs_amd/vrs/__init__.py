@@ -225,7 +225,10 @@ class Context:
                                       _ptr(pe_shift), C.byref(out), _stream(stream)))
 
     def detect_postprocess(self, boxes, scores, nc, img_h, img_w, strides=(8, 16, 32), thr=0.25, max_det=300,
-                           stream=None):
+                           stream=None, outs=None, workspace=None):
+        """outs: the (count, score, cls, anchor, xywh) of an earlier call with
+        the same shapes, written again instead of allocated; workspace: a
+        uint8 device tensor of at least vrs_detect_workspace_size bytes."""
         import torch
         n = boxes.shape[0]
         st = (C.c_int32 * 4)(*list(strides), *([0] * (4 - len(strides))))
@@ -234,15 +237,25 @@ class Context:
         if ws_bytes == 0:
             raise VrsError(-1, lib().vrs_last_error().decode(errors="replace"))
         dev = boxes.device
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        count = torch.empty(n, dtype=torch.int32, device=dev)
-        score = torch.empty(n, max_det, dtype=torch.float32, device=dev)
-        cls = torch.empty(n, max_det, dtype=torch.int32, device=dev)
-        anchor = torch.empty(n, max_det, dtype=torch.int32, device=dev)
-        xywh = torch.empty(n, max_det, 4, dtype=torch.float32, device=dev)
+        if workspace is not None:
+            ws = workspace
+            if ws.numel() * ws.element_size() < ws_bytes:
+                raise VrsError(-1, f"detect_postprocess: workspace of {ws.numel()} bytes, {ws_bytes} needed")
+        else:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        if outs is not None:
+            count, score, cls, anchor, xywh = outs
+        else:
+            count = torch.empty(n, dtype=torch.int32, device=dev)
+            score = torch.empty(n, max_det, dtype=torch.float32, device=dev)
+            cls = torch.empty(n, max_det, dtype=torch.int32, device=dev)
+            anchor = torch.empty(n, max_det, dtype=torch.int32, device=dev)
+            xywh = torch.empty(n, max_det, 4, dtype=torch.float32, device=dev)
         check(lib().vrs_detect_postprocess(self.handle, C.byref(d), _ptr(boxes), _ptr(scores), _ptr(ws), ws_bytes,
                                            _ptr(count), _ptr(score), _ptr(cls), _ptr(anchor), _ptr(xywh),
                                            _stream(stream)))
+        if outs is not None:
+            return outs
         return count, score, cls, anchor, xywh
 
     def detect_unletterbox(self, count, xywh, orig_wh, img_size, stream=None):
