@@ -11,9 +11,12 @@
 // ascending anchor order); sigmoid scores are non-negative so their IEEE bits
 // order like the values.
 //
-// Stage 2 (one workgroup per image): exact top-k.  A most-significant-digit
-// radix select over the keys finds the k-th largest key (k = min(count,
-// max_det)); the keys >= it are gathered into LDS and bitonic-sorted.
+// Stage 2 (one workgroup per image): exact top-k (k = min(count, max_det)).
+// With at most TOPK_MAX kept anchors every key is gathered into LDS and
+// bitonic-sorted.  Otherwise a most-significant-digit radix select raises a
+// threshold 8 bits at a time and stops as soon as the keys at or above it
+// fit the LDS buffer (at the latest after the 8th digit, when the threshold
+// is the k-th largest key itself); those keys are gathered and sorted.
 #include "common.h"
 
 extern "C" __global__ __launch_bounds__(256) void vrs_detect_stage1(vrs_det1_args a) {
@@ -54,7 +57,7 @@ constexpr int TOPK_MAX = 1024;
 extern "C" __global__ __launch_bounds__(1024) void vrs_detect_stage2(vrs_det2_args a) {
   __shared__ uint32_t hist[256];
   __shared__ uint64_t sel[TOPK_MAX];
-  __shared__ uint32_t s_count, s_nsel, s_digit, s_krem;
+  __shared__ uint32_t s_count, s_nsel, s_digit, s_krem, s_ntop;
   const int b = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
   const uint64_t* keys = a.keys + (int64_t)b * a.A;
 
@@ -67,49 +70,65 @@ extern "C" __global__ __launch_bounds__(1024) void vrs_detect_stage2(vrs_det2_ar
   const uint32_t count = s_count;
   const uint32_t k = count < (uint32_t)a.max_det ? count : (uint32_t)a.max_det;
 
-  uint64_t prefix = 0, pmask = 0;
-  if (tid == 0) s_krem = k;
-  for (int shift = 56; shift >= 0 && k > 0; shift -= 8) {
-    for (int i = tid; i < 256; i += nt) hist[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < a.A; i += nt) {
-      const uint64_t key = keys[i];
-      if (key != 0ull && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t cum = 0, krem = s_krem;
-      int d = 255;
-      for (; d > 0; --d) {
-        if (cum + hist[d] >= krem) break;
-        cum += hist[d];
+  // gather threshold: every nonzero key when they all fit the buffer
+  uint64_t thr_key = 1ull;
+  if (count > (uint32_t)TOPK_MAX && k > 0) {
+    uint64_t prefix = 0, pmask = 0;
+    if (tid == 0) s_krem = k;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+      for (int i = tid; i < 256; i += nt) hist[i] = 0;
+      __syncthreads();
+      for (int i = tid; i < a.A; i += nt) {
+        const uint64_t key = keys[i];
+        if (key != 0ull && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
       }
-      s_digit = (uint32_t)d;
-      s_krem = krem - cum;
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t cum = 0, krem = s_krem;
+        int d = 255;
+        for (; d > 0; --d) {
+          if (cum + hist[d] >= krem) break;
+          cum += hist[d];
+        }
+        s_digit = (uint32_t)d;
+        s_krem = krem - cum;
+        // keys whose digits so far are >= the new prefix: above it at the
+        // earlier digits (k - krem), in the higher bins of this one (cum),
+        // and in bin d
+        s_ntop = (k - krem) + cum + hist[d];
+      }
+      __syncthreads();
+      prefix |= ((uint64_t)s_digit) << shift;
+      pmask |= 255ull << shift;
+      const bool fits = s_ntop <= (uint32_t)TOPK_MAX;
+      __syncthreads();
+      if (fits) break;
     }
-    __syncthreads();
-    prefix |= ((uint64_t)s_digit) << shift;
-    pmask |= 255ull << shift;
-    __syncthreads();
+    // lower bits zero: the keys >= prefix are exactly those counted in s_ntop,
+    // and they include the k largest
+    thr_key = prefix;
   }
-  const uint64_t kth = prefix;  // exact k-th largest key (keys are unique)
 
   for (int i = tid; i < TOPK_MAX; i += nt) sel[i] = 0ull;
   __syncthreads();
   if (k > 0)
     for (int i = tid; i < a.A; i += nt) {
       const uint64_t key = keys[i];
-      if (key != 0ull && key >= kth) {
+      if (key != 0ull && key >= thr_key) {
         const uint32_t slot = atomicAdd(&s_nsel, 1u);
         if (slot < (uint32_t)TOPK_MAX) sel[slot] = key;
       }
     }
   __syncthreads();
+  // sort the smallest power of two of slots holding every gathered key
+  const uint32_t nsel = s_nsel < (uint32_t)TOPK_MAX ? s_nsel : (uint32_t)TOPK_MAX;
+  int P = 2;
+  while ((uint32_t)P < nsel) P <<= 1;
 
-  // bitonic sort, descending, over TOPK_MAX slots (zeros sink to the end)
-  for (int size = 2; size <= TOPK_MAX; size <<= 1)
+  // bitonic sort, descending, over P slots (zeros sink to the end)
+  for (int size = 2; size <= P; size <<= 1)
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < TOPK_MAX; i += nt) {
+      for (int i = tid; i < P; i += nt) {
         const int j = i ^ stride;
         if (j > i) {
           const bool desc = (i & size) == 0;
