@@ -265,6 +265,35 @@ def pmc_table(dirs, copy_bytes=2 ** 30):
     return "\n".join(out)
 
 
+def layers_summary(path, peak_tflops=PEAK_BF16_TFLOPS):
+    """Markdown table of the per-layer lines `bench.py --layers` writes to
+    stderr: each launch's time (HIP events around every launch of one
+    eager forward, averaged over 3), its algorithmic work and the fraction of
+    its bounding roofline (MFMA or HBM, whichever the work's arithmetic
+    intensity puts it under)."""
+    rows = []
+    with open(path) as f:
+        for line in f:
+            if line.startswith('{"layer"'):
+                rows.append(json.loads(line))
+    ridge = peak_tflops * 1e12 / (PEAK_HBM_GBS * 1e9)
+    out = ["| launch | kernel | us | GFLOP | MB | bound | achieved | roofline frac |", "|---|---|---|---|---|---|---|---|"]
+    tot = ideal = 0.0
+    for r in rows:
+        lab, sym = r["layer"].rsplit(":", 1)
+        fl, mb, us = r["gflop"] * 1e9, r["mb"] * 1e6, r["us"]
+        if fl > 0 and fl / max(mb, 1.0) > ridge:
+            ach, bound, frac = f"{fl / us / 1e6:.0f} TFLOP/s", "mfma", fl / us / 1e6 / peak_tflops
+        else:
+            ach, bound, frac = f"{mb / us / 1e3:.0f} GB/s", "hbm", mb / us / 1e3 / PEAK_HBM_GBS
+        tot += us
+        ideal += max(fl / (peak_tflops * 1e12), mb / (PEAK_HBM_GBS * 1e9)) * 1e6
+        out.append(f"| {lab} | {sym} | {us:.1f} | {r['gflop']:.2f} | {r['mb']:.1f} | {bound} | {ach} | {frac:.3f} |")
+    out += ["", f"{len(rows)} launches, {tot:.0f} us in sum (eager, one launch at a time; the hipGraph replay "
+                f"overlaps branches on 4 streams); at the MI355X peaks the same work needs {ideal:.0f} us."]
+    return "\n".join(out)
+
+
 def traffic_lookup(sym, names):
     """HBM bytes per launch of `sym` in this forward, from the committed
     per-launch table (launches whose layer ran the same kernel there)."""
@@ -549,9 +578,14 @@ def main() -> int:
     ap.add_argument("--mfma-summary", metavar="PMC_DIR",
                     help="instead (no GPU): print the per-launch MFMA busy table from a GRBM_GUI_ACTIVE + "
                          "SQ_VALU_MFMA_BUSY_CYCLES pass over the --traffic-pass workload")
+    ap.add_argument("--layers-summary", metavar="STDERR_FILE",
+                    help="instead (no GPU): per-layer roofline table from a --layers run's stderr")
     ap.add_argument("--pmc-table", nargs="+", metavar="PMC_DIR",
                     help="instead (no GPU): per-kernel medians of the counters in these --pmc passes")
     a = ap.parse_args()
+    if a.layers_summary:
+        print(layers_summary(a.layers_summary))
+        return 0
     if a.pmc_table:
         print(pmc_table(a.pmc_table))
         return 0
