@@ -259,6 +259,41 @@ def test_yolo26m_bf16_vs_oracle():
         assert np.array_equal(gan[b, :k][sep], ran[b, :k][sep])
 
 
+def test_yolo26m_bf16_bs64_640_full_size():
+    """BASELINE config 5 at its full size (YOLO26m, batch 64, 640x640,
+    bfloat16, per-layer autotuned tiles, as bench.py runs it): images 0 and 31
+    of the batch against the oracle run on each image alone (the bf16 bar and
+    the class argmax where the reference margin exceeds it), every output
+    finite, and image 0 repeated at index 63 gives bit-identical outputs (no
+    kernel lets one image's pixels reach another's)."""
+    import torch
+    x = np.random.default_rng(7).uniform(0, 1, (64, 3, 640, 640)).astype(np.float32)
+    x[63] = x[0]
+    x = bf16_round(x)
+    desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="m", one2one=True)
+    m = vrs.Model(ctx(), desc, 64, 640, 640, vrs.BF16, 1e-3)
+    P = _yolo_params(m, bf16=True)
+    m.load(P)
+    boxes, scores = [o.cpu().numpy() for o in m.forward(dev(x))]
+    torch.cuda.synchronize()
+    assert boxes.shape == (64, 33600) and scores.shape == (64, 672000)
+    assert np.all(np.isfinite(boxes)) and np.all(np.isfinite(scores))
+    assert np.array_equal(boxes[63], boxes[0]) and np.array_equal(scores[63], scores[0])
+    a_s = [(640 // s) ** 2 for s in (8, 16, 32)]
+    for i in (0, 31):
+        rb, rs = Y.yolo26(80, "m")(Y.Params(P, eps=1e-3, act_q=bf16_round), x[i:i + 1])
+        eb, mb = bf16_block_errors(boxes[i:i + 1], rb)
+        es, ms = bf16_block_errors(scores[i:i + 1], rs)
+        print(f"yolo26m bf16 bs64 image {i}: normwise rel boxes {eb:.2e} scores {es:.2e}; "
+              f"elementwise boxes {mb:.2e} scores {ms:.2e}")
+        assert eb < 2e-2 and es < 2e-2
+        assert mb < 5e-2 * 4 and ms < 5e-2 * 4
+        cg, _ = _argmax_last(scores[i:i + 1], 80, a_s)
+        cr, margin = _argmax_last(rs, 80, a_s)
+        sure = margin > 2e-2
+        assert np.array_equal(cg[sure], cr[sure]), int(np.sum(cg[sure] != cr[sure]))
+
+
 def test_yolo26m_fp8_vs_oracle():
     """YOLO26m with e4m3 weights/activations on the fp8 MFMA (
     second run) at batch 2, 320x320, calibrated on the input batch.
