@@ -294,6 +294,41 @@ def layers_summary(path, peak_tflops=PEAK_BF16_TFLOPS):
     return "\n".join(out)
 
 
+def trace_summary(trace_dir, bench_json, steps, profile_iters=3):
+    """Per-kernel launch durations from a `rocprofv3 --kernel-trace` run of
+    `bench.py --no-cpu --no-fp8 --steps S` against that run's own JSON line:
+    the last profile_iters x launches dispatches of each kernel are bench.py's
+    per-kernel profile passes (one launch at a time with HIP events; the
+    source of `kernels` and `roofline.avg_launch_us`), the steps x launches
+    before them the timed hipGraph replays (branches overlapping on 4
+    streams)."""
+    import csv
+    import glob
+    with open(bench_json) as f:
+        d = json.loads([l for l in f if l.startswith("{")][-1])
+    disp = []
+    for fn in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        with open(fn) as f:
+            for r in csv.DictReader(f):
+                disp.append((int(r["Start_Timestamp"]), r["Kernel_Name"],
+                             (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    disp.sort()
+    out = ["| kernel | launches per forward | bench.py avg us (HIP events) | rocprofv3 avg us, same launches | "
+           "rocprofv3 avg us, timed graph replays |", "|---|---|---|---|---|"]
+    for sym, k in d["kernels"].items():
+        n = k["launches"]
+        durs = [us for _, name, us in disp if name == sym]
+        prof = durs[-profile_iters * n:]
+        rep = durs[-(profile_iters + steps) * n:-profile_iters * n]
+        out.append(f"| {sym} | {n} | {k['ms'] * 1e3 / n:.1f} | {sum(prof) / max(len(prof), 1):.1f} | "
+                   f"{sum(rep) / max(len(rep), 1):.1f} |")
+    r = d["roofline"]
+    out += ["", f"bench.py line: {d['value']} images/s, {d['ms_per_step']} ms per forward; dominant kernel "
+                f"{r['kernel']} avg_launch_us {r['avg_launch_us']}, {r['achieved']} {r['unit']} = {r['frac']:.1%} "
+                f"of {r['peak']}."]
+    return "\n".join(out)
+
+
 def traffic_lookup(sym, names):
     """HBM bytes per launch of `sym` in this forward, from the committed
     per-launch table (launches whose layer ran the same kernel there)."""
@@ -580,11 +615,17 @@ def main() -> int:
                          "SQ_VALU_MFMA_BUSY_CYCLES pass over the --traffic-pass workload")
     ap.add_argument("--layers-summary", metavar="STDERR_FILE",
                     help="instead (no GPU): per-layer roofline table from a --layers run's stderr")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("TRACE_DIR", "BENCH_JSON"),
+                    help="instead (no GPU): per-kernel durations of a rocprofv3 --kernel-trace run of "
+                         "bench.py --no-cpu --no-fp8 against its JSON line (pass the run's --steps)")
     ap.add_argument("--pmc-table", nargs="+", metavar="PMC_DIR",
                     help="instead (no GPU): per-kernel medians of the counters in these --pmc passes")
     a = ap.parse_args()
     if a.layers_summary:
         print(layers_summary(a.layers_summary))
+        return 0
+    if a.trace_summary:
+        print(trace_summary(*a.trace_summary, steps=a.steps))
         return 0
     if a.pmc_table:
         print(pmc_table(a.pmc_table))
