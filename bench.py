@@ -12,7 +12,8 @@ Prints ONE JSON line.  Besides the contract fields it carries:
   roofline      the dominant kernel (largest total time per forward): its
                 algorithmic FLOPs (or bytes) per launch over its average
                 launch time, measured here with HIP events around each launch
-                on the stream the kernels run on, against the MI355X peak
+                (run 3 times back to back) on the stream the kernels run on,
+                against the MI355X peak
   cpu_baseline  the CPU oracle (oracle/, float32, OpenMP) on a bounded sample
                 of the same workload, timed on this host
   kernels       per-kernel-symbol time / work breakdown of one forward
@@ -40,8 +41,14 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def kernel_profile(m, iters=3):
-    """Per-launch time with events between launches (same stream as the kernels)."""
+PROFILE_ITERS, PROFILE_REPS = 3, 3
+
+
+def kernel_profile(m, iters=PROFILE_ITERS, reps=PROFILE_REPS):
+    """Per-launch time with HIP events on the kernels' stream: each launch of
+    the forward runs `reps` times back to back between two events (so the
+    event records add their ~6 us once per `reps` launches), in forward
+    order, `iters` times; the model's buffers hold garbage afterwards."""
     import torch
     names = m.launch_names()
     work = m.launch_work()
@@ -52,11 +59,12 @@ def kernel_profile(m, iters=3):
         evs = [torch.cuda.Event(enable_timing=True) for _ in range(L + 1)]
         evs[0].record(stream)
         for i in range(L):
-            m.run_launches(i, 1, stream.cuda_stream)
+            for _ in range(reps):
+                m.run_launches(i, 1, stream.cuda_stream)
             evs[i + 1].record(stream)
         torch.cuda.synchronize()
         for i in range(L):
-            tot[i] += evs[i].elapsed_time(evs[i + 1]) / iters
+            tot[i] += evs[i].elapsed_time(evs[i + 1]) / iters / reps
     per_sym = {}
     for (label, (fl, by), ms) in zip(names, work, tot):
         sym = label.split(":")[-1]
@@ -294,14 +302,13 @@ def layers_summary(path, peak_tflops=PEAK_BF16_TFLOPS):
     return "\n".join(out)
 
 
-def trace_summary(trace_dir, bench_json, steps, profile_iters=3):
+def trace_summary(trace_dir, bench_json, steps, profile_iters=PROFILE_ITERS * PROFILE_REPS):
     """Per-kernel launch durations from a `rocprofv3 --kernel-trace` run of
     `bench.py --no-cpu --no-fp8 --steps S` against that run's own JSON line:
     the last profile_iters x launches dispatches of each kernel are bench.py's
-    per-kernel profile passes (one launch at a time with HIP events; the
-    source of `kernels` and `roofline.avg_launch_us`), the steps x launches
-    before them the timed hipGraph replays (branches overlapping on 4
-    streams)."""
+    per-kernel profile (kernel_profile: the source of `kernels` and
+    `roofline.avg_launch_us`), the steps x launches before them the timed
+    hipGraph replays (branches overlapping on 4 streams)."""
     import csv
     import glob
     with open(bench_json) as f:
