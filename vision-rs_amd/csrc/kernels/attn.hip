@@ -34,8 +34,11 @@ __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
   __shared__ __attribute__((aligned(16))) T smem[2 * BUF];
 
   const int N = a.H * a.W;
-  const int qblk = blockIdx.x % a.q_blocks;
-  const int bh = blockIdx.x / a.q_blocks;
+  // the q_blocks workgroups of one (b, h) read the same K and V: keep them
+  // on one XCD so the re-reads hit its L2
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int qblk = logical % a.q_blocks;
+  const int bh = logical / a.q_blocks;
   const int h = bh % a.heads, b = bh / a.heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lq = lane & 15, lg = lane >> 4;

@@ -219,3 +219,13 @@ __device__ __forceinline__ uint32_t bf16x2_to_fp8x2(uint32_t v, uint32_t lim, fl
   const i16x2_t r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16((i16x2_t){0, 0}, __builtin_bit_cast(bf16x2_t, c), scale, false);
   return (uint32_t)(uint16_t)r[0];
 }
+
+// blockIdx.x -> logical block id so that each XCD (workgroups are dealt
+// round-robin over the 8 XCDs) receives a contiguous range of logical ids
+// (a bijection on [0, G)): neighbouring tiles -- the Cout tiles of one pixel
+// tile, the query blocks of one attention head -- then share that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int bid, int G) {
+  const int q = G >> 3, r = G & 7;
+  const int xcd = bid & 7, idx = bid >> 3;
+  return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+}

@@ -18,15 +18,6 @@
 namespace {
 
 
-// blockIdx.x -> logical tile id so that each XCD (blocks are dealt round-robin
-// over the 8 XCDs) receives a contiguous range of tiles: neighbouring Cout
-// tiles of one pixel tile then share that XCD's L2.
-__device__ __forceinline__ int xcd_remap(int bid, int G) {
-  const int q = G >> 3, r = G & 7;
-  const int xcd = bid & 7, idx = bid >> 3;
-  return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
-}
-
 // Instruction interleave of one pipelined K step (NM MFMAs, NRK fragment
 // reads per 16-deep k slice of NMK MFMAs, NX global loads and as many LDS
 // writes): the fragment reads of slice kk+1 ride on the MFMAs of slice kk,
