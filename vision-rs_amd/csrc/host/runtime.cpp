@@ -413,8 +413,12 @@ int prep_pool(vrs_ctx* ctx, const vrs_nhwc& buf, int dtype, std::vector<Launch>&
   const int c = buf.c / 4;
   const int hw = buf.h * buf.w;
   const int64_t per_group = 2ll * hw * 8 * (int64_t)elt_size(dtype);
-  int cg = (int)std::min<int64_t>(c / 8, (48 * 1024) / per_group);
+  int cg = (int)std::min<int64_t>(c / 8, (64 * 1024) / per_group);
   if (cg < 1) return fail(VRS_EUNSUPPORTED, "sppf: %dx%d map does not fit the LDS plane", buf.h, buf.w);
+  // a power of two of channel groups per workgroup: each pixel's writes then
+  // cover whole 64-byte spans where the budget allows (at 3 groups, 48-byte
+  // spans cost 1.8x the algorithmic HBM bytes in partial-line traffic)
+  while (cg & (cg - 1)) cg &= cg - 1;
   vrs_pool_args a{};
   a.buf = const_cast<void*>(at(buf, dtype));
   a.N = buf.n; a.H = buf.h; a.W = buf.w; a.c = c; a.pitch = buf.pitch; a.cgroups_per_block = cg;
