@@ -11,8 +11,9 @@
 //
 // Workgroup = (b, h, block of QW*16 queries); each wave64 owns 16 queries.
 // S^T = K Q^T on MFMA (keys are rows), so each lane holds 4 keys x 1 query and
-// softmax row statistics need only two cross-lane steps (xor 16, 32).  The
-// probabilities feed O^T += V^T P^T straight from registers: the k-slot order
+// softmax row statistics need only two cross-lane steps (xor 16, 32: one
+// v_permlane swap each).  The probabilities feed O^T += V^T P^T straight
+// from registers: the k-slot order
 // of P^T is the lane's natural key order and V^T is read from LDS in that same
 // order.  K and V^T are streamed through double-buffered LDS 64 keys at a
 // time (one barrier per chunk); V^T is written as packed key pairs so the
@@ -22,6 +23,26 @@
 namespace {
 constexpr int KC = 64;     // keys per LDS chunk
 constexpr int KD = 32, VD = 64;
+
+// x combined with the value of lane ^ 16 (SPAN 16) or lane ^ 32 (SPAN 32) by
+// one v_permlane16/32_swap (a VALU op; __shfl_xor goes through the LDS
+// crossbar).  The swap returns this lane's value and its partner's in an
+// order that depends on the lane, so only symmetric combinations are formed:
+// fmaxf and + give the same bits whichever operand comes first.
+template <int SPAN>
+__device__ __forceinline__ float xor_max(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = SPAN == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                            : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+template <int SPAN>
+__device__ __forceinline__ float xor_sum(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = SPAN == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                            : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 template <typename T, int QW>
 __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
@@ -113,8 +134,8 @@ __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
         s[t][r] = v;
         cmax = fmaxf(cmax, v);
       }
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+    cmax = xor_max<16>(cmax);
+    cmax = xor_max<32>(cmax);
     const float m_new = fmaxf(m_run, cmax);
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     m_run = m_new;
@@ -167,9 +188,8 @@ __device__ __forceinline__ void attn_body(const vrs_attn_args& a) {
     __syncthreads();  // next chunk staged; this chunk's buffer is free
   }
 
-  float l_tot = l_part;
-  l_tot += __shfl_xor(l_tot, 16);
-  l_tot += __shfl_xor(l_tot, 32);
+  float l_tot = xor_sum<16>(l_part);
+  l_tot = xor_sum<32>(l_tot);
   if (qn >= N) return;
   const float inv = 1.f / l_tot;
 
