@@ -646,7 +646,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: every box in this build has one MI355X and the path shards by "
-              "batch with no collectives (see DESIGN.md); run without --gpus or with --gpus 1.", file=sys.stderr)
+              "batch with no collectives; run without --gpus or with --gpus 1.", file=sys.stderr)
         return 2
 
     import numpy as np

@@ -40,7 +40,7 @@ def test_yolo26m_640_outputs_and_params():
     assert m.output_shapes() == [(64, 4 * 8400), (64, 80 * 8400)]
     specs = m.params()
     numel = sum(int(np.prod(s)) for _, s in specs)
-    assert 20.0e6 < numel < 20.6e6  # ~20.3 M parameters (BASELINE/SURVEY appendix A)
+    assert 20.0e6 < numel < 20.6e6  # ~20.3 M parameters (YOLO26m)
     convs = [n for n, s in specs if len(s) == 4]
     assert len(convs) == 102  # 94 dense + 8 depthwise
     assert sum(1 for n, s in specs if len(s) == 4 and s[1] == 1 and s[2] == 3) == 8
