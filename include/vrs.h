@@ -203,6 +203,21 @@ int vrs_detect_postprocess(vrs_ctx* ctx, const vrs_detect_desc* d, const float* 
                            int32_t* count, float* score, int32_t* cls, int32_t* anchor, float* xywh,
                            void* stream);
 
+/* Allocation-free vrs_detect_postprocess.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, checks and results as vrs_detect_postprocess, with the workspace
+ * in a fixed device array of the library (VRS_DETECT_SCRATCH_BYTES per GPU,
+ * held until the process ends) instead of a caller buffer; requires
+ * n * anchors * 28 <= VRS_DETECT_SCRATCH_BYTES (64 images at 640x640 fit),
+ * else VRS_EUNSUPPORTED.  It allocates nothing.  Every call on one GPU shares
+ * that array: calls that overlap in time on one GPU (other streams, threads
+ * or contexts) race; serialise them. */
+#define VRS_DETECT_SCRATCH_BYTES (16 << 20)
+int vrs_detect_postprocess_noalloc(vrs_ctx* ctx, const vrs_detect_desc* d, const float* boxes,
+                                   const float* scores, int32_t* count, float* score, int32_t* cls,
+                                   int32_t* anchor, float* xywh, void* stream);
+
 /* Un-letterbox (examples/yolo26.rs:1531-1547): the post-processed xywh in
  * letterbox pixels ([n][max_det][4], vrs_detect_postprocess) -> [cx, cy, w, h]
  * normalised to each original image, i.e. Detection::bbox

@@ -44,14 +44,17 @@ def _run(cmd):
 def build(jobs: int = 8, verbose: bool = False) -> None:
     os.makedirs(LIB, exist_ok=True)
     kernels = sorted(glob.glob(os.path.join(CSRC, "kernels", "*.hip")))
-    hosts = sorted(glob.glob(os.path.join(CSRC, "host", "*.cpp")))
+    # host runtime: C++ sources plus the HIP source holding the library's own
+    # device array (the allocation-free entry point's workspace)
+    hosts = sorted(glob.glob(os.path.join(CSRC, "host", "*.cpp"))) + \
+        sorted(glob.glob(os.path.join(CSRC, "host", "*.hip")))
     cmds = []
     for k in kernels:
         name = os.path.splitext(os.path.basename(k))[0]
         out = os.path.join(LIB, f"{name}.hsaco")
         cmds.append([HIPCC, "--genco", *DEVICE_FLAGS, "-o", out + ".tmp", k])
     so = os.path.join(LIB, "libvrs.so")
-    cmds.append([HIPCC, *HOST_FLAGS, "-o", so + ".tmp", *hosts])
+    cmds.append([HIPCC, *HOST_FLAGS, *DEVICE_FLAGS[2:], "-o", so + ".tmp", *hosts])
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         for cmd, out in zip(cmds, ex.map(_run, cmds)):
             if verbose and out.strip():

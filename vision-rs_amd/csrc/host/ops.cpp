@@ -203,13 +203,17 @@ int vrs_psa_attention(vrs_ctx* ctx, const vrs_psa_desc* d, const vrs_nhwc* qkv, 
   return rc ? rc : run_all(ls, stream);
 }
 
-static int64_t det_anchors(const vrs_detect_desc* d) {
+}  // extern "C"
+
+namespace vrs {
+
+int64_t det_anchors(const vrs_detect_desc* d) {
   int64_t a = 0;
   for (int s = 0; s < d->nscales; ++s) a += (int64_t)(d->img_h / d->strides[s]) * (d->img_w / d->strides[s]);
   return a;
 }
 
-static int det_check(const vrs_detect_desc* d) {
+int det_check(const vrs_detect_desc* d) {
   if (!d) return fail(VRS_EINVAL, "detect: null descriptor");
   if (d->n <= 0 || d->nc <= 0 || d->nscales < 1 || d->nscales > 4 || d->img_h <= 0 || d->img_w <= 0)
     return fail(VRS_EBADSHAPE, "detect: bad descriptor");
@@ -220,6 +224,10 @@ static int det_check(const vrs_detect_desc* d) {
   if (det_anchors(d) >= (1ll << 31) / 80) return fail(VRS_EBADSHAPE, "detect: too many anchors");
   return VRS_OK;
 }
+
+}  // namespace vrs
+
+extern "C" {
 
 size_t vrs_detect_workspace_size(const vrs_detect_desc* d) {
   if (det_check(d)) return 0;

@@ -574,6 +574,7 @@ int vrs_ctx_create(int device, const char* hsaco_dir, vrs_ctx** out) {
     }
     ctx->modules.push_back(m);
   }
+  scratch_attach(ctx);   // device address of the fixed detect workspace on this device
   *out = ctx;
   return VRS_OK;
 }

@@ -17,6 +17,10 @@ struct vrs_ctx {
   std::vector<hipModule_t> modules;
   std::unordered_map<std::string, hipFunction_t> fns;
   int num_cu = 0;
+  // device address of the library's fixed detect workspace on this device
+  // (scratch.hip; null with the reason in scratch_err if the lookup failed)
+  void* scratch = nullptr;
+  std::string scratch_err;
 };
 
 namespace vrs {
@@ -45,6 +49,14 @@ struct StFile {
 int st_open(const char* path, StFile& f);
 const StTensor* st_find(const StFile& f, const std::string& name);
 int st_to_f32(const StFile& f, const std::string& name, const StTensor& t, std::vector<float>& out);
+
+// Fixed device workspace of vrs_detect_postprocess_noalloc: look up this
+// device's copy (ctx->device current) at context creation (scratch.hip).
+void scratch_attach(vrs_ctx* ctx);
+// Detect descriptor checks and anchor count shared by both post-process
+// entry points (ops.cpp).
+int det_check(const vrs_detect_desc* d);
+int64_t det_anchors(const vrs_detect_desc* d);
 
 // Resolve a kernel by name from the loaded code objects.
 int get_fn(vrs_ctx* ctx, const char* name, hipFunction_t* out);

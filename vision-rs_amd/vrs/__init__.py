@@ -93,6 +93,7 @@ SIGNATURES = {
     "vrs_psa_attention": (C.c_int, [_vp, _P(PsaDesc), _P(Nhwc), _vp, _vp, _vp, _P(Nhwc), _vp]),
     "vrs_detect_workspace_size": (_sz, [_P(DetectDesc)]),
     "vrs_detect_postprocess": (C.c_int, [_vp, _P(DetectDesc), _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "vrs_detect_postprocess_noalloc": (C.c_int, [_vp, _P(DetectDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vrs_detect_decode_grid": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "vrs_detect_unletterbox": (C.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "vrs_letterbox": (C.c_int, [_vp, _i32, _i32, _vp, _i64, _P(_i64), _P(_i32), _vp, _vp]),
@@ -257,6 +258,21 @@ class Context:
         if outs is not None:
             return outs
         return count, score, cls, anchor, xywh
+
+    def detect_postprocess_noalloc(self, boxes, scores, nc, img_h, img_w, outs, strides=(8, 16, 32), thr=0.25,
+                                   stream=None):
+        """vrs_detect_postprocess_noalloc: the same post-process with the
+        library's fixed device workspace (nothing allocated); outs = the
+        caller's (count, score, cls, anchor, xywh) tensors, max_det from
+        their shape."""
+        count, score, cls, anchor, xywh = outs
+        n, max_det = score.shape
+        st = (C.c_int32 * 4)(*list(strides), *([0] * (4 - len(strides))))
+        d = DetectDesc(n, nc, img_h, img_w, len(strides), st, thr, max_det)
+        check(lib().vrs_detect_postprocess_noalloc(self.handle, C.byref(d), _ptr(boxes), _ptr(scores), _ptr(count),
+                                                   _ptr(score), _ptr(cls), _ptr(anchor), _ptr(xywh),
+                                                   _stream(stream)))
+        return outs
 
     def detect_unletterbox(self, count, xywh, orig_wh, img_size, stream=None):
         """Letterbox-pixel xywh [n][max_det][4] (detect_postprocess) -> boxes
