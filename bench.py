@@ -95,6 +95,32 @@ def roofline_of(sym, d, dtype_peak):
 
 
 TRAFFIC_MD = os.path.join(ROOT, "profiles", "yolo26m_bf16_bs64_traffic.md")
+PLAN_DIR = os.path.join(ROOT, "vision-rs_amd", "plans")
+
+
+def plan_path(variant, dtype_name, batch, size):
+    """Committed tile plan of a workload (vrs_model_get_plan of an autotuned
+    model): every run that loads it -- the bench line and each profiler pass
+    -- runs the same kernels."""
+    return os.path.join(PLAN_DIR, f"yolo26{variant}_{dtype_name}_bs{batch}_{size}.json")
+
+
+def load_plan(path, n_convs):
+    try:
+        with open(path) as f:
+            d = json.load(f)
+    except OSError:
+        return None
+    plan = [int(code) for _, code in d.get("plan", [])]
+    return plan if len(plan) == n_convs else None
+
+
+def save_plan(path, m, note):
+    os.makedirs(os.path.dirname(path), exist_ok=True)
+    names = [pre for pre, _, _ in m.conv_info()]
+    rows = ",\n".join(f"  [{json.dumps(n)}, {c}]" for n, c in zip(names, m.get_plan()))
+    with open(path, "w") as f:
+        f.write(f'{{"note": {json.dumps(note)},\n "plan": [\n{rows}\n]}}\n')
 
 
 def traffic_pass(a, ctx, labels_out):
@@ -112,6 +138,11 @@ def traffic_pass(a, ctx, labels_out):
     dt = vrs.BF16 if a.dtype == "bf16" else vrs.F32
     m = vrs.Model(ctx, vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant=a.variant, one2one=True),
                   a.batch, a.size, a.size, dt, 1e-3)
+    # the committed tile plan, so each counter pass runs the kernels the bench line times
+    plan = None if a.autotune else load_plan(plan_path(a.variant, a.dtype, a.batch, a.size), len(m.conv_info()))
+    if plan is not None:
+        m.set_plan(plan)
+    log(f"[traffic] tile plan: {'committed' if plan is not None else 'autotuned'}")
     m.load(seeded_params(m.params(), seed=0, bn="identity"))
     x = torch.from_numpy(images(a.batch, a.size, a.size, seed=0)).cuda()
     outs = m.alloc_outputs()
@@ -355,28 +386,38 @@ def traffic_lookup(sym, names):
     return sum(got) / len(got), len(got) / len(mine)
 
 
-def cpu_baseline(variant, size, P, budget_s=15.0):
-    """CPU oracle (float32, OpenMP) on a bounded sample of the same workload."""
-    import numpy as np
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(variant, size, batch, P, max_images=64):
+    """CPU oracle (float32, OpenMP over the host's cores): one warm forward of
+    the whole workload batch (one warm iteration at bs64), capped
+    at max_images."""
     import oracle
     from oracle import yolo26 as Y
     from vrs.synth import images
     net = Y.yolo26(80, variant)
     PP = Y.Params(P, eps=1e-3)
-    # batches parallelise better than single images: size the sample from a
-    # 4-image probe so the timed batch is ~budget_s of CPU work (at most 64)
-    x4 = images(4, size, size, seed=1)
-    t0 = time.perf_counter()
-    net(PP, x4)
-    t4 = (time.perf_counter() - t0) / 4
-    n = int(max(1, min(64, budget_s // max(t4, 1e-3))))
+    net(PP, images(1, size, size, seed=1))   # warm: page in weights, spin up the thread pool
+    n = min(batch, max_images)
     xs = images(n, size, size, seed=2)
     t0 = time.perf_counter()
     net(PP, xs)
     dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 3), "unit": "images/s", "cores": oracle.num_threads(), "kind": "port",
-            "sample": f"YOLO26{variant} float32 forward of {n} image(s) at {size}x{size} in one batch "
-                      f"({dt:.1f} s) on the C oracle (oracle/vrs_oracle.c, OpenMP); the reference has no CPU path"}
+    threads = oracle.num_threads()
+    return {"value": round(n / dt, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"one warm YOLO26{variant} float32 forward of a batch of {n} image(s) at {size}x{size} "
+                      f"({dt:.1f} s) on the C oracle (oracle/vrs_oracle.c); the reference has no CPU path",
+            "batch": n, "seconds": round(dt, 2), "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+            "omp_threads": threads, "compiler": oracle.build_info()}
 
 
 def _time_launches(fn, n_sets, iters=20, warmup=3):
@@ -611,6 +652,12 @@ def main() -> int:
     ap.add_argument("--streams", type=int, default=4,
                     help="streams the graph capture spreads independent launches over (1 = serial)")
     ap.add_argument("--layers", action="store_true", help="also print the per-layer table to stderr")
+    ap.add_argument("--autotune", action="store_true",
+                    help="autotune the tiles instead of loading the committed plan (vision-rs_amd/plans/)")
+    ap.add_argument("--save-plans", action="store_true",
+                    help="write the tile plans this run used to vision-rs_amd/plans/")
+    ap.add_argument("--no-micro", action="store_true",
+                    help="skip the isolated BASELINE configs 2-4 in the default line's `micro` object")
     ap.add_argument("--micro", action="store_true",
                     help="instead: BASELINE configs 2-4 as isolated kernels, one JSON line each")
     ap.add_argument("--traffic-pass", metavar="LABELS_JSON",
@@ -667,12 +714,27 @@ def main() -> int:
     x = torch.from_numpy(images(a.batch, a.size, a.size, seed=0)).cuda()
     stream = torch.cuda.Stream()
 
-    def run(dtype):
+    plans_used = {}
+
+    def run(dtype, tune_mode=1):
         """Build, (calibrate,) capture and time one forward per step; returns
-        (model, elapsed seconds, per-kernel, per-layer)."""
-        log(f"[bench] YOLO26{a.variant} {['f32', 'bf16', 'fp8'][dtype]} bs{a.batch} {a.size}x{a.size}: building")
-        m = vrs.Model(ctx, desc, a.batch, a.size, a.size, dtype, 1e-3)
+        (model, elapsed seconds, per-kernel, per-layer).  Tiles: the committed
+        plan of the workload if there is one (and --autotune is not given),
+        else autotuned (tune_mode 2: fp8 forced on every eligible conv)."""
+        dname = ["f32", "bf16", "fp8"][dtype] + ("_forced" if tune_mode == 2 else "")
+        log(f"[bench] YOLO26{a.variant} {dname} bs{a.batch} {a.size}x{a.size}: building")
+        m = vrs.Model(ctx, desc, a.batch, a.size, a.size, dtype, 1e-3, autotune=tune_mode)
+        pp = plan_path(a.variant, dname, a.batch, a.size)
+        plan = None if a.autotune else load_plan(pp, len(m.conv_info()))
+        if plan is not None:
+            m.set_plan(plan)
+            plans_used[dname] = os.path.relpath(pp, ROOT)
+        else:
+            plans_used[dname] = "autotuned in this run"
         m.load(P)
+        if a.save_plans:
+            save_plan(pp, m, f"YOLO26{a.variant} {dname} batch {a.batch} {a.size}x{a.size}: per-conv tile codes "
+                             "(vrs_model_get_plan; | 0x10000 = fp8) from an autotuned MI355X run")
         m.set_streams(a.streams)
         outs = m.alloc_outputs()
         with torch.cuda.stream(stream):
@@ -697,20 +759,47 @@ def main() -> int:
 
     P = seeded_params(vrs.Model(None, desc, a.batch, a.size, a.size).params(), seed=0, bn="identity")
     m, elapsed, per_sym, layers = run(dt)
-    fp8_run = None
+    fp8_run = fp8_forced = None
+
+    def fp8_summary(m8, el8, ps8, note):
+        top = sorted(ps8.items(), key=lambda kv: -kv[1]["ms"])[:4]
+        return {"value": round(a.batch * a.steps / el8, 1), "unit": "images/s",
+                "ms_per_step": round(el8 * 1e3 / a.steps, 3),
+                "fp8_convs": sum(1 for _, f8, _ in m8.conv_info() if f8), "convs": len(m8.conv_info()),
+                "note": note,
+                "kernels": {s: {"launches": d["launches"], "ms": round(d["ms"], 4),
+                                "tflops": round(d["flops"] / max(d["ms"], 1e-9) / 1e9, 2)} for s, d in top}}
+
     if dt == vrs.BF16 and not a.no_fp8:
         m8, el8, ps8, _ = run(vrs.FP8)
-        top = sorted(ps8.items(), key=lambda kv: -kv[1]["ms"])[:4]
-        fp8_run = {"value": round(a.batch * a.steps / el8, 1), "unit": "images/s",
-                   "ms_per_step": round(el8 * 1e3 / a.steps, 3),
-                   "fp8_convs": sum(1 for _, f8, _ in m8.conv_info() if f8), "convs": len(m8.conv_info()),
-                   "note": "e4m3 weights (per-channel absmax/448) and e4m3 activations (per-tensor power-of-two "
-                           "step calibrated on this batch) on the fp8 MFMA for convs with Cin % 64 == 0 whose "
-                           "fastest fp8 tile beats their fastest bf16 tile (autotuned per layer); the rest bf16; "
-                           "activations stored bf16",
-                   "kernels": {s: {"launches": d["launches"], "ms": round(d["ms"], 4),
-                                   "tflops": round(d["flops"] / max(d["ms"], 1e-9) / 1e9, 2)} for s, d in top}}
+        fp8_run = fp8_summary(m8, el8, ps8,
+                              "e4m3 weights (per-channel absmax/448) and e4m3 activations (per-tensor power-of-two "
+                              "step calibrated on this batch) on the fp8 MFMA for convs with Cin % 64 == 0 whose "
+                              "fastest fp8 tile beats their fastest bf16 tile (per-layer plan); the rest bf16; "
+                              "activations stored bf16")
         m8.close()
+        m8, el8, ps8, _ = run(vrs.FP8, tune_mode=2)
+        fp8_forced = fp8_summary(m8, el8, ps8,
+                                 "every conv with Cin % 64 == 0 forced onto the fp8 MFMA (fastest fp8 tile per "
+                                 "layer), the rest (stem, depthwise, fused-upsample, Cin % 64 != 0) bf16")
+        m8.close()
+    micro_summary = None
+    if not a.no_micro:
+        log("[bench] isolated BASELINE configs 2-4")
+        rows = []
+        micro(ctx, rows.append, cpu=not a.no_cpu)
+        micro_summary = {}
+        for r in rows:
+            cfg = r.get("config", "")
+            if cfg.startswith(("c2", "c3", "c4")):
+                key = cfg.split()[0]
+                us = r.get("us", r.get("core_us"))
+                frac = r.get("frac_mfma", r.get("frac_hbm", r.get("core_frac_mfma")))
+                micro_summary[key] = {"config": cfg, "us": us, "frac": frac,
+                                      "bound": "hbm" if "frac_hbm" in r else "mfma",
+                                      "cpu_ms": r.get("cpu_ms", r.get("cpu_core_ms"))}
+                if key == "c2":
+                    micro_summary[key]["block_us"] = r.get("block_us")
     ms = elapsed * 1e3 / a.steps
     value = a.batch * a.steps / elapsed
     peak = PEAK_BF16_TFLOPS if dt == vrs.BF16 else PEAK_FP8_TFLOPS if dt == vrs.FP8 else PEAK_F32_TFLOPS
@@ -733,7 +822,7 @@ def main() -> int:
     cpu = None
     if not a.no_cpu:
         log("[bench] cpu baseline (oracle)")
-        cpu = cpu_baseline(a.variant, a.size, P)
+        cpu = cpu_baseline(a.variant, a.size, a.batch, P)
     line = {
         "metric": "YOLO26 images/s @640 bs64 bf16 on 1 GPU; per-kernel % of HBM/MFMA roofline",
         "value": round(value, 1), "unit": "images/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -743,10 +832,13 @@ def main() -> int:
                    "batch": a.batch, "size": a.size, "variant": a.variant, "classes": 80,
                    "weights": "seeded Kaiming-normal, identity BN folded", "graph": f"hipGraph replay, {a.streams} capture streams",
                    "forward_tflop": round(total_flops / 1e12, 3),
-                   "achieved_tflops_e2e": round(total_flops / (ms / 1e3) / 1e12, 1)},
+                   "achieved_tflops_e2e": round(total_flops / (ms / 1e3) / 1e12, 1),
+                   "tile_plans": plans_used},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "micro": micro_summary,
         "fp8_run": fp8_run,
+        "fp8_forced_run": fp8_forced,
         "kernels": kern,
     }
     print(json.dumps(line), flush=True)

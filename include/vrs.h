@@ -293,10 +293,26 @@ typedef struct {
  * without a GPU); finalize/forward then fail with VRS_ESTATE. */
 int vrs_model_create(vrs_ctx* ctx, const vrs_block_desc* d, int32_t batch, int32_t h, int32_t w,
                      int32_t dtype, float bn_eps, vrs_model** out);
-/* Per-layer tile autotuning at finalize (default on): every dense conv is
- * timed with each applicable VRS_TILE_* on the model's own buffers and the
- * fastest is kept.  Off: the shape heuristic of VRS_TILE_AUTO. */
-int vrs_model_set_autotune(vrs_model* m, int32_t on);
+/* Per-layer tile autotuning at finalize (replaces TritonLowering's
+ * shape-adaptive tile choice, examples/yolo26.rs:3027).  mode 1 (default):
+ * every dense conv is timed with each applicable VRS_TILE_* on the model's own
+ * buffers and the fastest is kept; in a VRS_FP8 model each eligible conv also
+ * keeps bf16 when its best bf16 tile is faster.  mode 2 (VRS_FP8 models):
+ * only fp8 tiles are timed, every eligible conv runs on fp8.  mode 0: the
+ * shape heuristic of VRS_TILE_AUTO. */
+int vrs_model_set_autotune(vrs_model* m, int32_t mode);
+/* Tile plan: one entry per conv (build order, vrs_model_num_convs): a
+ * VRS_TILE_* code, OR VRS_PLAN_FP8 for a conv that runs on e4m3 (VRS_FP8
+ * models); 0 for convs that take no tile (depthwise, stem, flat outputs) or
+ * the heuristic.  vrs_model_get_plan (after finalize) returns the plan in use
+ * (with plan == NULL: the entry count); vrs_model_set_plan (before finalize;
+ * n = 0 clears it) makes finalize apply that plan instead of autotuning, each
+ * entry checked against the kernels built for its conv.  A saved plan makes
+ * every later run (benchmarks, profiler passes) use the same kernels.
+ * No counterpart in the reference. */
+#define VRS_PLAN_FP8 0x10000
+int vrs_model_set_plan(vrs_model* m, const int32_t* plan, int32_t n);
+int vrs_model_get_plan(const vrs_model* m, int32_t* plan, int32_t n);
 int vrs_model_num_params(const vrs_model* m);
 /* name is owned by the model; dims[0..*ndim) (ndim <= 4). */
 int vrs_model_param_info(const vrs_model* m, int32_t i, const char** name, int32_t* dims, int32_t* ndim);
@@ -349,6 +365,28 @@ int vrs_model_calibrate(vrs_model* m, const float* x, void* stream);
  * fp8 and its activation scale (0 before calibration). */
 int vrs_model_num_convs(const vrs_model* m);
 int vrs_model_conv_info(const vrs_model* m, int32_t i, const char** prefix, int32_t* fp8, float* in_scale);
+/* Where conv i of the prepared forward reads and writes (device views of
+ * the model's own buffers), for per-layer inspection such as checking each
+ * layer against a CPU restatement on the layer's actual input (the analogue
+ * of reading a node's tensor from the reference's LoadedModel).  Valid after
+ * vrs_model_finalize; `launch` after the first forward/capture.  Views whose
+ * data is NULL are absent: x for the stem (which reads the model input), y
+ * for convs that write a model output (out_idx >= 0, float32 element
+ * (b, p, co) at output[out_idx] + out_off + b*out_sb + p*out_sp + co*out_sc). */
+typedef struct {
+  int32_t launch;          /* index among vrs_model_launch_name's launches, -1: none */
+  int32_t k, stride, groups, act;
+  int32_t plain;           /* conv_plain: bias, no BN */
+  int32_t stem;            /* reads the NCHW float32 model input */
+  int32_t fp8;             /* runs on the fp8 MFMA (input quantised with in_scale) */
+  float in_scale;
+  int32_t dtype;           /* element type of x, y, res, up */
+  int32_t cin, cout;       /* unpadded input channels, output channels */
+  vrs_nhwc x, y, res, up;  /* up: source of a fused nearest-2x upsample (first up.c input channels) */
+  int32_t out_idx;
+  int64_t out_off, out_sb, out_sp, out_sc;
+} vrs_conv_io;
+int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io);
 int vrs_model_destroy(vrs_model* m);
 
 #ifdef __cplusplus

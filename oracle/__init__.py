@@ -17,7 +17,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_SO = os.path.join(_HERE, "_build", "liboracle.so")
+# ORACLE_SO selects another build of the same source (the sanitizer build of
+# `make -C oracle sanitize`)
+_SO = os.environ.get("ORACLE_SO") or os.path.join(_HERE, "_build", "liboracle.so")
 _lib = None
 
 
@@ -52,6 +54,7 @@ def lib():
                                   f32p, f32p, f32p, C.c_int, C.c_int, f32p]
         _lib.orc_add.argtypes = [f32p, f32p, f32p, C.c_long]
         _lib.orc_num_threads.restype = C.c_int
+        _lib.orc_build_info.restype = C.c_char_p
     return _lib
 
 
@@ -65,6 +68,11 @@ def _i(a):
 
 def _c32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def build_info() -> str:
+    """Compiler and flags of the oracle library."""
+    return lib().orc_build_info().decode()
 
 
 def num_threads() -> int:

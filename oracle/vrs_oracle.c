@@ -37,6 +37,21 @@
 #include <omp.h>
 #endif
 
+/* Compiler and flags this library was built with (reported beside the CPU
+ * baseline's timings). */
+#ifndef ORC_FLAGS
+#define ORC_FLAGS "(flags not recorded)"
+#endif
+const char* orc_build_info(void) {
+#if defined(__clang__)
+  return "clang " __clang_version__ "; " ORC_FLAGS;
+#elif defined(__GNUC__)
+  return "gcc " __VERSION__ "; " ORC_FLAGS;
+#else
+  return "unknown compiler; " ORC_FLAGS;
+#endif
+}
+
 int orc_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

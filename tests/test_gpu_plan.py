@@ -1,0 +1,117 @@
+"""Tile plans (vrs_model_get_plan / vrs_model_set_plan), the fp8-forced
+autotune mode and vrs_model_conv_io, through the C ABI."""
+import numpy as np
+import pytest
+
+from gpu_util import bf16_round, ctx, dev, vrs
+from golden_io import seeded_params
+
+pytestmark = pytest.mark.gpu
+
+
+def _yolo(batch, size, dtype, autotune=True):
+    desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="m", one2one=True)
+    return vrs.Model(ctx(), desc, batch, size, size, dtype, 1e-3, autotune=autotune)
+
+
+def _params(m):
+    P = seeded_params(m.params(), 0, bn="random")
+    return {k: (bf16_round(v) if v.ndim == 4 else v) for k, v in P.items()}
+
+
+def test_plan_round_trip_bit_identical():
+    """An autotuned model's plan applied to a fresh model gives the same plan
+    and bit-identical outputs; a failed finalize (bad plan) leaves the model
+    usable with a good plan."""
+    import torch
+    m1 = _yolo(2, 256, vrs.BF16)
+    P = _params(m1)
+    m1.load(P)
+    plan = m1.get_plan()
+    assert len(plan) == len(m1.conv_info()) and any(plan)
+    x = dev(np.random.default_rng(3).uniform(0, 1, (2, 3, 256, 256)).astype(np.float32))
+    o1 = [o.clone() for o in m1.forward(x)]
+    m2 = _yolo(2, 256, vrs.BF16)
+    # a bad plan first: a persistent tile on a conv with a residual
+    # (model.2.m.0.cv2), which those kernels do not take
+    names = [pre for pre, _, _ in m2.conv_info()]
+    bad = list(plan)
+    bad[names.index("model.2.m.0.cv2")] = vrs.TILE_128x128 | vrs.TILE_K32 | vrs.TILE_PERSIST
+    m2.set_plan(bad)
+    with pytest.raises(vrs.VrsError) as e:
+        m2.load(P)
+    assert "model.2.m.0.cv2" in str(e.value)
+    m2.set_plan(plan)
+    m2.load(P)   # the parameters are still there: finalize retried with a valid plan
+    assert m2.get_plan() == plan
+    o2 = m2.forward(x)
+    torch.cuda.synchronize()
+    for a, b in zip(o1, o2):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_plan_rejections():
+    m = _yolo(1, 128, vrs.BF16)
+    n = len(m.conv_info())
+    with pytest.raises(vrs.VrsError):
+        m.set_plan([0] * (n - 1))        # wrong length
+    names = [pre for pre, _, _ in m.conv_info()]
+    bad = [0] * n
+    bad[names.index("model.23.one2one_cv3.0.0.0")] = vrs.TILE_128x128   # depthwise: takes no tile
+    m.set_plan(bad)
+    with pytest.raises(vrs.VrsError):
+        m.load(_params(m))
+    bad = [0] * n
+    bad[names.index("model.3")] = vrs.TILE_128x128 | vrs.PLAN_FP8       # fp8 in a bf16 model
+    m2 = _yolo(1, 128, vrs.BF16)
+    m2.set_plan(bad)
+    with pytest.raises(vrs.VrsError):
+        m2.load(_params(m2))
+    with pytest.raises(vrs.VrsError):
+        _yolo(1, 128, vrs.BF16, autotune=2)   # mode 2 is for fp8 models
+
+
+def test_fp8_forced_mode_keeps_every_eligible_conv_on_fp8():
+    import torch
+    m = _yolo(2, 256, vrs.FP8, autotune=2)
+    m.load(_params(m))
+    x = dev(np.random.default_rng(4).uniform(0, 1, (2, 3, 256, 256)).astype(np.float32))
+    m.calibrate(x)
+    m.forward(x)
+    torch.cuda.synchronize()
+    ios = [m.conv_io(i) for i in range(len(m.conv_info()))]
+    eligible = [io for io in ios if io.groups == 1 and not io.stem and io.up.data is None and io.cin % 64 == 0]
+    assert all(io.fp8 for io in eligible) and len(eligible) > 60
+    plan = m.get_plan()
+    assert sum(1 for p in plan if p & vrs.PLAN_FP8) == sum(
+        1 for io in eligible if io.y.data is not None)   # flat-output convs take no tile entry
+    assert all(io.in_scale > 0 for io in eligible)
+
+
+def test_conv_io_views():
+    """conv_io describes each conv: launch order, views inside the model's
+    buffers, the stem and the flat Detect outputs."""
+    import torch
+    m = _yolo(1, 128, vrs.BF16, autotune=False)
+    m.load(_params(m))
+    m.forward(dev(np.zeros((1, 3, 128, 128), np.float32)))
+    torch.cuda.synchronize()
+    info = m.conv_info()
+    names = m.launch_names()
+    seen = set()
+    for i, (pre, _, _) in enumerate(info):
+        io = m.conv_io(i)
+        if pre.endswith(".pe"):            # parameters of the fused attention launch
+            assert io.launch == -1
+            continue
+        assert 0 <= io.launch < len(names) and names[io.launch].startswith(pre + ":")
+        assert io.launch not in seen
+        seen.add(io.launch)
+        if pre == "model.0":
+            assert io.stem and io.x.data is None and io.y.data is not None
+        elif pre.endswith(".2") and "one2one" in pre:
+            assert io.y.data is None and io.out_idx in (0, 1) and io.plain
+        else:
+            assert io.x.data is not None and io.y.data is not None and io.x.c == io.cin
+    with pytest.raises(vrs.VrsError):
+        m.conv_io(len(info))

@@ -93,6 +93,13 @@ def test_errors(tmp_path):
     (tmp_path / "t.safetensors").write_bytes(raw[:-5])
     (tmp_path / "h.safetensors").write_bytes(struct.pack("<Q", len(raw)) + raw[8:])
     (tmp_path / "j.safetensors").write_bytes(struct.pack("<Q", 4) + b"[1,]")
+    # a shape whose element count overflows 64 bits (2^96 elements) must be
+    # rejected before any size arithmetic, whatever its byte span claims
+    hdr = b'{"%s":{"dtype":"F32","shape":[4294967296,4294967296,4294967296],"data_offsets":[0,4]}}' % k0.encode()
+    (tmp_path / "o.safetensors").write_bytes(struct.pack("<Q", len(hdr)) + hdr + b"\0" * 4)
+    with pytest.raises(vrs.VrsError) as e:
+        _model().load_safetensors(tmp_path / "o.safetensors", finalize=False)
+    assert e.value.code == -2 and "overflow" in str(e.value)
     for f in ("t", "h", "j"):
         with pytest.raises(vrs.VrsError):
             _model().load_safetensors(tmp_path / f"{f}.safetensors", finalize=False)

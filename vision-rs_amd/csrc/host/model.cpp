@@ -105,12 +105,18 @@ struct vrs_model {
   std::vector<Step> steps;
   std::vector<std::vector<int32_t>> out_dims;
   bool finalized = false;
-  bool autotune = true;
+  // 0: shape heuristic; 1: time every tile per layer (fp8 models: also fp8
+  // against bf16); 2 (fp8 models): time only the fp8 tiles, every eligible
+  // conv stays on fp8
+  int autotune = 1;
+  // per-conv tile plan set by the caller (replaces autotuning); empty = none
+  std::vector<int32_t> plan;
   std::vector<void*> allocs;
   // prepared launches for the last (x, outputs) pointers
   std::vector<Launch> launches;
   std::vector<std::string> labels;
   std::vector<LaunchIO> io;      // per launch: what it reads and writes
+  std::vector<int> conv_launch;  // per conv: index of its kernel launch (-1: none)
   int streams = 4;               // capture concurrency (1 = one serial chain)
   std::vector<hipStream_t> side; // extra capture streams (default priority)
   std::vector<hipEvent_t> evs;   // capture-time dependency events
@@ -525,6 +531,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
   std::vector<Launch> ls;
   std::vector<std::string> labels;
   std::vector<LaunchIO> io;
+  std::vector<int> conv_launch(m->convs.size(), -1);
   int rc = VRS_OK;
   auto acc = [](V v) { return Access{v.buf, v.c_off, v.c_off + v.c}; };
   constexpr int kAll = 1 << 30;
@@ -599,12 +606,14 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
                          view_of(m, c.y), ls);
         }
         if (rc) return rc;
+        conv_launch[st.conv] = (int)conv_first;
         for (size_t i = conv_first; i < ls.size(); ++i) labels.push_back(label + ":" + ls[i].name);
         flush_io();
         continue;
       }
       case Step::STEM: {
         const ConvStep& c = m->convs[st.conv];
+        conv_launch[st.conv] = (int)ls.size();
         rc = prep_stem(m->ctx, VRS_ACT_SILU, act_dt(m), x, m->batch, m->in_h, m->in_w, c.w, c.scale, c.shift,
                        c.cout, view_of(m, c.y), ls);
         label = c.pre;
@@ -637,6 +646,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
   m->launches = std::move(ls);
   m->labels = std::move(labels);
   m->io = std::move(io);
+  m->conv_launch = std::move(conv_launch);
   m->prep_x = x;
   m->prep_outs = o;
   return VRS_OK;
@@ -666,6 +676,7 @@ int autotune_tiles(vrs_model* m) {
    float best_of[2] = {1e30f, 1e30f};   // fastest bf16 / fp8 tile of this layer
    for (int pass = 0; pass < (c.f8 ? 2 : 1); ++pass) {
     if (c.dw || c.stem || c.out_idx >= 0 || c.y.buf < 0) continue;
+    if (pass == 0 && c.f8 && m->autotune == 2) continue;   // fp8 forced: no bf16 candidates
     const int dt = pass ? VRS_FP8 : act_dt(m);
     const std::vector<int> cand = conv_tile_candidates(c.cout, c.cin, dt);
     if (cand.size() < 2) continue;
@@ -713,7 +724,8 @@ int autotune_tiles(vrs_model* m) {
    }
    if (rc) break;
    // fp8 models: a layer whose bf16 tile is faster by 2% stays on bf16
-   if (c.f8) c.run_f8 = !(best_of[0] < 0.98f * best_of[1]);
+   // (unless fp8 is forced)
+   if (c.f8) c.run_f8 = m->autotune == 2 || !(best_of[0] < 0.98f * best_of[1]);
   }
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
@@ -768,6 +780,122 @@ void fuse_upsamples(vrs_model* m) {
     if (fuse) m->steps.erase(m->steps.begin() + (ptrdiff_t)i);
     else ++i;
   }
+}
+
+const Param* P(const vrs_model* m, const std::string& name);
+
+// Allocate the activation buffers, fold BN and upload every conv's packed
+// weights and epilogue vectors (vrs_model_finalize's first step; every
+// allocation is recorded in m->allocs).
+int finalize_upload(vrs_model* m) {
+  const size_t es = elt_size(act_dt(m));
+  for (Buf& b : m->bufs) {
+    const size_t bytes = (size_t)m->batch * b.h * b.w * b.pitch * es;
+    VRS_HIP(hipMalloc(&b.dev, bytes));
+    m->allocs.push_back(b.dev);
+    VRS_HIP(hipMemset(b.dev, 0, bytes));
+  }
+  for (ConvStep& c : m->convs) {
+    std::vector<float> scale(c.cout), shift(c.cout);
+    const Param* w;
+    if (c.kind == CK_PLAIN) {
+      w = P(m, J(c.pre, "weight"));
+      const Param* bias = P(m, J(c.pre, "bias"));
+      for (int i = 0; i < c.cout; ++i) { scale[i] = 1.f; shift[i] = bias->host[i]; }
+    } else {
+      w = P(m, J(c.pre, "conv.weight"));
+      const int rf = vrs_bn_fold(P(m, J(c.pre, "bn.weight"))->host.data(), P(m, J(c.pre, "bn.bias"))->host.data(),
+                                 P(m, J(c.pre, "bn.running_mean"))->host.data(),
+                                 P(m, J(c.pre, "bn.running_var"))->host.data(), m->eps, c.cout, scale.data(),
+                                 shift.data());
+      if (rf) return fail(rf, "%s: BN fold: %s", c.pre.c_str(), vrs_last_error());
+    }
+    const int cin_g = w->dims[1];
+    const int groups = c.dw ? c.cout : 1;
+    const int cin_pad = c.dw ? 1 : c.cin;
+    const int pdt = act_dt(m);
+    const int64_t bytes = c.stem ? vrs_pack_stem_weight(nullptr, c.cout, pdt, nullptr)
+                                 : vrs_pack_conv_weight(nullptr, c.cout, cin_g, c.k, groups, cin_pad, pdt, nullptr);
+    if (bytes < 0) return (int)bytes;
+    std::vector<uint8_t> packed((size_t)bytes);
+    const int64_t r =
+        c.stem ? vrs_pack_stem_weight(w->host.data(), c.cout, pdt, packed.data())
+               : vrs_pack_conv_weight(w->host.data(), c.cout, cin_g, c.k, groups, cin_pad, pdt, packed.data());
+    if (r < 0) return (int)r;
+    int rc;
+    if ((rc = dev_upload(m, packed.data(), packed.size(), &c.w))) return rc;
+    void* p;
+    if ((rc = dev_upload(m, scale.data(), scale.size() * 4, &p))) return rc;
+    c.scale = static_cast<float*>(p);
+    if ((rc = dev_upload(m, shift.data(), shift.size() * 4, &p))) return rc;
+    c.shift = static_cast<float*>(p);
+    // (a fused-upsample conv stays bfloat16: its kernels have no fp8 instance)
+    c.f8 = m->dtype == VRS_FP8 && !c.dw && !c.stem && !c.has_up && c.cin % 64 == 0 && cin_g == c.cin;
+    if (c.f8) {  // e4m3 copy of the weights; the bf16 one serves calibration
+      const int64_t qb = vrs_pack_conv_weight_fp8(nullptr, c.cout, cin_g, c.k, c.cin, nullptr, nullptr);
+      if (qb < 0) return (int)qb;
+      std::vector<uint8_t> q((size_t)qb);
+      std::vector<float> ws(c.cout);
+      const int64_t r8 = vrs_pack_conv_weight_fp8(w->host.data(), c.cout, cin_g, c.k, c.cin, q.data(), ws.data());
+      if (r8 < 0) return (int)r8;
+      if ((rc = dev_upload(m, q.data(), q.size(), &c.w8))) return rc;
+      c.scale8_host.resize(c.cout);
+      for (int i = 0; i < c.cout; ++i) c.scale8_host[i] = scale[i] * ws[i];
+      if ((rc = dev_upload(m, c.scale8_host.data(), c.cout * 4, &p))) return rc;  // times in_scale later
+      c.scale8 = static_cast<float*>(p);
+    }
+  }
+  if (m->dtype == VRS_FP8) {
+    void* p;
+    VRS_HIP(hipMalloc(&p, m->convs.size() * sizeof(unsigned)));
+    m->allocs.push_back(p);
+    m->absmax = static_cast<unsigned*>(p);
+  }
+  return VRS_OK;
+}
+
+// Tiles of a dense NHWC conv that the autotuner would consider (the convs a
+// plan entry applies to).
+bool tunable(const ConvStep& c) { return !c.dw && !c.stem && c.out_idx < 0 && c.y.buf >= 0; }
+
+// A caller's tile plan (vrs_model_set_plan) instead of autotuning: every
+// entry is checked against the kernels built for its conv's shape.
+int apply_plan(vrs_model* m) {
+  for (size_t i = 0; i < m->convs.size(); ++i) {
+    ConvStep& c = m->convs[i];
+    const int32_t e = m->plan[i];
+    const bool f8 = (e & VRS_PLAN_FP8) != 0;
+    const int tile = e & ~VRS_PLAN_FP8;
+    if (!tunable(c)) {
+      if (e != 0) return fail(VRS_EINVAL, "plan entry %zu (%s): this conv takes no tile (entry must be 0)", i,
+                              c.pre.c_str());
+      continue;
+    }
+    if (f8 && !c.f8)
+      return fail(VRS_EINVAL, "plan entry %zu (%s): fp8 requested for a conv that has no fp8 form", i, c.pre.c_str());
+    if (tile != VRS_TILE_AUTO) {   // validate by preparing the launch
+      ConvSpec cs;
+      cs.k = c.k; cs.stride = c.s; cs.dtype = f8 ? VRS_FP8 : act_dt(m);
+      cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
+      cs.in_scale = 1.f;
+      cs.tile = tile;
+      vrs_nhwc upv, r;
+      if (c.has_up) { upv = view_of(m, c.up); cs.up = &upv; }
+      if (c.has_res) r = view_of(m, c.res);
+      std::vector<Launch> ls;
+      const int rc = prep_conv(m->ctx, cs, view_of(m, c.x), f8 ? c.w8 : c.w, f8 ? c.scale8 : c.scale, c.shift,
+                               c.has_res ? &r : nullptr, view_of(m, c.y), ls);
+      if (rc) return fail(rc, "plan entry %zu (%s): %s", i, c.pre.c_str(), vrs_last_error());
+    }
+    if (c.f8) {
+      c.run_f8 = f8;
+      if (f8) c.tile8 = tile;
+      else c.tile = tile;
+    } else {
+      c.tile = tile;
+    }
+  }
+  return VRS_OK;
 }
 
 const Param* P(const vrs_model* m, const std::string& name) {
@@ -870,79 +998,62 @@ int vrs_model_finalize(vrs_model* m) {
   if (m->finalized) return VRS_OK;
   for (const Param& p : m->params)
     if (!p.loaded) return fail(VRS_ESTATE, "parameter '%s' not loaded", p.name.c_str());
-  const size_t es = elt_size(act_dt(m));
-  for (Buf& b : m->bufs) {
-    const size_t bytes = (size_t)m->batch * b.h * b.w * b.pitch * es;
-    VRS_HIP(hipMalloc(&b.dev, bytes));
-    m->allocs.push_back(b.dev);
-    VRS_HIP(hipMemset(b.dev, 0, bytes));
-  }
-  for (ConvStep& c : m->convs) {
-    std::vector<float> scale(c.cout), shift(c.cout);
-    const Param* w;
-    if (c.kind == CK_PLAIN) {
-      w = P(m, J(c.pre, "weight"));
-      const Param* bias = P(m, J(c.pre, "bias"));
-      for (int i = 0; i < c.cout; ++i) { scale[i] = 1.f; shift[i] = bias->host[i]; }
-    } else {
-      w = P(m, J(c.pre, "conv.weight"));
-      vrs_bn_fold(P(m, J(c.pre, "bn.weight"))->host.data(), P(m, J(c.pre, "bn.bias"))->host.data(),
-                  P(m, J(c.pre, "bn.running_mean"))->host.data(), P(m, J(c.pre, "bn.running_var"))->host.data(),
-                  m->eps, c.cout, scale.data(), shift.data());
+  // Everything this call allocates is released again if a later step fails,
+  // and the host parameters are kept until the end, so a failed finalize
+  // leaves the model as it was (a retry folds and uploads again).
+  const size_t first_alloc = m->allocs.size();
+  int rc = finalize_upload(m);
+  if (!rc) rc = m->plan.empty() ? (m->autotune ? autotune_tiles(m) : VRS_OK) : apply_plan(m);
+  if (rc) {
+    const std::string err = vrs_last_error();
+    for (size_t i = first_alloc; i < m->allocs.size(); ++i) (void)hipFree(m->allocs[i]);
+    m->allocs.resize(first_alloc);
+    for (Buf& b : m->bufs) b.dev = nullptr;
+    for (ConvStep& c : m->convs) {
+      c.w = c.w8 = nullptr;
+      c.scale = c.shift = c.scale8 = nullptr;
+      c.f8 = false;
     }
-    const int cin_g = w->dims[1];
-    const int groups = c.dw ? c.cout : 1;
-    const int cin_pad = c.dw ? 1 : c.cin;
-    const int pdt = act_dt(m);
-    const int64_t bytes = c.stem ? vrs_pack_stem_weight(nullptr, c.cout, pdt, nullptr)
-                                 : vrs_pack_conv_weight(nullptr, c.cout, cin_g, c.k, groups, cin_pad, pdt, nullptr);
-    if (bytes < 0) return (int)bytes;
-    std::vector<uint8_t> packed((size_t)bytes);
-    const int64_t r =
-        c.stem ? vrs_pack_stem_weight(w->host.data(), c.cout, pdt, packed.data())
-               : vrs_pack_conv_weight(w->host.data(), c.cout, cin_g, c.k, groups, cin_pad, pdt, packed.data());
-    if (r < 0) return (int)r;
-    int rc;
-    if ((rc = dev_upload(m, packed.data(), packed.size(), &c.w))) return rc;
-    void* p;
-    if ((rc = dev_upload(m, scale.data(), scale.size() * 4, &p))) return rc;
-    c.scale = static_cast<float*>(p);
-    if ((rc = dev_upload(m, shift.data(), shift.size() * 4, &p))) return rc;
-    c.shift = static_cast<float*>(p);
-    // (a fused-upsample conv stays bfloat16: its kernels have no fp8 instance)
-    c.f8 = m->dtype == VRS_FP8 && !c.dw && !c.stem && !c.has_up && c.cin % 64 == 0 && cin_g == c.cin;
-    if (c.f8) {  // e4m3 copy of the weights; the bf16 one serves calibration
-      std::vector<uint8_t> q((size_t)vrs_pack_conv_weight_fp8(nullptr, c.cout, cin_g, c.k, c.cin, nullptr, nullptr));
-      std::vector<float> ws(c.cout);
-      const int64_t r8 = vrs_pack_conv_weight_fp8(w->host.data(), c.cout, cin_g, c.k, c.cin, q.data(), ws.data());
-      if (r8 < 0) return (int)r8;
-      if ((rc = dev_upload(m, q.data(), q.size(), &c.w8))) return rc;
-      c.scale8_host.resize(c.cout);
-      for (int i = 0; i < c.cout; ++i) c.scale8_host[i] = scale[i] * ws[i];
-      if ((rc = dev_upload(m, c.scale8_host.data(), c.cout * 4, &p))) return rc;  // times in_scale later
-      c.scale8 = static_cast<float*>(p);
-    }
-  }
-  if (m->dtype == VRS_FP8) {
-    void* p;
-    VRS_HIP(hipMalloc(&p, m->convs.size() * sizeof(unsigned)));
-    m->allocs.push_back(p);
-    m->absmax = static_cast<unsigned*>(p);
+    m->absmax = nullptr;
+    (void)hipGetLastError();
+    return fail(rc, "%s", err.c_str());
   }
   for (Param& p : m->params) std::vector<float>().swap(p.host);
-  if (m->autotune) {
-    int rc = autotune_tiles(m);
-    if (rc) return rc;
-  }
   m->finalized = true;
   return VRS_OK;
 }
 
-int vrs_model_set_autotune(vrs_model* m, int32_t on) {
+int vrs_model_set_autotune(vrs_model* m, int32_t mode) {
   if (!m) return fail(VRS_EINVAL, "null model");
   if (m->finalized) return fail(VRS_ESTATE, "vrs_model_set_autotune: model already finalized");
-  m->autotune = on != 0;
+  if (mode < 0 || mode > 2) return fail(VRS_EINVAL, "vrs_model_set_autotune: mode %d (0, 1 or 2)", mode);
+  if (mode == 2 && m->dtype != VRS_FP8) return fail(VRS_EINVAL, "vrs_model_set_autotune: mode 2 is for fp8 models");
+  m->autotune = mode;
   return VRS_OK;
+}
+
+int vrs_model_set_plan(vrs_model* m, const int32_t* plan, int32_t n) {
+  if (!m || (!plan && n)) return fail(VRS_EINVAL, "vrs_model_set_plan: null argument");
+  if (m->finalized) return fail(VRS_ESTATE, "vrs_model_set_plan: model already finalized");
+  if (n != 0 && n != (int32_t)m->convs.size())
+    return fail(VRS_EINVAL, "vrs_model_set_plan: %d entries for %zu convs", n, m->convs.size());
+  m->plan.assign(plan, plan + n);
+  return VRS_OK;
+}
+
+int vrs_model_get_plan(const vrs_model* m, int32_t* plan, int32_t n) {
+  if (!m) return fail(VRS_EINVAL, "null model");
+  const int32_t nc = (int32_t)m->convs.size();
+  if (!plan) return nc;
+  if (!m->finalized) return fail(VRS_ESTATE, "vrs_model_get_plan: call vrs_model_finalize first");
+  if (n < nc) return fail(VRS_EINVAL, "vrs_model_get_plan: %d entries for %d convs", n, nc);
+  for (int32_t i = 0; i < nc; ++i) {
+    const ConvStep& c = m->convs[i];
+    if (!tunable(c)) plan[i] = 0;
+    else if (c.f8 && c.run_f8) plan[i] = c.tile8 | VRS_PLAN_FP8;
+    else plan[i] = c.tile;
+  }
+  return nc;
 }
 
 int vrs_model_num_outputs(const vrs_model* m) { return m ? (int)m->out_dims.size() : fail(VRS_EINVAL, "null model"); }
@@ -1157,6 +1268,36 @@ int vrs_model_conv_info(const vrs_model* m, int32_t i, const char** prefix, int3
   *prefix = c.pre.c_str();
   *fp8 = c.f8 && c.run_f8 ? 1 : 0;
   *in_scale = c.in_scale;
+  return VRS_OK;
+}
+
+int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io) {
+  if (!m || !io) return fail(VRS_EINVAL, "vrs_model_conv_io: null argument");
+  if (i < 0 || i >= (int)m->convs.size()) return fail(VRS_EINVAL, "vrs_model_conv_io: index %d", i);
+  if (!m->finalized) return fail(VRS_ESTATE, "vrs_model_conv_io: call vrs_model_finalize first");
+  const ConvStep& c = m->convs[i];
+  *io = vrs_conv_io{};
+  io->launch = i < (int)m->conv_launch.size() ? m->conv_launch[i] : -1;
+  io->k = c.k;
+  io->stride = c.s;
+  io->groups = c.dw ? c.cout : 1;
+  io->act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
+  io->plain = c.kind == CK_PLAIN;
+  io->stem = c.stem;
+  io->fp8 = c.f8 && c.run_f8;
+  io->in_scale = c.in_scale;
+  io->dtype = act_dt(m);
+  io->cin = c.cin_real;
+  io->cout = c.cout;
+  if (!c.stem) io->x = view_of(m, c.x);
+  if (c.out_idx < 0 && c.y.buf >= 0) io->y = view_of(m, c.y);
+  if (c.has_res) io->res = view_of(m, c.res);
+  if (c.has_up) io->up = view_of(m, c.up);
+  io->out_idx = c.out_idx;
+  io->out_off = c.out_off;
+  io->out_sb = c.sb;
+  io->out_sp = c.sp;
+  io->out_sc = c.sc;
   return VRS_OK;
 }
 

@@ -212,10 +212,18 @@ int st_open(const char* path, StFile& f) {
       }
       if (!have_off || !have_dt || !have_shape)
         return fail(VRS_EBADSHAPE, "safetensors: entry '%s' lacks dtype/shape/data_offsets", name.c_str());
+      // element and byte counts of an untrusted header: every product is
+      // checked before it is formed (a crafted shape must not overflow)
       int64_t numel = 1;
-      for (int64_t d : t.shape) numel *= d;
+      for (int64_t d : t.shape) {
+        if (d > 0 && numel > INT64_MAX / d)
+          return fail(VRS_EBADSHAPE, "safetensors: '%s' shape overflows 64-bit element counts", name.c_str());
+        numel *= d;
+      }
       const int es = dtype_size(t.dtype);
       if (es == 0) return fail(VRS_EUNSUPPORTED, "safetensors: '%s' has unknown dtype %s", name.c_str(), t.dtype.c_str());
+      if (numel > INT64_MAX / es)
+        return fail(VRS_EBADSHAPE, "safetensors: '%s' byte size overflows", name.c_str());
       if ((int64_t)(t.end - t.begin) != numel * es)
         return fail(VRS_EBADSHAPE, "safetensors: '%s' spans %zu bytes for %lld %s values", name.c_str(),
                     t.end - t.begin, (long long)numel, t.dtype.c_str());

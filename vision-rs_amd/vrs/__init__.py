@@ -18,7 +18,9 @@ import os
 
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_DIR = os.path.join(PKG, "lib")
-SO = os.path.join(LIB_DIR, "libvrs.so")
+# VRS_SO selects another build of the host library (the CPU sanitizer build of
+# `make -C oracle sanitize`); the code objects always come from LIB_DIR
+SO = os.environ.get("VRS_SO") or os.path.join(LIB_DIR, "libvrs.so")
 
 VRS_OK = 0
 F32, BF16, FP8 = 0, 1, 2
@@ -72,6 +74,16 @@ class BlockDesc(C.Structure):
                 ("variant", C.c_int32), ("one2one", C.c_int32)]
 
 
+class ConvIo(C.Structure):
+    _fields_ = [("launch", C.c_int32), ("k", C.c_int32), ("stride", C.c_int32), ("groups", C.c_int32),
+                ("act", C.c_int32), ("plain", C.c_int32), ("stem", C.c_int32), ("fp8", C.c_int32),
+                ("in_scale", C.c_float), ("dtype", C.c_int32), ("cin", C.c_int32), ("cout", C.c_int32),
+                ("x", Nhwc), ("y", Nhwc), ("res", Nhwc), ("up", Nhwc), ("out_idx", C.c_int32),
+                ("out_off", C.c_int64), ("out_sb", C.c_int64), ("out_sp", C.c_int64), ("out_sc", C.c_int64)]
+
+
+PLAN_FP8 = 0x10000
+
 # Every exported symbol of include/vrs.h with its ctypes signature.
 _vp, _i32, _i64, _f32, _sz = C.c_void_p, C.c_int32, C.c_int64, C.c_float, C.c_size_t
 _P = C.POINTER
@@ -118,6 +130,9 @@ SIGNATURES = {
     "vrs_model_calibrate": (C.c_int, [_vp, _vp, _vp]),
     "vrs_model_num_convs": (C.c_int, [_vp]),
     "vrs_model_conv_info": (C.c_int, [_vp, _i32, _P(C.c_char_p), _P(_i32), _P(_f32)]),
+    "vrs_model_set_plan": (C.c_int, [_vp, _P(_i32), _i32]),
+    "vrs_model_get_plan": (C.c_int, [_vp, _P(_i32), _i32]),
+    "vrs_model_conv_io": (C.c_int, [_vp, _i32, _P(ConvIo)]),
     "vrs_model_destroy": (C.c_int, [_vp]),
 }
 
@@ -154,6 +169,30 @@ def _stream(stream=None):
         return C.c_void_p(stream)
     import torch
     return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class _alloc_on:
+    """Allocate temporaries and outputs on the stream the kernels run on.
+
+    torch's caching allocator ties a block to the stream current at
+    allocation time; a buffer a kernel on another stream still uses could be
+    handed out again once its tensor is dropped.  With an explicit stream,
+    the tensors are allocated while that stream is current."""
+
+    def __init__(self, stream, device=None):
+        self.stream, self.device, self.ctx = stream, device, None
+
+    def __enter__(self):
+        if self.stream is not None:
+            import torch
+            self.ctx = torch.cuda.stream(torch.cuda.ExternalStream(self.stream, device=self.device))
+            self.ctx.__enter__()
+        return self
+
+    def __exit__(self, *exc):
+        if self.ctx is not None:
+            self.ctx.__exit__(*exc)
+        return False
 
 
 def nhwc(t, c=None, c_off=0):
@@ -238,23 +277,24 @@ class Context:
         if ws_bytes == 0:
             raise VrsError(-1, lib().vrs_last_error().decode(errors="replace"))
         dev = boxes.device
-        if workspace is not None:
-            ws = workspace
-            if ws.numel() * ws.element_size() < ws_bytes:
-                raise VrsError(-1, f"detect_postprocess: workspace of {ws.numel()} bytes, {ws_bytes} needed")
-        else:
-            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        if outs is not None:
-            count, score, cls, anchor, xywh = outs
-        else:
-            count = torch.empty(n, dtype=torch.int32, device=dev)
-            score = torch.empty(n, max_det, dtype=torch.float32, device=dev)
-            cls = torch.empty(n, max_det, dtype=torch.int32, device=dev)
-            anchor = torch.empty(n, max_det, dtype=torch.int32, device=dev)
-            xywh = torch.empty(n, max_det, 4, dtype=torch.float32, device=dev)
-        check(lib().vrs_detect_postprocess(self.handle, C.byref(d), _ptr(boxes), _ptr(scores), _ptr(ws), ws_bytes,
-                                           _ptr(count), _ptr(score), _ptr(cls), _ptr(anchor), _ptr(xywh),
-                                           _stream(stream)))
+        with _alloc_on(stream, dev):   # the workspace is dropped on return: allocate it on the launch stream
+            if workspace is not None:
+                ws = workspace
+                if ws.numel() * ws.element_size() < ws_bytes:
+                    raise VrsError(-1, f"detect_postprocess: workspace of {ws.numel()} bytes, {ws_bytes} needed")
+            else:
+                ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            if outs is not None:
+                count, score, cls, anchor, xywh = outs
+            else:
+                count = torch.empty(n, dtype=torch.int32, device=dev)
+                score = torch.empty(n, max_det, dtype=torch.float32, device=dev)
+                cls = torch.empty(n, max_det, dtype=torch.int32, device=dev)
+                anchor = torch.empty(n, max_det, dtype=torch.int32, device=dev)
+                xywh = torch.empty(n, max_det, 4, dtype=torch.float32, device=dev)
+            check(lib().vrs_detect_postprocess(self.handle, C.byref(d), _ptr(boxes), _ptr(scores), _ptr(ws),
+                                               ws_bytes, _ptr(count), _ptr(score), _ptr(cls), _ptr(anchor),
+                                               _ptr(xywh), _stream(stream)))
         if outs is not None:
             return outs
         return count, score, cls, anchor, xywh
@@ -279,7 +319,8 @@ class Context:
         normalised to each original image; orig_wh [n][2] int32 on the device."""
         import torch
         n, max_det, _ = xywh.shape
-        out = torch.empty_like(xywh)
+        with _alloc_on(stream, xywh.device):
+            out = torch.empty_like(xywh)
         check(lib().vrs_detect_unletterbox(self.handle, n, max_det, img_size, _ptr(orig_wh), _ptr(count),
                                            _ptr(xywh), _ptr(out), _stream(stream)))
         return out
@@ -291,7 +332,8 @@ class Context:
         import torch
         n = len(wh)
         if out is None:
-            out = torch.empty(n, 3, img_size, img_size, dtype=torch.float32, device=rgb.device)
+            with _alloc_on(stream, rgb.device):
+                out = torch.empty(n, 3, img_size, img_size, dtype=torch.float32, device=rgb.device)
         offs = (C.c_int64 * n)(*[int(o) for o in offsets])
         dims = (C.c_int32 * (2 * n))(*[int(v) for w_h in wh for v in w_h])
         check(lib().vrs_letterbox(self.handle, n, img_size, _ptr(rgb), rgb.numel() * rgb.element_size(), offs, dims,
@@ -367,7 +409,9 @@ class Model:
 
     def __init__(self, ctx, desc: BlockDesc, batch: int, h: int, w: int, dtype=BF16, bn_eps=1e-3,
                  autotune=True):
-        """ctx=None records the layers only (params()/output_shapes() work without a GPU)."""
+        """ctx=None records the layers only (params()/output_shapes() work without a GPU).
+        autotune: False/0 heuristic tiles, True/1 timed per layer, 2 (fp8
+        models) timed among fp8 tiles with every eligible conv kept on fp8."""
         self.ctx = ctx
         self.desc = desc
         self.batch, self.h, self.w, self.dtype = batch, h, w, dtype
@@ -423,7 +467,8 @@ class Model:
 
     def forward(self, x, outs=None, stream=None):
         if outs is None:
-            outs = self.alloc_outputs(x.device)
+            with _alloc_on(stream, x.device):
+                outs = self.alloc_outputs(x.device)
         ptrs = (C.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
         check(lib().vrs_model_forward(self.handle, _ptr(x), ptrs, _stream(stream)))
         return outs
@@ -463,6 +508,26 @@ class Model:
             check(lib().vrs_model_conv_info(self.handle, i, C.byref(pre), C.byref(f8), C.byref(sc)))
             out.append((pre.value.decode(), bool(f8.value), sc.value))
         return out
+
+    def set_plan(self, plan):
+        """Tile plan to apply at finalize instead of autotuning (list of ints,
+        one per conv; see get_plan)."""
+        arr = (C.c_int32 * len(plan))(*[int(v) for v in plan])
+        check(lib().vrs_model_set_plan(self.handle, arr, len(plan)))
+
+    def get_plan(self):
+        """Per-conv tile codes in use (| PLAN_FP8 for convs on e4m3)."""
+        n = check(lib().vrs_model_get_plan(self.handle, None, 0))
+        arr = (C.c_int32 * n)()
+        check(lib().vrs_model_get_plan(self.handle, arr, n))
+        return list(arr)
+
+    def conv_io(self, i):
+        """vrs_conv_io of conv i (launch index, views of its input, output,
+        residual and fused-upsample source)."""
+        io = ConvIo()
+        check(lib().vrs_model_conv_io(self.handle, i, C.byref(io)))
+        return io
 
     def run_launches(self, first, count, stream=None):
         check(lib().vrs_model_run_launches(self.handle, first, count, _stream(stream)))
