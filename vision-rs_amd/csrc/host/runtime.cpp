@@ -463,15 +463,36 @@ int prep_attn(vrs_ctx* ctx, int heads, int dtype, const vrs_nhwc& qkv, const voi
   a.out = const_cast<void*>(at(o, dtype));
   a.B = qkv.n; a.H = qkv.h; a.W = qkv.w; a.heads = heads; a.qkv_pitch = qkv.pitch; a.out_pitch = o.pitch;
   a.scale_log2e = (float)(1.0 / std::sqrt(32.0) * 1.4426950408889634);
-  a.q_blocks = (qkv.h * qkv.w + 79) / 80;  // 5 waves x 16 queries per workgroup
+  const int N = qkv.h * qkv.w;
+  {
+    const int64_t qb = ((int64_t)qkv.n * qkv.h * qkv.w * qkv.pitch - qkv.c_off) * (int64_t)elt_size(dtype);
+    a.qkv_bytes = qb < (1ll << 31) ? (int32_t)qb : 0;   // 0: the resident kernel is not used
+  }
   char name[48];
-  snprintf(name, sizeof name, "vrs_psa_attn_%s", dsuffix(dtype));
+  int threads;
+  if (dtype == VRS_BF16 && N <= 512 && a.qkv_bytes > 0) {
+    // the head's K and V^T resident in LDS, one wave per 32 queries: one
+    // workgroup per head when there are at least as many heads as CUs,
+    // else tiles of 7 query tiles (two workgroups per 20x20 head)
+    const int tiles = (N + 31) / 32;
+    const int ncu = ctx->num_cu > 0 ? ctx->num_cu : 256;
+    int qt = 7;
+    if ((int64_t)a.B * heads >= ncu) qt = tiles <= 7 ? 7 : tiles <= 13 ? 13 : 16;
+    a.q_blocks = (tiles + qt - 1) / qt;
+    threads = qt * 64;
+    snprintf(name, sizeof name, "vrs_psa_attn_res%d_bf16", qt);
+  } else {
+    a.q_blocks = (N + 79) / 80;  // streamed K/V: 5 waves x 16 queries per workgroup
+    threads = 320;
+    snprintf(name, sizeof name, "vrs_psa_attn_%s", dsuffix(dtype));
+  }
+  if ((int64_t)a.B * heads * a.q_blocks >= (1ll << 31)) return fail(VRS_EBADSHAPE, "psa: grid too large");
   hipFunction_t f;
   if ((rc = get_fn(ctx, name, &f))) return rc;
-  out.push_back(make_launch(name, f, dim3(a.B * heads * a.q_blocks), dim3(320), 0, a));
-  const double N = (double)qkv.h * qkv.w;
-  out.back().flops = 2.0 * a.B * heads * N * N * (32 + 64) + 2.0 * a.B * N * o.c * 9;
-  out.back().bytes = (double)a.B * N * (qkv.c + o.c) * elt_size(dtype) + (double)o.c * (9 * elt_size(dtype) + 8);
+  out.push_back(make_launch(name, f, dim3(a.B * heads * a.q_blocks), dim3(threads), 0, a));
+  const double Nd = (double)N;
+  out.back().flops = 2.0 * a.B * heads * Nd * Nd * (32 + 64) + 2.0 * a.B * Nd * o.c * 9;
+  out.back().bytes = (double)a.B * Nd * (qkv.c + o.c) * elt_size(dtype) + (double)o.c * (9 * elt_size(dtype) + 8);
   return VRS_OK;
 }
 

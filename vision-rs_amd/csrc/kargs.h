@@ -108,6 +108,7 @@ typedef struct {
   int32_t B, H, W, heads, qkv_pitch, out_pitch;
   float scale_log2e;    /* kd^-0.5 * log2(e) */
   int32_t q_blocks;
+  int32_t qkv_bytes;    /* readable bytes from qkv to the end of its buffer (< 2^31) */
 } vrs_attn_args;
 
 /* Detect post-process stage 1: per anchor decode + sigmoid/argmax + threshold. */
