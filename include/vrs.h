@@ -89,6 +89,11 @@ typedef struct {
 #define VRS_TILE_64x256 4
 #define VRS_TILE_32x256 5
 #define VRS_TILE_256x256 6   /* 512 threads; bf16, Cin % 64 == 0 */
+/* Halo-tiled 3x3 stride-1 kernel (bf16, Cin % 32 == 0, width >= 8): 64 (or,
+ * for Cout <= 32, 32) output channels x 256 output pixels of one image strip
+ * per workgroup, the strip rows plus a one-pixel halo staged in LDS once per
+ * 32 input channels and read for all nine taps. */
+#define VRS_TILE_H3 7
 #define VRS_TILE_K32 0x100
 /* OR VRS_TILE_PERSIST: persistent grid (resident workgroups loop over the
  * tiles with one continuous load stream) for memory-bound shapes; bf16,

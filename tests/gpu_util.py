@@ -43,7 +43,11 @@ def tdtype(dtype):
 
 
 def to_nhwc(x_nchw: np.ndarray, dtype, pitch=None, c_off=0):
-    """NCHW float32 -> device [n,h,w,pitch] tensor holding x in channels [c_off, c_off+c)."""
+    """NCHW float32 -> device [n,h,w,pitch] tensor holding x in channels [c_off, c_off+c).
+
+    vrs.nhwc() keeps only the tensor's address: keep the tensor itself alive
+    (a named variable) until the kernel reading it has run, or the caching
+    allocator may hand its memory to the next allocation first."""
     import torch
     n, c, h, w = x_nchw.shape
     pitch = c if pitch is None else pitch

@@ -45,7 +45,7 @@ def dense_tiles():
     ones a shape does not support are rejected with VRS_EUNSUPPORTED."""
     base = [vrs.TILE_128x128, vrs.TILE_256x128, vrs.TILE_128x256, vrs.TILE_64x256, vrs.TILE_32x256,
             vrs.TILE_256x256]
-    out = [vrs.TILE_AUTO]
+    out = [vrs.TILE_AUTO, vrs.TILE_H3]
     for t in base:
         out += [t, t | vrs.TILE_K32, t | vrs.TILE_PERSIST, t | vrs.TILE_K32 | vrs.TILE_PERSIST]
     return out
@@ -108,7 +108,8 @@ def test_config3c_depthwise_full_size():
     ref = oracle.affine_act(oracle.conv2d(x, w, 1, 1, groups=C), scale, shift, 1)
     ref32 = oracle.affine_act(oracle.conv2d(x32, w32, 1, 1, groups=C), scale, shift, 1)
     yt = torch.full((B, hw, hw, C), 7.0, dtype=torch.bfloat16, device="cuda")
-    ctx().conv2d(vrs.nhwc(to_nhwc(x, vrs.BF16)), dev(vrs.pack_conv_weight(w, C, 1, vrs.BF16)), dev(scale),
+    xt = to_nhwc(x, vrs.BF16)   # kept alive until the kernel has run
+    ctx().conv2d(vrs.nhwc(xt), dev(vrs.pack_conv_weight(w, C, 1, vrs.BF16)), dev(scale),
                  dev(shift), vrs.nhwc(yt), 3, 1, C, vrs.ACT_SILU, None, vrs.BF16)
     torch.cuda.synchronize()
     got = from_nhwc(yt)
@@ -182,7 +183,8 @@ def test_config2_attention_core_full_size():
     v = np.ascontiguousarray(qkv.reshape(B, heads, 128, hw, hw)[:, :, 64:].reshape(B, c, hw, hw))
     ref = att + oracle.affine_act(oracle.conv2d(v, pe_w, 1, 1, groups=c), pe_s, pe_t, 0)
     ot = torch.zeros((B, hw, hw, c), dtype=torch.bfloat16, device="cuda")
-    ctx().psa_attention(vrs.nhwc(to_nhwc(qkv, vrs.BF16)), dev(vrs.pack_conv_weight(pe_w, c, 1, vrs.BF16)),
+    qt = to_nhwc(qkv, vrs.BF16)   # kept alive until the kernel has run
+    ctx().psa_attention(vrs.nhwc(qt), dev(vrs.pack_conv_weight(pe_w, c, 1, vrs.BF16)),
                         dev(pe_s), dev(pe_t), vrs.nhwc(ot), heads, vrs.BF16)
     torch.cuda.synchronize()
     got = from_nhwc(ot)

@@ -166,6 +166,67 @@ def test_conv2d_every_tile(dtype, tile, yview):
     assert torch.all(rest == 7.0)
 
 
+H3_CASES = [
+    # n, cin, h, w, cout, residual, (y pitch, y c_off): strip widths (whole
+    # width up to 40, 20 or 32 beyond, partial last strip at 41/70), runs of
+    # 256 pixels that start mid-row and end past the image, Cout 32 (narrow
+    # kernel) / partial 64-channel tiles, several 32-channel stages
+    (2, 64, 160, 160, 32, False, None),
+    (1, 32, 80, 80, 64, True, None),
+    (2, 128, 20, 20, 128, True, (136, 8)),
+    (3, 64, 17, 8, 48, False, None),
+    (1, 96, 11, 41, 200, True, None),
+    (2, 256, 13, 70, 64, False, (80, 16)),
+    (1, 32, 40, 40, 16, True, None),
+    (1, 512, 9, 33, 96, False, None),
+]
+
+
+@pytest.mark.parametrize("case", H3_CASES)
+def test_conv2d_halo3(case):
+    """Halo-tiled 3x3 stride-1 kernel (VRS_TILE_H3) against the oracle, with
+    residual and channel-slice output views; bytes outside the view untouched."""
+    import torch
+    n, cin, h, w, cout, with_res, yv = case
+    dtype = vrs.BF16
+    rnd = rounder(dtype)
+    rng = np.random.default_rng(cin * 7 + cout + h)
+    x = rnd(rng.standard_normal((n, cin, h, w)).astype(np.float32))
+    wt = rnd((rng.standard_normal((cout, cin, 3, 3)) * np.sqrt(2.0 / (cin * 9))).astype(np.float32))
+    scale = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    ref = oracle.affine_act(oracle.conv2d(x, wt, 1, 1), scale, shift, 1)
+    res = rnd(rng.standard_normal((n, cout, h, w)).astype(np.float32)) if with_res else None
+    if with_res:
+        ref = ref + res
+    yp, yo = yv or (cout, 0)
+    yt = torch.full((n, h, w, yp), 7.0, dtype=torch.bfloat16, device="cuda")
+    rt = to_nhwc(res, dtype, yp, yo) if with_res else None
+    xt = to_nhwc(x, dtype)   # kept alive until the kernel has run
+    ctx().conv2d(vrs.nhwc(xt), dev(vrs.pack_conv_weight(wt, 1, cin, dtype)), dev(scale), dev(shift),
+                 vrs.nhwc(yt, cout, yo), 3, 1, 1, vrs.ACT_SILU, vrs.nhwc(rt, cout, yo) if with_res else None, dtype,
+                 tile=vrs.TILE_H3)
+    torch.cuda.synchronize()
+    assert rel_err(from_nhwc(yt, cout, yo), ref, FLOOR[dtype]) < TOL[dtype]
+    if yp > cout:
+        rest = torch.cat([yt[..., :yo], yt[..., yo + cout:]], -1).float()
+        assert torch.all(rest == 7.0)
+
+
+def test_conv2d_halo3_rejections():
+    import torch
+    s = torch.ones(64, device="cuda")
+    w = torch.zeros(64 * 9 * 64, dtype=torch.bfloat16, device="cuda")
+    for (cin, hw, k, st, dt) in [(48, 16, 3, 1, vrs.BF16), (64, 7, 3, 1, vrs.BF16), (64, 16, 3, 2, vrs.BF16),
+                                 (64, 16, 1, 1, vrs.BF16), (64, 16, 3, 1, vrs.F32)]:
+        tdt = torch.bfloat16 if dt == vrs.BF16 else torch.float32
+        x = torch.zeros((1, hw, hw, cin), dtype=tdt, device="cuda")
+        ho = (hw + 2 * (k // 2) - k) // st + 1
+        y = torch.zeros((1, ho, ho, 64), dtype=tdt, device="cuda")
+        with pytest.raises(vrs.VrsError):
+            ctx().conv2d(vrs.nhwc(x), w, s, s, vrs.nhwc(y), k, st, 1, vrs.ACT_SILU, None, dt, tile=vrs.TILE_H3)
+
+
 PERSIST_CASES = [
     # n, cin, h, w, cout, k, s, tile: several tiles per workgroup, ragged pixel
     # and channel tiles, padding taps, stride 2, both step depths

@@ -106,6 +106,7 @@ static const TileInfo* tile_info(int code) {
 // up: the fused-upsample instance (_u), built for 128x128, 256x128 and
 // 128x256 in bf16 and 128x128 and 64x256 in float32, aligned and not persistent
 static int tile_kernel(int code, int cin, int dtype, bool up, char* name, size_t n, int* bm, int* bn, int* threads) {
+  if ((code & 0xff) == VRS_TILE_H3) return fail(VRS_EINVAL, "conv: the halo tile is prepared separately");
   const TileInfo* t = tile_info(code);
   if (!t) return fail(VRS_EINVAL, "conv: unknown tile code %d", code);
   if (up) {
@@ -163,8 +164,19 @@ static int auto_tile(int cout, int cin, int64_t M, int dtype, int num_cu) {
   return VRS_TILE_128x128;
 }
 
-std::vector<int> conv_tile_candidates(int cout, int cin, int dtype) {
+// Strip width of the halo-tiled 3x3 kernel for an image width (0: not usable):
+// the whole width up to 40 pixels, else 20 or 32 when they divide it (no
+// partial strip), else 32.
+static int h3_strip_width(int w) {
+  if (w < 8) return 0;
+  if (w <= 40) return w;
+  if (w % 20 == 0) return 20;
+  return 32;
+}
+
+std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int stride, int w) {
   std::vector<int> c;
+  if (dtype == VRS_BF16 && k == 3 && stride == 1 && cin % 32 == 0 && h3_strip_width(w) > 0) c.push_back(VRS_TILE_H3);
   if (dtype == VRS_FP8) {
     if (cin % 64) return c;
     c.push_back(VRS_TILE_128x128);
@@ -258,6 +270,34 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   a.act = cs.act;
   char name[64];
   int bm, bn, threads;
+  if ((cs.tile & 0xff) == VRS_TILE_H3) {
+    // halo-tiled 3x3 stride-1 kernel (conv3.hip)
+    const int tw = h3_strip_width(x.w);
+    if (cs.dtype != VRS_BF16 || cs.k != 3 || cs.stride != 1 || x.c % 32 != 0 || tw == 0 || cs.up)
+      return fail(VRS_EUNSUPPORTED, "conv: the halo 3x3 tile needs bf16, k=3, stride 1, Cin %% 32 == 0, width >= 8 "
+                  "and no fused upsample (k=%d s=%d Cin=%d W=%d)", cs.k, cs.stride, x.c, x.w);
+    if (!a.stage || a.y_f32)
+      return fail(VRS_EUNSUPPORTED, "conv: the halo 3x3 tile stores whole 16-byte channel chunks of a bf16 NHWC view");
+    if (a.res && a.res_bytes < 0) return fail(VRS_EBADSHAPE, "conv: halo tile residual exceeds 2 GiB");
+    bm = cout <= 32 ? 32 : 64;
+    a.h3_tw = tw;
+    a.h3_strips = (x.w + tw - 1) / tw;
+    a.h3_chunks = (int)(((int64_t)x.h * tw + 255) / 256);
+    a.tiles_m = (cout + bm - 1) / bm;
+    a.tiles_n = 0;
+    const int64_t blocks = (int64_t)a.tiles_m * x.n * a.h3_strips * a.h3_chunks;
+    if (blocks >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: grid too large");
+    if ((int64_t)x.n * x.h * x.w * (int64_t)x.pitch * 2 >= (1ll << 31))
+      return fail(VRS_EBADSHAPE, "conv: halo tile input exceeds 2 GiB");
+    snprintf(name, sizeof name, "vrs_conv3h_bf16_%d", bm);
+    hipFunction_t f;
+    if ((rc = get_fn(ctx, name, &f))) return rc;
+    out.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(256), 0, a));
+    out.back().flops = 2.0 * (double)M * cout * 9.0 * (cs.cin_real > 0 ? cs.cin_real : x.c);
+    out.back().bytes = (double)x.n * x.h * x.w * x.c * 2.0 + (double)cout * 9.0 * x.c * 2.0 + (double)M * cout * 2.0 +
+                       (a.res ? (double)M * cout * 2.0 : 0.0) + 8.0 * cout;
+    return VRS_OK;
+  }
   const int tile = cs.tile ? cs.tile
                             : f8 ? (cout <= 64 ? VRS_TILE_64x256 : VRS_TILE_128x128)
                                  : cs.up ? VRS_TILE_128x128   // built in every fused-upsample dtype
@@ -346,6 +386,8 @@ int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w
       return fail(VRS_EBADSHAPE, "conv: residual shape differs from output");
     a.res = at(*res, cs.dtype);
     a.r_sb = (int64_t)res->h * res->w * res->pitch; a.r_sp = res->pitch; a.r_sc = 1;
+    const int64_t rb = ((int64_t)res->n * res->h * res->w * res->pitch - res->c_off) * (int64_t)elt_size(cs.dtype);
+    a.res_bytes = rb < (1ll << 31) ? (int32_t)rb : -1;   // -1: too large for 32-bit buffer offsets
   }
   a.y = const_cast<void*>(at(y, cs.dtype));
   a.y_sb = (int64_t)y.h * y.w * y.pitch; a.y_sp = y.pitch; a.y_sc = 1;

@@ -53,6 +53,13 @@ typedef struct {
    * from x as usual.  c_split = 0: no fusion. */
   const void* x2;
   int32_t x2_bytes, c_split, H2, W2, x2_pitch;
+  /* halo-tiled 3x3 stride-1 kernels: each image is cut into h3_strips
+   * vertical strips h3_tw pixels wide (the last one may be partial), and each
+   * strip into h3_chunks runs of 256 consecutive output pixels (row-major
+   * within the strip); y_bytes and res_bytes bound the raw-buffer stores and
+   * residual loads */
+  int32_t h3_tw, h3_strips, h3_chunks;
+  int32_t res_bytes;
 } vrs_conv_args;
 
 /* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the
