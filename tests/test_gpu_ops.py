@@ -420,14 +420,22 @@ def test_dwconv(dtype, act, shape):
 
 
 @pytest.mark.parametrize("dtype", DT)
-@pytest.mark.parametrize("hw", [(20, 20), (7, 5), (4, 4)])
+@pytest.mark.parametrize("hw", [(20, 20), (7, 5), (4, 4), (26, 26), (30, 22), (40, 40), (1, 9), (13, 1),
+                                (20, 20, 64), (9, 11, 96)])
 def test_sppf_pool_exact(dtype, hw):
+    """bf16 maps up to 1365 pixels run the wave-per-group kernel (four waves
+    per workgroup up to 426 pixels when the channel groups come in fours, two
+    up to 682, else one; 5 channel groups x 3 images leaves an idle wave), larger ones the plane kernel (float32 40x40 needs its
+    160 KB budget); max is exact, so bit-exact
+    against the oracle's cascade (with exact ties and signed zeros)."""
     import torch
-    h, w = hw
+    h, w = hw[:2]
     rnd = rounder(dtype)
     rng = np.random.default_rng(8)
-    n, c = 2, 32
+    n, c = 3, (hw[2] if len(hw) > 2 else 40)
     y = rnd(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    y[0, 0] = np.float32(-0.0)
+    y[0, 1, :, : max(1, w // 2)] = 1.5   # exact ties
     p1 = oracle.maxpool2d(y); p2 = oracle.maxpool2d(p1); p3 = oracle.maxpool2d(p2)
     buf = torch.zeros((n, h, w, 4 * c + 8), dtype=tdtype(dtype), device="cuda")
     buf[..., 8:8 + c] = to_nhwc(y, dtype)

@@ -454,8 +454,31 @@ int prep_pool(vrs_ctx* ctx, const vrs_nhwc& buf, int dtype, std::vector<Launch>&
   if (buf.c % 32) return fail(VRS_EBADSHAPE, "sppf: view must hold 4*c channels with c %% 8 == 0");
   const int c = buf.c / 4;
   const int hw = buf.h * buf.w;
+  if (dtype == VRS_BF16 && (int64_t)3 * hw * 16 <= 64 * 1024) {
+    // wave-per-channel-group kernel: three LDS planes of 16-byte pixels per
+    // wave, four waves per workgroup when two such workgroups fit a CU's
+    // 160 KB, else two when they fit 64 KB
+    const int64_t plane3 = 3ll * hw * 16;
+    const int G = (c / 8) % 4 == 0 && 4 * plane3 <= 80 * 1024 ? 4 : 2 * plane3 <= 64 * 1024 ? 2 : 1;
+    vrs_pool_args a{};
+    a.buf = const_cast<void*>(at(buf, dtype));
+    a.N = buf.n; a.H = buf.h; a.W = buf.w; a.c = c; a.pitch = buf.pitch; a.cgroups_per_block = 1;
+    const int64_t waves = (int64_t)buf.n * (c / 8);
+    if ((waves + G - 1) / G >= (1ll << 31)) return fail(VRS_EBADSHAPE, "sppf: grid too large");
+    char name[48];
+    snprintf(name, sizeof name, "vrs_sppf_pool_w%d_bf16", G);
+    hipFunction_t f;
+    if ((rc = get_fn(ctx, name, &f))) return rc;
+    out.push_back(make_launch(name, f, dim3((unsigned)((waves + G - 1) / G)), dim3(64 * G), (uint32_t)(G * 3 * hw * 16),
+                              a));
+    out.back().bytes = 4.0 * buf.n * hw * (double)c * elt_size(dtype);
+    return VRS_OK;
+  }
   const int64_t per_group = 2ll * hw * 8 * (int64_t)elt_size(dtype);
-  int cg = (int)std::min<int64_t>(c / 8, (64 * 1024) / per_group);
+  // 64 KB of planes per workgroup, or up to the CU's 160 KB for one group of
+  // a large map (one workgroup per CU then)
+  const int64_t budget = per_group <= 64 * 1024 ? 64 * 1024 : 160 * 1024;
+  int cg = (int)std::min<int64_t>(c / 8, budget / per_group);
   if (cg < 1) return fail(VRS_EUNSUPPORTED, "sppf: %dx%d map does not fit the LDS plane", buf.h, buf.w);
   // a power of two of channel groups per workgroup: each pixel's writes then
   // cover whole 64-byte spans where the budget allows (at 3 groups, 48-byte

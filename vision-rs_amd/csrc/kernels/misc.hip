@@ -323,6 +323,116 @@ __device__ __forceinline__ void pool_body(const vrs_pool_args& a) {
 extern "C" __global__ __launch_bounds__(256) void vrs_sppf_pool_bf16(vrs_pool_args a) { pool_body<bf16_t>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_sppf_pool_f32(vrs_pool_args a) { pool_body<float>(a); }
 
+// Wave-per-channel-group SPPF pool (bfloat16, maps of up to 682 pixels: the
+// 20x20 of YOLO26 at 640).  A wave owns one (image, 8-channel group) and keeps
+// three planes of the map in LDS; the G waves of a workgroup take adjacent
+// groups, so each pixel's reads and writes span 16*G contiguous bytes.  The cascade p1 = max5(y), p2 = max5(p1),
+// p3 = max5(p2) with -inf padding equals windows of 5, 9 and 13 clipped to
+// the map, computed separably: row windows R5 (five reads), R9 = max(R5 at
+// x-2, x+2), R13 = max(R9 at x-2, x+2) (neighbours clamped to the row: the
+// clamped position always lies inside the clipped window), then column
+// windows of 5, 9 and 13 rows of R5, R9, R13.  Each pass spreads the map's
+// pixels over the 64 lanes.  bfloat16 values are compared as ordered 16-bit
+// integers (the sign-magnitude bits with the magnitude flipped for negative
+// values), two per packed v_pk_max_i16.
+namespace {
+typedef short i16x8v_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint32_t ord_bf16x2(uint32_t u) { return u ^ (((u >> 15) & 0x00010001u) * 0x7fffu); }
+__device__ __forceinline__ u32x4_t ord16(u32x4_t v) {
+  return (u32x4_t){ord_bf16x2(v[0]), ord_bf16x2(v[1]), ord_bf16x2(v[2]), ord_bf16x2(v[3])};
+}
+__device__ __forceinline__ u32x4_t max16(u32x4_t a, u32x4_t b) {
+  return __builtin_bit_cast(u32x4_t, __builtin_elementwise_max(__builtin_bit_cast(i16x8v_t, a),
+                                                               __builtin_bit_cast(i16x8v_t, b)));
+}
+
+// Vertical window of 2R+1 rows (clipped to the map) over column x of plane
+// Pl for output rows y0..y0+3, stored at channel offset coff of each pixel.
+// Rows y0-R .. y0+3+R are read once (clamped to the map: a clamped row lies
+// inside every clipped window that asks for it); rows y0-R+3 .. y0+R lie in
+// all four windows.
+template <int R>
+__device__ __forceinline__ void pool_col4(const u32x4_t* Pl, int x, int y0, int W, int H, bf16_t* base, int pitch,
+                                          int coff) {
+  u32x4_t v[2 * R + 4];
+#pragma unroll
+  for (int k = 0; k < 2 * R + 4; ++k) v[k] = Pl[min(max(y0 - R + k, 0), H - 1) * W + x];
+  u32x4_t common = v[3];
+#pragma unroll
+  for (int k = 4; k <= 2 * R; ++k) common = max16(common, v[k]);
+  const u32x4_t o[4] = {max16(max16(max16(common, v[0]), v[1]), v[2]),
+                        max16(max16(max16(common, v[1]), v[2]), v[2 * R + 1]),
+                        max16(max16(max16(common, v[2]), v[2 * R + 1]), v[2 * R + 2]),
+                        max16(max16(max16(common, v[2 * R + 1]), v[2 * R + 2]), v[2 * R + 3])};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (y0 + i < H) *reinterpret_cast<u32x4_t*>(base + (int64_t)((y0 + i) * W + x) * pitch + coff) = ord16(o[i]);
+}
+
+template <int G>
+__device__ __forceinline__ void pool_wave_body(const vrs_pool_args& a) {
+  extern __shared__ __attribute__((aligned(16))) u32x4_t pw_sm[];
+  const int W = a.W, H = a.H, HW = H * W;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int groups = a.c >> 3;
+  // consecutive channel groups of an image stay on one XCD, so the partial
+  // 16-byte pixel reads and writes of its waves meet in the same L2
+  const int gid = xcd_remap(blockIdx.x, gridDim.x) * G + wave;
+  const bool live = gid < a.N * groups;       // idle waves still take part in the barriers
+  const int b = live ? gid / groups : 0, g = live ? gid % groups : 0;
+  u32x4_t* P0 = pw_sm + wave * 3 * HW;
+  u32x4_t* P1 = P0 + HW;
+  u32x4_t* P2 = P1 + HW;
+  bf16_t* base = reinterpret_cast<bf16_t*>(a.buf) + (int64_t)b * HW * a.pitch + g * 8;
+  if (live)
+    for (int p0 = lane; p0 < HW; p0 += 8 * 64) {   // eight loads in flight per lane
+      u32x4_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (p0 + j * 64 < HW) v[j] = *reinterpret_cast<const u32x4_t*>(base + (int64_t)(p0 + j * 64) * a.pitch);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (p0 + j * 64 < HW) P0[p0 + j * 64] = ord16(v[j]);
+    }
+  __syncthreads();
+  if (live)
+    for (int p = lane; p < HW; p += 64) {   // R5 -> P1
+      const int x = p % W, row = p - x;
+      u32x4_t m = P0[p];
+#pragma unroll
+      for (int d = 1; d <= 2; ++d) m = max16(max16(m, P0[row + max(x - d, 0)]), P0[row + min(x + d, W - 1)]);
+      P1[p] = m;
+    }
+  __syncthreads();
+  if (live)
+    for (int p = lane; p < HW; p += 64) {   // R9 -> P2
+      const int x = p % W, row = p - x;
+      P2[p] = max16(P1[row + max(x - 2, 0)], P1[row + min(x + 2, W - 1)]);
+    }
+  __syncthreads();
+  if (live)
+    for (int p = lane; p < HW; p += 64) {   // R13 -> P0 (y is no longer needed)
+      const int x = p % W, row = p - x;
+      P0[p] = max16(P2[row + max(x - 2, 0)], P2[row + min(x + 2, W - 1)]);
+    }
+  __syncthreads();
+  if (!live) return;
+  // column windows -> p1, p2, p3: a lane takes four rows y0..y0+3 of one
+  // column (lanes on consecutive columns), reading each needed row once
+  const int QH = (H + 3) >> 2;
+  for (int it = lane; it < W * QH; it += 64) {
+    const int x = it % W, y0 = (it / W) * 4;
+    pool_col4<2>(P1, x, y0, W, H, base, a.pitch, a.c);
+    pool_col4<4>(P2, x, y0, W, H, base, a.pitch, 2 * a.c);
+    pool_col4<6>(P0, x, y0, W, H, base, a.pitch, 3 * a.c);
+  }
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void vrs_sppf_pool_w4_bf16(vrs_pool_args a) { pool_wave_body<4>(a); }
+extern "C" __global__ __launch_bounds__(128) void vrs_sppf_pool_w2_bf16(vrs_pool_args a) { pool_wave_body<2>(a); }
+extern "C" __global__ __launch_bounds__(64) void vrs_sppf_pool_w1_bf16(vrs_pool_args a) { pool_wave_body<1>(a); }
+
 // ---------------------------------------------------------------------------
 // Nearest 2x upsample (blocks/upsample.rs:23-35) into a channel slice of a
 // concat buffer (blocks/concat.rs:24-38): y[b, oy, ox, c] = x[b, oy/2, ox/2, c].
