@@ -94,6 +94,13 @@ typedef struct {
  * per workgroup, the strip rows plus a one-pixel halo staged in LDS once per
  * 32 input channels and read for all nine taps. */
 #define VRS_TILE_H3 7
+/* Weight-stationary 1x1 kernels (bf16, k = 1, stride 1, Cin a multiple of 64
+ * up to 192 (_256) or 256 (_128), no residual, output channel offset/pitch/
+ * count multiples of 8, no fused upsample): a persistent workgroup keeps a
+ * 256- or 128-channel slice of the weights in LDS and streams 64-pixel tiles
+ * of whole input pixel rows through it. */
+#define VRS_TILE_W1_256 8
+#define VRS_TILE_W1_128 9
 #define VRS_TILE_K32 0x100
 /* OR VRS_TILE_PERSIST: persistent grid (resident workgroups loop over the
  * tiles with one continuous load stream) for memory-bound shapes; bf16,

@@ -227,6 +227,79 @@ def test_conv2d_halo3_rejections():
             ctx().conv2d(vrs.nhwc(x), w, s, s, vrs.nhwc(y), k, st, 1, vrs.ACT_SILU, None, dt, tile=vrs.TILE_H3)
 
 
+W1_CASES = [
+    # n, cin, h, w, cout, tile, input view (pitch, c_off), act: several tiles
+    # per workgroup (odd and even counts), a ragged last pixel tile, partial
+    # channel slices, idle workgroups (fewer tiles than streams), an input
+    # channel view, every Cin instance
+    (2, 192, 40, 40, 256, vrs.TILE_W1_256, None, vrs.ACT_SILU),
+    (3, 128, 33, 17, 200, vrs.TILE_W1_256, None, vrs.ACT_SILU),
+    (2, 64, 64, 64, 256, vrs.TILE_W1_256, (128, 32), vrs.ACT_NONE),
+    (1, 256, 20, 20, 136, vrs.TILE_W1_128, None, vrs.ACT_SILU),
+    (2, 128, 50, 70, 128, vrs.TILE_W1_128, (256, 64), vrs.ACT_SILU),
+    (1, 192, 9, 9, 64, vrs.TILE_W1_128, None, vrs.ACT_SILU),
+    (64, 128, 40, 40, 128, vrs.TILE_W1_128, None, vrs.ACT_SILU),
+    (4, 64, 31, 29, 40, vrs.TILE_W1_128, None, vrs.ACT_SILU),
+]
+
+
+@pytest.mark.parametrize("case", W1_CASES)
+def test_conv2d_weight_stationary_1x1(case):
+    """Weight-stationary 1x1 kernels against the oracle (a sample of images)
+    and against the dense 128x128 kernel (every image), into a channel view
+    whose other bytes stay untouched."""
+    import torch
+    n, cin, h, w, cout, tile, xv, act = case
+    dtype = vrs.BF16
+    rnd = rounder(dtype)
+    rng = np.random.default_rng(cin * 3 + cout + h)
+    x = rnd(rng.standard_normal((n, cin, h, w)).astype(np.float32))
+    wt = rnd((rng.standard_normal((cout, cin, 1, 1)) * np.sqrt(2.0 / cin)).astype(np.float32))
+    scale = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    xp, xo = xv or (cin, 0)
+    xt = to_nhwc(x, dtype, xp, xo)
+    yp, yo = cout + 16, 8
+    yt = torch.full((n, h, w, yp), 7.0, dtype=tdtype(dtype), device="cuda")
+    wp = dev(vrs.pack_conv_weight(wt, 1, cin, dtype))
+    sd, hd = dev(scale), dev(shift)
+    ctx().conv2d(vrs.nhwc(xt, cin, xo), wp, sd, hd, vrs.nhwc(yt, cout, yo), 1, 1, 1, act, None, dtype, tile=tile)
+    torch.cuda.synchronize()
+    ns = min(n, 2)
+    ref = oracle.affine_act(oracle.conv2d(x[:ns], wt, 1, 0), scale, shift, act)
+    assert rel_err(from_nhwc(yt[:ns], cout, yo), ref, FLOOR[dtype]) < TOL[dtype]
+    y2 = torch.full_like(yt, 7.0)
+    ctx().conv2d(vrs.nhwc(xt, cin, xo), wp, sd, hd, vrs.nhwc(y2, cout, yo), 1, 1, 1, act, None, dtype,
+                 tile=vrs.TILE_128x128)
+    torch.cuda.synchronize()
+    assert rel_err(from_nhwc(yt, cout, yo), from_nhwc(y2, cout, yo), FLOOR[dtype]) < TOL[dtype]
+    rest = torch.cat([yt[..., :yo], yt[..., yo + cout:]], -1).float()
+    assert torch.all(rest == 7.0)
+
+
+def test_conv2d_weight_stationary_rejections():
+    import torch
+    s = torch.ones(512, device="cuda")
+    w = torch.zeros(512 * 9 * 320, dtype=torch.bfloat16, device="cuda")
+    x64 = torch.zeros((1, 8, 8, 64), dtype=torch.bfloat16, device="cuda")
+    y64 = torch.zeros((1, 8, 8, 64), dtype=torch.bfloat16, device="cuda")
+    for (cin, k, tile) in [(96, 1, vrs.TILE_W1_128), (320, 1, vrs.TILE_W1_128), (256, 1, vrs.TILE_W1_256),
+                           (64, 3, vrs.TILE_W1_128)]:
+        x = torch.zeros((1, 8, 8, cin), dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(vrs.VrsError):
+            ctx().conv2d(vrs.nhwc(x), w, s, s, vrs.nhwc(y64), k, 1, 1, vrs.ACT_SILU, None, vrs.BF16, tile=tile)
+    with pytest.raises(vrs.VrsError):   # residual
+        ctx().conv2d(vrs.nhwc(x64), w, s, s, vrs.nhwc(y64), 1, 1, 1, vrs.ACT_SILU, vrs.nhwc(y64), vrs.BF16,
+                     tile=vrs.TILE_W1_128)
+    with pytest.raises(vrs.VrsError):   # float32
+        xf = torch.zeros((1, 8, 8, 64), dtype=torch.float32, device="cuda")
+        ctx().conv2d(vrs.nhwc(xf), w, s, s, vrs.nhwc(xf), 1, 1, 1, vrs.ACT_SILU, None, vrs.F32, tile=vrs.TILE_W1_128)
+    with pytest.raises(vrs.VrsError):   # output channel count not a multiple of 8
+        y60 = torch.zeros((1, 8, 8, 60), dtype=torch.bfloat16, device="cuda")
+        ctx().conv2d(vrs.nhwc(x64), w, s, s, vrs.nhwc(y60), 1, 1, 1, vrs.ACT_SILU, None, vrs.BF16,
+                     tile=vrs.TILE_W1_128)
+
+
 PERSIST_CASES = [
     # n, cin, h, w, cout, k, s, tile: several tiles per workgroup, ragged pixel
     # and channel tiles, padding taps, stride 2, both step depths

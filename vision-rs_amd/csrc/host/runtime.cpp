@@ -106,7 +106,8 @@ static const TileInfo* tile_info(int code) {
 // up: the fused-upsample instance (_u), built for 128x128, 256x128 and
 // 128x256 in bf16 and 128x128 and 64x256 in float32, aligned and not persistent
 static int tile_kernel(int code, int cin, int dtype, bool up, char* name, size_t n, int* bm, int* bn, int* threads) {
-  if ((code & 0xff) == VRS_TILE_H3) return fail(VRS_EINVAL, "conv: the halo tile is prepared separately");
+  if ((code & 0xff) == VRS_TILE_H3 || (code & 0xff) == VRS_TILE_W1_256 || (code & 0xff) == VRS_TILE_W1_128)
+    return fail(VRS_EINVAL, "conv: the halo and weight-stationary tiles are prepared separately");
   const TileInfo* t = tile_info(code);
   if (!t) return fail(VRS_EINVAL, "conv: unknown tile code %d", code);
   if (up) {
@@ -177,6 +178,10 @@ static int h3_strip_width(int w) {
 std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int stride, int w) {
   std::vector<int> c;
   if (dtype == VRS_BF16 && k == 3 && stride == 1 && cin % 32 == 0 && h3_strip_width(w) > 0) c.push_back(VRS_TILE_H3);
+  if (dtype == VRS_BF16 && k == 1 && stride == 1 && cin % 64 == 0 && cin <= 256 && w > 0) {
+    if (cout > 128 && cin <= 192) c.push_back(VRS_TILE_W1_256);
+    c.push_back(VRS_TILE_W1_128);
+  }
   if (dtype == VRS_FP8) {
     if (cin % 64) return c;
     c.push_back(VRS_TILE_128x128);
@@ -296,6 +301,33 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
     out.back().flops = 2.0 * (double)M * cout * 9.0 * (cs.cin_real > 0 ? cs.cin_real : x.c);
     out.back().bytes = (double)x.n * x.h * x.w * x.c * 2.0 + (double)cout * 9.0 * x.c * 2.0 + (double)M * cout * 2.0 +
                        (a.res ? (double)M * cout * 2.0 : 0.0) + 8.0 * cout;
+    return VRS_OK;
+  }
+  if ((cs.tile & 0xff) == VRS_TILE_W1_256 || (cs.tile & 0xff) == VRS_TILE_W1_128) {
+    // weight-stationary 1x1 kernel (conv1w.hip)
+    bm = (cs.tile & 0xff) == VRS_TILE_W1_256 ? 256 : 128;
+    if (cs.dtype != VRS_BF16 || cs.k != 1 || cs.stride != 1 || cs.up || x.c % 64 != 0 || x.c > (bm == 256 ? 192 : 256))
+      return fail(VRS_EUNSUPPORTED, "conv: the weight-stationary %d-channel tile needs bf16, k=1, stride 1, no fused "
+                  "upsample and Cin a multiple of 64 up to %d (k=%d s=%d Cin=%d)", bm, bm == 256 ? 192 : 256, cs.k,
+                  cs.stride, x.c);
+    if (a.res || !a.stage || a.y_f32)
+      return fail(VRS_EUNSUPPORTED, "conv: the weight-stationary tile takes no residual and stores 8-channel-aligned "
+                  "chunks of a bf16 NHWC view");
+    const int64_t yb = ((int64_t)(a.N - 1) * a.y_sb + (int64_t)ho * wo * a.y_sp) * 2;
+    if (yb >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: weight-stationary tile: output view exceeds 2 GiB");
+    a.y_bytes = (int32_t)yb;
+    a.tiles_m = (cout + bm - 1) / bm;
+    a.tiles_n = (int32_t)((M + 63) / 64);
+    snprintf(name, sizeof name, "vrs_conv1w_bf16_%d_c%d", bm, x.c);
+    hipFunction_t f;
+    if ((rc = get_fn(ctx, name, &f))) return rc;
+    // persistent grid: the resident workgroups, a whole number of streams
+    // (one workgroup per channel slice each), no more streams than tiles
+    const int64_t resident = (int64_t)resident_wgs(f, 512) * (ctx->num_cu > 0 ? ctx->num_cu : 256);
+    const int64_t streams = std::max<int64_t>(1, std::min<int64_t>(resident / a.tiles_m, a.tiles_n));
+    out.push_back(make_launch(name, f, dim3((unsigned)(streams * a.tiles_m)), dim3(512), 0, a));
+    out.back().flops = 2.0 * (double)M * cout * (cs.cin_real > 0 ? cs.cin_real : x.c);
+    out.back().bytes = (double)M * x.c * 2.0 + (double)cout * x.c * 2.0 + (double)M * cout * 2.0 + 8.0 * cout;
     return VRS_OK;
   }
   const int tile = cs.tile ? cs.tile

@@ -1,0 +1,206 @@
+// Weight-stationary 1x1 convolution + folded BatchNorm + SiLU for gfx950
+// (bfloat16, stride 1, no residual).
+//
+// Semantics as the dense conv (blocks/conv.rs:31-46 with k = 1):
+// y[p, co] = act(scale[co] * sum_ci W[co, ci] x[p, ci] + shift[co]).
+//
+// The memory-bound 1x1 layers (Cin <= 256) spend most of a tiled GEMM's
+// in-flight capacity re-reading the weight tile from L2 for every pixel
+// tile.  Here a persistent workgroup keeps one BM-channel slice of the
+// weights in LDS for its whole run and streams 64-pixel tiles through it:
+//
+// * 512 threads (8 wave64), one slice of BM output channels (the grid is a
+//   multiple of the slice count; the slices of one pixel stream are
+//   neighbouring logical blocks, so they share an XCD and its L2 serves the
+//   later slices' pixel reads);
+// * a tile is 64 pixels x all Cin channels, loaded as whole pixel rows
+//   (Cin*2 contiguous bytes) into registers two tiles ahead and written into
+//   one of two LDS buffers one tile ahead: one barrier per tile;
+// * wave tile 32 channels x (64 / waves-per-column) pixels on
+//   v_mfma_f32_32x32x16_bf16, the whole K = Cin per tile from LDS;
+// * epilogue straight from the accumulators: each lane owns 4 consecutive
+//   channels of one pixel per register quad, stored as one 8-byte raw-buffer
+//   store (out-of-range pixels and channels get an offset the resource
+//   rejects).  The folded-BN constants of the wave's channels are read once.
+//
+// LDS rows are Cin + 8 elements: the 32 rows a fragment read touches start
+// on distinct 4-bank groups for every Cin that is a multiple of 64.
+#include "common.h"
+
+namespace {
+
+constexpr int W1_BN = 64;    // pixels per tile
+constexpr int W1_NT = 512;   // threads per workgroup
+
+template <int BM, int CIN>
+__device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
+  using E = Elt<bf16_t>;
+  using G = E::group;
+  constexpr int LDK = CIN + 8;                 // LDS row stride (elements)
+  constexpr int CPR = CIN / 8;                 // 16-byte chunks per row
+  constexpr int NCH = W1_BN * CPR / W1_NT;     // pixel chunks per thread per tile
+  constexpr int NWI = BM * CPR / W1_NT;        // weight chunks per thread
+  static_assert(CIN % 64 == 0 && W1_BN * CPR % W1_NT == 0 && BM * CPR % W1_NT == 0, "whole chunks");
+  constexpr int WGM = BM / 32 < 8 ? BM / 32 : 8, WGN = 8 / WGM;
+  constexpr int WTM = BM / WGM, WTN = W1_BN / WGN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+  __shared__ __attribute__((aligned(16))) bf16_t sW[BM * LDK];
+  __shared__ __attribute__((aligned(16))) bf16_t sB0[W1_BN * LDK];
+  __shared__ __attribute__((aligned(16))) bf16_t sB1[W1_BN * LDK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int frag_row = lane & 31, hq = lane >> 5;
+  // workgroup -> (channel slice, pixel stream); the host sizes the grid as a
+  // multiple of tiles_m
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int slice = L % a.tiles_m, stream = L / a.tiles_m;
+  const int streams = gridDim.x / a.tiles_m;
+  const int T = a.tiles_n;
+  const int nt = stream < T ? (T - 1 - stream) / streams + 1 : 0;   // tiles of this workgroup
+  if (nt == 0) return;   // uniform over the workgroup, before any barrier
+  const int m0 = slice * BM;
+
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, a.w_bytes);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, a.y_bytes);
+
+  // weight slice -> LDS, once (rows past Cout read zeros)
+  {
+    G wv[NWI];
+#pragma unroll
+    for (int i = 0; i < NWI; ++i) {
+      const int q = tid + i * W1_NT, r = q / CPR, c = q % CPR;
+      wv[i] = E::bload(rw, m0 + r < a.Cout ? (uint32_t)(((m0 + r) * CIN + c * 8) * 2) : kOOB, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NWI; ++i) {
+      const int q = tid + i * W1_NT;
+      E::store(&sW[(q / CPR) * LDK + (q % CPR) * 8], wv[i]);
+    }
+  }
+
+  // this thread's pixel chunks: row (pixel within the tile) and byte column,
+  // the same for every tile
+  int b_row[NCH], b_col[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int q = tid + i * W1_NT;
+    b_row[i] = q / CPR;
+    b_col[i] = (q % CPR) * 8;
+  }
+  const uint32_t pitch_b = (uint32_t)a.x_pitch * 2u;
+  auto load_tile = [&](int k, G (&R)[NCH]) {
+    const int n0 = (stream + k * streams) * W1_BN;
+    const bool live = k < nt;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int m = n0 + b_row[i];
+      R[i] = E::bload(rx, live && m < a.M ? (uint32_t)m * pitch_b + (uint32_t)b_col[i] * 2u : kOOB, 0);
+    }
+  };
+  auto store_tile = [&](bf16_t* sB, const G (&R)[NCH]) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) E::store(&sB[b_row[i] * LDK + b_col[i]], R[i]);
+  };
+
+  // folded-BN constants of this lane's channels: register quad g of MFMA
+  // row block i holds channels m0 + wm*WTM + i*32 + g*8 + hq*4 + 0..3
+  const ChanConst c_scale(a.scale, a.Cout), c_shift(a.shift, a.Cout);
+  const uint32_t hmask = upper_half_mask();
+  float sc[TM][4][4], sh[TM][4][4];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      c_scale.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sc[i][g]);
+      c_shift.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sh[i][g]);
+    }
+  const int HWo = a.Ho * a.Wo;
+  const float inv_hwo = 1.0f / (float)HWo;
+
+  f32x16_t acc[TM][TN];
+  auto compute = [&](const bf16_t* sB) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    const bf16_t* pa = sW + (wm * WTM + frag_row) * LDK + hq * 8;
+    const bf16_t* pb = sB + (wn * WTN + frag_row) * LDK + hq * 8;
+#pragma unroll
+    for (int kk = 0; kk < CIN / 16; ++kk) {
+      G fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = E::load(pa + i * 32 * LDK + kk * 16);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = E::load(pb + j * 32 * LDK + kk * 16);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32_k16(fa[i], fb[j], acc[i][j]);
+    }
+  };
+  auto epilogue = [&](int k) {
+    const int n0 = (stream + k * streams) * W1_BN;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int m = n0 + wn * WTN + j * 32 + frag_row;
+      int pp;
+      const int bb = fdivmod(m < a.M ? m : 0, HWo, inv_hwo, pp);
+      const uint32_t pix = (uint32_t)(((int64_t)bb * a.y_sb + (int64_t)pp * a.y_sp) * 2);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int co = m0 + wm * WTM + i * 32 + g * 8 + hq * 4;
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = acc[i][j][g * 4 + r] * sc[i][g][r] + sh[i][g][r];
+            if (a.act == VRS_ACT_SILU) t = silu_fast(t);
+            v[r] = t;
+          }
+          const uint32_t off = m < a.M && co < a.Cout ? pix + (uint32_t)co * 2u : kOOB;
+          __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, ry,
+                                                off, 0, 0);
+        }
+    }
+  };
+
+  // tile k: LDS buffer k&1 holds it; register set (k+1)&1 holds tile k+1
+  // (written to the other buffer during tile k); set k&1 receives tile k+2
+  G r0[NCH], r1[NCH];
+  load_tile(0, r0);
+  load_tile(1, r1);
+  store_tile(sB0, r0);
+  __syncthreads();
+  auto step = [&](const bf16_t* cur, bf16_t* nxt, G (&ld)[NCH], const G (&st)[NCH], int k) {
+    load_tile(k + 2, ld);
+    store_tile(nxt, st);
+    compute(cur);
+    epilogue(k);
+    __syncthreads();
+  };
+  for (int k = 0; k < nt; k += 2) {
+    step(sB0, sB1, r0, r1, k);
+    if (k + 1 < nt) step(sB1, sB0, r1, r0, k + 1);
+  }
+}
+}  // namespace
+
+// vrs_conv1w_bf16_<BM>_c<Cin>: LDS = (BM + 128) * (Cin + 8) * 2 bytes
+// (256 x 192: 150 KB, one workgroup per CU; 128 x 64: 24.8 KB).
+#define VRS_CONV1W(BM, CIN)                                                                        \
+  extern "C" __global__ __launch_bounds__(512) void vrs_conv1w_bf16_##BM##_c##CIN(vrs_conv_args a) { \
+    conv1w_body<BM, CIN>(a);                                                                       \
+  }
+VRS_CONV1W(256, 64)
+VRS_CONV1W(256, 128)
+VRS_CONV1W(256, 192)
+VRS_CONV1W(128, 64)
+VRS_CONV1W(128, 128)
+VRS_CONV1W(128, 192)
+VRS_CONV1W(128, 256)
