@@ -21,7 +21,9 @@
 // * epilogue straight from the accumulators: each lane owns 4 consecutive
 //   channels of one pixel per register quad, stored as one 8-byte raw-buffer
 //   store (out-of-range pixels and channels get an offset the resource
-//   rejects).  The folded-BN constants of the wave's channels are read once.
+//   rejects).  The folded-BN constants of the wave's channels are read once;
+//   tile k-1's epilogue is interleaved with tile k's MFMAs (two accumulator
+//   sets).
 //
 // LDS rows are Cin + 8 elements: the 32 rows a fragment read touches start
 // on distinct 4-bank groups for every Cin that is a multiple of 64.
@@ -120,18 +122,50 @@ __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
   const int HWo = a.Ho * a.Wo;
   const float inv_hwo = 1.0f / (float)HWo;
 
-  f32x16_t acc[TM][TN];
-  auto compute = [&](const bf16_t* sB) {
+  // Tile k's MFMAs run into one accumulator set while the epilogue of tile
+  // k-1 drains the other, a few store units (4 channels of one pixel) after
+  // each 16-deep k slice: its VALU work (two transcendentals per value)
+  // issues between MFMAs instead of after them.
+  constexpr int KK = CIN / 16;
+  constexpr int NU = TN * TM * 4;   // store units per tile and lane
+  struct Out { uint32_t pix[TN]; bool ok[TN]; };
+  auto out_addr = [&](int k) {   // tile k's per-lane pixel offsets (none for k < 0)
+    Out o;
+    const int n0 = (stream + k * streams) * W1_BN;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int m = n0 + wn * WTN + j * 32 + frag_row;
+      o.ok[j] = k >= 0 && m < a.M;
+      int pp;
+      const int bb = fdivmod(o.ok[j] ? m : 0, HWo, inv_hwo, pp);
+      o.pix[j] = (uint32_t)(((int64_t)bb * a.y_sb + (int64_t)pp * a.y_sp) * 2);
+    }
+    return o;
+  };
+  auto epi_unit = [&](int u, const f32x16_t (&ap)[TM][TN], const Out& o) {
+    const int j = u / (TM * 4), i = (u / 4) % TM, g = u % 4;
+    const int co = m0 + wm * WTM + i * 32 + g * 8 + hq * 4;
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float t = ap[i][j][g * 4 + r] * sc[i][g][r] + sh[i][g][r];
+      if (a.act == VRS_ACT_SILU) t = silu_fast(t);
+      v[r] = t;
+    }
+    const uint32_t off = o.ok[j] && co < a.Cout ? o.pix[j] + (uint32_t)co * 2u : kOOB;
+    __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, ry, off, 0, 0);
+  };
+  auto compute = [&](const bf16_t* sB, f32x16_t (&ac)[TM][TN], const f32x16_t (&ap)[TM][TN], const Out& op) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        for (int r = 0; r < 16; ++r) ac[i][j][r] = 0.f;
     const bf16_t* pa = sW + (wm * WTM + frag_row) * LDK + hq * 8;
     const bf16_t* pb = sB + (wn * WTN + frag_row) * LDK + hq * 8;
 #pragma unroll
-    for (int kk = 0; kk < CIN / 16; ++kk) {
+    for (int kk = 0; kk < KK; ++kk) {
       G fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) fa[i] = E::load(pa + i * 32 * LDK + kk * 16);
@@ -140,53 +174,46 @@ __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32_k16(fa[i], fb[j], acc[i][j]);
-    }
-  };
-  auto epilogue = [&](int k) {
-    const int n0 = (stream + k * streams) * W1_BN;
+        for (int j = 0; j < TN; ++j) ac[i][j] = mfma32_k16(fa[i], fb[j], ac[i][j]);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int m = n0 + wn * WTN + j * 32 + frag_row;
-      int pp;
-      const int bb = fdivmod(m < a.M ? m : 0, HWo, inv_hwo, pp);
-      const uint32_t pix = (uint32_t)(((int64_t)bb * a.y_sb + (int64_t)pp * a.y_sp) * 2);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int co = m0 + wm * WTM + i * 32 + g * 8 + hq * 4;
-          float v[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float t = acc[i][j][g * 4 + r] * sc[i][g][r] + sh[i][g][r];
-            if (a.act == VRS_ACT_SILU) t = silu_fast(t);
-            v[r] = t;
-          }
-          const uint32_t off = m < a.M && co < a.Cout ? pix + (uint32_t)co * 2u : kOOB;
-          __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, ry,
-                                                off, 0, 0);
-        }
+      for (int u = kk * NU / KK; u < (kk + 1) * NU / KK; ++u) epi_unit(u, ap, op);
     }
   };
 
   // tile k: LDS buffer k&1 holds it; register set (k+1)&1 holds tile k+1
-  // (written to the other buffer during tile k); set k&1 receives tile k+2
+  // (written to the other buffer during tile k); set k&1 receives tile k+2;
+  // accumulator set k&1 receives tile k while set (k+1)&1 drains tile k-1
   G r0[NCH], r1[NCH];
+  f32x16_t acc0[TM][TN], acc1[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc1[i][j][r] = 0.f;
   load_tile(0, r0);
   load_tile(1, r1);
   store_tile(sB0, r0);
   __syncthreads();
-  auto step = [&](const bf16_t* cur, bf16_t* nxt, G (&ld)[NCH], const G (&st)[NCH], int k) {
+  auto step = [&](const bf16_t* cur, bf16_t* nxt, G (&ld)[NCH], const G (&st)[NCH], f32x16_t (&ac)[TM][TN],
+                  const f32x16_t (&ap)[TM][TN], int k) {
     load_tile(k + 2, ld);
     store_tile(nxt, st);
-    compute(cur);
-    epilogue(k);
+    compute(cur, ac, ap, out_addr(k - 1));
     __syncthreads();
   };
   for (int k = 0; k < nt; k += 2) {
-    step(sB0, sB1, r0, r1, k);
-    if (k + 1 < nt) step(sB1, sB0, r1, r0, k + 1);
+    step(sB0, sB1, r0, r1, acc0, acc1, k);
+    if (k + 1 < nt) step(sB1, sB0, r1, r0, acc1, acc0, k + 1);
+  }
+  // the last tile's epilogue
+  const Out ol = out_addr(nt - 1);
+  if ((nt - 1) & 1) {
+#pragma unroll
+    for (int u = 0; u < NU; ++u) epi_unit(u, acc1, ol);
+  } else {
+#pragma unroll
+    for (int u = 0; u < NU; ++u) epi_unit(u, acc0, ol);
   }
 }
 }  // namespace
