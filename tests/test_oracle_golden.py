@@ -40,11 +40,25 @@ def _shapes(family, table):
 
 @pytest.mark.parametrize("sub,cin,cout,g", [("depthwise", 128, 128, 128), ("g4", 8, 8, 4)])
 def test_conv_grouped(sub, cin, cout, g):
+    """The reference's grouped-conv fixtures against the oracle.  The g4 case
+    pins the oracle only: the library takes groups 1 (Conv, blocks/conv.rs:31-46)
+    or groups == C (DWConv, blocks/conv.rs:75-85) -- every YOLO26 conv is one of
+    the two -- and rejects any other group count with VRS_EUNSUPPORTED
+    (test_grouped_conv_other_than_depthwise_is_rejected)."""
     x = load(f"conv_grouped/{sub}/x.bin", (2, cin, 4, 4))
     w = load(f"conv_grouped/{sub}/conv_w.bin", (cout, cin // g, 3, 3))
     exp = load(f"conv_grouped/{sub}/expected_output.bin", (2, cout, 4, 4))
     y = oracle.conv2d(x, w, stride=1, pad=1, groups=g)
     assert np.max(np.abs(y - exp)) < 1e-5
+
+
+def test_grouped_conv_other_than_depthwise_is_rejected():
+    """groups not in {1, C}: the weight packer (and vrs_conv2d) refuse it."""
+    from gpu_util import vrs
+    w = load("conv_grouped/g4/conv_w.bin", (8, 2, 3, 3))
+    with pytest.raises(vrs.VrsError) as e:
+        vrs.pack_conv_weight(w, groups=4)
+    assert e.value.code == -3   # VRS_EUNSUPPORTED
 
 
 def test_conv_stem_train_bn():
