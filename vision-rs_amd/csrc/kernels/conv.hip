@@ -115,6 +115,22 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   const int tile_m = logical % a.tiles_m, tile_n = logical / a.tiles_m;
   const int m0 = tile_m * BM;   // first output channel
   const int n0 = tile_n * BN;   // first output pixel
+  // folded-BN constants of the tile's BM channels, staged in LDS for the
+  // epilogue (visible after the K loop's first barrier): each lane then reads
+  // its 4 channels as one 16-byte LDS load instead of selecting them from
+  // scalar registers per value
+  // (bf16 tiles; the fp8 tiles, whose registers are tighter, and the float32
+  // ones, whose two workgroups per CU leave no LDS for it, select them from
+  // the scalar cache)
+  constexpr bool LDS_CONST = !F8 && sizeof(T) == 2;
+  __shared__ __attribute__((aligned(16))) float s_scale[LDS_CONST ? BM : 4];
+  __shared__ __attribute__((aligned(16))) float s_shift[LDS_CONST ? BM : 4];
+  if (LDS_CONST)
+  for (int c = threadIdx.x; c < BM; c += 64 * WGM * WGN) {
+    const bool ok = m0 + c < a.Cout;
+    s_scale[c] = ok ? a.scale[m0 + c] : 0.f;
+    s_shift[c] = ok ? a.shift[m0 + c] : 0.f;
+  }
 
   const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
   const T* __restrict__ w = reinterpret_cast<const T*>(a.w);
@@ -426,118 +442,134 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
 
   // Epilogue: folded BN, activation, residual.  Accumulator register
   // g*4 + r of MFMA tile (i, j) is channel i*32 + g*8 + hq*4 + r of pixel
-  // j*32 + (lane & 31), hq = lane >> 5.
+  // j*32 + (lane & 31), hq = lane >> 5.  Instantiated per activation so the
+  // identity layers carry no SiLU and the SiLU layers no per-value select.
   const int hq = lane >> 5;
   const ChanConst c_scale(a.scale, a.Cout), c_shift(a.shift, a.Cout);
   const uint32_t hmask = upper_half_mask();
-  if (a.stage) {
-    // Staged store: every wave writes its (WTN pixel x WTM channel) tile to
-    // LDS, then stores whole 16-byte channel chunks per lane, so consecutive
-    // lanes write contiguous bytes of a pixel's NHWC row.
-    constexpr int HW_ = WGM * WGN / 2;
-    T* st = sbuf(wave / HW_) + (wave % HW_) * WTN * (WTM + SPAD);
+  auto chan4 = [&](const float* s, int i, int g) {
+    if constexpr (!LDS_CONST) {
+      float q[4];
+      (s == s_scale ? c_scale : c_shift).quad(m0 + wm * WTM + i * 32 + g * 8, hmask, q);
+      return (f32x4_t){q[0], q[1], q[2], q[3]};
+    } else {
+      return *reinterpret_cast<const f32x4_t*>(&s[wm * WTM + i * 32 + g * 8 + hq * 4]);
+    }
+  };
+  // MODE 0: identity, 1: SiLU, 2: chosen per value at run time (the fp8
+  // tiles: a second epilogue copy costs them registers)
+  auto epilogue = [&](auto mode_tag) {
+    constexpr int MODE = decltype(mode_tag)::value;
+    if (a.stage) {
+      // Staged store: every wave writes its (WTN pixel x WTM channel) tile to
+      // LDS, then stores whole 16-byte channel chunks per lane, so consecutive
+      // lanes write contiguous bytes of a pixel's NHWC row.
+      constexpr int HW_ = WGM * WGN / 2;
+      T* st = sbuf(wave / HW_) + (wave % HW_) * WTN * (WTM + SPAD);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int cl = i * 32 + g * 8 + hq * 4;   // channel within the wave tile
+          const int co = m0 + wm * WTM + cl;
+          const f32x4_t sc = chan4(s_scale, i, g), sh = chan4(s_shift, i, g);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int pl = j * 32 + (lane & 31);
+            const int m = n0 + wn * WTN + pl;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float t = acc[i][j][g * 4 + r] * sc[r] + sh[r];
+              if constexpr (MODE == 1) t = silu_t<T>(t);
+              if constexpr (MODE == 2) if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
+              v[r] = t;
+            }
+            if (a.res && m < a.M && co < a.Cout) {
+              int pp;
+              const int bb = fdivmod(m, HWo, inv_hwo, pp);
+              const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + co;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) v[r] += E::to_f(rp[r]);
+            }
+            T* sp = st + pl * (WTM + SPAD) + cl;
+            if constexpr (sizeof(T) == 2) {
+              *reinterpret_cast<u32x2_t*>(sp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            } else {
+              *reinterpret_cast<f32x4_t*>(sp) = (f32x4_t){v[0], v[1], v[2], v[3]};
+            }
+          }
+        }
+      __syncthreads();
+      constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+      constexpr int CPP = WTM / EPC;            // chunks per pixel row
+      const int co_w = m0 + wm * WTM;
+      for (int c = lane; c < WTN * CPP; c += 64) {
+        const int pl = c / CPP, part = c % CPP;
+        const int m = n0 + wn * WTN + pl;
+        const int co = co_w + part * EPC;
+        if (m >= a.M || co >= a.Cout) continue;
+        int pp;
+        const int bb = fdivmod(m, HWo, inv_hwo, pp);
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + pl * (WTM + SPAD) + part * EPC);
+        *reinterpret_cast<u32x4_t*>(reinterpret_cast<T*>(a.y) + bb * a.y_sb + pp * a.y_sp + co) = v;
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int cl = i * 32 + g * 8 + hq * 4;   // channel within the wave tile
-        const int co = m0 + wm * WTM + cl;
-        float sc[4], sh[4];
-        c_scale.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sc);
-        c_shift.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sh);
+        const int co = m0 + wm * WTM + i * 32 + g * 8 + hq * 4;
+        const f32x4_t sc = chan4(s_scale, i, g), sh = chan4(s_shift, i, g);
+        if (co >= a.Cout) continue;
+        const bool full4 = (co + 3 < a.Cout);
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const int pl = j * 32 + (lane & 31);
-          const int m = n0 + wn * WTN + pl;
+          const int m = n0 + wn * WTN + j * 32 + (lane & 31);
+          if (m >= a.M) continue;
+          int pp;
+          const int bb = fdivmod(m, HWo, inv_hwo, pp);
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float t = acc[i][j][g * 4 + r] * sc[r] + sh[r];
-            if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
+            if constexpr (MODE == 1) t = silu_t<T>(t);
+            if constexpr (MODE == 2) if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
             v[r] = t;
           }
-          if (a.res && m < a.M && co < a.Cout) {
-            int pp;
-            const int bb = fdivmod(m, HWo, inv_hwo, pp);
-            const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + co;
+          if (a.res) {
+            const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + (int64_t)co * a.r_sc;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] += E::to_f(rp[r]);
+            for (int r = 0; r < 4; ++r)
+              if (co + r < a.Cout) v[r] += E::to_f(rp[r * a.r_sc]);
           }
-          T* sp = st + pl * (WTM + SPAD) + cl;
-          if constexpr (sizeof(T) == 2) {
-            *reinterpret_cast<u32x2_t*>(sp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          const int64_t yo = bb * a.y_sb + pp * a.y_sp + (int64_t)co * a.y_sc;
+          if (a.y_f32) {
+            float* yp = reinterpret_cast<float*>(a.y) + yo;
+            if (a.y_sc == 1 && full4) {
+              *reinterpret_cast<f32x4_t*>(yp) = (f32x4_t){v[0], v[1], v[2], v[3]};
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (co + r < a.Cout) yp[r * a.y_sc] = v[r];
+            }
           } else {
-            *reinterpret_cast<f32x4_t*>(sp) = (f32x4_t){v[0], v[1], v[2], v[3]};
+            T* yp = reinterpret_cast<T*>(a.y) + yo;
+            if (sizeof(T) == 2 && a.y_sc == 1 && full4) {
+              *reinterpret_cast<u32x2_t*>(yp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (co + r < a.Cout) yp[r * a.y_sc] = E::from_f(v[r]);
+            }
           }
         }
       }
-    __syncthreads();
-    constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
-    constexpr int CPP = WTM / EPC;            // chunks per pixel row
-    const int co_w = m0 + wm * WTM;
-    for (int c = lane; c < WTN * CPP; c += 64) {
-      const int pl = c / CPP, part = c % CPP;
-      const int m = n0 + wn * WTN + pl;
-      const int co = co_w + part * EPC;
-      if (m >= a.M || co >= a.Cout) continue;
-      int pp;
-      const int bb = fdivmod(m, HWo, inv_hwo, pp);
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + pl * (WTM + SPAD) + part * EPC);
-      *reinterpret_cast<u32x4_t*>(reinterpret_cast<T*>(a.y) + bb * a.y_sb + pp * a.y_sp + co) = v;
-    }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int co = m0 + wm * WTM + i * 32 + g * 8 + hq * 4;
-      float sc[4], sh[4];
-      c_scale.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sc);
-      c_shift.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sh);
-      if (co >= a.Cout) continue;
-      const bool full4 = (co + 3 < a.Cout);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int m = n0 + wn * WTN + j * 32 + (lane & 31);
-        if (m >= a.M) continue;
-        int pp;
-        const int bb = fdivmod(m, HWo, inv_hwo, pp);
-        float v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float t = acc[i][j][g * 4 + r] * sc[r] + sh[r];
-          if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
-          v[r] = t;
-        }
-        if (a.res) {
-          const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + (int64_t)co * a.r_sc;
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (co + r < a.Cout) v[r] += E::to_f(rp[r * a.r_sc]);
-        }
-        const int64_t yo = bb * a.y_sb + pp * a.y_sp + (int64_t)co * a.y_sc;
-        if (a.y_f32) {
-          float* yp = reinterpret_cast<float*>(a.y) + yo;
-          if (a.y_sc == 1 && full4) {
-            *reinterpret_cast<f32x4_t*>(yp) = (f32x4_t){v[0], v[1], v[2], v[3]};
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (co + r < a.Cout) yp[r * a.y_sc] = v[r];
-          }
-        } else {
-          T* yp = reinterpret_cast<T*>(a.y) + yo;
-          if (sizeof(T) == 2 && a.y_sc == 1 && full4) {
-            *reinterpret_cast<u32x2_t*>(yp) = (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (co + r < a.Cout) yp[r * a.y_sc] = E::from_f(v[r]);
-          }
-        }
-      }
-    }
+  };
+  if constexpr (F8) epilogue(std::integral_constant<int, 2>{});
+  else if (a.act == VRS_ACT_SILU) epilogue(std::integral_constant<int, 1>{});
+  else epilogue(std::integral_constant<int, 0>{});
 }
 
 
