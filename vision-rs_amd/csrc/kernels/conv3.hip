@@ -76,6 +76,15 @@ __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, a.w_bytes);
   const uint32_t xrow = (uint32_t)a.x_pitch * 2u;   // bytes per input pixel
+  // folded-BN constants of the BM channels, in LDS for the epilogue (visible
+  // after the first stage's barrier): one 16-byte read per channel quad
+  __shared__ __attribute__((aligned(16))) float s_scale[BM];
+  __shared__ __attribute__((aligned(16))) float s_shift[BM];
+  for (int c = tid; c < BM; c += NT) {
+    const bool ok = m0 + c < a.Cout;
+    s_scale[c] = ok ? a.scale[m0 + c] : 0.f;
+    s_shift[c] = ok ? a.shift[m0 + c] : 0.f;
+  }
 
   // this thread's staging items (fixed over the chunks; the channel offset
   // moves): weight chunk -> (row, tap, 8-channel group); halo chunk ->
@@ -168,41 +177,45 @@ __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
   // epilogue: register g*4 + r of tile (i, j) is channel m0 + i*32 + g*8 +
   // hq*4 + r of pixel slot wave*64 + j*32 + l32
   __syncthreads();   // every wave is done with the stage buffers (reused for staging)
-  const ChanConst c_scale(a.scale, a.Cout), c_shift(a.shift, a.Cout);
-  const uint32_t hmask = upper_half_mask();
   const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res, a.res ? a.res_bytes : 0);
   bf16_t* stg = smem + wave * 64 * SROW;
+  // instantiated per activation: no per-value SiLU select
+  auto epilogue = [&](auto silu_on) {
+    constexpr bool SILU = decltype(silu_on)::value;
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int cl = i * 32 + g * 8 + hq * 4;
-      const int co = m0 + cl;
-      float sc[4], sh[4];
-      c_scale.quad(m0 + i * 32 + g * 8, hmask, sc);
-      c_shift.quad(m0 + i * 32 + g * 8, hmask, sh);
+      for (int g = 0; g < 4; ++g) {
+        const int cl = i * 32 + g * 8 + hq * 4;
+        const int co = m0 + cl;
+        const f32x4_t sc = *reinterpret_cast<const f32x4_t*>(&s_scale[cl]);
+        const f32x4_t sh = *reinterpret_cast<const f32x4_t*>(&s_shift[cl]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        float v[4];
+        for (int j = 0; j < TN; ++j) {
+          float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float t = acc[i][j][g * 4 + r] * sc[r] + sh[r];
-          if (a.act == VRS_ACT_SILU) t = silu_fast(t);
-          v[r] = t;
+          for (int r = 0; r < 4; ++r) {
+            float t = acc[i][j][g * 4 + r] * sc[r] + sh[r];
+            if constexpr (SILU) t = silu_fast(t);
+            v[r] = t;
+          }
+          if (a.res) {
+            const uint32_t ro = pv[j] && co < a.Cout
+                                    ? (uint32_t)((b * a.r_sb + (int64_t)py[j] * a.Wo * a.r_sp + (int64_t)px[j] * a.r_sp +
+                                                  co) * 2)
+                                    : kOOB;
+            const u32x2_t rv = __builtin_amdgcn_raw_buffer_load_b64(rr, ro, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              v[r] += __uint_as_float((r & 1) ? (rv[r >> 1] & 0xffff0000u) : (rv[r >> 1] << 16));
+          }
+          *reinterpret_cast<u32x2_t*>(stg + (j * 32 + l32) * SROW + cl) =
+              (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
-        if (a.res) {
-          const uint32_t ro = pv[j] && co < a.Cout
-                                  ? (uint32_t)((b * a.r_sb + (int64_t)py[j] * a.Wo * a.r_sp + (int64_t)px[j] * a.r_sp +
-                                                co) * 2)
-                                  : kOOB;
-          const u32x2_t rv = __builtin_amdgcn_raw_buffer_load_b64(rr, ro, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) v[r] += __uint_as_float((r & 1) ? (rv[r >> 1] & 0xffff0000u) : (rv[r >> 1] << 16));
-        }
-        *reinterpret_cast<u32x2_t*>(stg + (j * 32 + l32) * SROW + cl) =
-            (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
       }
-    }
+  };
+  if (a.act == VRS_ACT_SILU) epilogue(std::true_type{});
+  else epilogue(std::false_type{});
   __builtin_amdgcn_wave_barrier();   // this wave reads back only its own staging
   constexpr int CPP = BM / 8;        // 16-byte chunks per pixel
   for (int c = lane; c < 64 * CPP; c += 64) {
