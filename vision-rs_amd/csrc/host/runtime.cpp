@@ -312,10 +312,7 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
                   cs.stride, x.c);
     if (a.res || !a.stage || a.y_f32)
       return fail(VRS_EUNSUPPORTED, "conv: the weight-stationary tile takes no residual and stores 8-channel-aligned "
-                  "chunks of a bf16 NHWC view");
-    const int64_t yb = ((int64_t)(a.N - 1) * a.y_sb + (int64_t)ho * wo * a.y_sp) * 2;
-    if (yb >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: weight-stationary tile: output view exceeds 2 GiB");
-    a.y_bytes = (int32_t)yb;
+                  "chunks of a bf16 NHWC view under 2 GiB");
     a.tiles_m = (cout + bm - 1) / bm;
     a.tiles_n = (int32_t)((M + 63) / 64);
     snprintf(name, sizeof name, "vrs_conv1w_bf16_%d_c%d", bm, x.c);
@@ -346,9 +343,6 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
     if (a.res || !a.stage || a.y_f32 || a.K % (2 * bk) != 0)
       return fail(VRS_EUNSUPPORTED, "conv: persistent tile needs no residual, a staged bf16 output and an even "
                   "number of %d-deep K steps (K=%d)", bk, a.K);
-    const int64_t yb = ((int64_t)(a.N - 1) * a.y_sb + (int64_t)ho * wo * a.y_sp) * 2;
-    if (yb >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: persistent tile: output view exceeds 2 GiB");
-    a.y_bytes = (int32_t)yb;
     blocks = std::min<int64_t>(blocks, (int64_t)resident_wgs(f, threads) * (ctx->num_cu > 0 ? ctx->num_cu : 256));
   }
   out.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(threads), 0, a));
@@ -424,9 +418,14 @@ int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w
   a.y = const_cast<void*>(at(y, cs.dtype));
   a.y_sb = (int64_t)y.h * y.w * y.pitch; a.y_sp = y.pitch; a.y_sc = 1;
   a.y_f32 = 0;
-  // 16-byte chunks of 8 (bf16) or 4 (f32) channels must be whole and aligned
+  // 16-byte chunks of 8 (bf16) or 4 (f32) channels must be whole and aligned;
+  // the staged stores (and residual loads) address the views with 32-bit
+  // raw-buffer byte offsets: pixel m at m * pitch from the view's base
   const int chunk = cs.dtype == VRS_F32 ? 4 : 8;
-  a.stage = (y.c % 8 == 0 && y.c_off % chunk == 0 && y.pitch % chunk == 0) ? 1 : 0;
+  const int64_t yb = ((int64_t)y.n * y.h * y.w * y.pitch - y.c_off) * (int64_t)elt_size(cs.dtype);
+  a.y_bytes = yb < (1ll << 31) ? (int32_t)yb : 0;
+  a.stage = (y.c % 8 == 0 && y.c_off % chunk == 0 && y.pitch % chunk == 0 && a.y_bytes > 0 &&
+             (!res || a.res_bytes >= 0)) ? 1 : 0;
   return prep_dense(ctx, cs, x, w, scale, shift, y.c, y.h, y.w, a, out);
 }
 

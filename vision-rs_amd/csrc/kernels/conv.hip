@@ -466,6 +466,10 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
       // lanes write contiguous bytes of a pixel's NHWC row.
       constexpr int HW_ = WGM * WGN / 2;
       T* st = sbuf(wave / HW_) + (wave % HW_) * WTN * (WTM + SPAD);
+      // the host stages only views addressable with 32-bit byte offsets
+      // (y_bytes, res_bytes): pixel m of an NHWC view starts at m * pitch
+      const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, a.y_bytes);
+      const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res, a.res ? a.res_bytes : 0);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -485,12 +489,20 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
               if constexpr (MODE == 2) if (a.act == VRS_ACT_SILU) t = silu_t<T>(t);
               v[r] = t;
             }
-            if (a.res && m < a.M && co < a.Cout) {
-              int pp;
-              const int bb = fdivmod(m, HWo, inv_hwo, pp);
-              const T* rp = reinterpret_cast<const T*>(a.res) + bb * a.r_sb + pp * a.r_sp + co;
+            if (a.res) {   // NHWC view: pixel m at m * pitch (raw buffer, out-of-range lanes read 0)
+              const uint32_t ro = m < a.M && co < a.Cout
+                                      ? ((uint32_t)m * (uint32_t)a.r_sp + (uint32_t)co) * (uint32_t)sizeof(T)
+                                      : kOOB;
+              if constexpr (sizeof(T) == 2) {
+                const u32x2_t rv = __builtin_amdgcn_raw_buffer_load_b64(rr, ro, 0, 0);
 #pragma unroll
-              for (int r = 0; r < 4; ++r) v[r] += E::to_f(rp[r]);
+                for (int r = 0; r < 4; ++r)
+                  v[r] += __uint_as_float((r & 1) ? (rv[r >> 1] & 0xffff0000u) : (rv[r >> 1] << 16));
+              } else {
+                const u32x4_t rv = __builtin_amdgcn_raw_buffer_load_b128(rr, ro, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] += __uint_as_float(rv[r]);
+              }
             }
             T* sp = st + pl * (WTM + SPAD) + cl;
             if constexpr (sizeof(T) == 2) {
@@ -504,15 +516,18 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
       constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
       constexpr int CPP = WTM / EPC;            // chunks per pixel row
       const int co_w = m0 + wm * WTM;
-      for (int c = lane; c < WTN * CPP; c += 64) {
+      static_assert((WTN * CPP) % 64 == 0, "whole store rounds");
+#pragma unroll
+      for (int s = 0; s < WTN * CPP / 64; ++s) {
+        const int c = lane + s * 64;
         const int pl = c / CPP, part = c % CPP;
         const int m = n0 + wn * WTN + pl;
         const int co = co_w + part * EPC;
-        if (m >= a.M || co >= a.Cout) continue;
-        int pp;
-        const int bb = fdivmod(m, HWo, inv_hwo, pp);
         const u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + pl * (WTM + SPAD) + part * EPC);
-        *reinterpret_cast<u32x4_t*>(reinterpret_cast<T*>(a.y) + bb * a.y_sb + pp * a.y_sp + co) = v;
+        const uint32_t off = m < a.M && co < a.Cout
+                                 ? ((uint32_t)m * (uint32_t)a.y_sp + (uint32_t)co) * (uint32_t)sizeof(T)
+                                 : kOOB;
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, off, 0, 0);
       }
       return;
     }
@@ -759,9 +774,7 @@ __device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
       const int pl = c / CPP, part = c % CPP;
       const int m = n0 + wn * WTN + pl;
       const int co = m0 + wm * WTM + part * EPC;
-      int pp;
-      const int bb = fdivmod(m < a.M ? m : 0, HWo, inv_hwo, pp);
-      const uint32_t off = m < a.M && co < a.Cout ? (uint32_t)((bb * a.y_sb + pp * a.y_sp + co) * 2) : kOOB;
+      const uint32_t off = m < a.M && co < a.Cout ? ((uint32_t)m * (uint32_t)a.y_sp + (uint32_t)co) * 2u : kOOB;
       __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4_t*>(st + pl * SROW + part * EPC), ry, off,
                                              0, 0);
     }
