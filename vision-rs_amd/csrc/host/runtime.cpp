@@ -165,11 +165,17 @@ static int auto_tile(int cout, int cin, int64_t M, int dtype, int num_cu) {
   return VRS_TILE_128x128;
 }
 
-// Strip width of the halo-tiled 3x3 kernel for an image width (0: not usable):
-// the whole width up to 40 pixels, else 20 or 32 when they divide it (no
-// partial strip), else 32.
+// Strip width of the halo-tiled 3x3 kernel for an image width (0: not usable).
+// 32 or 16 when they divide the width: a 16-lane group of the MFMA operand
+// reads then never spans a strip row (a row change skips the two halo
+// columns and puts two lanes of the group on the same LDS banks), and the
+// strip's pixel count is a multiple of the 256-pixel run (no padded run) for
+// any height.  Else the whole width up to 40 pixels, else 20 when it divides
+// the width, else 32.
 static int h3_strip_width(int w) {
   if (w < 8) return 0;
+  if (w % 32 == 0) return 32;
+  if (w % 16 == 0) return 16;
   if (w <= 40) return w;
   if (w % 20 == 0) return 20;
   return 32;
