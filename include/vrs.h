@@ -386,7 +386,11 @@ int vrs_model_conv_info(const vrs_model* m, int32_t i, const char** prefix, int3
  * for convs that write a model output (out_idx >= 0, float32 element
  * (b, p, co) at output[out_idx] + out_off + b*out_sb + p*out_sp + co*out_sc). */
 typedef struct {
-  int32_t launch;          /* index among vrs_model_launch_name's launches, -1: none */
+  int32_t launch;          /* index among vrs_model_launch_name's launches of the conv's
+                              last launch (its output is complete after it; a conv
+                              whose last partial round of 256x256 tiles is split
+                              over K runs three: full tiles, K slices, fix-up),
+                              -1: none */
   int32_t k, stride, groups, act;
   int32_t plain;           /* conv_plain: bias, no BN */
   int32_t stem;            /* reads the NCHW float32 model input */

@@ -115,3 +115,49 @@ def test_conv_io_views():
             assert io.x.data is not None and io.y.data is not None and io.x.c == io.cin
     with pytest.raises(vrs.VrsError):
         m.conv_io(len(info))
+
+
+def test_leftover_tiles_run_on_the_128x128_tile():
+    """A 256x256-tile conv whose tiles leave the last round at most half full
+    (3x3/s2 256->256, 68 images of 64x64: 272 tiles on 256 CUs) runs its full
+    rounds on the 256x256 tile and the 16 leftover pixel tiles on the
+    128x128 k64 tile.  Both accumulate each output over K in the same step
+    order, so the result is bit-identical to the whole conv on the 128x128
+    tile; and within the bf16 bar of the oracle on the last two images (the
+    leftover tiles)."""
+    import torch
+    import oracle
+    from gpu_util import from_nhwc, rel_err, to_nhwc
+    TOL, FLOOR = 2e-2, 1e-1   # the bf16 single-kernel bar (elementwise, floor 0.1 * rms)
+    B, S = 68, 64
+    desc = vrs.block(vrs.BLOCK_CONV, 256, 256, k=3, s=2)
+    m = vrs.Model(ctx(), desc, B, S, S, vrs.BF16, 1e-3, autotune=False)
+    m.set_plan([vrs.TILE_256x256] * len(m.conv_info()))
+    P = _params(m)
+    m.load(P)
+    x = bf16_round(np.random.default_rng(5).standard_normal((B, 256, S, S)).astype(np.float32))
+    xd = dev(x)
+    out = m.forward(xd)[0]
+    torch.cuda.synchronize()
+    names = m.launch_names()
+    i256 = [k for k, n in enumerate(names) if n.endswith("vrs_conv_bf16_256x256_k64_a")]
+    assert len(i256) == 1 and names[i256[0] + 1].endswith("vrs_conv_bf16_128x128_k64_a"), names
+    io = m.conv_io(0)
+    assert io.launch == i256[0] + 1          # the conv is complete after the leftover launch
+    pre = m.conv_info()[0][0]
+    pfx = pre + "." if pre else ""
+    w = P[f"{pfx}conv.weight"]
+    sc, sh = oracle.bn_fold(P[f"{pfx}bn.weight"], P[f"{pfx}bn.bias"], P[f"{pfx}bn.running_mean"],
+                            P[f"{pfx}bn.running_var"], 1e-3)
+    xt = to_nhwc(x, vrs.BF16)
+    wd, scd, shd = dev(vrs.pack_conv_weight(w, 1, 256, vrs.BF16)), dev(sc), dev(sh)
+    y128 = torch.zeros((B, S // 2, S // 2, 256), dtype=torch.bfloat16, device="cuda")
+    y256 = torch.zeros_like(y128)
+    for yt, tile in ((y128, vrs.TILE_128x128), (y256, vrs.TILE_256x256)):
+        ctx().conv2d(vrs.nhwc(xt), wd, scd, shd, vrs.nhwc(yt), 3, 2, 1, vrs.ACT_SILU, None, vrs.BF16, tile=tile)
+    torch.cuda.synchronize()
+    assert torch.equal(y128.view(torch.int16), y256.view(torch.int16))
+    got = out.cpu().numpy().reshape(B, 256, S // 2, S // 2)
+    assert np.array_equal(got, from_nhwc(y128, 256, 0))
+    ref = oracle.affine_act(oracle.conv2d(x[-2:], w, 2, 1), sc, sh, 1)
+    assert rel_err(got[-2:], ref, FLOOR) < TOL

@@ -606,7 +606,9 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
                          view_of(m, c.y), ls);
         }
         if (rc) return rc;
-        conv_launch[st.conv] = (int)conv_first;
+        // the conv's output is complete after its last launch (a 256x256 conv
+        // with a partial last round: full rounds, then the leftover tiles)
+        conv_launch[st.conv] = (int)ls.size() - 1;
         for (size_t i = conv_first; i < ls.size(); ++i) labels.push_back(label + ":" + ls[i].name);
         flush_io();
         continue;
@@ -698,14 +700,17 @@ int autotune_tiles(vrs_model* m) {
       if (prep_conv(m->ctx, cs, view_of(m, c.x), pass ? c.w8 : c.w, pass ? c.scale8 : c.scale, c.shift,
                     c.has_res ? &r : nullptr, view_of(m, c.y), ls) != VRS_OK)
         continue;
-      if ((rc = run(ls[0], s))) break;
-      // best of three rounds of five launches: one slow round (a clock
-      // dip, another process) does not decide the tile
+      for (const Launch& l : ls)
+        if ((rc = run(l, s))) break;
+      if (rc) break;
+      // best of three rounds of five runs (every launch of the candidate):
+      // one slow round (a clock dip, another process) does not decide the tile
       float ms = 1e30f;
       for (int round = 0; round < 3 && !rc; ++round) {
         VRS_HIP(hipEventRecord(e0, s));
-        for (int it = 0; it < 5; ++it)
-          if ((rc = run(ls[0], s))) break;
+        for (int it = 0; it < 5 && !rc; ++it)
+          for (const Launch& l : ls)
+            if ((rc = run(l, s))) break;
         if (rc) break;
         VRS_HIP(hipEventRecord(e1, s));
         VRS_HIP(hipEventSynchronize(e1));

@@ -351,14 +351,44 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
                   "number of %d-deep K steps (K=%d)", bk, a.K);
     blocks = std::min<int64_t>(blocks, (int64_t)resident_wgs(f, threads) * (ctx->num_cu > 0 ? ctx->num_cu : 256));
   }
-  out.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(threads), 0, a));
   const double es = (double)elt_size(cs.dtype);
   const double cin = cs.cin_real > 0 ? cs.cin_real : x.c;
   const double kk = (double)cs.k * cs.k;
-  out.back().flops = 2.0 * (double)M * cout * kk * cin;
+  const double flops = 2.0 * (double)M * cout * kk * cin;
   const double cin_up = cs.up ? (double)cs.up->c : 0.0;   // read at a quarter of the pixels
-  out.back().bytes = (double)x.n * x.h * x.w * (cin - 0.75 * cin_up) * es + (double)cout * kk * cin * (f8 ? 1.0 : es) +
-                     (double)M * cout * (a.y_f32 ? 4.0 : es) + (a.res ? (double)M * cout * es : 0.0) + 8.0 * cout;
+  const double bytes = (double)x.n * x.h * x.w * (cin - 0.75 * cin_up) * es + (double)cout * kk * cin * (f8 ? 1.0 : es) +
+                       (double)M * cout * (a.y_f32 ? 4.0 : es) + (a.res ? (double)M * cout * es : 0.0) + 8.0 * cout;
+  // Partial last round of 256x256 tiles (one workgroup per CU): when the
+  // tiles leave a last round at most half full, the full rounds run on the
+  // 256x256 tile and the leftover pixel tiles on the 128x128 tile of the
+  // same 64-deep K order (four times the workgroups for the same work, two
+  // per CU: the round takes about a quarter of the time).  Same results: each
+  // output is one workgroup's accumulation over K in the same step order.
+  if ((tile & 0xff) == VRS_TILE_256x256 && !(tile & VRS_TILE_PERSIST) && !f8 && !cs.up &&
+      cs.dtype == VRS_BF16 && a.K % 64 == 0 && cout % 256 == 0) {
+    const int64_t G = (int64_t)resident_wgs(f, threads) * (ctx->num_cu > 0 ? ctx->num_cu : 256);
+    const int64_t R = blocks % G;
+    if (blocks > G && R > 0 && 2 * R <= G && R % a.tiles_m == 0) {
+      hipFunction_t fr;
+      if ((rc = get_fn(ctx, "vrs_conv_bf16_128x128_k64_a", &fr))) return rc;
+      const double share = (double)R / (double)blocks;
+      out.push_back(make_launch(name, f, dim3((unsigned)(blocks - R)), dim3(threads), 0, a));
+      out.back().flops = flops * (1.0 - share);
+      out.back().bytes = bytes * (1.0 - share);
+      vrs_conv_args b = a;
+      b.tiles_m = cout / 128;
+      b.n_tile0 = (int32_t)((blocks - R) / a.tiles_m * 2);   // in 128-pixel tiles
+      b.tiles_n = (int32_t)((M + 127) / 128);
+      const int64_t rb = (int64_t)b.tiles_m * (b.tiles_n - b.n_tile0);
+      out.push_back(make_launch("vrs_conv_bf16_128x128_k64_a", fr, dim3((unsigned)rb), dim3(256), 0, b));
+      out.back().flops = flops * share;
+      out.back().bytes = bytes * share;
+      return VRS_OK;
+    }
+  }
+  out.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(threads), 0, a));
+  out.back().flops = flops;
+  out.back().bytes = bytes;
   return VRS_OK;
 }
 

@@ -60,6 +60,10 @@ typedef struct {
    * residual loads */
   int32_t h3_tw, h3_strips, h3_chunks;
   int32_t res_bytes;
+  /* first pixel tile of this launch (tiled kernels: tile_n = n_tile0 +
+   * logical / tiles_m); non-zero for the launch that takes the pixel tiles
+   * left over by a larger tile's full rounds */
+  int32_t n_tile0;
 } vrs_conv_args;
 
 /* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the

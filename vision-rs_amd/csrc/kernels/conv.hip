@@ -112,7 +112,7 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   static_assert(WGM * WGN == 4 || WGM * WGN == 8, "4 or 8 waves");
 
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int tile_m = logical % a.tiles_m, tile_n = logical / a.tiles_m;
+  const int tile_m = logical % a.tiles_m, tile_n = a.n_tile0 + logical / a.tiles_m;
   const int m0 = tile_m * BM;   // first output channel
   const int n0 = tile_n * BN;   // first output pixel
   // folded-BN constants of the tile's BM channels, staged in LDS for the
