@@ -6,25 +6,29 @@
 // tile per filter tap, so every input pixel is fetched and written to LDS
 // nine times.  Here a workgroup owns BM output channels x 256 output pixels
 // -- a run of 256 consecutive pixels of one vertical strip of the image,
-// TW pixels wide -- and per 32-channel chunk of the input stages
+// TW pixels wide -- and per 16-channel chunk of the input stages
 //   * the strip rows the run touches plus a one-pixel halo: at most
-//     (256/TW + 3) x (TW + 2) positions x 32 channels, 16-byte chunks
-//     XOR-swizzled by position (conflict-free 16-byte fragment reads), and
-//   * the chunk's weights for all nine taps (BM x 9 x 32, rows padded by
+//     (256/TW + 3) x (TW + 2) positions x 16 channels, the two 16-byte
+//     halves of a position swapped on every other group of 8 positions
+//     (16 consecutive positions -- one 16-lane group of an operand read --
+//     then cover the 64 banks once), and
+//   * the chunk's weights for all nine taps (BM x 9 x 16, rows padded by
 //     16 bytes),
-// then runs all nine taps x two 16-deep k slices from LDS: the B fragment of
-// tap (ky, kx) for output pixel (y, x) is halo position (y - y_first + ky) *
-// (TW + 2) + x + kx.  One LDS stage per chunk (~65 KB, two workgroups per CU);
-// the next chunk's global loads are in flight during the MFMAs.  4 waves, each
-// BM channels x 64 pixels (32x32x16 bf16 MFMAs).  Epilogue as the implicit-GEMM
-// kernels: scale*acc + shift, SiLU, residual, staged through LDS for 16-byte
-// NHWC stores.
+// then runs the nine taps' MFMAs from LDS: the B fragment of tap (ky, kx)
+// for output pixel (y, x) is halo position (y - y_first + ky) * (TW + 2) +
+// x + kx.  Two LDS stages (~33 KB each, two workgroups per CU) and two
+// register sets: chunk c+2's global loads are issued before chunk c's MFMAs
+// and written to LDS after chunk c+1's, so loads have two chunks' MFMAs to
+// land and each chunk costs one barrier.  4 waves, each BM channels x 64
+// pixels (32x32x16 bf16 MFMAs).  Epilogue as the implicit-GEMM kernels:
+// scale*acc + shift, SiLU, residual, staged through LDS for 16-byte NHWC
+// stores.
 #include "common.h"
 
 namespace {
 
 constexpr int H3_NP = 256;                   // output pixels per workgroup
-constexpr int H3_CK = 32;                    // input channels per stage
+constexpr int H3_CK = 16;                    // input channels per stage
 constexpr int H3_TW_MIN = 8, H3_TW_MAX = 40; // strip widths the host may choose
 // halo positions: rows (256/TW + 3) x cols (TW + 2), largest over TW in [8, 40]
 constexpr int h3_hpos_max() {
@@ -36,9 +40,10 @@ constexpr int h3_hpos_max() {
   return m;
 }
 constexpr int H3_HPOS = h3_hpos_max();
-constexpr int H3_WROW = 9 * H3_CK + 8;       // weight row (elements): 9 taps x 32 + 16-byte pad
+constexpr int H3_WROW = 9 * H3_CK + 8;       // weight row (elements): 9 taps x 16 + 16-byte pad
 
-__device__ __forceinline__ int h3_swz(int pos, int chunk) { return pos * H3_CK + ((chunk ^ ((pos >> 2) & 3)) << 3); }
+// element offset of 16-byte half `half` of halo position `pos`
+__device__ __forceinline__ int h3_swz(int pos, int half) { return pos * H3_CK + ((half ^ ((pos >> 3) & 1)) << 3); }
 
 template <int BM>
 __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
@@ -47,15 +52,13 @@ __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
   constexpr int NT = 256;
   constexpr int TM = BM / 32, TN = 2;        // wave tile BM x 64
   constexpr int SW_ELEMS = BM * H3_WROW, SH_ELEMS = H3_HPOS * H3_CK;
+  constexpr int STAGE = SW_ELEMS + SH_ELEMS;  // one LDS stage (elements)
   constexpr int SROW = BM + 8;               // epilogue staging row (channels + pad)
   constexpr int ST_ELEMS = 4 * 64 * SROW;
-  constexpr int MAIN = SW_ELEMS + SH_ELEMS > ST_ELEMS ? SW_ELEMS + SH_ELEMS : ST_ELEMS;
+  constexpr int MAIN = 2 * STAGE > ST_ELEMS ? 2 * STAGE : ST_ELEMS;
   __shared__ __attribute__((aligned(16))) bf16_t smem[MAIN];
-  bf16_t* sW = smem;
-  bf16_t* sH = smem + SW_ELEMS;
-  constexpr int WI = (BM * 9 * 4 + NT - 1) / NT;          // weight chunks per thread
-  constexpr int HI = (H3_HPOS * 4 + NT - 1) / NT;         // halo chunks per thread
-
+  constexpr int WI = (BM * 18 + NT - 1) / NT;             // weight chunks per thread (9 taps x 2 halves)
+  constexpr int HI = (H3_HPOS * 2 + NT - 1) / NT;         // halo chunks per thread
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hq = lane >> 5;
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -94,36 +97,41 @@ __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
 #pragma unroll
   for (int i = 0; i < WI; ++i) {
     const int it = tid + i * NT;
-    const int row = it / 36, r36 = it % 36, tap = r36 >> 2, g = r36 & 3;
+    const int row = it / 18, r18 = it % 18, tap = r18 >> 1, g = r18 & 1;
     const int co = m0 + row;
-    const bool ok = it < BM * 36 && co < a.Cout;
+    const bool ok = it < BM * 18 && co < a.Cout;
     w_off[i] = ok ? (uint32_t)(((co * 9 + tap) * a.Cin + g * 8) * 2) : kOOB;
-    w_lds[i] = it < BM * 36 ? row * H3_WROW + tap * H3_CK + g * 8 : -1;
+    w_lds[i] = it < BM * 18 ? row * H3_WROW + tap * H3_CK + g * 8 : -1;
   }
 #pragma unroll
   for (int i = 0; i < HI; ++i) {
     const int it = tid + i * NT;
-    const int pos = it >> 2, g = it & 3;
+    const int pos = it >> 1, g = it & 1;
     const int hr = pos / HCW, hc = pos - hr * HCW;
     const int yy = y_first + hr, xx = x0 - 1 + hc;
     const bool ok = pos < hpos && (unsigned)yy < (unsigned)a.H && (unsigned)xx < (unsigned)a.W;
     h_off[i] = ok ? (uint32_t)((b * a.H + yy) * a.W + xx) * xrow + (uint32_t)(g * 16) : kOOB;
     h_lds[i] = pos < hpos ? h3_swz(pos, g) : -1;
   }
-  u32x4_t wreg[WI], hreg[HI];
-  auto load_stage = [&](int ci0) {
+  // chunk c lives in register set c & 1 between its loads and its LDS write,
+  // and in LDS stage c & 1 while its MFMAs run
+  u32x4_t wreg0[WI], hreg0[HI], wreg1[WI], hreg1[HI];
+  auto load_stage = [&](int c, u32x4_t (&wr)[WI], u32x4_t (&hr)[HI]) {
+    const uint32_t ci0 = (uint32_t)(c * H3_CK * 2);
 #pragma unroll
-    for (int i = 0; i < WI; ++i) wreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[i], ci0 * 2, 0);
+    for (int i = 0; i < WI; ++i) wr[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[i], ci0, 0);
 #pragma unroll
-    for (int i = 0; i < HI; ++i) hreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, h_off[i], ci0 * 2, 0);
+    for (int i = 0; i < HI; ++i) hr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, h_off[i], ci0, 0);
   };
-  auto store_stage = [&]() {
+  auto store_stage = [&](int buf, const u32x4_t (&wr)[WI], const u32x4_t (&hr)[HI]) {
+    bf16_t* sW = smem + buf * STAGE;
+    bf16_t* sH = sW + SW_ELEMS;
 #pragma unroll
     for (int i = 0; i < WI; ++i)
-      if (w_lds[i] >= 0) *reinterpret_cast<u32x4_t*>(sW + w_lds[i]) = wreg[i];
+      if (w_lds[i] >= 0) *reinterpret_cast<u32x4_t*>(sW + w_lds[i]) = wr[i];
 #pragma unroll
     for (int i = 0; i < HI; ++i)
-      if (h_lds[i] >= 0) *reinterpret_cast<u32x4_t*>(sH + h_lds[i]) = hreg[i];
+      if (h_lds[i] >= 0) *reinterpret_cast<u32x4_t*>(sH + h_lds[i]) = hr[i];
   };
 
   // this lane's output pixels (B fragment columns): slot wave*64 + j*32 + l32
@@ -148,35 +156,61 @@ __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nst = a.Cin / H3_CK;
-  load_stage(0);
-  for (int st = 0; st < nst; ++st) {
-    if (st > 0) __syncthreads();   // the previous chunk's fragments have been read
-    store_stage();
-    __syncthreads();
-    if (st + 1 < nst) load_stage((st + 1) * H3_CK);   // in flight during the MFMAs
-#pragma unroll
-    for (int tap = 0; tap < 9; ++tap) {
+  const int nst = a.Cin / H3_CK;   // >= 2 (host: Cin % 32 == 0)
+  // one tap's operands are read while the previous tap's MFMAs run (two
+  // fragment register sets, the order pinned with scheduling groups)
+  auto compute = [&](int buf) {
+    const bf16_t* sW = smem + buf * STAGE;
+    const bf16_t* sH = sW + SW_ELEMS;
+    G fa[2][TM], fb[2][TN];
+    auto read_tap = [&](int tap, G (&ra)[TM], G (&rb)[TN]) {
       const int toff = (tap / 3) * HCW + (tap % 3);
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        G fa[TM], fb[TN];
+      for (int i = 0; i < TM; ++i) ra[i] = E::load(sW + (i * 32 + l32) * H3_WROW + tap * H3_CK + hq * 8);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          fa[i] = E::load(sW + (i * 32 + l32) * H3_WROW + tap * H3_CK + kk * 16 + hq * 8);
+      for (int j = 0; j < TN; ++j) rb[j] = E::load(sH + h3_swz(hbase[j] + toff, hq));
+    };
+    read_tap(0, fa[0], fb[0]);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) fb[j] = E::load(sH + h3_swz(hbase[j] + toff, kk * 2 + hq));
+    for (int tap = 0; tap < 9; ++tap) {
+      if (tap + 1 < 9) read_tap(tap + 1, fa[(tap + 1) & 1], fb[(tap + 1) & 1]);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32_k16(fa[i], fb[j], acc[i][j]);
-      }
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32_k16(fa[tap & 1][i], fb[tap & 1][j], acc[i][j]);
     }
+    // schedule: tap 0's reads, then per tap the next tap's reads ahead of
+    // this tap's MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+      if (tap + 1 < 9) __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+    }
+  };
+  // chunk c: loads of chunk c+2 go out first, then chunk c's MFMAs, then
+  // chunk c+1 (loaded during chunk c-1) is written to the other stage -- it
+  // was last read by chunk c-1, before the previous barrier -- and one
+  // barrier publishes it
+  auto step = [&](int c, u32x4_t (&wl)[WI], u32x4_t (&hl)[HI], const u32x4_t (&ws)[WI], const u32x4_t (&hs)[HI]) {
+    if (c + 2 < nst) load_stage(c + 2, wl, hl);
+    compute(c & 1);
+    if (c + 1 < nst) store_stage((c + 1) & 1, ws, hs);
+    __syncthreads();
+  };
+  load_stage(0, wreg0, hreg0);
+  load_stage(1, wreg1, hreg1);
+  store_stage(0, wreg0, hreg0);
+  __syncthreads();
+  for (int c = 0; c < nst; c += 2) {
+    step(c, wreg0, hreg0, wreg1, hreg1);
+    if (c + 1 < nst) step(c + 1, wreg1, hreg1, wreg0, hreg0);
   }
 
   // epilogue: register g*4 + r of tile (i, j) is channel m0 + i*32 + g*8 +
   // hq*4 + r of pixel slot wave*64 + j*32 + l32
-  __syncthreads();   // every wave is done with the stage buffers (reused for staging)
+  // (the last chunk's barrier: every wave is done with the stage buffers,
+  // which the staging reuses)
   const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res, a.res ? a.res_bytes : 0);
   bf16_t* stg = smem + wave * 64 * SROW;
   // instantiated per activation: no per-value SiLU select
