@@ -101,6 +101,9 @@ typedef struct {
  * of whole input pixel rows through it. */
 #define VRS_TILE_W1_256 8
 #define VRS_TILE_W1_128 9
+/* 64x64 tile (bf16, Cin % 32 == 0; 4 waves of 32x32): four times the
+ * workgroups of 128x128 for the small maps whose larger tiles leave CUs idle */
+#define VRS_TILE_64x64 10
 #define VRS_TILE_K32 0x100
 /* OR VRS_TILE_PERSIST: persistent grid (resident workgroups loop over the
  * tiles with one continuous load stream) for memory-bound shapes; bf16,

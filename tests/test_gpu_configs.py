@@ -44,7 +44,7 @@ def dense_tiles():
     """Every dense-conv tile code the C ABI accepts in some configuration; the
     ones a shape does not support are rejected with VRS_EUNSUPPORTED."""
     base = [vrs.TILE_128x128, vrs.TILE_256x128, vrs.TILE_128x256, vrs.TILE_64x256, vrs.TILE_32x256,
-            vrs.TILE_256x256]
+            vrs.TILE_256x256, vrs.TILE_64x64]
     out = [vrs.TILE_AUTO, vrs.TILE_H3]
     for t in base:
         out += [t, t | vrs.TILE_K32, t | vrs.TILE_PERSIST, t | vrs.TILE_K32 | vrs.TILE_PERSIST]

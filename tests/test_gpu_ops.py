@@ -134,12 +134,13 @@ def test_conv2d_random(case, dtype):
     assert torch.all(rest == 7.0)
 
 
-TILES_BF16 = [vrs.TILE_128x128, vrs.TILE_256x128, vrs.TILE_128x256, vrs.TILE_64x256, vrs.TILE_32x256]
+TILES_BF16 = [vrs.TILE_128x128, vrs.TILE_256x128, vrs.TILE_128x256, vrs.TILE_64x256, vrs.TILE_32x256,
+              vrs.TILE_64x64]
 TILES_F32 = [vrs.TILE_128x128, vrs.TILE_64x256, vrs.TILE_32x256]
 
 
 @pytest.mark.parametrize("dtype,tile", [(vrs.BF16, t) for t in TILES_BF16 + [vrs.TILE_256x256]] +
-                         [(vrs.BF16, t | vrs.TILE_K32) for t in TILES_BF16[:4]] +
+                         [(vrs.BF16, t | vrs.TILE_K32) for t in TILES_BF16[:4] + [vrs.TILE_64x64]] +
                          [(vrs.F32, t) for t in TILES_F32])
 @pytest.mark.parametrize("yview", [(264, 8), (260, 4)])  # staged (16-byte chunks) / direct epilogue
 def test_conv2d_every_tile(dtype, tile, yview):

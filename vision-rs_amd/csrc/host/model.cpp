@@ -680,7 +680,9 @@ int autotune_tiles(vrs_model* m) {
     if (c.dw || c.stem || c.out_idx >= 0 || c.y.buf < 0) continue;
     if (pass == 0 && c.f8 && m->autotune == 2) continue;   // fp8 forced: no bf16 candidates
     const int dt = pass ? VRS_FP8 : act_dt(m);
-    const std::vector<int> cand = conv_tile_candidates(c.cout, c.cin, dt, c.k, c.s, c.has_up ? 0 : m->bufs[c.x.buf].w);
+    const std::vector<int> cand =
+        conv_tile_candidates(c.cout, c.cin, dt, c.k, c.s, c.has_up ? 0 : m->bufs[c.x.buf].w,
+                             (int64_t)m->batch * m->bufs[c.y.buf].h * m->bufs[c.y.buf].w, m->ctx->num_cu);
     if (cand.size() < 2) continue;
     ConvSpec cs;
     cs.k = c.k; cs.stride = c.s; cs.dtype = dt; cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;

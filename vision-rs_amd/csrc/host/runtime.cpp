@@ -94,6 +94,7 @@ static const TileInfo kTiles[] = {
     {VRS_TILE_128x256, 128, 256, "128x256", false, true, 256}, {VRS_TILE_64x256, 64, 256, "64x256", true, true, 256},
     {VRS_TILE_32x256, 32, 256, "32x256", true, true, 256},
     {VRS_TILE_256x256, 256, 256, "256x256", false, false, 512},  // 64-deep K steps only
+    {VRS_TILE_64x64, 64, 64, "64x64", false, true, 256},          // bf16, Cin % 32 == 0
 };
 
 static const TileInfo* tile_info(int code) {
@@ -119,7 +120,8 @@ static int tile_kernel(int code, int cin, int dtype, bool up, char* name, size_t
   }
   if (dtype == VRS_FP8) {
     if (cin % 64 != 0) return fail(VRS_EUNSUPPORTED, "conv fp8: needs Cin %% 64 == 0 (Cin=%d)", cin);
-    if (t->code == VRS_TILE_32x256) return fail(VRS_EUNSUPPORTED, "conv fp8: tile %s not built", t->tag);
+    if (t->code == VRS_TILE_32x256 || t->code == VRS_TILE_64x64)
+      return fail(VRS_EUNSUPPORTED, "conv fp8: tile %s not built", t->tag);
     snprintf(name, n, "vrs_conv_fp8_%s_k64_a", t->tag);
     *bm = t->bm;
     *bn = t->bn;
@@ -181,7 +183,8 @@ static int h3_strip_width(int w) {
   return 32;
 }
 
-std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int stride, int w) {
+std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int stride, int w, int64_t m,
+                                      int num_cu) {
   std::vector<int> c;
   if (dtype == VRS_BF16 && k == 3 && stride == 1 && cin % 32 == 0 && h3_strip_width(w) > 0) c.push_back(VRS_TILE_H3);
   if (dtype == VRS_BF16 && k == 1 && stride == 1 && cin % 64 == 0 && cin <= 256 && w > 0) {
@@ -203,6 +206,10 @@ std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int s
     if (g && t.code != VRS_TILE_128x128 && t.code != VRS_TILE_64x256 && t.code != VRS_TILE_32x256) continue;
     if (t.bm >= 2 * 128 && cout <= 128) continue;   // mostly empty rows
     if (t.bm <= 64 && cout > 4 * t.bm) continue;     // too many passes over the input
+    if (t.code == VRS_TILE_64x64) {   // only where 128x128 leaves the chip under-filled
+      const int64_t b128 = (int64_t)((cout + 127) / 128) * ((m + 127) / 128);
+      if (g || (m > 0 && b128 >= 2ll * (num_cu > 0 ? num_cu : 256))) continue;
+    }
     if (!t.k32) {  // 64-deep only
       if (dtype == VRS_BF16 && cin % 64 == 0 && cout >= t.bm) c.push_back(t.code);
       continue;

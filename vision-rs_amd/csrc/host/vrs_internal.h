@@ -112,7 +112,8 @@ int prep_absmax(vrs_ctx* ctx, const vrs_nhwc& x, unsigned* out, std::vector<Laun
 // float -> e4m3 (OCP, max 448) with round-to-nearest-even; |v| > 448 saturates
 uint8_t f32_to_e4m3(float v);
 // Dense conv tiles worth trying for a layer (autotuning candidates).
-std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int stride, int w);
+// m: output pixels (0: unknown), num_cu: the device's CUs
+std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int stride, int w, int64_t m, int num_cu);
 int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
               const float* shift, const vrs_nhwc* res, const vrs_nhwc& y, std::vector<Launch>& out);
 // Dense conv storing float32 into a strided (flat) output: element (b, p, co)

@@ -792,8 +792,8 @@ __device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
   }
 
 // Kernel names: vrs_conv_<type>_<BM>x<BN>_k<BK>_<a|g>.  Wave tiles: 128x128
-// and 64x256 -> 64x64, 256x128 -> 128x64, 128x256 -> 64x128, 32x256 -> 32x64
-// (in 32x32 MFMA tiles).
+// and 64x256 -> 64x64, 256x128 -> 128x64, 128x256 -> 64x128, 32x256 -> 32x64,
+// 64x64 -> 32x32 (in 32x32 MFMA tiles).
 VRS_CONV_KERNEL(vrs_conv_bf16_128x128_k32_a, bf16_t, 128, 128, 32, 2, 2, true)
 VRS_CONV_KERNEL(vrs_conv_bf16_128x128_k32_g, bf16_t, 128, 128, 32, 2, 2, false)
 VRS_CONV_KERNEL(vrs_conv_bf16_128x128_k64_a, bf16_t, 128, 128, 64, 2, 2, true)
@@ -805,6 +805,9 @@ VRS_CONV_KERNEL(vrs_conv_bf16_64x256_k32_a, bf16_t, 64, 256, 32, 1, 4, true)
 VRS_CONV_KERNEL(vrs_conv_bf16_64x256_k32_g, bf16_t, 64, 256, 32, 1, 4, false)
 VRS_CONV_KERNEL(vrs_conv_bf16_64x256_k64_a, bf16_t, 64, 256, 64, 1, 4, true)
 VRS_CONV_KERNEL(vrs_conv_bf16_32x256_k32_a, bf16_t, 32, 256, 32, 1, 4, true)
+// 64x64 (wave tiles 32x32): small maps, where the larger tiles leave CUs idle
+VRS_CONV_KERNEL(vrs_conv_bf16_64x64_k32_a, bf16_t, 64, 64, 32, 2, 2, true)
+VRS_CONV_KERNEL(vrs_conv_bf16_64x64_k64_a, bf16_t, 64, 64, 64, 2, 2, true)
 VRS_CONV_KERNEL(vrs_conv_bf16_32x256_k32_g, bf16_t, 32, 256, 32, 1, 4, false)
 // 8 waves (512 threads), wave tile 128x64: half the global loads per MFMA of
 // the 4-wave tiles, for the large layers with Cout >= 256 and Cin % 64 == 0.

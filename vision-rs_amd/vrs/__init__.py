@@ -34,6 +34,7 @@ TILE_PERSIST = 0x200
 TILE_H3 = 7   # halo-tiled 3x3 stride-1 kernel (bf16)
 TILE_W1_256 = 8   # weight-stationary 1x1 kernels (bf16): 256- or 128-channel weight slice in LDS
 TILE_W1_128 = 9
+TILE_64x64 = 10   # bf16: small maps (four times the workgroups of 128x128)
 
 ERRORS = {-1: "EINVAL", -2: "EBADSHAPE", -3: "EUNSUPPORTED", -4: "ENOMODULE", -5: "EHIP", -6: "ENOTFOUND",
           -7: "ESTATE"}
