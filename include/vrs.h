@@ -92,7 +92,7 @@ typedef struct {
 /* Halo-tiled 3x3 stride-1 kernel (bf16, Cin % 32 == 0, width >= 8): 64 (or,
  * for Cout <= 32, 32) output channels x 256 output pixels of one image strip
  * per workgroup, the strip rows plus a one-pixel halo staged in LDS once per
- * 32 input channels and read for all nine taps. */
+ * 16 input channels and read for all nine taps. */
 #define VRS_TILE_H3 7
 /* Weight-stationary 1x1 kernels (bf16, k = 1, stride 1, Cin a multiple of 64
  * up to 192 (_256) or 256 (_128), no residual, output channel offset/pitch/
@@ -104,6 +104,10 @@ typedef struct {
 /* 64x64 tile (bf16, Cin % 32 == 0; 4 waves of 32x32): four times the
  * workgroups of 128x128 for the small maps whose larger tiles leave CUs idle */
 #define VRS_TILE_64x64 10
+/* Model plans only: the conv right after a 64-channel stem (3x3/s2, 64 -> 128,
+ * BN + SiLU, bf16; it must be the stem output's only reader) runs fused with
+ * the stem as one vrs_conv_stem_pair launch. */
+#define VRS_TILE_STEM_PAIR 11
 #define VRS_TILE_K32 0x100
 /* OR VRS_TILE_PERSIST: persistent grid (resident workgroups loop over the
  * tiles with one continuous load stream) for memory-bound shapes; bf16,
@@ -167,6 +171,21 @@ int64_t vrs_pack_stem_weight(const float* w_oihw, int32_t cout, int32_t dtype, v
 int vrs_conv_stem(vrs_ctx* ctx, const vrs_conv_desc* d, const float* x_nchw, int32_t n, int32_t c, int32_t h,
                   int32_t w, const void* w_packed, const float* scale, const float* shift, const vrs_nhwc* y,
                   void* stream);
+
+/* The stem pair model.0 + model.1 (yolo26/mod.rs:126-195: conv(3, 64, 3, 2)
+ * then conv(64, 128, 3, 2), each blocks/conv.rs:31-46) in one kernel, for
+ * the m and l widths in bf16 with SiLU on both: replaces vrs_conv_stem +
+ * vrs_conv2d for these two layers, and the 64-channel stem map (the
+ * network's largest activation) is never written to memory.
+ *   y = silu(scale1 * conv3x3s2(s, w1) + shift1),
+ *   s = bf16(silu(scale0 * conv3x3s2(x, w0) + shift0))
+ * with the same results as the two calls.  w0 from vrs_pack_stem_weight
+ * (Cout 64), w1 from vrs_pack_conv_weight ([128][3][3][64]); y: 128 channels,
+ * image width a multiple of 4. */
+int vrs_conv_stem_pair(vrs_ctx* ctx, const vrs_conv_desc* d0, const vrs_conv_desc* d1, const float* x_nchw,
+                       int32_t n, int32_t c, int32_t h, int32_t w, const void* w0_packed, const float* scale0,
+                       const float* shift0, const void* w1_packed, const float* scale1, const float* shift1,
+                       const vrs_nhwc* y, void* stream);
 
 /* NCHW float32 -> NHWC dtype, zero-padding channels C..y->c-1 (C <= y->c < C+8). */
 int vrs_pack_input(vrs_ctx* ctx, const float* x_nchw, int32_t n, int32_t c, int32_t h, int32_t w,
@@ -387,16 +406,20 @@ int vrs_model_conv_info(const vrs_model* m, int32_t i, const char** prefix, int3
  * vrs_model_finalize; `launch` after the first forward/capture.  Views whose
  * data is NULL are absent: x for the stem (which reads the model input), y
  * for convs that write a model output (out_idx >= 0, float32 element
- * (b, p, co) at output[out_idx] + out_off + b*out_sb + p*out_sp + co*out_sc). */
+ * (b, p, co) at output[out_idx] + out_off + b*out_sb + p*out_sp + co*out_sc).
+ * A stem pair (VRS_TILE_STEM_PAIR): the stem has no launch (-1) and no y; the
+ * conv after it has stem = 2 and no x (its input is the stem of the model
+ * input, computed on chip). */
 typedef struct {
   int32_t launch;          /* index among vrs_model_launch_name's launches of the conv's
-                              last launch (its output is complete after it; a conv
-                              whose last partial round of 256x256 tiles is split
-                              over K runs three: full tiles, K slices, fix-up),
-                              -1: none */
+                              last launch (its output is complete after it; a
+                              256x256 conv whose last round of tiles is at most
+                              half full runs two: the full rounds, then the
+                              leftover tiles on the 128x128 tile), -1: none */
   int32_t k, stride, groups, act;
   int32_t plain;           /* conv_plain: bias, no BN */
-  int32_t stem;            /* reads the NCHW float32 model input */
+  int32_t stem;            /* 1: reads the NCHW float32 model input; 2: reads it
+                              through the stem before it (a stem pair) */
   int32_t fp8;             /* runs on the fp8 MFMA (input quantised with in_scale) */
   float in_scale;
   int32_t dtype;           /* element type of x, y, res, up */

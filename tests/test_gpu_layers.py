@@ -166,6 +166,7 @@ def test_yolo26m_bs64_640_layer_by_layer(dtype):
     for i, (pre, f8, sc) in enumerate(info):
         io = m.conv_io(i)
         io.prefix = pre
+        io.index = i
         ios.append(io)
     if dtype == vrs.FP8:
         n_f8 = sum(io.fp8 for io in ios)
@@ -178,7 +179,9 @@ def test_yolo26m_bs64_640_layer_by_layer(dtype):
     for li in range(n):
         io = by_launch.get(li)
         if io is not None:
-            if io.stem:
+            if io.stem == 2:   # stem pair: the input is the stem of the image, computed on chip
+                xin = bf16_round(conv_reference(ios[io.index - 1], P, 1e-3, x[list(IMAGES)], None))
+            elif io.stem:
                 xin = x[list(IMAGES)]
             else:
                 xin = read_view(io.x, io.dtype, IMAGES)

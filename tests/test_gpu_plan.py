@@ -161,3 +161,54 @@ def test_leftover_tiles_run_on_the_128x128_tile():
     assert np.array_equal(got, from_nhwc(y128, 256, 0))
     ref = oracle.affine_act(oracle.conv2d(x[-2:], w, 2, 1), sc, sh, 1)
     assert rel_err(got[-2:], ref, FLOOR) < TOL
+
+
+def test_stem_pair_plan():
+    """VRS_TILE_STEM_PAIR on model.1: one launch replaces model.0 + model.1,
+    bit-identical to the unfused pair on the 128x128 tile (the same MFMA K
+    order); conv_io reports the stem as launch-less and model.1 as reading the
+    model input (stem = 2).  The entry is refused on any other conv and on a
+    width whose stem is not 64 channels (YOLO26n)."""
+    import torch
+    B, S = 2, 96
+    names = [pre for pre, _, _ in _yolo(B, S, vrs.BF16, autotune=False).conv_info()]
+    i1 = names.index("model.1")
+    plans = {}
+    for tile in (vrs.TILE_STEM_PAIR, vrs.TILE_128x128):
+        plan = [0] * len(names)
+        plan[i1] = tile
+        plans[tile] = plan
+    x = dev(np.random.default_rng(9).uniform(0, 1, (B, 3, S, S)).astype(np.float32))
+    outs = {}
+    for tile, plan in plans.items():
+        m = _yolo(B, S, vrs.BF16, autotune=False)
+        m.set_plan(plan)
+        m.load(_params(m))
+        outs[tile] = [o.clone() for o in m.forward(x)]
+        torch.cuda.synchronize()
+        launches = m.launch_names()
+        io0, io1 = m.conv_io(names.index("model.0")), m.conv_io(i1)
+        if tile == vrs.TILE_STEM_PAIR:
+            assert m.get_plan()[i1] == vrs.TILE_STEM_PAIR
+            assert io0.launch == -1 and io0.y.data is None
+            assert io1.stem == 2 and io1.x.data is None and io1.y.data is not None
+            assert launches[io1.launch] == "model.1:vrs_stem_pair_bf16"
+            assert not any(l.startswith("model.0:") for l in launches)
+        else:
+            assert io0.launch >= 0 and io1.stem == 0
+    for a, b in zip(outs[vrs.TILE_STEM_PAIR], outs[vrs.TILE_128x128]):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    m = _yolo(1, 128, vrs.BF16, autotune=False)
+    bad = [0] * len(names)
+    bad[names.index("model.3")] = vrs.TILE_STEM_PAIR
+    m.set_plan(bad)
+    with pytest.raises(vrs.VrsError):
+        m.load(_params(m))
+    dn = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="n", one2one=True)
+    mn = vrs.Model(ctx(), dn, 1, 128, 128, vrs.BF16, 1e-3, autotune=False)
+    names_n = [pre for pre, _, _ in mn.conv_info()]
+    bad = [0] * len(names_n)
+    bad[names_n.index("model.1")] = vrs.TILE_STEM_PAIR
+    mn.set_plan(bad)
+    with pytest.raises(vrs.VrsError):
+        mn.load(_params(mn))

@@ -524,6 +524,42 @@ vrs_nhwc view_of(const vrs_model* m, V v) {
   return r;
 }
 
+// Conv i as the second layer of a stem pair (vrs_conv_stem_pair): it
+// directly follows the stem and reads exactly the stem's output, which
+// nothing else reads; 3x3 stride 2, 64 -> 128 channels, BN + SiLU on both,
+// bf16 activations, image width a multiple of 4.
+bool pair_eligible(const vrs_model* m, size_t i) {
+  if (i == 0 || i >= m->convs.size()) return false;
+  const ConvStep& s = m->convs[i - 1];
+  const ConvStep& c = m->convs[i];
+  if (!s.stem || s.cout != 64 || s.kind != CK_BN_SILU || s.y.buf < 0) return false;
+  if (c.dw || c.stem || c.k != 3 || c.s != 2 || c.cin != 64 || c.cout != 128 || c.kind != CK_BN_SILU || c.has_res ||
+      c.has_up || c.out_idx >= 0 || c.y.buf < 0)
+    return false;
+  if (c.x.buf != s.y.buf || c.x.c_off != s.y.c_off || c.x.c != s.y.c) return false;
+  if (act_dt(m) != VRS_BF16 || stem_pair_check(VRS_BF16, VRS_ACT_SILU, VRS_ACT_SILU, m->in_h, m->in_w) != VRS_OK) {
+    (void)vrs_last_error();
+    return false;
+  }
+  const int b = s.y.buf;
+  for (size_t k = 0; k < m->convs.size(); ++k) {
+    const ConvStep& o = m->convs[k];
+    if (k == i || o.stem) continue;
+    if (o.x.buf == b || (o.has_res && o.res.buf == b) || (o.has_up && o.up.buf == b)) return false;
+  }
+  for (const Step& st : m->steps)
+    if ((st.type == Step::POOL || st.type == Step::UP || st.type == Step::ATTN || st.type == Step::UNPACK) &&
+        st.a.buf == b)
+      return false;
+  return true;
+}
+
+// conv i runs as the second layer of a stem pair in this forward
+bool pair_fused(const vrs_model* m, size_t i) {
+  return !m->calib_mode && i < m->convs.size() && m->convs[i].tile == VRS_TILE_STEM_PAIR &&
+         !(m->convs[i].f8 && m->convs[i].run_f8);
+}
+
 int prepare(vrs_model* m, const float* x, float* const* outs) {
   const int nout = (int)m->out_dims.size();
   std::vector<float*> o(outs, outs + nout);
@@ -543,6 +579,11 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
       case Step::PACK: sio.rd = {{kResInput, 0, kAll}}; sio.wr = {acc(st.b)}; break;
       case Step::CONV: {
         const ConvStep& c = m->convs[st.conv];
+        if (pair_fused(m, st.conv)) {   // reads the image through the fused stem
+          sio.rd = {{kResInput, 0, kAll}};
+          sio.wr = {acc(c.y)};
+          break;
+        }
         sio.rd = {acc(c.x)};
         if (c.has_res) sio.rd.push_back(acc(c.res));
         if (c.has_up) sio.rd.push_back(acc(c.up));
@@ -563,11 +604,19 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         break;
       case Step::CONV: {
         const ConvStep& c = m->convs[st.conv];
+        if (pair_fused(m, st.conv)) {
+          const ConvStep& s0 = m->convs[st.conv - 1];
+          conv_launch[st.conv] = (int)ls.size();
+          rc = prep_stem_pair(m->ctx, x, m->batch, m->in_h, m->in_w, s0.w, s0.scale, s0.shift, c.w, c.scale,
+                              c.shift, view_of(m, c.y), ls);
+          label = c.pre;
+          break;
+        }
         ConvSpec cs;
         cs.k = c.k; cs.stride = c.s; cs.dtype = act_dt(m); cs.depthwise = c.dw;
         cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
         cs.cin_real = c.cin_real != c.cin ? c.cin_real : 0;
-        cs.tile = c.tile;
+        cs.tile = c.tile == VRS_TILE_STEM_PAIR ? VRS_TILE_AUTO : c.tile;   // unfused: fp8 calibration
         vrs_nhwc upv;
         if (c.has_up) {
           upv = view_of(m, c.up);
@@ -615,6 +664,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
       }
       case Step::STEM: {
         const ConvStep& c = m->convs[st.conv];
+        if (pair_fused(m, st.conv + 1)) continue;   // computed inside the next conv's launch
         conv_launch[st.conv] = (int)ls.size();
         rc = prep_stem(m->ctx, VRS_ACT_SILU, act_dt(m), x, m->batch, m->in_h, m->in_w, c.w, c.scale, c.shift,
                        c.cout, view_of(m, c.y), ls);
@@ -674,7 +724,28 @@ int autotune_tiles(vrs_model* m) {
   VRS_HIP(hipEventCreate(&e0));
   VRS_HIP(hipEventCreate(&e1));
   int rc = VRS_OK;
-  for (ConvStep& c : m->convs) {
+  // best of three rounds of five runs (every launch of the candidate): one
+  // slow round (a clock dip, another process) does not decide the tile
+  auto timed = [&](const std::vector<Launch>& ls, float& ms) -> int {
+    ms = 1e30f;
+    for (const Launch& l : ls)
+      if (int r = run(l, s)) return r;
+    for (int round = 0; round < 3; ++round) {
+      VRS_HIP(hipEventRecord(e0, s));
+      for (int it = 0; it < 5; ++it)
+        for (const Launch& l : ls)
+          if (int r = run(l, s)) return r;
+      VRS_HIP(hipEventRecord(e1, s));
+      VRS_HIP(hipEventSynchronize(e1));
+      float r = 0.f;
+      VRS_HIP(hipEventElapsedTime(&r, e0, e1));
+      ms = std::min(ms, r);
+    }
+    return VRS_OK;
+  };
+  float* img = nullptr;   // a zero image for timing the stem pair (values do not matter)
+  for (size_t ci = 0; ci < m->convs.size() && !rc; ++ci) {
+   ConvStep& c = m->convs[ci];
    float best_of[2] = {1e30f, 1e30f};   // fastest bf16 / fp8 tile of this layer
    for (int pass = 0; pass < (c.f8 ? 2 : 1); ++pass) {
     if (c.dw || c.stem || c.out_idx >= 0 || c.y.buf < 0) continue;
@@ -702,25 +773,8 @@ int autotune_tiles(vrs_model* m) {
       if (prep_conv(m->ctx, cs, view_of(m, c.x), pass ? c.w8 : c.w, pass ? c.scale8 : c.scale, c.shift,
                     c.has_res ? &r : nullptr, view_of(m, c.y), ls) != VRS_OK)
         continue;
-      for (const Launch& l : ls)
-        if ((rc = run(l, s))) break;
-      if (rc) break;
-      // best of three rounds of five runs (every launch of the candidate):
-      // one slow round (a clock dip, another process) does not decide the tile
-      float ms = 1e30f;
-      for (int round = 0; round < 3 && !rc; ++round) {
-        VRS_HIP(hipEventRecord(e0, s));
-        for (int it = 0; it < 5 && !rc; ++it)
-          for (const Launch& l : ls)
-            if ((rc = run(l, s))) break;
-        if (rc) break;
-        VRS_HIP(hipEventRecord(e1, s));
-        VRS_HIP(hipEventSynchronize(e1));
-        float r = 0.f;
-        VRS_HIP(hipEventElapsedTime(&r, e0, e1));
-        ms = std::min(ms, r);
-      }
-      if (rc) break;
+      float ms;
+      if ((rc = timed(ls, ms))) break;
       // a later candidate must win by 2%: near-ties keep the earlier one, so
       // the choice does not flip with timing noise from run to run
       if (ms < 0.98f * best) { best = ms; best_tile = t; }
@@ -730,10 +784,37 @@ int autotune_tiles(vrs_model* m) {
     best_of[pass] = best;
    }
    if (rc) break;
+   // the stem pair (this conv fused with the stem before it) against this
+   // conv's best bf16 tile plus the stem's own launch
+   if (pair_eligible(m, ci) && best_of[0] < 1e29f) {
+     const ConvStep& s0 = m->convs[ci - 1];
+     const size_t bytes = (size_t)m->batch * 3 * m->in_h * m->in_w * sizeof(float);
+     if (!img) {
+       hipError_t he = hipMalloc(&img, bytes);
+       if (he == hipSuccess) he = hipMemsetAsync(img, 0, bytes, s);
+       if (he != hipSuccess) {
+         rc = hip_check(he, "stem pair timing image");
+         break;
+       }
+     }
+     std::vector<Launch> l0, lp;
+     if (prep_stem(m->ctx, VRS_ACT_SILU, VRS_BF16, img, m->batch, m->in_h, m->in_w, s0.w, s0.scale, s0.shift,
+                   s0.cout, view_of(m, s0.y), l0) == VRS_OK &&
+         prep_stem_pair(m->ctx, img, m->batch, m->in_h, m->in_w, s0.w, s0.scale, s0.shift, c.w, c.scale, c.shift,
+                        view_of(m, c.y), lp) == VRS_OK) {
+       float t0, tp;
+       if ((rc = timed(l0, t0)) || (rc = timed(lp, tp))) break;
+       if (tp < 0.98f * (best_of[0] + t0)) {
+         c.tile = VRS_TILE_STEM_PAIR;
+         best_of[0] = tp - t0;
+       }
+     }
+   }
    // fp8 models: a layer whose bf16 tile is faster by 2% stays on bf16
    // (unless fp8 is forced)
    if (c.f8) c.run_f8 = m->autotune == 2 || !(best_of[0] < 0.98f * best_of[1]);
   }
+  if (img) (void)hipFree(img);
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   (void)hipStreamDestroy(s);
@@ -880,7 +961,13 @@ int apply_plan(vrs_model* m) {
     }
     if (f8 && !c.f8)
       return fail(VRS_EINVAL, "plan entry %zu (%s): fp8 requested for a conv that has no fp8 form", i, c.pre.c_str());
-    if (tile != VRS_TILE_AUTO) {   // validate by preparing the launch
+    if (tile == VRS_TILE_STEM_PAIR) {
+      if (f8 || !pair_eligible(m, i))
+        return fail(VRS_EINVAL,
+                    "plan entry %zu (%s): the stem pair applies only to a bf16 3x3/s2 64->128 conv reading a "
+                    "64-channel stem's output alone (image width a multiple of 4)",
+                    i, c.pre.c_str());
+    } else if (tile != VRS_TILE_AUTO) {   // validate by preparing the launch
       ConvSpec cs;
       cs.k = c.k; cs.stride = c.s; cs.dtype = f8 ? VRS_FP8 : act_dt(m);
       cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
@@ -1290,14 +1377,17 @@ int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io) {
   io->groups = c.dw ? c.cout : 1;
   io->act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
   io->plain = c.kind == CK_PLAIN;
-  io->stem = c.stem;
+  // a stem pair: the stem has no launch and no output of its own; the conv
+  // after it reads the model input (stem = 2)
+  const bool fused_out = c.stem && pair_fused(m, i + 1), fused_in = pair_fused(m, i);
+  io->stem = fused_in ? 2 : c.stem;
   io->fp8 = c.f8 && c.run_f8;
   io->in_scale = c.in_scale;
   io->dtype = act_dt(m);
   io->cin = c.cin_real;
   io->cout = c.cout;
-  if (!c.stem) io->x = view_of(m, c.x);
-  if (c.out_idx < 0 && c.y.buf >= 0) io->y = view_of(m, c.y);
+  if (!c.stem && !fused_in) io->x = view_of(m, c.x);
+  if (c.out_idx < 0 && c.y.buf >= 0 && !fused_out) io->y = view_of(m, c.y);
   if (c.has_res) io->res = view_of(m, c.res);
   if (c.has_up) io->up = view_of(m, c.up);
   io->out_idx = c.out_idx;

@@ -153,6 +153,20 @@ int vrs_conv_stem(vrs_ctx* ctx, const vrs_conv_desc* d, const float* x, int32_t 
   return rc ? rc : run_all(ls, stream);
 }
 
+int vrs_conv_stem_pair(vrs_ctx* ctx, const vrs_conv_desc* d0, const vrs_conv_desc* d1, const float* x, int32_t n,
+                       int32_t c, int32_t h, int32_t w, const void* w0, const float* scale0, const float* shift0,
+                       const void* w1, const float* scale1, const float* shift1, const vrs_nhwc* y, void* stream) {
+  if (!ctx || !d0 || !d1 || !x || !y) return fail(VRS_EINVAL, "vrs_conv_stem_pair: null argument");
+  if (c != 3 || d0->k != 3 || d0->stride != 2 || d0->groups != 1 || d1->k != 3 || d1->stride != 2 || d1->groups != 1)
+    return fail(VRS_EUNSUPPORTED, "vrs_conv_stem_pair: two 3x3 stride-2 dense convs on a 3-channel image only");
+  if (d0->dtype != d1->dtype) return fail(VRS_EINVAL, "vrs_conv_stem_pair: the two layers' dtypes differ");
+  int rc = stem_pair_check(d0->dtype, d0->act, d1->act, h, w);
+  if (rc) return rc;
+  std::vector<Launch> ls;
+  rc = prep_stem_pair(ctx, x, n, h, w, w0, scale0, shift0, w1, scale1, shift1, *y, ls);
+  return rc ? rc : run_all(ls, stream);
+}
+
 int vrs_bn_fold(const float* gamma, const float* beta, const float* mean, const float* var, float eps, int32_t c,
                 float* scale, float* shift) {
   if (!gamma || !beta || !mean || !var || !scale || !shift || c <= 0) return fail(VRS_EINVAL, "vrs_bn_fold: bad args");

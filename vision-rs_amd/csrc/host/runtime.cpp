@@ -691,6 +691,51 @@ int prep_stem(vrs_ctx* ctx, int act, int dtype, const float* x, int n, int h, in
   return VRS_OK;
 }
 
+int stem_pair_check(int dtype, int act0, int act1, int h, int w) {
+  if (dtype != VRS_BF16) return fail(VRS_EUNSUPPORTED, "stem pair: bf16 only");
+  if (act0 != VRS_ACT_SILU || act1 != VRS_ACT_SILU) return fail(VRS_EUNSUPPORTED, "stem pair: SiLU on both layers only");
+  if (w % 4) return fail(VRS_EUNSUPPORTED, "stem pair: image width %d not a multiple of 4", w);
+  if ((int64_t)3 * h * w * 4 >= (1ll << 31)) return fail(VRS_EBADSHAPE, "stem pair: one image must be under 2 GiB");
+  return VRS_OK;
+}
+
+int prep_stem_pair(vrs_ctx* ctx, const float* x, int n, int h, int w, const void* w0, const float* scale0,
+                   const float* shift0, const void* w1, const float* scale1, const float* shift1, const vrs_nhwc& y,
+                   std::vector<Launch>& ls) {
+  int rc;
+  if ((rc = stem_pair_check(VRS_BF16, VRS_ACT_SILU, VRS_ACT_SILU, h, w))) return rc;
+  if (!x || !w0 || !scale0 || !shift0 || !w1 || !scale1 || !shift1) return fail(VRS_EINVAL, "stem pair: null argument");
+  if (reinterpret_cast<uintptr_t>(x) % 16) return fail(VRS_EBADSHAPE, "stem pair: image not 16-byte aligned");
+  if ((rc = check_view(y, "stem pair output", 8))) return rc;
+  const int h0 = out_size(h, 3, 2), w0o = out_size(w, 3, 2);
+  const int h1 = out_size(h0, 3, 2), w1o = out_size(w0o, 3, 2);
+  if (y.n != n || y.h != h1 || y.w != w1o || y.c != 128)
+    return fail(VRS_EBADSHAPE, "stem pair: output view %dx%dx%dx%d for input %dx3x%dx%d (expects %dx%dx%dx128)", y.n,
+                y.h, y.w, y.c, n, h, w, n, h1, w1o);
+  if ((int64_t)h1 * w1o * y.pitch * 2 >= (1ll << 31))
+    return fail(VRS_EBADSHAPE, "stem pair: one output image must be under 2 GiB");
+  vrs_stem_pair_args a{};
+  a.x = x; a.w0 = w0; a.scale0 = scale0; a.shift0 = shift0;
+  a.w1 = w1; a.scale1 = scale1; a.shift1 = shift1;
+  a.y = const_cast<void*>(at(y, VRS_BF16));
+  a.N = n; a.H = h; a.W = w; a.H0 = h0; a.W0 = w0o; a.H1 = h1; a.W1 = w1o; a.y_pitch = y.pitch;
+  a.strips = (w1o + 31) / 32;
+  a.sps = (h1 + 1) / 2;
+  const int64_t total = (int64_t)n * a.strips * a.sps;
+  if (total >= (1ll << 31)) return fail(VRS_EBADSHAPE, "stem pair: grid too large");
+  a.total = (int32_t)total;
+  const char* name = "vrs_stem_pair_bf16";
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  // persistent: one workgroup per CU, each walking total / grid consecutive steps
+  const int64_t wgs = std::min<int64_t>(total, (int64_t)resident_wgs(f, 512) * (ctx->num_cu > 0 ? ctx->num_cu : 256));
+  ls.push_back(make_launch(name, f, dim3((unsigned)wgs), dim3(512), 0, a));
+  ls.back().flops = 2.0 * n * h0 * w0o * 64.0 * 27 + 2.0 * n * h1 * w1o * 128.0 * 576;
+  ls.back().bytes = (double)n * 3 * h * w * 4 + (double)n * h1 * w1o * 128 * 2 + 64.0 * 32 * 2 + 128.0 * 576 * 2 +
+                    8.0 * (64 + 128);
+  return VRS_OK;
+}
+
 }  // namespace vrs
 
 using namespace vrs;

@@ -107,6 +107,13 @@ struct ConvSpec {
 // packed by vrs_pack_stem_weight
 int prep_stem(vrs_ctx* ctx, int act, int dtype, const float* x, int n, int h, int w, const void* wp,
               const float* scale, const float* shift, int cout, const vrs_nhwc& y, std::vector<Launch>& ls);
+// stem pair (model.0 + model.1, 64 -> 128 channels, bf16, SiLU) in one
+// kernel from the NCHW float32 image; w0 from vrs_pack_stem_weight, w1 the
+// dense [128][3][3][64] packing.  stem_pair_check: the shape/type conditions.
+int stem_pair_check(int dtype, int act0, int act1, int h, int w);
+int prep_stem_pair(vrs_ctx* ctx, const float* x, int n, int h, int w, const void* w0, const float* scale0,
+                   const float* shift0, const void* w1, const float* scale1, const float* shift1, const vrs_nhwc& y,
+                   std::vector<Launch>& ls);
 // max |x| of a bfloat16 NHWC view into *out (float bits; caller zeroes it)
 int prep_absmax(vrs_ctx* ctx, const vrs_nhwc& x, unsigned* out, std::vector<Launch>& ls);
 // float -> e4m3 (OCP, max 448) with round-to-nearest-even; |v| > 448 saturates

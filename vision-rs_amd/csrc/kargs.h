@@ -225,4 +225,25 @@ typedef struct {
   int32_t segs;        /* 64-pixel segments per output row */
 } vrs_stem_args;
 
+/* Stem pair: the stem conv (64 output channels) and the 3x3 stride-2 conv
+ * 64 -> 128 that reads it, in one kernel (bf16, SiLU on both).  A step is 2
+ * output rows x 32 output columns of one image strip; step q of the batch is
+ * (image, strip, row pair) = (q / (strips*sps), q / sps % strips, q % sps). */
+typedef struct {
+  const float* x;       /* NCHW float32 images */
+  const void* w0;       /* stem weights [64][32] bf16 (vrs_pack_stem_weight) */
+  const float* scale0;
+  const float* shift0;
+  const void* w1;       /* [128][3][3][64] bf16 */
+  const float* scale1;
+  const float* shift1;
+  void* y;              /* view base (pixel 0, first channel of the view) */
+  int32_t N, H, W;      /* images */
+  int32_t H0, W0;       /* stem output */
+  int32_t H1, W1;       /* output */
+  int32_t y_pitch;
+  int32_t strips, sps;  /* 32-column strips per image, row pairs per strip */
+  int32_t total;        /* N * strips * sps */
+} vrs_stem_pair_args;
+
 #endif

@@ -35,6 +35,7 @@ TILE_H3 = 7   # halo-tiled 3x3 stride-1 kernel (bf16)
 TILE_W1_256 = 8   # weight-stationary 1x1 kernels (bf16): 256- or 128-channel weight slice in LDS
 TILE_W1_128 = 9
 TILE_64x64 = 10   # bf16: small maps (four times the workgroups of 128x128)
+TILE_STEM_PAIR = 11   # model plans: the conv after a 64-channel stem, fused with it (bf16)
 
 ERRORS = {-1: "EINVAL", -2: "EBADSHAPE", -3: "EUNSUPPORTED", -4: "ENOMODULE", -5: "EHIP", -6: "ENOTFOUND",
           -7: "ESTATE"}
@@ -101,6 +102,8 @@ SIGNATURES = {
     "vrs_pack_conv_weight_fp8": (_i64, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "vrs_pack_stem_weight": (_i64, [_vp, _i32, _i32, _vp]),
     "vrs_conv_stem": (C.c_int, [_vp, _P(ConvDesc), _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _P(Nhwc), _vp]),
+    "vrs_conv_stem_pair": (C.c_int, [_vp, _P(ConvDesc), _P(ConvDesc), _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp,
+                                     _vp, _vp, _vp, _P(Nhwc), _vp]),
     "vrs_bn_fold": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _i32, _vp, _vp]),
     "vrs_pack_input": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _P(Nhwc), _i32, _vp]),
     "vrs_unpack_output": (C.c_int, [_vp, _P(Nhwc), _i32, _vp, _vp]),
@@ -249,6 +252,18 @@ class Context:
         d = ConvDesc(3, 2, 1, act, dtype, TILE_AUTO, 1.0)
         check(lib().vrs_conv_stem(self.handle, C.byref(d), _ptr(x_nchw), n, c, h, w_, _ptr(w), _ptr(scale),
                                   _ptr(shift), C.byref(y), _stream(stream)))
+
+    def conv_stem_pair(self, x_nchw, w0, scale0, shift0, w1, scale1, shift1, y, act=ACT_SILU, dtype=BF16,
+                       stream=None):
+        """model.0 + model.1 (3 -> 64 -> 128 channels, both 3x3 s2) in one kernel from the NCHW
+        float32 image into the 128-channel NHWC view y; w0 from pack_stem_weight, w1 from
+        pack_conv_weight."""
+        n, c, h, w_ = x_nchw.shape
+        d0 = ConvDesc(3, 2, 1, act, dtype, TILE_AUTO, 1.0)
+        d1 = ConvDesc(3, 2, 1, act, dtype, TILE_AUTO, 1.0)
+        check(lib().vrs_conv_stem_pair(self.handle, C.byref(d0), C.byref(d1), _ptr(x_nchw), n, c, h, w_, _ptr(w0),
+                                       _ptr(scale0), _ptr(shift0), _ptr(w1), _ptr(scale1), _ptr(shift1),
+                                       C.byref(y), _stream(stream)))
 
     def pack_input(self, x_nchw, y, dtype, stream=None):
         n, c, h, w = x_nchw.shape
