@@ -479,6 +479,16 @@ int prep_conv_flat(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const vo
   vrs_conv_args a{};
   a.y = y; a.y_sb = sb; a.y_sp = sp; a.y_sc = sc; a.y_f32 = 1;
   const int ho = out_size(x.h, cs.k, cs.stride), wo = out_size(x.w, cs.k, cs.stride);
+  // bf16 tiles stage a channel-major output (sp == 1) through LDS for 16-byte
+  // stores of 4 pixels of one channel: whole pixel quads per image, 16-byte
+  // aligned rows, and every touched byte within 32-bit raw-buffer offsets
+  const int64_t hw = (int64_t)ho * wo;
+  const int64_t last = (int64_t)(x.n - 1) * sb + (hw - 1) * sp + (int64_t)(cout - 1) * sc + 1;
+  if (cs.dtype == VRS_BF16 && sp == 1 && hw % 4 == 0 && sb % 4 == 0 && sc % 4 == 0 && sb >= 0 && sc >= 0 &&
+      reinterpret_cast<uintptr_t>(y) % 16 == 0 && last * 4 < (1ll << 31)) {
+    a.stage = 2;
+    a.y_bytes = (int32_t)(last * 4);
+  }
   return prep_dense(ctx, cs, x, w, scale, shift, cout, ho, wo, a, out);
 }
 

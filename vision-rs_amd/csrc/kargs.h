@@ -35,7 +35,10 @@ typedef struct {
   int32_t tiles_m, tiles_n; /* grid decomposition: Cout tiles x pixel tiles */
   int32_t stage;  /* 1: NHWC output staged through LDS for 16-byte stores
                      (element-type output, y_sc == 1, Cout % 8 == 0, 16-byte
-                     aligned channel offset and pitch) */
+                     aligned channel offset and pitch); 2 (bf16 tiles): a
+                     channel-major float32 output (y_sp == 1) staged for
+                     16-byte stores of 4 pixels of one channel, y_bytes the
+                     extent written */
   int32_t x_bytes;  /* readable bytes from x to the end of its buffer (< 2^31) */
   int32_t w_bytes;  /* bytes of the packed weights (< 2^31) */
   /* fp8 kernels: activations are quantised to e4m3 as x / in_scale (a power

@@ -460,6 +460,66 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   // tiles: a second epilogue copy costs them registers)
   auto epilogue = [&](auto mode_tag) {
     constexpr int MODE = decltype(mode_tag)::value;
+    if constexpr (sizeof(T) == 2 && !F8) {
+      if (a.stage == 2) {
+        // Channel-major float32 output (the Detect heads' flat layout:
+        // element (b, p, co) at y + b*y_sb + p + co*y_sc): the wave tile goes
+        // through LDS as [channel][pixel] rows, CH channels per pass, and
+        // each lane stores 4 consecutive pixels of one channel as one 16-byte
+        // raw-buffer store (the host checks that 4 pixels never straddle two
+        // images and the 16-byte alignment of y, y_sb and y_sc).  Each wave
+        // reads back only what it wrote, so the passes need no barrier.
+        constexpr int HW_ = WGM * WGN / 2;              // waves per pipeline buffer
+        constexpr int PR = WTN + 8;                     // staging row (floats): the
+                                                        // two half-waves' rows 32 banks apart
+        constexpr int WB = TILE_ELEMS * (int)sizeof(T) / HW_ / 4;   // floats per wave
+        constexpr int FIT = WB / PR;
+        constexpr int CH = (FIT >= 128 && WTM >= 128) ? 128
+                           : (FIT >= 64 && WTM >= 64) ? 64
+                           : FIT >= 32 ? 32 : FIT >= 16 ? 16 : 8;
+        static_assert(FIT >= 8 && WTM % CH == 0, "flat staging fits the pipeline buffers");
+        constexpr int QPR = WTN / 4;                    // pixel quads per staged row
+        constexpr int NSQ = CH * QPR / 64;              // stores per lane per pass
+        static_assert(CH * QPR % 64 == 0, "whole store rounds");
+        float* st = reinterpret_cast<float*>(sbuf(wave / HW_)) + (wave % HW_) * WB;
+        const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, a.y_bytes);
+#pragma unroll
+        for (int pass = 0; pass < WTM / CH; ++pass) {
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const int cb = i * 32 + g * 8;
+              if (cb < pass * CH || cb >= (pass + 1) * CH) continue;
+              const int cl = cb - pass * CH + hq * 4;
+              const f32x4_t sc = chan4(s_scale, i, g), sh = chan4(s_shift, i, g);
+#pragma unroll
+              for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  float t = acc[i][j][g * 4 + r] * sc[r] + sh[r];
+                  if constexpr (MODE == 1) t = silu_t<T>(t);
+                  st[(cl + r) * PR + j * 32 + (lane & 31)] = t;
+                }
+            }
+#pragma unroll
+          for (int q = 0; q < NSQ; ++q) {
+            const int c = lane + q * 64, cl = c / QPR, pq = c % QPR;
+            const int co = m0 + wm * WTM + pass * CH + cl;
+            const int m = n0 + wn * WTN + pq * 4;
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&st[cl * PR + pq * 4]);
+            uint32_t off = kOOB;
+            if (m < a.M && co < a.Cout) {
+              int p;
+              const int b = fdivmod(m, HWo, inv_hwo, p);
+              off = (uint32_t)(((int64_t)b * a.y_sb + p + (int64_t)co * a.y_sc) * 4);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(v, ry, off, 0, 0);
+          }
+        }
+        return;
+      }
+    }
     if (a.stage) {
       // Staged store: every wave writes its (WTN pixel x WTM channel) tile to
       // LDS, then stores whole 16-byte channel chunks per lane, so consecutive
