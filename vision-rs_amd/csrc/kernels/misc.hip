@@ -103,15 +103,20 @@ __device__ __forceinline__ void dw_body(const vrs_dw_args& a) {
 // the lanes 8 below/above (ds_bpermute), and only the patch's edge lanes load
 // the halo column.  Every input row feeds the three output rows it touches
 // through a 3-slot accumulator ring, so an input pixel is read once per band
-// (plus the 2-row band halo) instead of once per tap; loads run two rows
-// ahead.  The four waves of a workgroup take adjacent column patches so
+// (plus the 2-row band halo) instead of once per tap.  Loads run five rows
+// ahead in a 6-slot ring (bf16; the kernel is bound by the bytes it keeps in
+// flight: two waves per SIMD at ~230 registers), and rows past the band are
+// not fetched.  The four waves of a workgroup take adjacent column patches so
 // their edge columns meet in L1.
 template <typename T, int RB>
 __device__ __forceinline__ void dww_body(const vrs_dw_args& a) {
   using E = Elt<T>;
   using G = typename E::group;
   constexpr int NW = (int)sizeof(G) / 4;          // dwords per group
-  static_assert((RB + 2) % 3 == 0, "rows per band: RB + 2 must be a multiple of 3");
+  // prefetch ring slots (rows in flight + 1); float32 rows take twice the
+  // registers, so the parity path keeps three
+  constexpr int NP = sizeof(T) == 2 ? 6 : 3;
+  static_assert((RB + 2) % NP == 0, "rows per band: RB + 2 must be a multiple of the ring");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int gl = lane & 7, cx = lane >> 3;
   // workgroup -> (image, band, channel block, 4 adjacent patches)
@@ -122,6 +127,7 @@ __device__ __forceinline__ void dww_body(const vrs_dw_args& a) {
   const int band = wgi % a.bands;
   const int b = wgi / a.bands;
   const int patch = pquad * 4 + wave;
+  if (patch >= a.patches) return;                 // a workgroup's spare waves (no barriers here)
   const int ox = patch * 8 + cx;
   const int c0 = cb * 64 + gl * 8;
   const bool cok = c0 < a.C && patch < a.patches;
@@ -157,10 +163,12 @@ __device__ __forceinline__ void dww_body(const vrs_dw_args& a) {
                ? (uint32_t)((((img + iy) * a.W + xx) * a.x_pitch + c0) * (int)sizeof(T))
                : kOOB;
   };
-  G own[3], halo[3];   // prefetch ring of input rows (own column, halo column)
-  auto fetch = [&](int slot, int iy) {
-    own[slot] = E::bload(rx, row_off(iy, ox, colok), 0);
-    halo[slot] = E::bload(rx, row_off(iy, hx, hok), 0);
+  G own[NP], halo[NP];   // prefetch ring of input rows (own column, halo column)
+  // band row u (0..RB+1) into slot u % NP; rows past the band read nothing
+  auto fetch = [&](int slot, int u) {
+    const bool in = u < RB + 2;
+    own[slot] = E::bload(rx, row_off(oy0 - 1 + u, ox, colok && in), 0);
+    halo[slot] = E::bload(rx, row_off(oy0 - 1 + u, hx, hok && in), 0);
   };
 
   float acc[3][8];
@@ -170,13 +178,13 @@ __device__ __forceinline__ void dww_body(const vrs_dw_args& a) {
     for (int c = 0; c < 8; ++c) acc[s][c] = 0.f;
 
   T* y = reinterpret_cast<T*>(a.y);
-  const int iy0 = oy0 - 1;
-  // Input row u of the band (0..RB+1) sits in prefetch slot u % 3 and feeds
+  // Input row u of the band (0..RB+1) sits in prefetch slot u % NP and feeds
   // output rows v = u - ky (ky = 0..2) through accumulator slot v % 3; after
-  // row u, output row u - 2 is complete (slot (u + 1) % 3).
-  auto process = [&](int p, int u) {
-    const uint32_t* ov = reinterpret_cast<const uint32_t*>(&own[p]);
-    const uint32_t* hv = reinterpret_cast<const uint32_t*>(&halo[p]);
+  // row u, output row u - 2 is complete (slot (u + 1) % 3).  q = u % NP.
+  auto process = [&](int q, int u) {
+    const int p = q % 3;
+    const uint32_t* ov = reinterpret_cast<const uint32_t*>(&own[q]);
+    const uint32_t* hv = reinterpret_cast<const uint32_t*>(&halo[q]);
     uint32_t lw[NW], rw[NW];
 #pragma unroll
     for (int d = 0; d < NW; ++d) {
@@ -220,22 +228,23 @@ __device__ __forceinline__ void dww_body(const vrs_dw_args& a) {
     for (int c = 0; c < 8; ++c) acc[sv][c] = 0.f;
   };
 
-  fetch(0, iy0);
-  fetch(1, iy0 + 1);
-  for (int u = 0; u < RB + 2; u += 3) {
-    fetch(2, iy0 + u + 2);
-    process(0, u);
-    fetch(0, iy0 + u + 3);
-    process(1, u + 1);
-    fetch(1, iy0 + u + 4);
-    process(2, u + 2);
+#pragma unroll
+  for (int q = 0; q < NP - 1; ++q) fetch(q, q);
+  for (int u = 0; u < RB + 2; u += NP) {
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      fetch((q + NP - 1) % NP, u + q + NP - 1);
+      process(q, u + q);
+    }
   }
 }
 
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w16_bf16(vrs_dw_args a) { dww_body<bf16_t, 16>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w10_bf16(vrs_dw_args a) { dww_body<bf16_t, 10>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w22_bf16(vrs_dw_args a) { dww_body<bf16_t, 22>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w16_f32(vrs_dw_args a) { dww_body<float, 16>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w10_f32(vrs_dw_args a) { dww_body<float, 10>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w22_f32(vrs_dw_args a) { dww_body<float, 22>(a); }
 
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1_bf16(vrs_dw_args a) { dw_body<bf16_t, 1>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s2_bf16(vrs_dw_args a) { dw_body<bf16_t, 2>(a); }
