@@ -180,6 +180,7 @@ H3_CASES = [
     (2, 256, 13, 70, 64, False, (80, 16)),
     (1, 32, 40, 40, 16, True, None),
     (1, 512, 9, 33, 96, False, None),
+    (6, 32, 160, 160, 64, True, None),   # 2400 workgroups (residual prefetch across several waves of them)
 ]
 
 

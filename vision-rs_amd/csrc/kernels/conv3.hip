@@ -20,9 +20,10 @@
 // register sets: chunk c+2's global loads are issued before chunk c's MFMAs
 // and written to LDS after chunk c+1's, so loads have two chunks' MFMAs to
 // land and each chunk costs one barrier.  4 waves, each BM channels x 64
-// pixels (32x32x16 bf16 MFMAs).  Epilogue as the implicit-GEMM kernels:
-// scale*acc + shift, SiLU, residual, staged through LDS for 16-byte NHWC
-// stores.
+// pixels (32x32x16 bf16 MFMAs).  The residual is loaded with the first two
+// chunks (its latency passes under the K loop).  Epilogue as the
+// implicit-GEMM kernels: scale*acc + shift, SiLU, residual, staged through
+// LDS for 16-byte NHWC stores.
 #include "common.h"
 
 namespace {
@@ -200,6 +201,22 @@ __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
   };
   load_stage(0, wreg0, hreg0);
   load_stage(1, wreg1, hreg1);
+  // the residual this lane adds (4 channels of each accumulator quad), loaded
+  // now so that its latency passes under the K loop instead of the epilogue
+  const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res, a.res ? a.res_bytes : 0);
+  u32x2_t rres[TM][4][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int co = m0 + i * 32 + g * 8 + hq * 4;
+        const uint32_t ro = a.res && pv[j] && co < a.Cout
+                                ? (uint32_t)((b * a.r_sb + (int64_t)py[j] * a.Wo * a.r_sp + (int64_t)px[j] * a.r_sp + co) * 2)
+                                : kOOB;
+        rres[i][g][j] = __builtin_amdgcn_raw_buffer_load_b64(rr, ro, 0, 0);
+      }
   store_stage(0, wreg0, hreg0);
   __syncthreads();
   for (int c = 0; c < nst; c += 2) {
@@ -211,7 +228,6 @@ __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
   // hq*4 + r of pixel slot wave*64 + j*32 + l32
   // (the last chunk's barrier: every wave is done with the stage buffers,
   // which the staging reuses)
-  const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res, a.res ? a.res_bytes : 0);
   bf16_t* stg = smem + wave * 64 * SROW;
   // instantiated per activation: no per-value SiLU select
   auto epilogue = [&](auto silu_on) {
@@ -221,7 +237,6 @@ __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int cl = i * 32 + g * 8 + hq * 4;
-        const int co = m0 + cl;
         const f32x4_t sc = *reinterpret_cast<const f32x4_t*>(&s_scale[cl]);
         const f32x4_t sh = *reinterpret_cast<const f32x4_t*>(&s_shift[cl]);
 #pragma unroll
@@ -234,11 +249,7 @@ __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
             v[r] = t;
           }
           if (a.res) {
-            const uint32_t ro = pv[j] && co < a.Cout
-                                    ? (uint32_t)((b * a.r_sb + (int64_t)py[j] * a.Wo * a.r_sp + (int64_t)px[j] * a.r_sp +
-                                                  co) * 2)
-                                    : kOOB;
-            const u32x2_t rv = __builtin_amdgcn_raw_buffer_load_b64(rr, ro, 0, 0);
+            const u32x2_t rv = rres[i][g][j];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
               v[r] += __uint_as_float((r & 1) ? (rv[r >> 1] & 0xffff0000u) : (rv[r >> 1] << 16));
