@@ -98,7 +98,8 @@ typedef struct {
  * up to 192 (_256) or 256 (_128), no residual, output channel offset/pitch/
  * count multiples of 8, no fused upsample): a persistent workgroup keeps a
  * 256- or 128-channel slice of the weights in LDS and streams 64-pixel tiles
- * of whole input pixel rows through it. */
+ * of whole input pixel rows through it.  In model plans, _128 also serves the
+ * Detect head's channel-major float32 output convs with Cin 64 or 256. */
 #define VRS_TILE_W1_256 8
 #define VRS_TILE_W1_128 9
 /* 64x64 tile (bf16, Cin % 32 == 0; 4 waves of 32x32): four times the

@@ -83,8 +83,8 @@ def test_fp8_forced_mode_keeps_every_eligible_conv_on_fp8():
     eligible = [io for io in ios if io.groups == 1 and not io.stem and io.up.data is None and io.cin % 64 == 0]
     assert all(io.fp8 for io in eligible) and len(eligible) > 60
     plan = m.get_plan()
-    assert sum(1 for p in plan if p & vrs.PLAN_FP8) == sum(
-        1 for io in eligible if io.y.data is not None)   # flat-output convs take no tile entry
+    # every eligible conv has an fp8 plan entry, the Detect output convs included
+    assert sum(1 for p in plan if p & vrs.PLAN_FP8) == len(eligible)
     assert all(io.in_scale > 0 for io in eligible)
 
 
@@ -212,3 +212,35 @@ def test_stem_pair_plan():
     mn.set_plan(bad)
     with pytest.raises(vrs.VrsError):
         mn.load(_params(mn))
+
+
+def test_head_outputs_on_the_weight_stationary_tile():
+    """The Detect head's channel-major float32 output convs (box 64 -> 4,
+    class 256 -> 80, plain convs with bias) on the weight-stationary 1x1 tile
+    give bit-identical outputs to the 128x128 tile: the same K order and the
+    same epilogue arithmetic, one dword store per value."""
+    import torch
+    x = dev(np.random.default_rng(11).uniform(0, 1, (2, 3, 320, 320)).astype(np.float32))
+    m0 = _yolo(2, 320, vrs.BF16, autotune=False)
+    P = _params(m0)
+    m0.load(P)
+    names = [pre for pre, _, _ in m0.conv_info()]
+    heads = [i for i, nm in enumerate(names) if nm.startswith("model.23.") and nm.endswith(".2")]
+    assert len(heads) == 6, [names[i] for i in heads]
+    outs = []
+    for tile in (vrs.TILE_128x128, vrs.TILE_W1_128):
+        plan = m0.get_plan()
+        for i in heads:
+            plan[i] = tile
+        m = _yolo(2, 320, vrs.BF16, autotune=False)
+        m.set_plan(plan)
+        m.load(P)
+        outs.append([o.clone() for o in m.forward(x)])
+        launches = m.launch_names()
+        for i in heads:
+            got = launches[m.conv_io(i).launch]
+            want = "vrs_conv_bf16_128x128_k64_a" if tile == vrs.TILE_128x128 else "vrs_conv1w_bf16_128_c"
+            assert got.split(":")[1].startswith(want) and (tile == vrs.TILE_128x128 or got.endswith("_f")), got
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))

@@ -717,6 +717,26 @@ int dev_upload(vrs_model* m, const void* host, size_t bytes, void** dev) {
 // buffers (contents do not matter for timing; a forward rewrites them all)
 // and keep the fastest.  Replaces the reference's shape-adaptive tile choice
 // in TritonLowering (examples/yolo26.rs:3027).
+// convs with a tile choice: dense ones, into a buffer or a Detect output
+bool tunable(const ConvStep& c) { return !c.dw && !c.stem && (c.out_idx >= 0 || c.y.buf >= 0); }
+
+// The launches of conv c with spec cs (tile, dtype, activation set by the
+// caller) and weights w / scale: into its NHWC view, or, for a Detect output
+// conv, into its channel-major float32 slice of the output tensor at `outs`.
+int prep_conv_step(const vrs_model* m, const ConvStep& c, ConvSpec cs, const void* w, const float* scale,
+                   float* const* outs, std::vector<Launch>& ls) {
+  vrs_nhwc upv, r;
+  if (c.has_up) {
+    upv = view_of(m, c.up);
+    cs.up = &upv;
+  }
+  if (c.out_idx >= 0)
+    return prep_conv_flat(m->ctx, cs, view_of(m, c.x), w, scale, c.shift, c.cout, outs[c.out_idx] + c.out_off, c.sb,
+                          c.sp, c.sc, ls);
+  if (c.has_res) r = view_of(m, c.res);
+  return prep_conv(m->ctx, cs, view_of(m, c.x), w, scale, c.shift, c.has_res ? &r : nullptr, view_of(m, c.y), ls);
+}
+
 int autotune_tiles(vrs_model* m) {
   hipStream_t s;
   VRS_HIP(hipStreamCreate(&s));
@@ -744,34 +764,39 @@ int autotune_tiles(vrs_model* m) {
     return VRS_OK;
   };
   float* img = nullptr;   // a zero image for timing the stem pair (values do not matter)
+  // scratch float32 outputs for timing the Detect output convs
+  std::vector<float*> outs(m->out_dims.size(), nullptr);
   for (size_t ci = 0; ci < m->convs.size() && !rc; ++ci) {
    ConvStep& c = m->convs[ci];
    float best_of[2] = {1e30f, 1e30f};   // fastest bf16 / fp8 tile of this layer
    for (int pass = 0; pass < (c.f8 ? 2 : 1); ++pass) {
-    if (c.dw || c.stem || c.out_idx >= 0 || c.y.buf < 0) continue;
+    if (!tunable(c)) continue;
     if (pass == 0 && c.f8 && m->autotune == 2) continue;   // fp8 forced: no bf16 candidates
     const int dt = pass ? VRS_FP8 : act_dt(m);
+    const Buf& xb = m->bufs[c.x.buf];
+    const int64_t npix = (int64_t)m->batch * ((xb.h + 2 * (c.k / 2) - c.k) / c.s + 1) *
+                         ((xb.w + 2 * (c.k / 2) - c.k) / c.s + 1);
     const std::vector<int> cand =
-        conv_tile_candidates(c.cout, c.cin, dt, c.k, c.s, c.has_up ? 0 : m->bufs[c.x.buf].w,
-                             (int64_t)m->batch * m->bufs[c.y.buf].h * m->bufs[c.y.buf].w, m->ctx->num_cu);
+        conv_tile_candidates(c.cout, c.cin, dt, c.k, c.s, c.has_up ? 0 : xb.w, npix, m->ctx->num_cu);
     if (cand.size() < 2) continue;
+    if (c.out_idx >= 0 && !outs[c.out_idx]) {
+      size_t n = 1;
+      for (int32_t d : m->out_dims[c.out_idx]) n *= (size_t)d;
+      if (hipMalloc(&outs[c.out_idx], n * sizeof(float)) != hipSuccess) {
+        outs[c.out_idx] = nullptr;
+        rc = fail(VRS_EHIP, "autotune: scratch output");
+        break;
+      }
+    }
     ConvSpec cs;
     cs.k = c.k; cs.stride = c.s; cs.dtype = dt; cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
     cs.in_scale = 1.f;  // timing only: values do not matter
-    vrs_nhwc upv;
-    if (c.has_up) {
-      upv = view_of(m, c.up);
-      cs.up = &upv;
-    }
-    vrs_nhwc r;
-    if (c.has_res) r = view_of(m, c.res);
     float best = 1e30f;
     int best_tile = VRS_TILE_AUTO;
     for (int t : cand) {
       cs.tile = t;
       std::vector<Launch> ls;
-      if (prep_conv(m->ctx, cs, view_of(m, c.x), pass ? c.w8 : c.w, pass ? c.scale8 : c.scale, c.shift,
-                    c.has_res ? &r : nullptr, view_of(m, c.y), ls) != VRS_OK)
+      if (prep_conv_step(m, c, cs, pass ? c.w8 : c.w, pass ? c.scale8 : c.scale, outs.data(), ls) != VRS_OK)
         continue;
       float ms;
       if ((rc = timed(ls, ms))) break;
@@ -815,6 +840,8 @@ int autotune_tiles(vrs_model* m) {
    if (c.f8) c.run_f8 = m->autotune == 2 || !(best_of[0] < 0.98f * best_of[1]);
   }
   if (img) (void)hipFree(img);
+  for (float* o : outs)
+    if (o) (void)hipFree(o);
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   (void)hipStreamDestroy(s);
@@ -944,7 +971,6 @@ int finalize_upload(vrs_model* m) {
 
 // Tiles of a dense NHWC conv that the autotuner would consider (the convs a
 // plan entry applies to).
-bool tunable(const ConvStep& c) { return !c.dw && !c.stem && c.out_idx < 0 && c.y.buf >= 0; }
 
 // A caller's tile plan (vrs_model_set_plan) instead of autotuning: every
 // entry is checked against the kernels built for its conv's shape.
@@ -973,12 +999,12 @@ int apply_plan(vrs_model* m) {
       cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
       cs.in_scale = 1.f;
       cs.tile = tile;
-      vrs_nhwc upv, r;
-      if (c.has_up) { upv = view_of(m, c.up); cs.up = &upv; }
-      if (c.has_res) r = view_of(m, c.res);
+      // a Detect output conv is prepared against a stand-in output address
+      // (16-byte aligned, as every output tensor the model is given must be):
+      // preparing only builds the launch arguments, nothing is launched
+      std::vector<float*> probe(m->out_dims.size(), reinterpret_cast<float*>(uintptr_t{1} << 20));
       std::vector<Launch> ls;
-      const int rc = prep_conv(m->ctx, cs, view_of(m, c.x), f8 ? c.w8 : c.w, f8 ? c.scale8 : c.scale, c.shift,
-                               c.has_res ? &r : nullptr, view_of(m, c.y), ls);
+      const int rc = prep_conv_step(m, c, cs, f8 ? c.w8 : c.w, f8 ? c.scale8 : c.scale, probe.data(), ls);
       if (rc) return fail(rc, "plan entry %zu (%s): %s", i, c.pre.c_str(), vrs_last_error());
     }
     if (c.f8) {

@@ -323,12 +323,16 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
       return fail(VRS_EUNSUPPORTED, "conv: the weight-stationary %d-channel tile needs bf16, k=1, stride 1, no fused "
                   "upsample and Cin a multiple of 64 up to %d (k=%d s=%d Cin=%d)", bm, bm == 256 ? 192 : 256, cs.k,
                   cs.stride, x.c);
-    if (a.res || !a.stage || a.y_f32)
+    const bool flat = a.y_f32 && a.stage == 2;   // channel-major float32 (the Detect head's outputs)
+    if (a.res || (!flat && (!a.stage || a.y_f32)) || (flat && bm != 128))
       return fail(VRS_EUNSUPPORTED, "conv: the weight-stationary tile takes no residual and stores 8-channel-aligned "
-                  "chunks of a bf16 NHWC view under 2 GiB");
+                  "chunks of a bf16 NHWC view under 2 GiB (or, on the 128-channel tile, a channel-major float32 "
+                  "output)");
     a.tiles_m = (cout + bm - 1) / bm;
     a.tiles_n = (int32_t)((M + 63) / 64);
-    snprintf(name, sizeof name, "vrs_conv1w_bf16_%d_c%d", bm, x.c);
+    snprintf(name, sizeof name, "vrs_conv1w_bf16_%d_c%d%s", bm, x.c, flat ? "_f" : "");
+    if (flat && x.c != 64 && x.c != 256)
+      return fail(VRS_EUNSUPPORTED, "conv: the weight-stationary float32 output tile takes Cin 64 or 256 (Cin=%d)", x.c);
     hipFunction_t f;
     if ((rc = get_fn(ctx, name, &f))) return rc;
     // persistent grid: the resident workgroups, a whole number of streams
@@ -337,7 +341,8 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
     const int64_t streams = std::max<int64_t>(1, std::min<int64_t>(resident / a.tiles_m, a.tiles_n));
     out.push_back(make_launch(name, f, dim3((unsigned)(streams * a.tiles_m)), dim3(512), 0, a));
     out.back().flops = 2.0 * (double)M * cout * (cs.cin_real > 0 ? cs.cin_real : x.c);
-    out.back().bytes = (double)M * x.c * 2.0 + (double)cout * x.c * 2.0 + (double)M * cout * 2.0 + 8.0 * cout;
+    out.back().bytes = (double)M * x.c * 2.0 + (double)cout * x.c * 2.0 + (double)M * cout * (flat ? 4.0 : 2.0) +
+                       8.0 * cout;
     return VRS_OK;
   }
   const int tile = cs.tile ? cs.tile

@@ -34,7 +34,11 @@ namespace {
 constexpr int W1_BN = 64;    // pixels per tile
 constexpr int W1_NT = 512;   // threads per workgroup
 
-template <int BM, int CIN>
+// FLAT: float32 output with the channel stride a.y_sc (the Detect head's
+// channel-major outputs, y_sp == 1): each value of a store unit goes out as
+// its own dword store, the 32 lanes of a half-wave covering 32 consecutive
+// pixels of one channel.
+template <int BM, int CIN, bool FLAT = false>
 __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
   using E = Elt<bf16_t>;
   using G = E::group;
@@ -138,7 +142,7 @@ __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
       o.ok[j] = k >= 0 && m < a.M;
       int pp;
       const int bb = fdivmod(o.ok[j] ? m : 0, HWo, inv_hwo, pp);
-      o.pix[j] = (uint32_t)(((int64_t)bb * a.y_sb + (int64_t)pp * a.y_sp) * 2);
+      o.pix[j] = (uint32_t)(((int64_t)bb * a.y_sb + (int64_t)pp * a.y_sp) * (FLAT ? 4 : 2));
     }
     return o;
   };
@@ -152,8 +156,17 @@ __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
       if (a.act == VRS_ACT_SILU) t = silu_fast(t);
       v[r] = t;
     }
-    const uint32_t off = o.ok[j] && co < a.Cout ? o.pix[j] + (uint32_t)co * 2u : kOOB;
-    __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, ry, off, 0, 0);
+    if constexpr (FLAT) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t off = o.ok[j] && co + r < a.Cout ? o.pix[j] + (uint32_t)((co + r) * a.y_sc * 4) : kOOB;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), ry, off, 0, 0);
+      }
+    } else {
+      const uint32_t off = o.ok[j] && co < a.Cout ? o.pix[j] + (uint32_t)co * 2u : kOOB;
+      __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, ry, off, 0,
+                                            0);
+    }
   };
   auto compute = [&](const bf16_t* sB, f32x16_t (&ac)[TM][TN], const f32x16_t (&ap)[TM][TN], const Out& op) {
 #pragma unroll
@@ -231,3 +244,10 @@ VRS_CONV1W(128, 64)
 VRS_CONV1W(128, 128)
 VRS_CONV1W(128, 192)
 VRS_CONV1W(128, 256)
+// float32 channel-major outputs (the Detect head's box and class convs)
+#define VRS_CONV1W_F(BM, CIN)                                                                        \
+  extern "C" __global__ __launch_bounds__(512) void vrs_conv1w_bf16_##BM##_c##CIN##_f(vrs_conv_args a) { \
+    conv1w_body<BM, CIN, true>(a);                                                                     \
+  }
+VRS_CONV1W_F(128, 64)
+VRS_CONV1W_F(128, 256)
