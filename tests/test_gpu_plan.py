@@ -244,3 +244,36 @@ def test_head_outputs_on_the_weight_stationary_tile():
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_fused_upsample_on_the_256x256_tile():
+    """The neck's fused-upsample 1x1 convs (model.13.cv1, model.16.cv1) on the
+    256x256 tile, and model.16.cv1's leftover pixel tiles on the 128x128
+    fused-upsample tile (batch 44 at 320: 275 tiles on 256 CUs), give outputs
+    bit-identical to the whole convs on the 128x128 tile (the same 64-deep K
+    step order)."""
+    import torch
+    x = dev(np.random.default_rng(12).uniform(0, 1, (44, 3, 320, 320)).astype(np.float32))
+    m0 = _yolo(44, 320, vrs.BF16, autotune=False)
+    P = _params(m0)
+    m0.load(P)
+    names = [pre for pre, _, _ in m0.conv_info()]
+    ups = [names.index("model.13.cv1"), names.index("model.16.cv1")]
+    outs = []
+    for tile in (vrs.TILE_128x128, vrs.TILE_256x256):
+        plan = m0.get_plan()
+        for i in ups:
+            plan[i] = tile
+        m = _yolo(44, 320, vrs.BF16, autotune=False)
+        m.set_plan(plan)
+        m.load(P)
+        outs.append([o.clone() for o in m.forward(x)])
+        if tile == vrs.TILE_256x256:
+            launches = m.launch_names()
+            k16 = [n for n in launches if n.startswith("model.16.cv1:")]
+            assert k16 == ["model.16.cv1:vrs_conv_bf16_256x256_k64_u", "model.16.cv1:vrs_conv_bf16_128x128_k64_u"], k16
+            assert "model.13.cv1:vrs_conv_bf16_256x256_k64_u" in launches
+        m.close()
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))

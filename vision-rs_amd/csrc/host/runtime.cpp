@@ -104,8 +104,9 @@ static const TileInfo* tile_info(int code) {
 }
 
 // Kernel name for a tile, or an error when the combination is not built.
-// up: the fused-upsample instance (_u), built for 128x128, 256x128 and
-// 128x256 in bf16 and 128x128 and 64x256 in float32, aligned and not persistent
+// up: the fused-upsample instance (_u), built for 128x128, 256x128, 128x256
+// and 256x256 in bf16 and 128x128 and 64x256 in float32, aligned and not
+// persistent
 static int tile_kernel(int code, int cin, int dtype, bool up, char* name, size_t n, int* bm, int* bn, int* threads) {
   if ((code & 0xff) == VRS_TILE_H3 || (code & 0xff) == VRS_TILE_W1_256 || (code & 0xff) == VRS_TILE_W1_128)
     return fail(VRS_EINVAL, "conv: the halo and weight-stationary tiles are prepared separately");
@@ -113,7 +114,7 @@ static int tile_kernel(int code, int cin, int dtype, bool up, char* name, size_t
   if (!t) return fail(VRS_EINVAL, "conv: unknown tile code %d", code);
   if (up) {
     const bool built = dtype == VRS_BF16 ? (t->code == VRS_TILE_128x128 || t->code == VRS_TILE_256x128 ||
-                                            t->code == VRS_TILE_128x256)
+                                            t->code == VRS_TILE_128x256 || t->code == VRS_TILE_256x256)
                                          : dtype == VRS_F32 && (t->code == VRS_TILE_128x128 || t->code == VRS_TILE_64x256);
     if (!built || (code & VRS_TILE_PERSIST) || cin % 32 != 0)
       return fail(VRS_EUNSUPPORTED, "conv: no fused-upsample kernel for tile %s (dtype %d, Cin %d)", t->tag, dtype, cin);
@@ -376,13 +377,14 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   // same 64-deep K order (four times the workgroups for the same work, two
   // per CU: the round takes about a quarter of the time).  Same results: each
   // output is one workgroup's accumulation over K in the same step order.
-  if ((tile & 0xff) == VRS_TILE_256x256 && !(tile & VRS_TILE_PERSIST) && !f8 && !cs.up &&
+  if ((tile & 0xff) == VRS_TILE_256x256 && !(tile & VRS_TILE_PERSIST) && !f8 &&
       cs.dtype == VRS_BF16 && a.K % 64 == 0 && cout % 256 == 0) {
     const int64_t G = (int64_t)resident_wgs(f, threads) * (ctx->num_cu > 0 ? ctx->num_cu : 256);
     const int64_t R = blocks % G;
     if (blocks > G && R > 0 && 2 * R <= G && R % a.tiles_m == 0) {
+      const char* rname = cs.up ? "vrs_conv_bf16_128x128_k64_u" : "vrs_conv_bf16_128x128_k64_a";
       hipFunction_t fr;
-      if ((rc = get_fn(ctx, "vrs_conv_bf16_128x128_k64_a", &fr))) return rc;
+      if ((rc = get_fn(ctx, rname, &fr))) return rc;
       const double share = (double)R / (double)blocks;
       out.push_back(make_launch(name, f, dim3((unsigned)(blocks - R)), dim3(threads), 0, a));
       out.back().flops = flops * (1.0 - share);
@@ -392,7 +394,7 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
       b.n_tile0 = (int32_t)((blocks - R) / a.tiles_m * 2);   // in 128-pixel tiles
       b.tiles_n = (int32_t)((M + 127) / 128);
       const int64_t rb = (int64_t)b.tiles_m * (b.tiles_n - b.n_tile0);
-      out.push_back(make_launch("vrs_conv_bf16_128x128_k64_a", fr, dim3((unsigned)rb), dim3(256), 0, b));
+      out.push_back(make_launch(rname, fr, dim3((unsigned)rb), dim3(256), 0, b));
       out.back().flops = flops * share;
       out.back().bytes = bytes * share;
       return VRS_OK;

@@ -883,6 +883,7 @@ VRS_CONV_KERNEL_U(vrs_conv_bf16_256x128_k32_u, bf16_t, 256, 128, 32, 2, 2)
 VRS_CONV_KERNEL_U(vrs_conv_bf16_256x128_k64_u, bf16_t, 256, 128, 64, 2, 2)
 VRS_CONV_KERNEL_U(vrs_conv_bf16_128x256_k32_u, bf16_t, 128, 256, 32, 2, 2)
 VRS_CONV_KERNEL_U(vrs_conv_bf16_128x256_k64_u, bf16_t, 128, 256, 64, 2, 2)
+VRS_CONV_KERNEL_U(vrs_conv_bf16_256x256_k64_u, bf16_t, 256, 256, 64, 2, 4)
 VRS_CONV_KERNEL_U(vrs_conv_f32_128x128_k32_u, float, 128, 128, 32, 2, 2)
 VRS_CONV_KERNEL_U(vrs_conv_f32_64x256_k32_u, float, 64, 256, 32, 1, 4)
 // fp8 e4m3 weights + e4m3-quantised bf16 activations (32x32x64 fp8 MFMA),
