@@ -111,9 +111,10 @@ typedef struct {
 #define VRS_TILE_STEM_PAIR 11
 #define VRS_TILE_K32 0x100
 /* OR VRS_TILE_PERSIST: persistent grid (resident workgroups loop over the
- * tiles with one continuous load stream) for memory-bound shapes; bf16,
- * 128x128 or 64x256, Cin % step == 0, an even number of K steps, no residual,
- * output channel offset/pitch/count multiples of 8. */
+ * tiles with one continuous load stream, so a tile's epilogue overlaps the
+ * next tile's first loads); bf16, 128x128, 64x256 or 256x256 (64-deep steps),
+ * Cin % step == 0, an even number of K steps, no residual, output channel
+ * offset/pitch/count multiples of 8. */
 #define VRS_TILE_PERSIST 0x200
 
 typedef struct {

@@ -311,6 +311,12 @@ PERSIST_CASES = [
     (4, 64, 60, 60, 64, 3, 1, vrs.TILE_64x256 | vrs.TILE_K32 | vrs.TILE_PERSIST),
     (2, 64, 41, 37, 32, 3, 2, vrs.TILE_64x256 | vrs.TILE_K32 | vrs.TILE_PERSIST),
     (2, 128, 30, 22, 128, 3, 1, vrs.TILE_128x128 | vrs.TILE_PERSIST),
+    # 256x256 (8 waves, epilogue stored from the accumulators): 966 tiles on
+    # 256 workgroups (3-4 each); 576 tiles = 2 rounds + 64 leftover tiles on
+    # the 128x128 tile; a 3x3/s2 conv with 273 tiles (1 round + 17 leftover)
+    (16, 128, 112, 138, 256, 1, 1, vrs.TILE_256x256 | vrs.TILE_PERSIST),
+    (16, 128, 96, 96, 256, 1, 1, vrs.TILE_256x256 | vrs.TILE_PERSIST),
+    (64, 128, 66, 66, 256, 3, 2, vrs.TILE_256x256 | vrs.TILE_PERSIST),
 ]
 
 

@@ -133,8 +133,9 @@ static int tile_kernel(int code, int cin, int dtype, bool up, char* name, size_t
   const bool g = cin % 32 != 0;
   bool k64 = !(code & VRS_TILE_K32) && dtype == VRS_BF16 && cin % 64 == 0 && t->code != VRS_TILE_32x256;
   if (code & VRS_TILE_PERSIST) {
-    if (dtype != VRS_BF16 || g || (t->code != VRS_TILE_128x128 && t->code != VRS_TILE_64x256) ||
-        (t->code == VRS_TILE_64x256 && k64))
+    if (dtype != VRS_BF16 || g ||
+        (t->code != VRS_TILE_128x128 && t->code != VRS_TILE_64x256 && t->code != VRS_TILE_256x256) ||
+        (t->code == VRS_TILE_64x256 && k64) || (t->code == VRS_TILE_256x256 && !k64))
       return fail(VRS_EUNSUPPORTED, "conv: persistent tile %s%s not built for this dtype/Cin", t->tag,
                   k64 ? " k64" : "");
     snprintf(name, n, "vrs_conv_bf16_%s_k%d_p", t->tag, k64 ? 64 : 32);
@@ -211,8 +212,11 @@ std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int s
       const int64_t b128 = (int64_t)((cout + 127) / 128) * ((m + 127) / 128);
       if (g || (m > 0 && b128 >= 2ll * (num_cu > 0 ? num_cu : 256))) continue;
     }
-    if (!t.k32) {  // 64-deep only
-      if (dtype == VRS_BF16 && cin % 64 == 0 && cout >= t.bm) c.push_back(t.code);
+    if (!t.k32) {  // 64-deep only (256x256), also persistent with an even step count
+      if (dtype == VRS_BF16 && cin % 64 == 0 && cout >= t.bm) {
+        c.push_back(t.code);
+        if ((k * k * cin / 64) % 2 == 0) c.push_back(t.code | VRS_TILE_PERSIST);
+      }
       continue;
     }
     c.push_back(t.code);
@@ -357,6 +361,7 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   if (blocks >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: grid too large");
   hipFunction_t f;
   if ((rc = get_fn(ctx, name, &f))) return rc;
+  const int64_t tiles_total = blocks;
   if (tile & VRS_TILE_PERSIST) {
     const int bk = strstr(name, "_k64_") ? 64 : 32;
     if (a.res || !a.stage || a.y_f32 || a.K % (2 * bk) != 0)
@@ -373,25 +378,31 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
                        (double)M * cout * (a.y_f32 ? 4.0 : es) + (a.res ? (double)M * cout * es : 0.0) + 8.0 * cout;
   // Partial last round of 256x256 tiles (one workgroup per CU): when the
   // tiles leave a last round at most half full, the full rounds run on the
-  // 256x256 tile and the leftover pixel tiles on the 128x128 tile of the
+  // 256x256 tile (persistent: one workgroup per CU looping over an equal
+  // share of them) and the leftover pixel tiles on the 128x128 tile of the
   // same 64-deep K order (four times the workgroups for the same work, two
   // per CU: the round takes about a quarter of the time).  Same results: each
   // output is one workgroup's accumulation over K in the same step order.
-  if ((tile & 0xff) == VRS_TILE_256x256 && !(tile & VRS_TILE_PERSIST) && !f8 &&
-      cs.dtype == VRS_BF16 && a.K % 64 == 0 && cout % 256 == 0) {
+  if ((tile & 0xff) == VRS_TILE_256x256 && !f8 && cs.dtype == VRS_BF16 && a.K % 64 == 0 && cout % 256 == 0) {
     const int64_t G = (int64_t)resident_wgs(f, threads) * (ctx->num_cu > 0 ? ctx->num_cu : 256);
-    const int64_t R = blocks % G;
-    if (blocks > G && R > 0 && 2 * R <= G && R % a.tiles_m == 0) {
+    const int64_t R = tiles_total % G;
+    if (tiles_total > G && R > 0 && 2 * R <= G && R % a.tiles_m == 0) {
       const char* rname = cs.up ? "vrs_conv_bf16_128x128_k64_u" : "vrs_conv_bf16_128x128_k64_a";
       hipFunction_t fr;
       if ((rc = get_fn(ctx, rname, &fr))) return rc;
-      const double share = (double)R / (double)blocks;
-      out.push_back(make_launch(name, f, dim3((unsigned)(blocks - R)), dim3(threads), 0, a));
+      const double share = (double)R / (double)tiles_total;
+      if (tile & VRS_TILE_PERSIST) {   // one workgroup per CU, each taking the same number of tiles
+        vrs_conv_args p = a;
+        p.tiles_n = (int32_t)((tiles_total - R) / a.tiles_m);
+        out.push_back(make_launch(name, f, dim3((unsigned)G), dim3(threads), 0, p));
+      } else {
+        out.push_back(make_launch(name, f, dim3((unsigned)(tiles_total - R)), dim3(threads), 0, a));
+      }
       out.back().flops = flops * (1.0 - share);
       out.back().bytes = bytes * (1.0 - share);
       vrs_conv_args b = a;
       b.tiles_m = cout / 128;
-      b.n_tile0 = (int32_t)((blocks - R) / a.tiles_m * 2);   // in 128-pixel tiles
+      b.n_tile0 = (int32_t)((tiles_total - R) / a.tiles_m * 2);   // in 128-pixel tiles
       b.tiles_n = (int32_t)((M + 127) / 128);
       const int64_t rb = (int64_t)b.tiles_m * (b.tiles_n - b.n_tile0);
       out.push_back(make_launch(rname, fr, dim3((unsigned)rb), dim3(256), 0, b));

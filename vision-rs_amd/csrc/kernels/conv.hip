@@ -656,7 +656,10 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
 // its own LDS area, not the pipeline buffers -- runs while they land.  Stores
 // are raw buffer stores with a fixed count per lane (out-of-range chunks use
 // out-of-range offsets), so waiting for the next loads never waits for them.
-template <int BM, int BN, int BK, int WGM, int WGN>
+// DIRECT (the 8-wave 256x256 tile, whose two pipeline stages leave no LDS
+// for a staging area): the epilogue stores each lane's 4 channels of a pixel
+// as one 8-byte raw-buffer store straight from the accumulators.
+template <int BM, int BN, int BK, int WGM, int WGN, bool DIRECT = false>
 __device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
   using T = bf16_t;
   using E = Elt<T>;
@@ -675,7 +678,7 @@ __device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
   static_assert(WTN * CPP % 64 == 0, "whole store rounds");
   __shared__ __attribute__((aligned(16))) T smem0[TILE_ELEMS];
   __shared__ __attribute__((aligned(16))) T smem1[TILE_ELEMS];
-  __shared__ __attribute__((aligned(16))) T sstage[WGM * WGN * WTN * SROW];
+  __shared__ __attribute__((aligned(16))) T sstage[DIRECT ? 8 : WGM * WGN * WTN * SROW];
   auto sbuf = [&](int b) -> T* { return b ? smem1 : smem0; };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   static_assert(!SWZ || (NT / GPR) % 4 == 0, "swizzle period");
@@ -803,6 +806,32 @@ __device__ __forceinline__ void conv_persist_body(const vrs_conv_args& a) {
       step(0, ra1, rb1, ra0, rb0);
       step(1, ra0, rb0, ra1, rb1);
     }
+    if constexpr (DIRECT) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float sc[4], sh[4];
+          c_scale.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sc);
+          c_shift.quad(m0 + wm * WTM + i * 32 + g * 8, hmask, sh);
+          const int co = m0 + wm * WTM + i * 32 + g * 8 + hq * 4;
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float t = acc[i][j][g * 4 + r] * sc[r] + sh[r];
+              if (a.act == VRS_ACT_SILU) t = silu_fast(t);
+              v[r] = t;
+            }
+            const int m = n0 + wn * WTN + j * 32 + (lane & 31);
+            const uint32_t off = m < a.M && co < a.Cout ? ((uint32_t)m * (uint32_t)a.y_sp + (uint32_t)co) * 2u : kOOB;
+            __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, ry,
+                                                  off, 0, 0);
+          }
+        }
+      continue;
+    }
     // epilogue: this wave's (WTN pixel x WTM channel) tile -> its staging
     // area -> 16-byte NHWC chunks.  Register g*4 + r of MFMA tile (i, j) is
     // channel i*32 + g*8 + hq*4 + r of pixel j*32 + (lane & 31).
@@ -900,6 +929,10 @@ VRS_CONV_KERNEL_U(vrs_conv_f32_64x256_k32_u, float, 64, 256, 32, 1, 4)
 VRS_CONV_P(vrs_conv_bf16_128x128_k32_p, 128, 128, 32, 2, 2)
 VRS_CONV_P(vrs_conv_bf16_64x256_k32_p, 64, 256, 32, 1, 4)
 VRS_CONV_P(vrs_conv_bf16_128x128_k64_p, 128, 128, 64, 2, 2)
+// 8 waves of 128x64 (as the 256x256 tile), epilogue stored from the accumulators
+extern "C" __global__ __launch_bounds__(512, 2) void vrs_conv_bf16_256x256_k64_p(vrs_conv_args a) {
+  conv_persist_body<256, 256, 64, 2, 4, true>(a);
+}
 
 VRS_CONV_F8(vrs_conv_fp8_128x128_k64_a, 128, 128, 2, 2)
 VRS_CONV_F8(vrs_conv_fp8_256x128_k64_a, 256, 128, 2, 2)
