@@ -713,11 +713,8 @@ int dev_upload(vrs_model* m, const void* host, size_t bytes, void** dev) {
   return VRS_OK;
 }
 
-// Time every applicable tile of each dense NHWC conv on the model's own
-// buffers (contents do not matter for timing; a forward rewrites them all)
-// and keep the fastest.  Replaces the reference's shape-adaptive tile choice
-// in TritonLowering (examples/yolo26.rs:3027).
-// convs with a tile choice: dense ones, into a buffer or a Detect output
+// The convs with a tile choice (the ones a plan entry applies to): the dense
+// convs, into a buffer or a Detect output.
 bool tunable(const ConvStep& c) { return !c.dw && !c.stem && (c.out_idx >= 0 || c.y.buf >= 0); }
 
 // The launches of conv c with spec cs (tile, dtype, activation set by the
@@ -737,6 +734,11 @@ int prep_conv_step(const vrs_model* m, const ConvStep& c, ConvSpec cs, const voi
   return prep_conv(m->ctx, cs, view_of(m, c.x), w, scale, c.shift, c.has_res ? &r : nullptr, view_of(m, c.y), ls);
 }
 
+// Time every applicable tile of each dense conv on the model's own buffers
+// (contents do not matter for timing; a forward rewrites them all; the
+// Detect output convs write scratch outputs) and keep the fastest.  Replaces
+// the reference's shape-adaptive tile choice in TritonLowering
+// (examples/yolo26.rs:3027).
 int autotune_tiles(vrs_model* m) {
   hipStream_t s;
   VRS_HIP(hipStreamCreate(&s));
@@ -968,9 +970,6 @@ int finalize_upload(vrs_model* m) {
   }
   return VRS_OK;
 }
-
-// Tiles of a dense NHWC conv that the autotuner would consider (the convs a
-// plan entry applies to).
 
 // A caller's tile plan (vrs_model_set_plan) instead of autotuning: every
 // entry is checked against the kernels built for its conv's shape.
