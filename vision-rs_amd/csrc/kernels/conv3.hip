@@ -262,15 +262,25 @@ __device__ __forceinline__ void conv3h_body(const vrs_conv_args& a) {
   if (a.act == VRS_ACT_SILU) epilogue(std::true_type{});
   else epilogue(std::false_type{});
   __builtin_amdgcn_wave_barrier();   // this wave reads back only its own staging
+  // 16-byte raw-buffer stores at 32-bit offsets (the host bounds the view by
+  // y_bytes < 2^31); the pixel's row in the strip by float-reciprocal divmod
   constexpr int CPP = BM / 8;        // 16-byte chunks per pixel
-  for (int c = lane; c < 64 * CPP; c += 64) {
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, a.y_bytes);
+  const float inv_tw = 1.0f / (float)TW;
+#pragma unroll
+  for (int s = 0; s < CPP; ++s) {
+    const int c = lane + 64 * s;
     const int pl = c / CPP, part = c % CPP;
-    const int q = q0 + wave * 64 + pl;
-    const int yy = q / TW, xx = x0 + (q - yy * TW);
+    int xl;
+    const int yy = fdivmod(q0 + wave * 64 + pl, TW, inv_tw, xl);
+    const int xx = x0 + xl;
     const int co = m0 + part * 8;
-    if (yy >= a.H || xx >= a.W || co >= a.Cout) continue;
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stg + pl * SROW + part * 8);
-    *reinterpret_cast<u32x4_t*>(reinterpret_cast<bf16_t*>(a.y) + b * a.y_sb + ((int64_t)yy * a.Wo + xx) * a.y_sp + co) = v;
+    const uint32_t off = yy < a.H && xx < a.W && co < a.Cout
+                             ? ((uint32_t)b * (uint32_t)a.y_sb + (uint32_t)(yy * a.Wo + xx) * (uint32_t)a.y_sp +
+                                (uint32_t)co) * 2u
+                             : kOOB;
+    __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4_t*>(stg + pl * SROW + part * 8), ry, off, 0,
+                                           0);
   }
 }
 
