@@ -120,7 +120,8 @@ typedef struct {
 typedef struct {
   int32_t k;        /* square kernel size; padding = k/2 (blocks/conv.rs:36) */
   int32_t stride;
-  int32_t groups;   /* 1 = dense (implicit GEMM on MFMA); == channels = depthwise */
+  int32_t groups;   /* 1 = dense (implicit GEMM on MFMA); == channels = depthwise;
+                       else grouped (Cin and Cout divisible by groups) */
   int32_t act;      /* VRS_ACT_NONE or VRS_ACT_SILU */
   int32_t dtype;    /* VRS_BF16 or VRS_F32: element type of x, y, res;
                        VRS_FP8 (dense, Cin % 64 == 0): bf16 x/y/res, e4m3 weights */
@@ -135,9 +136,15 @@ typedef struct {
  * blocks/bottleneck.rs:24-63 record them.
  *   y = act(scale[co] * conv(x, w)[co] + shift[co]) + res
  * w: packed by vrs_pack_conv_weight in `dtype` elements (dense
- *    [Cout][k][k][Cin]; depthwise tap-major [k*k][C]).
+ *    [Cout][k][k][Cin]; depthwise tap-major [k*k][C]; grouped
+ *    [Cout][k][k][Cin/groups]).
  * Dense requires x->c % 8 == 0; depthwise is 3x3 with stride 1 or 2;
- * res may be NULL (dense only). */
+ * res may be NULL (not taken by depthwise).  Grouped (1 < groups, not
+ * depthwise; conv_bn's Conv2d::new_grouped, blocks/conv.rs:51-69): groups
+ * with Cin/groups % 8 == 0, Cout/groups % 4 == 0 and Cin*Cout/groups^2 >=
+ * 1024 run as one implicit-GEMM launch per group on channel slices (VRS_FP8
+ * also needs Cin/groups % 64 == 0), others on a direct kernel (bf16/f32, any
+ * channel offsets). */
 int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const void* w,
                const float* scale, const float* shift, const vrs_nhwc* res, const vrs_nhwc* y,
                void* stream);
@@ -145,7 +152,9 @@ int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const vo
 /* Host-side weight repack from the reference's OIHW float32 layout
  * (nn::Conv2d weight) into the device layout vrs_conv2d reads:
  *   dense:  [Cout][k][k][cin_pad] in `dtype` (cin_pad >= Cin, zero filled)
- *   depthwise (groups == Cout): tap-major [k*k][Cout] in `dtype`.
+ *   depthwise (groups == Cout, cin_per_group == 1): tap-major [k*k][Cout]
+ *   grouped (other groups > 1): [Cout][k][k][cin_per_group], cin_pad ==
+ *     cin_per_group, Cout % groups == 0.
  * Returns the byte count needed when out == NULL. */
 int64_t vrs_pack_conv_weight(const float* w_oihw, int32_t cout, int32_t cin_per_group, int32_t k,
                              int32_t groups, int32_t cin_pad, int32_t dtype, void* out);
@@ -310,7 +319,8 @@ int vrs_msda(vrs_ctx* ctx, const vrs_msda_desc* d, const float* value, const flo
 typedef struct {
   int32_t kind;
   int32_t c_in, c_out;
-  int32_t k, s, g;          /* VRS_BLOCK_CONV */
+  int32_t k, s, g;          /* VRS_BLOCK_CONV; g: groups (1 dense, c_in == c_out
+                               depthwise, else grouped; conv_plain is dense) */
   int32_t conv_kind;        /* VRS_CONV_* for VRS_BLOCK_CONV */
   int32_t n;                /* repeats (c3k2, c2psa, c3k2_psa) */
   int32_t c3k, shortcut;    /* c3k2 flags; sppf shortcut */

@@ -87,6 +87,29 @@ def test_depthwise_fixture_f32():
     assert np.max(np.abs(y - exp)) < 1e-5
 
 
+@pytest.mark.parametrize("dtype", [vrs.F32, vrs.BF16])
+@pytest.mark.parametrize("cin,cout,g,kernel", [
+    (128, 128, 2, "vrs_conv_"),    # 64 x 64 channels per group: one implicit-GEMM launch per group
+    (64, 96, 16, "vrs_gconv_"),    # 4 x 6 per group: the direct kernel
+    (12, 8, 4, "vrs_gconv_"),      # 3 x 2 per group; the packed input carries 4 zero channels
+])
+def test_grouped_conv_block(dtype, cin, cout, g, kernel):
+    """conv_bn with 1 < g < c (blocks/conv.rs:51-69) through the model runtime
+    against the oracle's conv_bn, and the launches it takes."""
+    desc = vrs.block(vrs.BLOCK_CONV, cin, cout, k=3, s=1, g=g, conv_kind=vrs.CONV_BN)
+    rnd = bf16_round if dtype == vrs.BF16 else (lambda v: v)
+    m = vrs.Model(ctx(), desc, 2, 13, 11, dtype, 1e-3)
+    P = {k: (rnd(v) if v.ndim == 4 else v) for k, v in seeded_params(m.params(), 5, bn="random").items()}
+    x = rnd(np.random.default_rng(6).standard_normal((2, cin, 13, 11)).astype(np.float32))
+    (y,), mm = run_model(desc, P, x, dtype, 1e-3)
+    ref = Y.conv_bn(cin, cout, 3, 1, g)(Y.Params(P, eps=1e-3), "", x)
+    tol, floor = (2e-2, 1e-1) if dtype == vrs.BF16 else (1e-4, 5e-2)
+    assert rel_err(y, ref, floor) < tol
+    names = [n for n in mm.launch_names() if n.startswith("conv:")]
+    assert all(n.startswith("conv:" + kernel) for n in names), names
+    assert len(names) == (g if kernel == "vrs_conv_" else 1)
+
+
 # ------------------------------------------------------- bf16 vs the oracle --
 
 def bf16_block_errors(got, ref):

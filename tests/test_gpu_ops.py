@@ -500,6 +500,70 @@ def test_dwconv(dtype, act, shape):
         assert torch.all(rest == 7.0)
 
 
+GCONV_CASES = [
+    # n, cin, h, w, cout, groups, k, s, residual, (x pitch, x c_off), (y pitch, y c_off)
+    (2, 8, 9, 7, 12, 4, 3, 1, False, None, None),              # direct kernel: 2 -> 3 channels per group
+    (2, 24, 10, 11, 36, 3, 3, 2, True, (40, 5), (48, 3)),      # direct: odd channel offsets, residual
+    (1, 6, 5, 5, 4, 2, 1, 1, False, None, None),               # direct, 1x1
+    (2, 64, 7, 6, 64, 8, 5, 1, False, None, None),             # direct, 5x5, 8 x 8 per group
+    (2, 128, 12, 12, 128, 2, 3, 1, True, None, None),          # one dense launch per group (64 x 64)
+    (2, 256, 9, 9, 128, 4, 1, 1, False, (272, 16), (144, 8)),  # dense per group on channel slices
+    (1, 96, 11, 13, 192, 3, 3, 2, False, None, None),          # dense per group (32 x 64), stride 2
+]
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("case", GCONV_CASES)
+def test_grouped_conv2d(case, dtype):
+    """groups not in {1, C} (conv_bn's Conv2d::new_grouped, blocks/conv.rs:51-69)
+    against the oracle's grouped conv."""
+    import torch
+    n, cin, h, w, cout, G, k, s, with_res, xv, yv = case
+    rnd = rounder(dtype)
+    rng = np.random.default_rng(zlib.crc32(repr(case).encode()))
+    x = rnd(rng.standard_normal((n, cin, h, w)).astype(np.float32))
+    cg = cin // G
+    wt = rnd((rng.standard_normal((cout, cg, k, k)) * np.sqrt(2.0 / (cg * k * k))).astype(np.float32))
+    scale = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    ho, wo = (h + 2 * (k // 2) - k) // s + 1, (w + 2 * (k // 2) - k) // s + 1
+    res = rnd(rng.standard_normal((n, cout, ho, wo)).astype(np.float32)) if with_res else None
+    ref = oracle.affine_act(oracle.conv2d(x, wt, s, k // 2, groups=G), scale, shift, 1)
+    if with_res:
+        ref = ref + res
+    xp, xo = xv or (cin, 0)
+    yp, yo = yv or (cout, 0)
+    xt = to_nhwc(x, dtype, xp, xo)
+    yt = torch.full((n, ho, wo, yp), 7.0, dtype=tdtype(dtype), device="cuda")
+    rt = to_nhwc(res, dtype, yp, yo) if with_res else None
+    ctx().conv2d(vrs.nhwc(xt, cin, xo), dev(vrs.pack_conv_weight(wt, G, None, dtype)), dev(scale), dev(shift),
+                 vrs.nhwc(yt, cout, yo), k, s, G, vrs.ACT_SILU, vrs.nhwc(rt, cout, yo) if with_res else None, dtype)
+    torch.cuda.synchronize()
+    err = rel_err(from_nhwc(yt, cout, yo), ref, FLOOR[dtype])
+    assert err < TOL[dtype], err
+    if yp > cout:
+        rest = torch.cat([yt[..., :yo], yt[..., yo + cout:]], -1).float()
+        assert torch.all(rest == 7.0)
+
+
+def test_grouped_fixture_f32():
+    """The reference's g4 grouped-conv fixture (tests/test_conv_grouped_cuda.rs,
+    groups 4, 2 input channels per group; 1e-5 absolute) through vrs_conv2d
+    with unit scale, zero shift and no activation."""
+    import torch
+    from golden_io import load
+    x = load("conv_grouped/g4/x.bin", (2, 8, 4, 4))
+    w = load("conv_grouped/g4/conv_w.bin", (8, 2, 3, 3))
+    exp = load("conv_grouped/g4/expected_output.bin", (2, 8, 4, 4))
+    xt = to_nhwc(x, vrs.F32)
+    yt = torch.zeros((2, 4, 4, 8), dtype=torch.float32, device="cuda")
+    one, zero = np.ones(8, np.float32), np.zeros(8, np.float32)
+    ctx().conv2d(vrs.nhwc(xt), dev(vrs.pack_conv_weight(w, 4, None, vrs.F32)), dev(one), dev(zero), vrs.nhwc(yt),
+                 3, 1, 4, vrs.ACT_NONE, None, vrs.F32)
+    torch.cuda.synchronize()
+    assert np.max(np.abs(from_nhwc(yt, 8, 0) - exp)) < 1e-5
+
+
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("hw", [(20, 20), (7, 5), (4, 4), (26, 26), (30, 22), (40, 40), (1, 9), (13, 1),
                                 (20, 20, 64), (9, 11, 96)])
@@ -724,5 +788,6 @@ def test_errors_are_reported_not_fatal():
     with pytest.raises(vrs.VrsError) as e:  # Cin 12 is not a multiple of 8
         C.conv2d(vrs.nhwc(x), w, s, s, vrs.nhwc(y), 1, 1, 1, vrs.ACT_SILU, None, vrs.BF16)
     assert e.value.code == -2
-    with pytest.raises(vrs.VrsError):  # groups other than 1 / depthwise
-        C.conv2d(vrs.nhwc(y), w, s, s, vrs.nhwc(y), 3, 1, 2, vrs.ACT_SILU, None, vrs.BF16)
+    with pytest.raises(vrs.VrsError) as e:  # groups must divide both channel counts
+        C.conv2d(vrs.nhwc(y), w, s, s, vrs.nhwc(y), 3, 1, 3, vrs.ACT_SILU, None, vrs.BF16)
+    assert e.value.code == -2

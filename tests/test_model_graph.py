@@ -86,3 +86,16 @@ def test_record_only_model_cannot_run():
     with pytest.raises(vrs.VrsError) as e:
         m.load(seeded_params(m.params()))
     assert e.value.code == -7
+
+
+def test_grouped_conv_block_params():
+    # conv_bn with 1 < g < c (blocks/conv.rs:51-69): weight [c_out, c_in/g, k, k];
+    # g = c_in = c_out is the depthwise form; g must divide both channel counts
+    specs = dict(record(vrs.block(vrs.BLOCK_CONV, 64, 96, k=3, g=4, conv_kind=vrs.CONV_BN), 8, 8).params())
+    assert specs["conv.weight"] == (96, 16, 3, 3) and specs["bn.running_var"] == (96,)
+    specs = dict(record(vrs.block(vrs.BLOCK_CONV, 64, 64, k=3, g=64, conv_kind=vrs.CONV_BN), 8, 8).params())
+    assert specs["conv.weight"] == (64, 1, 3, 3)
+    for c_in, c_out, g, kind, code in [(64, 96, 5, vrs.CONV_BN, -2), (64, 64, 2, vrs.CONV_PLAIN, -3)]:
+        with pytest.raises(vrs.VrsError) as e:
+            record(vrs.block(vrs.BLOCK_CONV, c_in, c_out, k=3, g=g, conv_kind=kind), 8, 8)
+        assert e.value.code == code

@@ -40,11 +40,9 @@ def _shapes(family, table):
 
 @pytest.mark.parametrize("sub,cin,cout,g", [("depthwise", 128, 128, 128), ("g4", 8, 8, 4)])
 def test_conv_grouped(sub, cin, cout, g):
-    """The reference's grouped-conv fixtures against the oracle.  The g4 case
-    pins the oracle only: the library takes groups 1 (Conv, blocks/conv.rs:31-46)
-    or groups == C (DWConv, blocks/conv.rs:75-85) -- every YOLO26 conv is one of
-    the two -- and rejects any other group count with VRS_EUNSUPPORTED
-    (test_grouped_conv_other_than_depthwise_is_rejected)."""
+    """The reference's grouped-conv fixtures against the oracle (the GPU runs
+    the same fixtures: test_gpu_blocks.test_depthwise_fixture_f32 and
+    test_gpu_ops.test_grouped_fixture_f32)."""
     x = load(f"conv_grouped/{sub}/x.bin", (2, cin, 4, 4))
     w = load(f"conv_grouped/{sub}/conv_w.bin", (cout, cin // g, 3, 3))
     exp = load(f"conv_grouped/{sub}/expected_output.bin", (2, cout, 4, 4))
@@ -52,13 +50,30 @@ def test_conv_grouped(sub, cin, cout, g):
     assert np.max(np.abs(y - exp)) < 1e-5
 
 
-def test_grouped_conv_other_than_depthwise_is_rejected():
-    """groups not in {1, C}: the weight packer (and vrs_conv2d) refuse it."""
+def test_grouped_weight_pack_layout():
+    """groups not in {1, C}: the packer writes each output channel's Cin/groups
+    inputs in the dense order [Cout][k][k][Cin/groups] (the OIHW weight with
+    I moved last); channel padding and Cout not divisible by groups are refused.
+    Depthwise (groups == Cout, one input per group) stays tap-major."""
     from gpu_util import vrs
     w = load("conv_grouped/g4/conv_w.bin", (8, 2, 3, 3))
-    with pytest.raises(vrs.VrsError) as e:
-        vrs.pack_conv_weight(w, groups=4)
-    assert e.value.code == -3   # VRS_EUNSUPPORTED
+    got = np.frombuffer(vrs.pack_conv_weight(w, groups=4, dtype=vrs.F32).tobytes(), np.float32)
+    assert np.array_equal(got, w.transpose(0, 2, 3, 1).ravel())
+    got = np.frombuffer(vrs.pack_conv_weight(w, groups=4).tobytes(), np.uint16)
+    assert np.array_equal(got, (bf16_bits(w.transpose(0, 2, 3, 1).ravel())))
+    for kw in ({"groups": 4, "cin_pad": 8}, {"groups": 3}):
+        with pytest.raises(vrs.VrsError) as e:
+            vrs.pack_conv_weight(w, **kw)
+        assert e.value.code == -1   # VRS_EINVAL
+    wd = load("conv_grouped/depthwise/conv_w.bin", (128, 1, 3, 3))
+    got = np.frombuffer(vrs.pack_conv_weight(wd, groups=128, dtype=vrs.F32).tobytes(), np.float32)
+    assert np.array_equal(got, wd.reshape(128, 9).T.ravel())
+
+
+def bf16_bits(v):
+    """float32 -> bfloat16 bits, round to nearest even (finite inputs)."""
+    u = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
 def test_conv_stem_train_bn():

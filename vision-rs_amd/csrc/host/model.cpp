@@ -42,6 +42,7 @@ struct ConvStep {
   std::string pre;
   int kind = CK_BN_SILU;
   bool dw = false;
+  int groups = 1;            // 1 < groups < channels: grouped conv_bn (dw: groups == channels)
   int k = 1, s = 1, cin = 0, cout = 0;
   V x, y;
   bool has_res = false;
@@ -161,10 +162,10 @@ class Builder {
     m_->params.push_back(std::move(p));
   }
 
-  int conv_common(const std::string& pre, V x, int cout, int k, int s, int kind, bool dw) {
+  int conv_common(const std::string& pre, V x, int cout, int k, int s, int kind, bool dw, int groups = 1) {
     ConvStep c;
-    c.pre = pre; c.kind = kind; c.dw = dw; c.k = k; c.s = s; c.cin = x.c; c.cout = cout; c.x = x;
-    const int cin_g = dw ? 1 : real_cin(x);
+    c.pre = pre; c.kind = kind; c.dw = dw; c.groups = groups; c.k = k; c.s = s; c.cin = x.c; c.cout = cout; c.x = x;
+    const int cin_g = dw ? 1 : groups > 1 ? x.c / groups : real_cin(x);
     c.cin_real = real_cin(x);
     if (kind == CK_PLAIN) {
       add_param(J(pre, "weight"), {cout, cin_g, k, k});
@@ -187,6 +188,14 @@ class Builder {
   // dwconv() (SiLU) and conv_bn(g = c) (no act): blocks/conv.rs:53-85
   void dwconv(const std::string& pre, V x, V y, int k, int s, int kind) {
     const int i = conv_common(pre, x, y.c, k, s, kind, true);
+    m_->convs[i].y = y;
+    push_conv(i);
+  }
+  // conv_bn() with 1 < g < channels (blocks/conv.rs:51-69)
+  void gconv(const std::string& pre, V x, V y, int k, int s, int kind, int g) {
+    // the input view without the packed input's zero channels (they would
+    // shift every group's channel range)
+    const int i = conv_common(pre, slice(x, 0, real_cin(x)), y.c, k, s, kind, false, g);
     m_->convs[i].y = y;
     push_conv(i);
   }
@@ -385,10 +394,11 @@ int build(vrs_model* m) {
   switch (d.kind) {
     case VRS_BLOCK_CONV: {
       V x = b.input(d.c_in);
-      const bool dw = d.g > 1;
-      if (dw && (d.g != d.c_in || d.c_in != d.c_out)) return fail(VRS_EUNSUPPORTED, "conv block: groups 1 or depthwise");
+      const bool dw = d.g > 1 && d.g == d.c_in && d.c_in == d.c_out;
+      if (d.g < 1 || d.c_in % d.g || d.c_out % d.g)
+        return fail(VRS_EBADSHAPE, "conv block: channels %d -> %d not divisible by groups %d", d.c_in, d.c_out, d.g);
       if (d.conv_kind == VRS_CONV_PLAIN) {
-        if (dw) return fail(VRS_EUNSUPPORTED, "conv_plain is dense");
+        if (d.g > 1) return fail(VRS_EUNSUPPORTED, "conv_plain is dense");
         const int ho = (m->in_h + 2 * (d.k / 2) - d.k) / d.s + 1, wo = (m->in_w + 2 * (d.k / 2) - d.k) / d.s + 1;
         if (d.s != 1) return fail(VRS_EUNSUPPORTED, "conv_plain block: stride 1 only");
         const int64_t hw = (int64_t)ho * wo;
@@ -400,6 +410,7 @@ int build(vrs_model* m) {
       const int ho = (m->in_h + 2 * (d.k / 2) - d.k) / d.s + 1, wo = (m->in_w + 2 * (d.k / 2) - d.k) / d.s + 1;
       V y = b.alloc(ho, wo, d.c_out);
       if (dw) b.dwconv("", x, y, d.k, d.s, kind);
+      else if (d.g > 1) b.gconv("", x, y, d.k, d.s, kind, d.g);
       else b.conv("", x, y, d.k, d.s, kind);
       b.output(y);
       return VRS_OK;
@@ -533,7 +544,7 @@ bool pair_eligible(const vrs_model* m, size_t i) {
   const ConvStep& s = m->convs[i - 1];
   const ConvStep& c = m->convs[i];
   if (!s.stem || s.cout != 64 || s.kind != CK_BN_SILU || s.y.buf < 0) return false;
-  if (c.dw || c.stem || c.k != 3 || c.s != 2 || c.cin != 64 || c.cout != 128 || c.kind != CK_BN_SILU || c.has_res ||
+  if (c.dw || c.groups > 1 || c.stem || c.k != 3 || c.s != 2 || c.cin != 64 || c.cout != 128 || c.kind != CK_BN_SILU || c.has_res ||
       c.has_up || c.out_idx >= 0 || c.y.buf < 0)
     return false;
   if (c.x.buf != s.y.buf || c.x.c_off != s.y.c_off || c.x.c != s.y.c) return false;
@@ -614,6 +625,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         }
         ConvSpec cs;
         cs.k = c.k; cs.stride = c.s; cs.dtype = act_dt(m); cs.depthwise = c.dw;
+        cs.groups = c.groups;
         cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
         cs.cin_real = c.cin_real != c.cin ? c.cin_real : 0;
         cs.tile = c.tile == VRS_TILE_STEM_PAIR ? VRS_TILE_AUTO : c.tile;   // unfused: fp8 calibration
@@ -715,7 +727,7 @@ int dev_upload(vrs_model* m, const void* host, size_t bytes, void** dev) {
 
 // The convs with a tile choice (the ones a plan entry applies to): the dense
 // convs, into a buffer or a Detect output.
-bool tunable(const ConvStep& c) { return !c.dw && !c.stem && (c.out_idx >= 0 || c.y.buf >= 0); }
+bool tunable(const ConvStep& c) { return !c.dw && c.groups == 1 && !c.stem && (c.out_idx >= 0 || c.y.buf >= 0); }
 
 // The launches of conv c with spec cs (tile, dtype, activation set by the
 // caller) and weights w / scale: into its NHWC view, or, for a Detect output
@@ -887,7 +899,7 @@ void fuse_upsamples(vrs_model* m) {
     bool fuse = nreaders == 1 && m->steps[reader].type == Step::CONV;
     if (fuse) {
       ConvStep& c = m->convs[m->steps[reader].conv];
-      fuse = !c.dw && !c.stem && c.k == 1 && c.s == 1 && c.out_idx < 0 && c.x.buf == up.b.buf &&
+      fuse = !c.dw && c.groups == 1 && !c.stem && c.k == 1 && c.s == 1 && c.out_idx < 0 && c.x.buf == up.b.buf &&
              c.x.c_off == up.b.c_off && c.x.c > up.b.c && up.b.c % 64 == 0 && up.a.c == up.b.c;
       if (fuse) {
         c.up = up.a;
@@ -928,8 +940,8 @@ int finalize_upload(vrs_model* m) {
       if (rf) return fail(rf, "%s: BN fold: %s", c.pre.c_str(), vrs_last_error());
     }
     const int cin_g = w->dims[1];
-    const int groups = c.dw ? c.cout : 1;
-    const int cin_pad = c.dw ? 1 : c.cin;
+    const int groups = c.dw ? c.cout : c.groups;
+    const int cin_pad = c.dw ? 1 : c.groups > 1 ? cin_g : c.cin;
     const int pdt = act_dt(m);
     const int64_t bytes = c.stem ? vrs_pack_stem_weight(nullptr, c.cout, pdt, nullptr)
                                  : vrs_pack_conv_weight(nullptr, c.cout, cin_g, c.k, groups, cin_pad, pdt, nullptr);
@@ -1399,7 +1411,7 @@ int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io) {
   io->launch = i < (int)m->conv_launch.size() ? m->conv_launch[i] : -1;
   io->k = c.k;
   io->stride = c.s;
-  io->groups = c.dw ? c.cout : 1;
+  io->groups = c.dw ? c.cout : c.groups;
   io->act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
   io->plain = c.kind == CK_PLAIN;
   // a stem pair: the stem has no launch and no output of its own; the conv

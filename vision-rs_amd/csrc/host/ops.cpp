@@ -57,9 +57,9 @@ int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const vo
   ConvSpec cs;
   cs.k = d->k; cs.stride = d->stride; cs.act = d->act; cs.dtype = d->dtype; cs.tile = d->tile;
   cs.in_scale = d->in_scale;
-  if (d->groups == 1) cs.depthwise = false;
-  else if (d->groups == x->c && d->groups == y->c) cs.depthwise = true;
-  else return fail(VRS_EUNSUPPORTED, "vrs_conv2d: groups=%d (only 1 or depthwise)", d->groups);
+  if (d->groups < 1) return fail(VRS_EINVAL, "vrs_conv2d: groups=%d", d->groups);
+  if (d->groups > 1 && d->groups == x->c && d->groups == y->c) cs.depthwise = true;
+  else cs.groups = d->groups;
   if (d->act != VRS_ACT_NONE && d->act != VRS_ACT_SILU) return fail(VRS_EINVAL, "vrs_conv2d: act %d", d->act);
   std::vector<Launch> ls;
   int rc = prep_conv(ctx, cs, *x, w, scale, shift, res, *y, ls);
@@ -70,8 +70,13 @@ int64_t vrs_pack_conv_weight(const float* w, int32_t cout, int32_t cin_g, int32_
                              int32_t dtype, void* out) {
   if (cout <= 0 || cin_g <= 0 || k <= 0 || groups <= 0) return fail(VRS_EINVAL, "pack_conv_weight: bad dims");
   if (dtype != VRS_BF16 && dtype != VRS_F32) return fail(VRS_EUNSUPPORTED, "pack_conv_weight: dtype");
-  if (groups > 1) {
-    if (groups != cout || cin_g != 1) return fail(VRS_EUNSUPPORTED, "pack_conv_weight: groups must be 1 or Cout");
+  if (cout % groups) return fail(VRS_EINVAL, "pack_conv_weight: Cout %d not divisible by groups %d", cout, groups);
+  // other groups > 1: the dense layout over each output channel's cin_g inputs
+  // (OIHW already holds cin_g input channels per output channel)
+  const bool depthwise = groups > 1 && groups == cout && cin_g == 1;
+  if (groups > 1 && !depthwise && cin_pad != cin_g)
+    return fail(VRS_EINVAL, "pack_conv_weight: grouped weights take no channel padding");
+  if (depthwise) {
     const int64_t n = (int64_t)cout * k * k;
     const int64_t bytes = n * (int64_t)elt_size(dtype);
     if (!out) return bytes;

@@ -417,9 +417,89 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   return VRS_OK;
 }
 
+// Grouped conv, 1 < groups < channels: conv_bn with any g (blocks/conv.rs:
+// 51-69).  Weights [Cout][k][k][cin_g], so group g's output channels are the
+// rows from g*cout_g on.  Groups that fit the implicit-GEMM kernels
+// (cin_g % 8 == 0, cout_g % 4 == 0, aligned channel offsets and pitches) and
+// bring a tile enough work per pixel (cin_g * cout_g >= 1024) run as one dense
+// launch per group on channel slices of the views; the rest on the direct
+// kernel (one thread per output element).  fp8 only on the dense route.
+static int prep_grouped(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
+                        const float* shift, const vrs_nhwc* res, const vrs_nhwc& y, std::vector<Launch>& out) {
+  int rc;
+  const int G = cs.groups;
+  if (x.c % G || y.c % G)
+    return fail(VRS_EBADSHAPE, "grouped conv: channels %d -> %d not divisible by groups %d", x.c, y.c, G);
+  if (cs.up) return fail(VRS_EUNSUPPORTED, "grouped conv: no fused upsample");
+  if (!w || !scale || !shift) return fail(VRS_EINVAL, "grouped conv: null weight/scale/shift");
+  if (cs.k < 1 || cs.k > 7 || cs.k % 2 == 0 || cs.stride < 1)
+    return fail(VRS_EBADSHAPE, "grouped conv: k=%d s=%d", cs.k, cs.stride);
+  if (y.n != x.n || y.h != out_size(x.h, cs.k, cs.stride) || y.w != out_size(x.w, cs.k, cs.stride))
+    return fail(VRS_EBADSHAPE, "grouped conv: output shape");
+  if (res && (res->n != y.n || res->h != y.h || res->w != y.w || res->c != y.c))
+    return fail(VRS_EBADSHAPE, "grouped conv: residual shape differs from output");
+  const int cin_g = x.c / G, cout_g = y.c / G;
+  const bool aligned = x.c_off % 8 == 0 && x.pitch % 8 == 0 && y.c_off % 4 == 0 && y.pitch % 4 == 0 &&
+                       (!res || (res->c_off % 4 == 0 && res->pitch % 4 == 0));
+  const bool dense = aligned && cin_g % 8 == 0 && cout_g % 4 == 0 && (int64_t)cin_g * cout_g >= 1024 &&
+                     (cs.dtype != VRS_FP8 || cin_g % 64 == 0);
+  if (dense) {
+    const int64_t wrow = (int64_t)cs.k * cs.k * cin_g * (cs.dtype == VRS_FP8 ? 1 : (int64_t)elt_size(cs.dtype));
+    ConvSpec gs = cs;
+    gs.groups = 1;
+    gs.cin_real = 0;
+    for (int g = 0; g < G; ++g) {
+      vrs_nhwc xg = x, yg = y, rg{};
+      xg.c_off += g * cin_g;
+      xg.c = cin_g;
+      yg.c_off += g * cout_g;
+      yg.c = cout_g;
+      if (res) {
+        rg = *res;
+        rg.c_off += g * cout_g;
+        rg.c = cout_g;
+      }
+      if ((rc = prep_conv(ctx, gs, xg, static_cast<const char*>(w) + (int64_t)g * cout_g * wrow, scale + g * cout_g,
+                          shift + g * cout_g, res ? &rg : nullptr, yg, out)))
+        return rc;
+    }
+    return VRS_OK;
+  }
+  if (cs.dtype == VRS_FP8)
+    return fail(VRS_EUNSUPPORTED, "grouped conv fp8: needs Cin/groups %% 64 == 0 (got %d) and aligned views", cin_g);
+  if ((rc = check_dtype(cs.dtype))) return rc;
+  if ((rc = check_view(x, "grouped conv input", 1)) || (rc = check_view(y, "grouped conv output", 1))) return rc;
+  if (res && (rc = check_view(*res, "grouped conv residual", 1))) return rc;
+  vrs_gconv_args a{};
+  a.x = at(x, cs.dtype);
+  a.w = w;
+  a.scale = scale;
+  a.shift = shift;
+  a.res = res ? at(*res, cs.dtype) : nullptr;
+  a.y = const_cast<void*>(at(y, cs.dtype));
+  a.total = (int64_t)y.n * y.h * y.w * y.c;
+  a.H = x.h; a.W = x.w; a.x_pitch = x.pitch;
+  a.Ho = y.h; a.Wo = y.w; a.y_pitch = y.pitch; a.r_pitch = res ? res->pitch : 0;
+  a.cin_g = cin_g; a.cout = y.c; a.cout_g = cout_g;
+  a.k = cs.k; a.stride = cs.stride; a.pad = cs.k / 2; a.act = cs.act;
+  const int64_t blocks = (a.total + 255) / 256;
+  if (blocks >= (1ll << 31)) return fail(VRS_EBADSHAPE, "grouped conv: grid too large");
+  char name[32];
+  snprintf(name, sizeof name, "vrs_gconv_%s", dsuffix(cs.dtype));
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  out.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(256), 0, a));
+  const double es = (double)elt_size(cs.dtype);
+  out.back().flops = 2.0 * (double)a.total * cs.k * cs.k * cin_g;
+  out.back().bytes = ((double)x.n * x.h * x.w * x.c + (double)a.total * (res ? 2 : 1) +
+                      (double)y.c * cs.k * cs.k * cin_g) * es + 8.0 * y.c;
+  return VRS_OK;
+}
+
 int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w, const float* scale,
               const float* shift, const vrs_nhwc* res, const vrs_nhwc& y, std::vector<Launch>& out) {
   int rc;
+  if (cs.groups > 1 && !cs.depthwise) return prep_grouped(ctx, cs, x, w, scale, shift, res, y, out);
   if ((rc = check_view(y, "conv output", cs.depthwise ? 8 : 4))) return rc;
   if (y.n != x.n) return fail(VRS_EBADSHAPE, "conv: batch mismatch %d vs %d", x.n, y.n);
   if (cs.depthwise) {

@@ -96,6 +96,8 @@ inline const char* dsuffix(int dtype) { return dtype == VRS_F32 ? "f32" : "bf16"
 struct ConvSpec {
   int k = 1, stride = 1, act = VRS_ACT_NONE, dtype = VRS_BF16;
   bool depthwise = false;
+  // 1 < groups < channels (not depthwise): per-group channel slices
+  int groups = 1;
   int cin_real = 0;  // unpadded input channels for work accounting (0: the view's)
   int tile = VRS_TILE_AUTO;  // dense conv tile (VRS_TILE_*)
   float in_scale = 1.f;      // VRS_FP8: activation quantisation step (power of two)

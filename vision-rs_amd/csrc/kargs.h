@@ -86,6 +86,24 @@ typedef struct {
   int32_t x_bytes, cblocks, patches, bands;
 } vrs_dw_args;
 
+/* Grouped conv (1 < groups < channels), NHWC, direct form.  x, y, res point
+ * at the views' first channels; weights [Cout][kh][kw][cin_g] in the element
+ * type; output channel co reads input channels [g*cin_g, (g+1)*cin_g) of
+ * group g = co / cout_g.  out = act(acc*scale[co] + shift[co]) + res. */
+typedef struct {
+  const void* x;
+  const void* w;
+  const float* scale;
+  const float* shift;
+  const void* res;
+  void* y;
+  int64_t total;        /* N*Ho*Wo*Cout output elements */
+  int32_t H, W, x_pitch;
+  int32_t Ho, Wo, y_pitch, r_pitch;
+  int32_t cin_g, cout, cout_g;
+  int32_t k, stride, pad, act;
+} vrs_gconv_args;
+
 /* SPPF pooling: reads channels [0,c) of a NHWC buffer (pitch) and writes the
  * cascade p1 = max5(y), p2 = max5(p1), p3 = max5(p2) (stride 1, pad 2, -inf
  * padding) into channels [c,2c), [2c,3c), [3c,4c) of the same buffer. */

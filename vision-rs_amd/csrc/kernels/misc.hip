@@ -1,7 +1,8 @@
 // Bandwidth-bound NHWC kernels for gfx950: depthwise conv, the SPPF pooling
 // cascade and nearest 2x upsample.  No MFMA: these move bytes, so each lane
 // moves 8 consecutive channels (one 16-byte bf16 group) and consecutive lanes
-// walk the channel dimension first for coalesced HBM access.
+// walk the channel dimension first for coalesced HBM access.  Also the direct
+// grouped conv for group shapes the implicit-GEMM tiles do not take.
 #include "common.h"
 
 // ---------------------------------------------------------------------------
@@ -250,6 +251,50 @@ extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1_bf16(vrs_dw_arg
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s2_bf16(vrs_dw_args a) { dw_body<bf16_t, 2>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1_f32(vrs_dw_args a) { dw_body<float, 1>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s2_f32(vrs_dw_args a) { dw_body<float, 2>(a); }
+
+// ---------------------------------------------------------------------------
+// Grouped conv with 1 < groups < channels + folded BN (+ SiLU) (+ residual):
+// conv_bn with any g (blocks/conv.rs:51-69, Conv2d::new_grouped) for groups
+// whose per-group channel counts do not fit the implicit-GEMM tiles.  Direct
+// form: one thread per output element, channel fastest across lanes, so the
+// lanes of one group read the same input pixels (one cache line) and each
+// lane streams its own weight row [k][k][cin_g].  float32 accumulation in
+// (ky, kx, ci) order.
+namespace {
+template <typename T>
+__device__ __forceinline__ void gconv_body(const vrs_gconv_args& a) {
+  using E = Elt<T>;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.total) return;
+  const int co = (int)(i % a.cout);
+  const int64_t pix = i / a.cout;                // (b*Ho + oy)*Wo + ox
+  const int ox = (int)(pix % a.Wo);
+  const int64_t bo = pix / a.Wo;
+  const int oy = (int)(bo % a.Ho);
+  const int64_t b = bo / a.Ho;
+  const T* x = static_cast<const T*>(a.x) + (int64_t)(co / a.cout_g) * a.cin_g;
+  const T* w = static_cast<const T*>(a.w) + (int64_t)co * a.k * a.k * a.cin_g;
+  float acc = 0.f;
+  for (int ky = 0; ky < a.k; ++ky) {
+    const int iy = oy * a.stride - a.pad + ky;
+    if (iy < 0 || iy >= a.H) continue;
+    for (int kx = 0; kx < a.k; ++kx) {
+      const int ix = ox * a.stride - a.pad + kx;
+      if (ix < 0 || ix >= a.W) continue;
+      const T* xp = x + ((b * a.H + iy) * a.W + ix) * a.x_pitch;
+      const T* wp = w + (ky * a.k + kx) * a.cin_g;
+      for (int c = 0; c < a.cin_g; ++c) acc = fmaf(E::to_f(xp[c]), E::to_f(wp[c]), acc);
+    }
+  }
+  float v = acc * a.scale[co] + a.shift[co];
+  if (a.act == VRS_ACT_SILU) v = silu_t<T>(v);
+  if (a.res) v += E::to_f(static_cast<const T*>(a.res)[pix * a.r_pitch + co]);
+  static_cast<T*>(a.y)[pix * a.y_pitch + co] = E::from_f(v);
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void vrs_gconv_bf16(vrs_gconv_args a) { gconv_body<bf16_t>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_gconv_f32(vrs_gconv_args a) { gconv_body<float>(a); }
 
 // ---------------------------------------------------------------------------
 // SPPF pooling cascade (blocks/sppf.rs:43-61): p1 = max5(y), p2 = max5(p1),
