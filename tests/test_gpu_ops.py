@@ -466,10 +466,12 @@ def test_conv2d_tile_rejections():
 
 DW_SHAPES = [
     # n, c, h, w, strides: band/patch/channel-block edges of the row-walking
-    # stride-1 kernel (bands of 10 rows below 64 rows, 16 above; 8-column
-    # patches; 64-channel blocks) and the generic stride-2 kernel
+    # stride-1 kernel (bands of 10 rows below 32 rows, 40 from there on;
+    # 8-column patches; 64-channel blocks) and the generic stride-2 kernel
     (2, 64, 11, 9, (1, 2)),
     (1, 200, 70, 20, (1,)),
+    (2, 72, 40, 12, (1,)),      # one whole 40-row band
+    (1, 64, 83, 9, (1,)),       # two whole bands and a 3-row one
     (2, 24, 3, 3, (1, 2)),
     (1, 136, 21, 17, (1,)),
 ]

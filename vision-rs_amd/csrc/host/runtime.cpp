@@ -522,9 +522,10 @@ int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w
     hipFunction_t f;
     const int64_t xb = ((int64_t)x.n * x.h * x.w * x.pitch - x.c_off) * (int64_t)elt_size(cs.dtype);
     if (cs.stride == 1 && xb < (1ll << 31)) {
-      // row-walking kernel: bands of 16 output rows on large maps, 22 on
-      // mid-size ones (fewer band halos and per-wave start-ups), 10 on small
-      const int rb = x.h >= 64 ? 16 : x.h >= 32 ? 22 : 10;
+      // row-walking kernel: bands of 40 output rows on maps of 32 rows or
+      // more (few band halos and per-wave start-ups: 80 and 40 rows divide
+      // evenly), 10 on small ones (enough waves to fill the chip)
+      const int rb = x.h >= 32 ? 40 : 10;
       a.x_bytes = (int32_t)xb;
       a.cblocks = (x.c + 63) / 64;
       a.patches = (x.w + 7) / 8;

@@ -240,12 +240,10 @@ __device__ __forceinline__ void dww_body(const vrs_dw_args& a) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w16_bf16(vrs_dw_args a) { dww_body<bf16_t, 16>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w40_bf16(vrs_dw_args a) { dww_body<bf16_t, 40>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w10_bf16(vrs_dw_args a) { dww_body<bf16_t, 10>(a); }
-extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w22_bf16(vrs_dw_args a) { dww_body<bf16_t, 22>(a); }
-extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w16_f32(vrs_dw_args a) { dww_body<float, 16>(a); }
+extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w40_f32(vrs_dw_args a) { dww_body<float, 40>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w10_f32(vrs_dw_args a) { dww_body<float, 10>(a); }
-extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1w22_f32(vrs_dw_args a) { dww_body<float, 22>(a); }
 
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s1_bf16(vrs_dw_args a) { dw_body<bf16_t, 1>(a); }
 extern "C" __global__ __launch_bounds__(256) void vrs_dwconv3_s2_bf16(vrs_dw_args a) { dw_body<bf16_t, 2>(a); }
