@@ -95,10 +95,11 @@ typedef struct {
  * 16 input channels and read for all nine taps. */
 #define VRS_TILE_H3 7
 /* Weight-stationary 1x1 kernels (bf16, k = 1, stride 1, Cin a multiple of 64
- * up to 192 (_256) or 256 (_128), no residual, output channel offset/pitch/
- * count multiples of 8, no fused upsample): a persistent workgroup keeps a
- * 256- or 128-channel slice of the weights in LDS and streams 64-pixel tiles
- * of whole input pixel rows through it.  In model plans, _128 also serves the
+ * up to 192 (_256) or 256 (_128), or Cin 384 (_128), no residual, output
+ * channel offset/pitch/count multiples of 8, no fused upsample): a persistent
+ * workgroup keeps a 256- or 128-channel slice of the weights in LDS and
+ * streams 64-pixel tiles of whole input pixel rows through it (Cin 384: as
+ * two 192-channel halves).  In model plans, _128 also serves the
  * Detect head's channel-major float32 output convs with Cin 64 or 256. */
 #define VRS_TILE_W1_256 8
 #define VRS_TILE_W1_128 9

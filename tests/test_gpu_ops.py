@@ -242,6 +242,11 @@ W1_CASES = [
     (1, 192, 9, 9, 64, vrs.TILE_W1_128, None, vrs.ACT_SILU),
     (64, 128, 40, 40, 128, vrs.TILE_W1_128, None, vrs.ACT_SILU),
     (4, 64, 31, 29, 40, vrs.TILE_W1_128, None, vrs.ACT_SILU),
+    # Cin 384: pixel tiles streamed in two 192-channel halves
+    (3, 384, 30, 27, 256, vrs.TILE_W1_128, None, vrs.ACT_SILU),
+    (2, 384, 17, 13, 136, vrs.TILE_W1_128, (448, 32), vrs.ACT_NONE),
+    (1, 384, 5, 5, 128, vrs.TILE_W1_128, None, vrs.ACT_SILU),     # one tile in all
+    (16, 384, 40, 40, 512, vrs.TILE_W1_128, None, vrs.ACT_SILU),  # several tiles per workgroup
 ]
 
 

@@ -189,7 +189,7 @@ std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int s
                                       int num_cu) {
   std::vector<int> c;
   if (dtype == VRS_BF16 && k == 3 && stride == 1 && cin % 32 == 0 && h3_strip_width(w) > 0) c.push_back(VRS_TILE_H3);
-  if (dtype == VRS_BF16 && k == 1 && stride == 1 && cin % 64 == 0 && cin <= 256 && w > 0) {
+  if (dtype == VRS_BF16 && k == 1 && stride == 1 && cin % 64 == 0 && (cin <= 256 || cin == 384) && w > 0) {
     if (cout > 128 && cin <= 192) c.push_back(VRS_TILE_W1_256);
     c.push_back(VRS_TILE_W1_128);
   }
@@ -324,10 +324,12 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   if ((cs.tile & 0xff) == VRS_TILE_W1_256 || (cs.tile & 0xff) == VRS_TILE_W1_128) {
     // weight-stationary 1x1 kernel (conv1w.hip)
     bm = (cs.tile & 0xff) == VRS_TILE_W1_256 ? 256 : 128;
-    if (cs.dtype != VRS_BF16 || cs.k != 1 || cs.stride != 1 || cs.up || x.c % 64 != 0 || x.c > (bm == 256 ? 192 : 256))
+    // Cin 384 on the 128-channel tile: each pixel tile streams in two halves
+    const bool cin_ok = bm == 256 ? x.c <= 192 : (x.c <= 256 || x.c == 384);
+    if (cs.dtype != VRS_BF16 || cs.k != 1 || cs.stride != 1 || cs.up || x.c % 64 != 0 || !cin_ok)
       return fail(VRS_EUNSUPPORTED, "conv: the weight-stationary %d-channel tile needs bf16, k=1, stride 1, no fused "
-                  "upsample and Cin a multiple of 64 up to %d (k=%d s=%d Cin=%d)", bm, bm == 256 ? 192 : 256, cs.k,
-                  cs.stride, x.c);
+                  "upsample and Cin a multiple of 64 up to %s (k=%d s=%d Cin=%d)", bm,
+                  bm == 256 ? "192" : "256, or 384", cs.k, cs.stride, x.c);
     const bool flat = a.y_f32 && a.stage == 2;   // channel-major float32 (the Detect head's outputs)
     if (a.res || (!flat && (!a.stage || a.y_f32)) || (flat && bm != 128))
       return fail(VRS_EUNSUPPORTED, "conv: the weight-stationary tile takes no residual and stores 8-channel-aligned "

@@ -27,6 +27,12 @@
 //
 // LDS rows are Cin + 8 elements: the 32 rows a fragment read touches start
 // on distinct 4-bank groups for every Cin that is a multiple of 64.
+//
+// NC > 1 (Cin 384: a 128-channel weight slice is 98 KB, and two whole
+// 64-pixel tiles would not fit beside it): a tile streams through the LDS
+// double buffer as NC chunks of Cin/NC channels (the pixel rows' matching
+// byte ranges), one barrier per chunk; the tile's accumulators carry over
+// its chunks and the previous tile's epilogue is spread over all of them.
 #include "common.h"
 
 namespace {
@@ -38,22 +44,25 @@ constexpr int W1_NT = 512;   // threads per workgroup
 // channel-major outputs, y_sp == 1): each value of a store unit goes out as
 // its own dword store, the 32 lanes of a half-wave covering 32 consecutive
 // pixels of one channel.
-template <int BM, int CIN, bool FLAT = false>
+template <int BM, int CIN, bool FLAT = false, int NC = 1>
 __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
   using E = Elt<bf16_t>;
   using G = E::group;
-  constexpr int LDK = CIN + 8;                 // LDS row stride (elements)
-  constexpr int CPR = CIN / 8;                 // 16-byte chunks per row
-  constexpr int NCH = W1_BN * CPR / W1_NT;     // pixel chunks per thread per tile
-  constexpr int NWI = BM * CPR / W1_NT;        // weight chunks per thread
-  static_assert(CIN % 64 == 0 && W1_BN * CPR % W1_NT == 0 && BM * CPR % W1_NT == 0, "whole chunks");
+  constexpr int KCH = CIN / NC;                // input channels per pixel chunk
+  constexpr int LDK = CIN + 8;                 // LDS row stride of the weights (elements)
+  constexpr int LDB = KCH + 8;                 // LDS row stride of a pixel chunk
+  constexpr int CPR = CIN / 8;                 // 16-byte pieces per weight row
+  constexpr int CPB = KCH / 8;                 // 16-byte pieces per pixel chunk row
+  constexpr int NCH = W1_BN * CPB / W1_NT;     // pixel pieces per thread per chunk
+  constexpr int NWI = BM * CPR / W1_NT;        // weight pieces per thread
+  static_assert(CIN % (64 * NC) == 0 && W1_BN * CPB % W1_NT == 0 && BM * CPR % W1_NT == 0, "whole pieces");
   constexpr int WGM = BM / 32 < 8 ? BM / 32 : 8, WGN = 8 / WGM;
   constexpr int WTM = BM / WGM, WTN = W1_BN / WGN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   __shared__ __attribute__((aligned(16))) bf16_t sW[BM * LDK];
-  __shared__ __attribute__((aligned(16))) bf16_t sB0[W1_BN * LDK];
-  __shared__ __attribute__((aligned(16))) bf16_t sB1[W1_BN * LDK];
+  __shared__ __attribute__((aligned(16))) bf16_t sB0[W1_BN * LDB];
+  __shared__ __attribute__((aligned(16))) bf16_t sB1[W1_BN * LDB];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
@@ -87,28 +96,31 @@ __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
     }
   }
 
-  // this thread's pixel chunks: row (pixel within the tile) and byte column,
-  // the same for every tile
+  // this thread's pixel pieces: row (pixel within the tile) and element
+  // column within the chunk, the same for every chunk
   int b_row[NCH], b_col[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int q = tid + i * W1_NT;
-    b_row[i] = q / CPR;
-    b_col[i] = (q % CPR) * 8;
+    b_row[i] = q / CPB;
+    b_col[i] = (q % CPB) * 8;
   }
   const uint32_t pitch_b = (uint32_t)a.x_pitch * 2u;
-  auto load_tile = [&](int k, G (&R)[NCH]) {
+  // chunk c = tile c / NC, channels (c % NC) * KCH onwards
+  auto load_chunk = [&](int c, G (&R)[NCH]) {
+    const int k = c / NC;
     const int n0 = (stream + k * streams) * W1_BN;
     const bool live = k < nt;
+    const int c0 = (c % NC) * KCH;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int m = n0 + b_row[i];
-      R[i] = E::bload(rx, live && m < a.M ? (uint32_t)m * pitch_b + (uint32_t)b_col[i] * 2u : kOOB, 0);
+      R[i] = E::bload(rx, live && m < a.M ? (uint32_t)m * pitch_b + (uint32_t)(c0 + b_col[i]) * 2u : kOOB, 0);
     }
   };
-  auto store_tile = [&](bf16_t* sB, const G (&R)[NCH]) {
+  auto store_chunk = [&](bf16_t* sB, const G (&R)[NCH]) {
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) E::store(&sB[b_row[i] * LDK + b_col[i]], R[i]);
+    for (int i = 0; i < NCH; ++i) E::store(&sB[b_row[i] * LDB + b_col[i]], R[i]);
   };
 
   // folded-BN constants of this lane's channels: register quad g of MFMA
@@ -130,8 +142,10 @@ __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
   // k-1 drains the other, a few store units (4 channels of one pixel) after
   // each 16-deep k slice: its VALU work (two transcendentals per value)
   // issues between MFMAs instead of after them.
-  constexpr int KK = CIN / 16;
+  constexpr int KK = KCH / 16;       // 16-deep k slices per chunk
   constexpr int NU = TN * TM * 4;   // store units per tile and lane
+  constexpr int NUC = NU / NC;      // of them drained per chunk
+  static_assert(NU % NC == 0, "store units per chunk");
   struct Out { uint32_t pix[TN]; bool ok[TN]; };
   auto out_addr = [&](int k) {   // tile k's per-lane pixel offsets (none for k < 0)
     Out o;
@@ -168,34 +182,39 @@ __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
                                             0);
     }
   };
-  auto compute = [&](const bf16_t* sB, f32x16_t (&ac)[TM][TN], const f32x16_t (&ap)[TM][TN], const Out& op) {
+  // chunk h of a tile: its first zeroes the accumulators
+  auto compute = [&](const bf16_t* sB, int h, f32x16_t (&ac)[TM][TN], const f32x16_t (&ap)[TM][TN],
+                     const Out& op) {
+    if (h == 0) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ac[i][j][r] = 0.f;
-    const bf16_t* pa = sW + (wm * WTM + frag_row) * LDK + hq * 8;
-    const bf16_t* pb = sB + (wn * WTN + frag_row) * LDK + hq * 8;
+          for (int r = 0; r < 16; ++r) ac[i][j][r] = 0.f;
+    }
+    const bf16_t* pa = sW + (wm * WTM + frag_row) * LDK + h * KCH + hq * 8;
+    const bf16_t* pb = sB + (wn * WTN + frag_row) * LDB + hq * 8;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       G fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) fa[i] = E::load(pa + i * 32 * LDK + kk * 16);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = E::load(pb + j * 32 * LDK + kk * 16);
+      for (int j = 0; j < TN; ++j) fb[j] = E::load(pb + j * 32 * LDB + kk * 16);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) ac[i][j] = mfma32_k16(fa[i], fb[j], ac[i][j]);
 #pragma unroll
-      for (int u = kk * NU / KK; u < (kk + 1) * NU / KK; ++u) epi_unit(u, ap, op);
+      for (int u = h * NUC + kk * NUC / KK; u < h * NUC + (kk + 1) * NUC / KK; ++u) epi_unit(u, ap, op);
     }
   };
 
-  // tile k: LDS buffer k&1 holds it; register set (k+1)&1 holds tile k+1
-  // (written to the other buffer during tile k); set k&1 receives tile k+2;
-  // accumulator set k&1 receives tile k while set (k+1)&1 drains tile k-1
+  // chunk c: LDS buffer c&1 holds it; register set (c+1)&1 holds chunk c+1
+  // (written to the other buffer during chunk c); set c&1 receives chunk
+  // c+2; accumulator set k&1 receives tile k = c / NC while set (k+1)&1
+  // drains tile k-1
   G r0[NCH], r1[NCH];
   f32x16_t acc0[TM][TN], acc1[TM][TN];
 #pragma unroll
@@ -204,20 +223,32 @@ __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc1[i][j][r] = 0.f;
-  load_tile(0, r0);
-  load_tile(1, r1);
-  store_tile(sB0, r0);
+  load_chunk(0, r0);
+  load_chunk(1, r1);
+  store_chunk(sB0, r0);
   __syncthreads();
   auto step = [&](const bf16_t* cur, bf16_t* nxt, G (&ld)[NCH], const G (&st)[NCH], f32x16_t (&ac)[TM][TN],
-                  const f32x16_t (&ap)[TM][TN], int k) {
-    load_tile(k + 2, ld);
-    store_tile(nxt, st);
-    compute(cur, ac, ap, out_addr(k - 1));
+                  const f32x16_t (&ap)[TM][TN], int k, int h) {   // h: a constant at every call
+    load_chunk(k * NC + h + 2, ld);
+    store_chunk(nxt, st);
+    compute(cur, h, ac, ap, out_addr(k - 1));
     __syncthreads();
   };
-  for (int k = 0; k < nt; k += 2) {
-    step(sB0, sB1, r0, r1, acc0, acc1, k);
-    if (k + 1 < nt) step(sB1, sB0, r1, r0, acc1, acc0, k + 1);
+  if constexpr (NC == 1) {
+    for (int k = 0; k < nt; k += 2) {
+      step(sB0, sB1, r0, r1, acc0, acc1, k, 0);
+      if (k + 1 < nt) step(sB1, sB0, r1, r0, acc1, acc0, k + 1, 0);
+    }
+  } else {
+    static_assert(NC == 2, "chunks per tile: 1 or 2");
+    for (int k = 0; k < nt; k += 2) {
+      step(sB0, sB1, r0, r1, acc0, acc1, k, 0);
+      step(sB1, sB0, r1, r0, acc0, acc1, k, 1);
+      if (k + 1 < nt) {
+        step(sB0, sB1, r0, r1, acc1, acc0, k + 1, 0);
+        step(sB1, sB0, r1, r0, acc1, acc0, k + 1, 1);
+      }
+    }
   }
   // the last tile's epilogue
   const Out ol = out_addr(nt - 1);
@@ -232,7 +263,8 @@ __device__ __forceinline__ void conv1w_body(const vrs_conv_args& a) {
 }  // namespace
 
 // vrs_conv1w_bf16_<BM>_c<Cin>: LDS = (BM + 128) * (Cin + 8) * 2 bytes
-// (256 x 192: 150 KB, one workgroup per CU; 128 x 64: 24.8 KB).
+// (256 x 192: 150 KB, one workgroup per CU; 128 x 64: 24.8 KB); _c384 in
+// two chunks: 128 * 392 * 2 + 128 * 200 * 2 = 148 KB.
 #define VRS_CONV1W(BM, CIN)                                                                        \
   extern "C" __global__ __launch_bounds__(512) void vrs_conv1w_bf16_##BM##_c##CIN(vrs_conv_args a) { \
     conv1w_body<BM, CIN>(a);                                                                       \
@@ -244,6 +276,9 @@ VRS_CONV1W(128, 64)
 VRS_CONV1W(128, 128)
 VRS_CONV1W(128, 192)
 VRS_CONV1W(128, 256)
+extern "C" __global__ __launch_bounds__(512) void vrs_conv1w_bf16_128_c384(vrs_conv_args a) {
+  conv1w_body<128, 384, false, 2>(a);
+}
 // float32 channel-major outputs (the Detect head's box and class convs)
 #define VRS_CONV1W_F(BM, CIN)                                                                        \
   extern "C" __global__ __launch_bounds__(512) void vrs_conv1w_bf16_##BM##_c##CIN##_f(vrs_conv_args a) { \
