@@ -419,6 +419,42 @@ def test_conv2d_fp8(case):
     assert rel_err(from_nhwc(yt), ref, FLOOR[vrs.BF16]) < TOL[vrs.BF16]
 
 
+@pytest.mark.parametrize("case", [(2, 128, 12, 10, 128, 2, 3, 1, True), (1, 256, 9, 9, 192, 2, 1, 1, False)])
+def test_grouped_conv2d_fp8(case):
+    """Grouped conv on the fp8 route (one e4m3 implicit-GEMM launch per group,
+    weights from pack_conv_weight_fp8 over Cin/groups inputs) against the
+    oracle's grouped conv of the same dequantised operands; Cin/groups not a
+    multiple of 64 is refused."""
+    import torch
+    n, cin, h, w, cout, G, k, s, with_res = case
+    rng = np.random.default_rng(41 + cin)
+    x = bf16_round(rng.standard_normal((n, cin, h, w)).astype(np.float32) * 3.0)
+    wt = (rng.standard_normal((cout, cin // G, k, k)) * np.sqrt(2.0 / (cin // G * k * k))).astype(np.float32)
+    bn_s = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    in_scale = float(2.0 ** np.ceil(np.log2(np.abs(x).max() / 448.0)))
+    q, ws = vrs.pack_conv_weight_fp8(wt)
+    from oracle.yolo26 import fp8_conv_inputs
+    xq, wq = fp8_conv_inputs(x, wt, in_scale)
+    ho, wo = (h + 2 * (k // 2) - k) // s + 1, (w + 2 * (k // 2) - k) // s + 1
+    res = bf16_round(rng.standard_normal((n, cout, ho, wo)).astype(np.float32)) if with_res else None
+    ref = oracle.affine_act(oracle.conv2d(xq, wq, s, k // 2, groups=G), bn_s, shift, 1)
+    if with_res:
+        ref = ref + res
+    xt = to_nhwc(x, vrs.BF16)
+    yt = torch.full((n, ho, wo, cout), 7.0, dtype=torch.bfloat16, device="cuda")
+    rt = to_nhwc(res, vrs.BF16) if with_res else None
+    sc = dev((bn_s * ws * in_scale).astype(np.float32))
+    ctx().conv2d(vrs.nhwc(xt), dev(q), sc, dev(shift), vrs.nhwc(yt), k, s, G, vrs.ACT_SILU,
+                 vrs.nhwc(rt) if with_res else None, vrs.FP8, in_scale=in_scale)
+    torch.cuda.synchronize()
+    assert rel_err(from_nhwc(yt), ref, FLOOR[vrs.BF16]) < TOL[vrs.BF16]
+    with pytest.raises(vrs.VrsError) as e:   # 4 groups: 32 (or 64 for Cin 256) inputs each
+        ctx().conv2d(vrs.nhwc(xt), dev(q), sc, dev(shift), vrs.nhwc(yt), k, s, 2 * G if cin == 128 else 8,
+                     vrs.ACT_SILU, None, vrs.FP8, in_scale=in_scale)
+    assert e.value.code == -3
+
+
 def test_conv2d_fp8_rejections():
     import torch
     x = torch.zeros((1, 4, 4, 32), dtype=torch.bfloat16, device="cuda")
