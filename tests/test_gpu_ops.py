@@ -651,9 +651,10 @@ def test_upsample_exact(dtype):
     (2, 2, 4, 4), (2, 4, 20, 20), (1, 1, 7, 9),
     # bf16 kernel choice: LDS-resident heads (N <= 512) in tiles of 7 query
     # tiles (few heads: 1, 2 or 3 workgroups per head), one workgroup per head
-    # of 13 or 16 query tiles (as many heads as CUs), and the streamed kernel
+    # of 13 or 16 query tiles (once the 7-tile workgroups would take more than
+    # one round over the CUs: 160 and 256 heads), and the streamed kernel
     # beyond 512 keys
-    (3, 2, 13, 17), (2, 4, 23, 22), (64, 4, 20, 20), (64, 4, 22, 22), (1, 1, 24, 24)])
+    (3, 2, 13, 17), (2, 4, 23, 22), (40, 4, 20, 20), (64, 4, 20, 20), (64, 4, 22, 22), (1, 1, 24, 24)])
 def test_psa_attention(dtype, shape):
     import torch
     b, heads, h, w = shape
