@@ -118,6 +118,9 @@ __device__ __forceinline__ void dww_body(const vrs_dw_args& a) {
   // registers, so the parity path keeps three
   constexpr int NP = sizeof(T) == 2 ? 6 : 3;
   static_assert((RB + 2) % NP == 0, "rows per band: RB + 2 must be a multiple of the ring");
+  // the accumulator slot of band row u (u % 3) is taken from its prefetch
+  // slot u % NP at compile time, which needs NP to be a multiple of 3
+  static_assert(NP % 3 == 0, "prefetch ring: a multiple of the 3-slot accumulator ring");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int gl = lane & 7, cx = lane >> 3;
   // workgroup -> (image, band, channel block, 4 adjacent patches)
