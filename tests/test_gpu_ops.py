@@ -552,6 +552,8 @@ GCONV_CASES = [
     (2, 128, 12, 12, 128, 2, 3, 1, True, None, None),          # one dense launch per group (64 x 64)
     (2, 256, 9, 9, 128, 4, 1, 1, False, (272, 16), (144, 8)),  # dense per group on channel slices
     (1, 96, 11, 13, 192, 3, 3, 2, False, None, None),          # dense per group (32 x 64), stride 2
+    (2, 16, 9, 9, 32, 16, 3, 1, False, None, None),            # groups = Cin, two outputs per input channel
+    (1, 128, 6, 6, 128, 2, 3, 1, True, None, (136, 3)),        # 64 x 64 groups, odd output offset: direct
 ]
 
 
