@@ -312,6 +312,16 @@ int vrs_msda(vrs_ctx* ctx, const vrs_msda_desc* d, const float* value, const flo
 #define VRS_BLOCK_PSA_ATTN 6    /* psa_attention (blocks/c2psa.rs:61-116) */
 #define VRS_BLOCK_DETECT_BOX 7  /* one Detect box branch cv2[i] (blocks/detect.rs:117-131) */
 #define VRS_BLOCK_YOLO26 8      /* yolo26() (yolo26/mod.rs:207-219) */
+/* detect::<D>(nc, &ch, head) (blocks/detect.rs:108-172): the whole Detect head
+ * on three feature maps with ch[0], ch[1], ch[2] channels at h x w, h/2 x w/2
+ * and h/4 x w/4 (the strides 8/16/32 maps of a YOLO26 neck; h, w multiples of
+ * 4; c_in == ch[0]).  The model input holds the three NCHW float32 tensors back
+ * to back ([batch][ch[0]][h][w], then [batch][ch[1]][h/2][w/2], then
+ * [batch][ch[2]][h/4][w/4]); the outputs are DetectOutput's boxes
+ * [batch][4A] and scores [batch][nc*A] (channel_cat_flat, blocks/detect.rs:
+ * 62-80), A = h*w + h*w/4 + h*w/16.  one2one selects the head's weight names
+ * (DetectHead::OneToOne "one2one_cv2/3", else OneToMany "cv2/3"). */
+#define VRS_BLOCK_DETECT 9
 
 #define VRS_CONV_BN_SILU 0      /* conv() */
 #define VRS_CONV_BN 1           /* conv_bn() */
@@ -329,7 +339,9 @@ typedef struct {
   int32_t heads;            /* psa_attention */
   int32_t nc;               /* yolo26: classes */
   int32_t variant;          /* yolo26: 'n','s','m','l','x' */
-  int32_t one2one;          /* yolo26: 1 = one2one_cv2/cv3 head (DetectHead::OneToOne) */
+  int32_t one2one;          /* yolo26, detect: 1 = one2one_cv2/cv3 head (DetectHead::OneToOne),
+                               0 = cv2/cv3 (DetectHead::OneToMany) */
+  int32_t ch[3];            /* detect: channels of the three feature maps */
 } vrs_block_desc;
 
 /* Record the block's layers for a fixed batch and input size, mirroring the
@@ -379,9 +391,13 @@ int vrs_model_finalize(vrs_model* m);
 int vrs_model_num_outputs(const vrs_model* m);
 /* Output i: float32 element count and (up to 4) dims. */
 int vrs_model_output_info(const vrs_model* m, int32_t i, int64_t* numel, int32_t* dims, int32_t* ndim);
-/* Input: float32 NCHW [batch][c_in][h][w] device buffer.  Outputs: caller
- * buffers of output_info sizes (yolo26: boxes [batch][4A], scores [batch][nc*A],
- * the reference's DetectOutput; blocks: NCHW float32). */
+/* Input: float32 NCHW [batch][c_in][h][w] device buffer (VRS_BLOCK_DETECT:
+ * its three feature maps back to back).  Outputs: caller buffers of
+ * output_info sizes (yolo26 and detect: boxes [batch][4A], scores
+ * [batch][nc*A], the reference's DetectOutput; other blocks: NCHW float32).
+ * 16-byte aligned outputs let the Detect output convs use the
+ * weight-stationary kernel a tile plan may name; on other addresses they run
+ * on the tiled kernels (same results). */
 int vrs_model_forward(vrs_model* m, const float* x, float* const* outputs, void* stream);
 /* capture_graph analogue (examples/yolo26.rs:3110): capture one forward with
  * these buffers into a hipGraph; vrs_model_replay launches it (run_inplace). */

@@ -61,13 +61,16 @@ class Params(dict):
     so a bfloat16 run can be compared against an oracle that stores its
     activations at the same precision and at the same points."""
 
-    def __init__(self, *a, eps=1e-3, act_q=None, fp8=None, **k):
+    def __init__(self, *a, eps=1e-3, act_q=None, fp8=None, observe=None, **k):
         super().__init__(*a, **k)
         self.eps = eps
         self.act_q = act_q if act_q is not None else (lambda t: t)
         # conv prefix -> activation step of the convs that run on e4m3
         # (weights per output channel, inputs per tensor; see fp8_conv_inputs)
         self.fp8 = fp8 or {}
+        # observe(prefix, x): called with every dense/depthwise conv's input
+        # before the conv (fp8_steps records max |x| through it)
+        self.observe = observe
 
 
 def e4m3_round(x):
@@ -95,8 +98,33 @@ def fp8_conv_inputs(x, w, in_scale):
     return e4m3_round(np.asarray(x, np.float32) / s) * s, wq.astype(np.float32)
 
 
+def fp8_step(amax):
+    """Activation step of an fp8 conv input as vrs_model_calibrate sets it:
+    the smallest power of two >= amax / 448 (1 for an all-zero input)."""
+    if not amax > 0 or not np.isfinite(amax):
+        return 1.0
+    f, e = math.frexp(float(np.float32(amax) / np.float32(448.0)))
+    return math.ldexp(1.0, e - 1 if f == 0.5 else e)
+
+
+def fp8_steps(net, P, x, prefixes):
+    """{prefix: step} for the convs in `prefixes` from one forward of `net`
+    (e.g. yolo26(...)) on x with P (its act_q sets the activation precision
+    of the calibrating forward): the per-tensor max |input| of each conv."""
+    amax = {}
+
+    def see(pre, t):
+        if pre in prefixes:
+            amax[pre] = max(amax.get(pre, 0.0), float(np.max(np.abs(t))))
+    Q = Params(P, eps=P.eps, act_q=P.act_q, observe=see)
+    net(Q, x)
+    return {pre: fp8_step(a) for pre, a in amax.items()}
+
+
 def _conv_bn_act(P, pre, x, k, s, g, act, res=None):
     w = P[_j(pre, "conv.weight")]
+    if P.observe is not None:
+        P.observe(pre, x)
     if pre in P.fp8:
         x, w = fp8_conv_inputs(x, w, P.fp8[pre])
     y = conv2d(x, w, stride=s, pad=k // 2, groups=g)
@@ -123,6 +151,8 @@ def dwconv(c, k, s):  # conv.rs:75-85: depthwise -> BN -> SiLU
 def conv_plain(c_in, c_out, k, s):  # conv.rs:90-99: conv with bias
     def f(P, pre, x):
         w = P[_j(pre, "weight")]
+        if P.observe is not None:
+            P.observe(pre, x)
         if pre in P.fp8:
             x, w = fp8_conv_inputs(x, w, P.fp8[pre])
         return conv2d(x, w, stride=s, pad=k // 2, bias=P[_j(pre, "bias")])

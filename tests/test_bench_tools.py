@@ -80,3 +80,26 @@ def test_trace_summary_matches_profile_launches(tmp_path):
     row = [l for l in out.splitlines() if l.startswith("| vrs_k")][0]
     c = [x.strip() for x in row.strip("|").split("|")]
     assert c[1] == "2" and c[2] == "21.0" and c[3] == "20.0" and c[4] == "10.0"
+
+
+def test_load_plan_checks_conv_names(tmp_path):
+    # a plan is applied only when its conv names are the model's, in order
+    p = tmp_path / "plan.json"
+    p.write_text(json.dumps({"note": "t", "plan": [["model.0", 0], ["model.1", 11], ["model.2.cv1", 1]]}))
+    assert bench.load_plan(str(p), ["model.0", "model.1", "model.2.cv1"]) == [0, 11, 1]
+    assert bench.load_plan(str(p), ["model.0", "model.2.cv1", "model.1"]) is None      # reordered
+    assert bench.load_plan(str(p), ["model.0", "model.1"]) is None                     # count differs
+    assert bench.load_plan(str(tmp_path / "missing.json"), ["model.0"]) is None
+
+
+def test_committed_plans_match_the_model_builder():
+    # the committed plans name the convs of the record-only YOLO26m model
+    sys.path.insert(0, os.path.join(ROOT, "vision-rs_amd"))
+    import vrs
+    m = vrs.Model(None, vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="m", one2one=True), 64, 640, 640,
+                  vrs.BF16, 1e-3)
+    names = [pre for pre, _, _ in m.conv_info()]
+    for kind in ("bf16", "fp8", "fp8_forced"):
+        path = bench.plan_path("m", kind, 64, 640)
+        if os.path.exists(path):
+            assert bench.load_plan(path, names) is not None, path

@@ -18,12 +18,23 @@ layers:
 
 The end-to-end outputs of the same run are then compared with the plain
 float32 oracle (the reference CPU path on the unrounded weights and input):
-normwise error, class argmax wherever the float32 top-2 logit margin exceeds
-2e-2, and the top-k anchors wherever neighbouring scores are separated by more
-than 2e-2.  bf16 is held to the normwise 2e-2 bar there; fp8's end-to-end
-numbers are reported (an e4m3 activation carries 3 mantissa bits, ~4% rms
-rounding per layer, so no fp8 network meets 2e-2 of the float32 result; the
-per-layer check above is its contract).
+
+* bf16: normwise error < 2e-2; identical class argmax wherever the float32
+  top-2 logit margin exceeds twice the tolerance, 2 * 2e-2 * std(logits) (two
+  logits each within 2e-2 of the logits' spread cannot trade places); the
+  device post-process's top-k anchors identical to the oracle's at every rank
+  whose float32 best-class logit is separated from both neighbours' by that
+  margin.
+* fp8: an e4m3 activation carries 3 mantissa bits, and one-ulp differences of
+  the bf16 values it is rounded from (the device and the oracle sum in
+  different orders) flip e4m3 roundings that compound over ~90 layers
+  (tests/test_fp8_sensitivity.py shows this on the oracle alone: 0.1 % of
+  activations moved by one bf16 ulp move the e4m3 emulation by 7.5e-2 /
+  9.3e-2).  No fp8 pipeline meets 2e-2 of float32 here; the stated fp8 bar is
+  normwise < 0.15 against float32 (the emulation itself is at 0.104 / 0.126)
+  and < 0.13 against the precision-matched emulation, and the device no
+  farther from float32 than 1.2x the emulation is.  Per layer, fp8 is held to
+  the same 2e-2 single-kernel bar as bf16 (above).
 """
 import ctypes as C
 
@@ -103,46 +114,62 @@ def normwise(got, ref):
     return float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
 
 
+TOL = 2e-2   # the north_star's bf16 relative tolerance
+
+
 def argmax_last(scores_flat, nc, a_s):
-    """Per-anchor class argmax (last maximal class wins, Rust max_by) and the top-2 margin."""
-    out, margins, base = [], [], 0
+    """Per-anchor class argmax (last maximal class wins, Rust max_by), the
+    best logit and the top-2 margin."""
+    out, best, margins, base = [], [], [], 0
     for a in a_s:
         blk = scores_flat[:, nc * base: nc * (base + a)].reshape(-1, nc, a)
         out.append(nc - 1 - np.argmax(blk[:, ::-1, :], axis=1))
         srt = np.sort(blk, axis=1)
+        best.append(srt[:, -1, :])
         margins.append(srt[:, -1, :] - srt[:, -2, :])
         base += a
-    return np.concatenate(out, 1), np.concatenate(margins, 1)
+    return np.concatenate(out, 1), np.concatenate(best, 1), np.concatenate(margins, 1)
 
 
-def e2e_report(tag, boxes, scores, rb, rs, size):
-    """Normwise errors, argmax agreement where the reference margin > 2e-2,
-    and top-k agreement at separated ranks, against reference outputs."""
+def detection_checks(boxes, scores, rb, rs, size, tol=TOL):
+    """Detections against reference outputs rb, rs (float32 oracle): class
+    argmax at every anchor whose reference top-2 logit margin exceeds
+    2 * tol * std(reference logits), and the device post-process's top-k
+    anchors at every rank whose reference best-class logit is separated from
+    both neighbours' by that margin.  Returns (checked anchors, argmax
+    mismatches, checked ranks, top-k mismatches, detection counts)."""
     import torch
-    eb, es = normwise(boxes, rb), normwise(scores, rs)
     a_s = [(size // s) ** 2 for s in (8, 16, 32)]
-    cg, _ = argmax_last(scores, 80, a_s)
-    cr, margin = argmax_last(rs, 80, a_s)
-    sure = margin > 2e-2
+    margin_min = 2.0 * tol * float(np.std(np.asarray(rs, np.float64)))
+    cg, _, _ = argmax_last(scores, 80, a_s)
+    cr, best, margin = argmax_last(rs, 80, a_s)
+    sure = margin > margin_min
     mism = int(np.sum(cg[sure] != cr[sure]))
     got = ctx().detect_postprocess(dev(boxes), dev(scores), 80, size, size, (8, 16, 32), 0.25, 300)
     torch.cuda.synchronize()
     gc, _, _, gan, _ = [t.cpu().numpy() for t in got]
-    rc, rsc, _, ran, _ = oracle.detect_postprocess(rb, rs, 80, size, size, (8, 16, 32), 0.25, 300)
+    rc, _, _, ran, _ = oracle.detect_postprocess(rb, rs, 80, size, size, (8, 16, 32), 0.25, 300)
     topk_bad, topk_n = 0, 0
     for b in range(boxes.shape[0]):
-        k = min(gc[b], rc[b])
-        s = rsc[b, :k]
+        k = int(min(gc[b], rc[b]))
+        lg = best[b][ran[b, :k]]   # reference best-class logit of each ranked anchor
         sep = np.ones(k, bool)
-        gap = np.abs(np.diff(s)) > 2e-2 * s[1:]
+        gap = (lg[:-1] - lg[1:]) > margin_min
         sep[1:] &= gap
         sep[:-1] &= gap
         topk_bad += int(np.sum(gan[b, :k][sep] != ran[b, :k][sep]))
         topk_n += int(np.sum(sep))
-    print(f"{tag}: normwise boxes {eb:.3e} scores {es:.3e}; argmax mismatches {mism} of {int(sure.sum())} anchors "
-          f"with margin > 2e-2 ({sure.mean():.3f} of all); top-k anchor mismatches {topk_bad} of {topk_n} "
-          f"separated ranks; detections {list(gc)} vs {list(rc)}")
-    return eb, es, mism, topk_bad
+    return int(sure.sum()), mism, topk_n, topk_bad, (list(gc), list(rc))
+
+
+def e2e_report(tag, boxes, scores, rb, rs, size):
+    """Normwise errors and the detection checks against reference outputs."""
+    eb, es = normwise(boxes, rb), normwise(scores, rs)
+    n_am, mism, n_tk, topk_bad, counts = detection_checks(boxes, scores, rb, rs, size)
+    print(f"{tag}: normwise boxes {eb:.3e} scores {es:.3e}; argmax mismatches {mism} of {n_am} anchors with "
+          f"margin > 2*{TOL}*std; top-k anchor mismatches {topk_bad} of {n_tk} separated ranks; "
+          f"detections {counts[0]} vs {counts[1]}")
+    return eb, es, mism, topk_bad, n_am
 
 
 @pytest.mark.parametrize("dtype", [vrs.BF16, vrs.FP8], ids=["bf16", "fp8"])
@@ -210,11 +237,22 @@ def test_yolo26m_bs64_640_layer_by_layer(dtype):
     tag = "fp8" if dtype == vrs.FP8 else "bf16"
     for i in IMAGES:
         rb32, rs32 = Y.yolo26(80, "m")(Y.Params(P32, eps=1e-3), x32[i:i + 1])
-        eb, es, mism, topk_bad = e2e_report(f"yolo26m {tag} bs64 image {i} vs float32", boxes[i:i + 1],
-                                            scores[i:i + 1], rb32, rs32, S)
+        eb, es, mism, topk_bad, n_am = e2e_report(f"yolo26m {tag} bs64 image {i} vs float32", boxes[i:i + 1],
+                                                  scores[i:i + 1], rb32, rs32, S)
         fp8 = {io.prefix: io.in_scale for io in ios if io.fp8}
         rbq, rsq = Y.yolo26(80, "m")(Y.Params(P, eps=1e-3, act_q=bf16_round, fp8=fp8), x[i:i + 1])
-        e2e_report(f"yolo26m {tag} bs64 image {i} vs the same-precision emulation", boxes[i:i + 1],
-                   scores[i:i + 1], rbq, rsq, S)
+        qb, qs, _, _, _ = e2e_report(f"yolo26m {tag} bs64 image {i} vs the same-precision emulation",
+                                     boxes[i:i + 1], scores[i:i + 1], rbq, rsq, S)
         if dtype == vrs.BF16:
             assert eb < 2e-2 and es < 2e-2, (eb, es)
+            # the detection contract: most anchors clear the margin, none flips
+            assert n_am > 0.5 * 8400 and mism == 0, (n_am, mism)
+            assert topk_bad == 0, topk_bad
+        else:
+            # the stated fp8 bar (module docstring): against float32 and against
+            # the precision-matched emulation, and as accurate as the emulation
+            eqb, eqs = normwise(rbq, rb32), normwise(rsq, rs32)
+            print(f"fp8 emulation vs float32: boxes {eqb:.3e} scores {eqs:.3e}")
+            assert eb < 0.15 and es < 0.15, (eb, es)
+            assert qb < 0.13 and qs < 0.13, (qb, qs)
+            assert eb < 1.2 * eqb + 5e-3 and es < 1.2 * eqs + 5e-3, (eb, eqb, es, eqs)

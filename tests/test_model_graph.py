@@ -18,6 +18,7 @@ class Recorder(dict):
         self.eps = eps
         self.act_q = lambda t: t
         self.fp8 = {}
+        self.observe = None
         self.used = set()
 
     def __getitem__(self, k):
@@ -99,3 +100,26 @@ def test_grouped_conv_block_params():
         with pytest.raises(vrs.VrsError) as e:
             record(vrs.block(vrs.BLOCK_CONV, c_in, c_out, k=3, g=g, conv_kind=kind), 8, 8)
         assert e.value.code == code
+
+
+@pytest.mark.parametrize("one2one", [True, False])
+def test_detect_block_params_and_outputs(one2one):
+    # detect::<D>(nc, &ch, head) (blocks/detect.rs:108-172) as its own block:
+    # the parameters the oracle's detect reads, DetectOutput's shapes
+    chs = (64, 128, 256)
+    m = record(vrs.block(vrs.BLOCK_DETECT, chs[0], nc=80, one2one=one2one, ch=chs), 16, 16, 2)
+    A = 16 * 16 + 8 * 8 + 4 * 4
+    assert m.output_shapes() == [(2, 4 * A), (2, 80 * A)]
+    P = Recorder(seeded_params(m.params()))
+    feats = [np.zeros((2, c, 16 >> i, 16 >> i), np.float32) for i, c in enumerate(chs)]
+    boxes, scores = Y.detect(80, list(chs), one2one)(P, "", feats)
+    assert P.used == set(n for n, _ in m.params())
+    assert boxes.shape == (2, 4 * A) and scores.shape == (2, 80 * A)
+    head = "one2one_cv" if one2one else "cv"
+    assert dict(m.params())[f"{head}2.0.0.conv.weight"] == (16, 64, 3, 3)   # c2 = max(16, 64/4, 4)
+
+
+def test_detect_block_rejections():
+    for ch, c_in, hw in [((64, 128, 0), 64, 16), ((64, 128, 256), 32, 16), ((64, 128, 256), 64, 18)]:
+        with pytest.raises(vrs.VrsError):
+            record(vrs.block(vrs.BLOCK_DETECT, c_in, nc=80, ch=ch), hw, hw, 1)

@@ -90,6 +90,10 @@ struct Step {
   V a, b;             // PACK: b = dest; POOL: a; UP: a -> b; ATTN: a = qkv, b = out; UNPACK: a
   int heads = 0;
   int out_idx = -1;   // UNPACK
+  // PACK: the input tensor's channels and size, and its float offset in the
+  // model input (a multi-input block's tensors lie back to back)
+  int in_c = 0, in_h = 0, in_w = 0;
+  int64_t in_off = 0;
 };
 
 }  // namespace
@@ -354,11 +358,15 @@ class Builder {
     m_->steps.push_back(st);
   }
 
-  V input(int c_real) {
-    V in = alloc(m_->in_h, m_->in_w, (c_real + 7) / 8 * 8);
+  V input(int c_real) { return input_at(c_real, m_->in_h, m_->in_w, 0); }
+
+  // Input tensor [batch][c_real][h][w] at float offset `off` of the model input.
+  V input_at(int c_real, int h, int w, int64_t off) {
+    V in = alloc(h, w, (c_real + 7) / 8 * 8);
     real_c_[in.buf] = c_real;
     Step st;
     st.type = Step::PACK; st.b = in;
+    st.in_c = c_real; st.in_h = h; st.in_w = w; st.in_off = off;
     m_->steps.push_back(st);
     return in;
   }
@@ -461,6 +469,26 @@ int build(vrs_model* m) {
       const int64_t hw = (int64_t)m->in_h * m->in_w;
       b.conv_flat("2", t2, 4, 1, CK_PLAIN, 0, 0, 4 * hw, 1, hw);
       m->out_dims = {{m->batch, 4, m->in_h, m->in_w}};
+      return VRS_OK;
+    }
+    case VRS_BLOCK_DETECT: {
+      // detect::<D>(nc, &ch, head) (blocks/detect.rs:108-172): the three
+      // feature maps at h x w, h/2 x w/2 and h/4 x w/4 (strides 8/16/32 of the
+      // image), back to back in the model input
+      if (d.nc < 1) return fail(VRS_EINVAL, "detect block: nc %d", d.nc);
+      if (d.ch[0] != d.c_in) return fail(VRS_EINVAL, "detect block: c_in must equal ch[0]");
+      if (m->in_h % 4 || m->in_w % 4) return fail(VRS_EBADSHAPE, "detect block: h and w must be multiples of 4");
+      V feats[3];
+      int chs[3];
+      int64_t off = 0;
+      for (int i = 0; i < 3; ++i) {
+        if (d.ch[i] < 1) return fail(VRS_EINVAL, "detect block: ch[%d] = %d", i, d.ch[i]);
+        chs[i] = d.ch[i];
+        const int hi = m->in_h >> i, wi = m->in_w >> i;
+        feats[i] = b.input_at(chs[i], hi, wi, off);
+        off += (int64_t)m->batch * chs[i] * hi * wi;
+      }
+      b.detect("", feats, chs, d.nc, d.one2one != 0);
       return VRS_OK;
     }
     case VRS_BLOCK_YOLO26: {
@@ -610,7 +638,8 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
     auto flush_io = [&]() { while (io.size() < ls.size()) io.push_back(sio); };
     switch (st.type) {
       case Step::PACK:
-        rc = prep_pack_input(m->ctx, x, m->batch, m->in_c, m->in_h, m->in_w, view_of(m, st.b), act_dt(m), ls);
+        rc = prep_pack_input(m->ctx, x + st.in_off, m->batch, st.in_c, st.in_h, st.in_w, view_of(m, st.b), act_dt(m),
+                             ls);
         label = "input";
         break;
       case Step::CONV: {
@@ -660,6 +689,16 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         if (c.out_idx >= 0) {
           rc = prep_conv_flat(m->ctx, cs, view_of(m, c.x), w, scale, c.shift, c.cout, o[c.out_idx] + c.out_off,
                               c.sb, c.sp, c.sc, ls);
+          // the weight-stationary float32-output tile stores 16-byte pixel
+          // quads, so it needs a 16-byte aligned output slice; on a caller's
+          // output that is not, the conv runs on the tiled kernel instead
+          // (same results: the same K order per output)
+          if (rc == VRS_EUNSUPPORTED && ((cs.tile & 0xff) == VRS_TILE_W1_128 || (cs.tile & 0xff) == VRS_TILE_W1_256)) {
+            ls.resize(conv_first);
+            cs.tile = VRS_TILE_AUTO;
+            rc = prep_conv_flat(m->ctx, cs, view_of(m, c.x), w, scale, c.shift, c.cout, o[c.out_idx] + c.out_off,
+                                c.sb, c.sp, c.sc, ls);
+          }
         } else {
           vrs_nhwc r;
           if (c.has_res) r = view_of(m, c.res);
@@ -1045,7 +1084,8 @@ int vrs_model_create(vrs_ctx* ctx, const vrs_block_desc* d, int32_t batch, int32
   if (batch <= 0 || h <= 0 || w <= 0) return fail(VRS_EBADSHAPE, "vrs_model_create: empty input");
   if (dtype != VRS_BF16 && dtype != VRS_F32 && dtype != VRS_FP8)
     return fail(VRS_EUNSUPPORTED, "vrs_model_create: dtype %d", dtype);
-  if (d->c_in <= 0 || (d->kind != VRS_BLOCK_YOLO26 && d->c_out <= 0 && d->kind != VRS_BLOCK_PSA_ATTN))
+  if (d->c_in <= 0 || (d->kind != VRS_BLOCK_YOLO26 && d->kind != VRS_BLOCK_DETECT && d->c_out <= 0 &&
+                       d->kind != VRS_BLOCK_PSA_ATTN))
     return fail(VRS_EINVAL, "vrs_model_create: channels");
   std::unique_ptr<vrs_model> m(new vrs_model);
   m->ctx = ctx; m->desc = *d; m->batch = batch; m->in_c = d->c_in; m->in_h = h; m->in_w = w; m->dtype = dtype;
@@ -1150,6 +1190,21 @@ int vrs_model_finalize(vrs_model* m) {
     return fail(rc, "%s", err.c_str());
   }
   for (Param& p : m->params) std::vector<float>().swap(p.host);
+  // A fused stem pair never writes the stem's output buffer (the network's
+  // largest activation: 839 MB for YOLO26m at batch 64, 640x640).  Release
+  // it, unless the model is fp8, whose calibration forward runs the stem on
+  // its own.
+  if (m->dtype != VRS_FP8)
+    for (size_t i = 1; i < m->convs.size(); ++i) {
+      if (m->convs[i].tile != VRS_TILE_STEM_PAIR || !pair_eligible(m, i)) continue;
+      Buf& b = m->bufs[m->convs[i - 1].y.buf];
+      auto it = std::find(m->allocs.begin(), m->allocs.end(), b.dev);
+      if (b.dev && it != m->allocs.end()) {
+        (void)hipFree(b.dev);
+        m->allocs.erase(it);
+        b.dev = nullptr;
+      }
+    }
   m->finalized = true;
   return VRS_OK;
 }

@@ -117,11 +117,15 @@ __device__ __forceinline__ void msda_any(const vrs_msda_args& a) {
 // L = 4, P = 4 split by level: workgroup = one (b, q), wave = one level, so a
 // query's 64 bilinear corner fetches per lane spread over four waves (4x the
 // waves in flight of one wave per query); the four partial sums meet in LDS.
+// Workgroups are dealt round-robin over the 8 XCDs; the XCD-aware order gives
+// each XCD a contiguous run of queries -- whole images at B*Q/8 queries per
+// XCD -- so the corner rows one image's queries share are fetched into one
+// L2 rather than into all eight.
 __device__ __forceinline__ void msda_split_body(const vrs_msda_args& a) {
   constexpr int P = 4;
   __shared__ f32x4_t part[4][64];
   const int lane = threadIdx.x & 63, l = threadIdx.x >> 6;
-  const int64_t bq = blockIdx.x;
+  const int64_t bq = xcd_remap(blockIdx.x, gridDim.x);
   const int h = lane >> 3, pc = lane & 7;   // head, 4-channel part
   const int b = (int)(bq / a.Q);
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};

@@ -27,6 +27,7 @@ F32, BF16, FP8 = 0, 1, 2
 ACT_NONE, ACT_SILU = 0, 1
 BLOCK_CONV, BLOCK_C3K2, BLOCK_C3K2_PSA, BLOCK_C2PSA, BLOCK_SPPF, BLOCK_PSA_ATTN, BLOCK_DETECT_BOX, BLOCK_YOLO26 = \
     1, 2, 3, 4, 5, 6, 7, 8
+BLOCK_DETECT = 9   # the whole Detect head on three feature maps (ch = their channels)
 CONV_BN_SILU, CONV_BN, CONV_PLAIN = 0, 1, 2
 TILE_AUTO, TILE_128x128, TILE_256x128, TILE_128x256, TILE_64x256, TILE_32x256, TILE_256x256, TILE_K32 = (
     0, 1, 2, 3, 4, 5, 6, 0x100)
@@ -76,7 +77,7 @@ class BlockDesc(C.Structure):
     _fields_ = [("kind", C.c_int32), ("c_in", C.c_int32), ("c_out", C.c_int32), ("k", C.c_int32), ("s", C.c_int32),
                 ("g", C.c_int32), ("conv_kind", C.c_int32), ("n", C.c_int32), ("c3k", C.c_int32),
                 ("shortcut", C.c_int32), ("e", C.c_float), ("heads", C.c_int32), ("nc", C.c_int32),
-                ("variant", C.c_int32), ("one2one", C.c_int32)]
+                ("variant", C.c_int32), ("one2one", C.c_int32), ("ch", C.c_int32 * 3)]
 
 
 class ConvIo(C.Structure):
@@ -564,6 +565,6 @@ class Model:
 
 
 def block(kind, c_in, c_out=0, k=1, s=1, g=1, conv_kind=CONV_BN_SILU, n=1, c3k=False, shortcut=False, e=0.5,
-          heads=0, nc=80, variant="m", one2one=True):
+          heads=0, nc=80, variant="m", one2one=True, ch=(0, 0, 0)):
     return BlockDesc(kind, c_in, c_out, k, s, g, conv_kind, n, int(c3k), int(shortcut), e, heads, nc,
-                     ord(variant), int(one2one))
+                     ord(variant), int(one2one), (C.c_int32 * 3)(*ch))
