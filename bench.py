@@ -714,7 +714,9 @@ def main() -> int:
     ap.add_argument("--autotune", action="store_true",
                     help="autotune the tiles instead of loading the committed plan (vision-rs_amd/plans/)")
     ap.add_argument("--save-plans", action="store_true",
-                    help="write the tile plans this run used to vision-rs_amd/plans/")
+                    help="write the tile plans this run used to vision-rs_amd/plans/ (or --plan-dir)")
+    ap.add_argument("--plan-dir", default=None,
+                    help="directory --save-plans writes to (e.g. gpurun_out/plans on a remote box)")
     ap.add_argument("--no-micro", action="store_true",
                     help="skip the isolated BASELINE configs 2-4 in the default line's `micro` object")
     ap.add_argument("--micro", action="store_true",
@@ -792,7 +794,7 @@ def main() -> int:
             plans_used[dname] = "autotuned in this run"
         m.load(P)
         if a.save_plans:
-            save_plan(pp, m, f"YOLO26{a.variant} {dname} batch {a.batch} {a.size}x{a.size}: per-conv tile codes "
+            save_plan(os.path.join(a.plan_dir, os.path.basename(pp)) if a.plan_dir else pp, m, f"YOLO26{a.variant} {dname} batch {a.batch} {a.size}x{a.size}: per-conv tile codes "
                              "(vrs_model_get_plan; | 0x10000 = fp8) from an autotuned MI355X run")
         m.set_streams(a.streams)
         outs = m.alloc_outputs()
@@ -822,9 +824,11 @@ def main() -> int:
 
     def fp8_summary(m8, el8, ps8, note):
         top = sorted(ps8.items(), key=lambda kv: -kv[1]["ms"])[:4]
+        ios = [m8.conv_io(i) for i in range(len(m8.conv_info()))]
         return {"value": round(a.batch * a.steps / el8, 1), "unit": "images/s",
                 "ms_per_step": round(el8 * 1e3 / a.steps, 3),
                 "fp8_convs": sum(1 for _, f8, _ in m8.conv_info() if f8), "convs": len(m8.conv_info()),
+                "e4m3_inputs": sum(io.x_e4m3 for io in ios), "e4m3_outputs": sum(io.y_e4m3 for io in ios),
                 "note": note,
                 "kernels": {s: {"launches": d["launches"], "ms": round(d["ms"], 4),
                                 "tflops": round(d["flops"] / max(d["ms"], 1e-9) / 1e9, 2)} for s, d in top}}
@@ -835,12 +839,13 @@ def main() -> int:
                               "e4m3 weights (per-channel absmax/448) and e4m3 activations (per-tensor power-of-two "
                               "step calibrated on this batch) on the fp8 MFMA for convs with Cin % 64 == 0 whose "
                               "fastest fp8 tile beats their fastest bf16 tile (per-layer plan); the rest bf16; "
-                              "activations stored bf16")
+                              "activations stored as e4m3 where every reader and writer is an fp8 conv, else bf16")
         m8.close()
         m8, el8, ps8, _ = run(vrs.FP8, tune_mode=2)
         fp8_forced = fp8_summary(m8, el8, ps8,
                                  "every conv with Cin % 64 == 0 forced onto the fp8 MFMA (fastest fp8 tile per "
-                                 "layer), the rest (stem, depthwise, fused-upsample, Cin % 64 != 0) bf16")
+                                 "layer), the rest (stem, depthwise) bf16; activations stored as e4m3 where every "
+                                 "reader and writer is an fp8 conv, else bf16")
         m8.close()
     micro_summary = None
     if not a.no_micro:

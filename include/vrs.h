@@ -48,8 +48,10 @@ extern "C" {
 #define VRS_BF16 1
 /* Dense convs with e4m3 weights (per-output-channel scale absmax/448) and
  * e4m3-quantised activations (a per-tensor power-of-two scale) on the fp8
- * MFMA; activations stay bfloat16 in memory.  No reference function: BASELINE
- * config 5's second run. */
+ * MFMA; activations in memory are bfloat16, or e4m3 where every reader of a
+ * tensor is an fp8 conv (vrs_conv_desc x_e4m3 / y_e4m3 / res_e4m3; inside a
+ * model, planned per buffer).  No reference function: BASELINE config 5's
+ * second run. */
 #define VRS_FP8 2
 
 #define VRS_ACT_NONE 0
@@ -129,6 +131,14 @@ typedef struct {
   int32_t tile;     /* dense only: VRS_TILE_* (0 = automatic) */
   float in_scale;   /* VRS_FP8: activation quantisation step, a power of two:
                        x8 = rne(clamp(x, +-448*in_scale) / in_scale) */
+  /* VRS_FP8 with activations stored as e4m3 (1 byte per channel, views
+   * 16-channel aligned; tiles 128x128, 256x128, 128x256, 64x256, 256x256):
+   * x_e4m3 -- x (and a fused-upsample source) already holds e4m3 on step
+   * in_scale; y_e4m3 -- y is written as rne(clamp(y, +-448*out_step) /
+   * out_step) of its bfloat16 value; res_e4m3 -- res holds e4m3 on step
+   * res_step.  Steps are powers of two; 0 / 0.f when unused. */
+  int32_t x_e4m3, y_e4m3, res_e4m3;
+  float out_step, res_step;
 } vrs_conv_desc;
 
 /* Conv2d + folded BN (+SiLU) (+residual).  Replaces teeny-kernels
@@ -456,6 +466,10 @@ typedef struct {
   vrs_nhwc x, y, res, up;  /* up: source of a fused nearest-2x upsample (first up.c input channels) */
   int32_t out_idx;
   int64_t out_off, out_sb, out_sp, out_sc;
+  /* VRS_FP8 models: views whose buffer is stored as e4m3 (1 byte per
+   * channel, value = e4m3 * step; the others hold dtype elements) */
+  int32_t x_e4m3, y_e4m3, res_e4m3, up_e4m3;
+  float x_step, y_step, res_step, up_step;
 } vrs_conv_io;
 int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io);
 int vrs_model_destroy(vrs_model* m);

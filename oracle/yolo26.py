@@ -61,13 +61,16 @@ class Params(dict):
     so a bfloat16 run can be compared against an oracle that stores its
     activations at the same precision and at the same points."""
 
-    def __init__(self, *a, eps=1e-3, act_q=None, fp8=None, observe=None, **k):
+    def __init__(self, *a, eps=1e-3, act_q=None, fp8=None, observe=None, store8=None, **k):
         super().__init__(*a, **k)
         self.eps = eps
         self.act_q = act_q if act_q is not None else (lambda t: t)
         # conv prefix -> activation step of the convs that run on e4m3
         # (weights per output channel, inputs per tensor; see fp8_conv_inputs)
         self.fp8 = fp8 or {}
+        # conv prefix -> step of the convs whose output is stored as e4m3: the
+        # stored value is e4m3(act_q(y) / step) * step
+        self.store8 = store8 or {}
         # observe(prefix, x): called with every dense/depthwise conv's input
         # before the conv (fp8_steps records max |x| through it)
         self.observe = observe
@@ -116,7 +119,7 @@ def fp8_steps(net, P, x, prefixes):
     def see(pre, t):
         if pre in prefixes:
             amax[pre] = max(amax.get(pre, 0.0), float(np.max(np.abs(t))))
-    Q = Params(P, eps=P.eps, act_q=P.act_q, observe=see)
+    Q = Params(P, eps=P.eps, act_q=P.act_q, observe=see, store8=P.store8)
     net(Q, x)
     return {pre: fp8_step(a) for pre, a in amax.items()}
 
@@ -133,7 +136,11 @@ def _conv_bn_act(P, pre, x, k, s, g, act, res=None):
     y = affine_act(y, scale, shift, act)
     if res is not None:  # elem_add(x, conv(...)) of the caller (bottleneck.rs:24-30)
         y = y + res
-    return P.act_q(y)
+    y = P.act_q(y)
+    if pre in P.store8:
+        st = np.float32(P.store8[pre])
+        y = e4m3_round(y / st) * st
+    return y
 
 
 def conv(c_in, c_out, k, s):  # conv.rs:31-46: Conv2d(no bias, pad k/2) -> BN -> SiLU

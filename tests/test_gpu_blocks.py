@@ -347,7 +347,11 @@ def test_yolo26m_fp8_vs_oracle():
     got = [o.cpu().numpy() for o in m.forward(xd)]
     torch.cuda.synchronize()
     assert any("fp8" in n for n in m.launch_names())
-    ref8 = Y.yolo26(80, "m")(Y.Params(P, eps=1e-3, act_q=bf16_round, fp8=fp8), x)
+    # outputs the model stores as e4m3, and their steps
+    ios = [m.conv_io(i) for i in range(len(fp8) and len(m.conv_info()))]
+    store8 = {pre: io.y_step for (pre, _, _), io in zip(m.conv_info(), ios) if io.y_e4m3}
+    print(f"yolo26m fp8: {len(store8)} convs store e4m3 outputs")
+    ref8 = Y.yolo26(80, "m")(Y.Params(P, eps=1e-3, act_q=bf16_round, fp8=fp8, store8=store8), x)
     ref16 = Y.yolo26(80, "m")(Y.Params(P, eps=1e-3, act_q=bf16_round), x)
     a_s = [(320 // s) ** 2 for s in (8, 16, 32)]
     for i, name in enumerate(("boxes", "scores")):

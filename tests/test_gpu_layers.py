@@ -44,6 +44,7 @@ import pytest
 import oracle
 from oracle import yolo26 as Y
 from gpu_util import bf16_round, ctx, dev, rel_err, vrs
+from test_gpu_ops import e4m3_bracket
 from golden_io import seeded_params
 
 pytestmark = pytest.mark.gpu
@@ -65,14 +66,29 @@ def _d2h(ptr, nbytes):
     return out
 
 
-def read_view(v, dtype, images):
-    """NCHW float32 [len(images), c, h, w] of an NHWC view of model memory."""
-    es = 4 if dtype == vrs.F32 else 2
+_E4M3 = None
+
+
+def e4m3_values():
+    """float32 value of each e4m3 byte (OCP E4M3FN, as torch.float8_e4m3fn)."""
+    global _E4M3
+    if _E4M3 is None:
+        import torch
+        _E4M3 = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    return _E4M3
+
+
+def read_view(v, dtype, images, e4m3=False, step=0.0):
+    """NCHW float32 [len(images), c, h, w] of an NHWC view of model memory
+    (e4m3: a view of a buffer stored as e4m3 bytes on `step`)."""
+    es = 1 if e4m3 else 4 if dtype == vrs.F32 else 2
     per = v.h * v.w * v.pitch * es
     out = []
     for i in images:
         raw = _d2h(v.data + i * per, per)
-        if es == 2:
+        if e4m3:
+            a = e4m3_values()[raw] * np.float32(step)
+        elif es == 2:
             a = (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
         else:
             a = raw.view(np.float32)
@@ -197,12 +213,14 @@ def test_yolo26m_bs64_640_layer_by_layer(dtype):
         ios.append(io)
     if dtype == vrs.FP8:
         n_f8 = sum(io.fp8 for io in ios)
-        eligible = sum(1 for io in ios if io.groups == 1 and not io.stem and io.up.data is None and io.cin % 64 == 0)
+        eligible = sum(1 for io in ios if io.groups == 1 and not io.stem and io.cin % 64 == 0 and
+                       (io.up.data is None or io.up.c % 64 == 0))
         print(f"fp8 forced: {n_f8} of {len(ios)} convs on e4m3 ({eligible} eligible)")
         assert n_f8 == eligible and n_f8 > 60
     by_launch = {io.launch: io for io in ios if io.launch >= 0}
     n = len(m.launch_names())
     worst = []
+    n_e4m3 = 0
     for li in range(n):
         io = by_launch.get(li)
         if io is not None:
@@ -211,25 +229,37 @@ def test_yolo26m_bs64_640_layer_by_layer(dtype):
             elif io.stem:
                 xin = x[list(IMAGES)]
             else:
-                xin = read_view(io.x, io.dtype, IMAGES)
+                xin = read_view(io.x, io.dtype, IMAGES, io.x_e4m3, io.x_step)
                 if io.up.data is not None:   # fused upsample: the first up.c channels are up2x(source)
-                    src = read_view(io.up, io.dtype, IMAGES)
+                    src = read_view(io.up, io.dtype, IMAGES, io.up_e4m3, io.up_step)
                     xin[:, :io.up.c] = oracle.upsample_nearest(src)
-            res = read_view(io.res, io.dtype, IMAGES) if io.res.data is not None else None
+            res = read_view(io.res, io.dtype, IMAGES, io.res_e4m3, io.res_step) if io.res.data is not None else None
         m.run_launches(li, 1)
         torch.cuda.synchronize()
         if io is None:
             continue
         ho = (xin.shape[2] + 2 * (io.k // 2) - io.k) // io.stride + 1
         wo = (xin.shape[3] + 2 * (io.k // 2) - io.k) // io.stride + 1
-        got = read_view(io.y, io.dtype, IMAGES) if io.y.data is not None else read_flat(io, outs, IMAGES, ho, wo)
+        got = (read_view(io.y, io.dtype, IMAGES, io.y_e4m3, io.y_step) if io.y.data is not None
+               else read_flat(io, outs, IMAGES, ho, wo))
         ref = conv_reference(io, P, 1e-3, xin, res)
+        if io.y_e4m3:
+            # stored as e4m3: the e4m3 rounding of a value within the bar
+            lo, hi = e4m3_bracket(ref, io.y_step)
+            bad = int(np.sum((got < lo) | (got > hi)))
+            assert bad == 0, (io.prefix, "fp8 e4m3 output", bad)
+            n_e4m3 += 1
+            continue
         err = rel_err(got, ref, 1e-1)
         worst.append((err, io.prefix, bool(io.fp8)))
         assert err < 2e-2, (io.prefix, "fp8" if io.fp8 else "bf16", err)
     worst.sort(reverse=True)
-    print(f"{len(worst)} convs checked on their own device inputs; largest errors: " +
+    print(f"{len(worst) + n_e4m3} convs checked on their own device inputs ({n_e4m3} with e4m3 outputs, held to "
+          f"the e4m3 bracket of the bar); largest errors of the others: " +
           ", ".join(f"{p}{' (fp8)' if f else ''} {e:.2e}" for e, p, f in worst[:5]))
+    if dtype == vrs.FP8:
+        n_x8 = sum(io.x_e4m3 for io in ios)
+        print(f"fp8: {n_x8} convs read e4m3 inputs, {n_e4m3} write e4m3 outputs")
 
     # end to end against the plain float32 oracle (and the precision-matched one)
     boxes, scores = [o.cpu().numpy() for o in outs]
@@ -240,7 +270,9 @@ def test_yolo26m_bs64_640_layer_by_layer(dtype):
         eb, es, mism, topk_bad, n_am = e2e_report(f"yolo26m {tag} bs64 image {i} vs float32", boxes[i:i + 1],
                                                   scores[i:i + 1], rb32, rs32, S)
         fp8 = {io.prefix: io.in_scale for io in ios if io.fp8}
-        rbq, rsq = Y.yolo26(80, "m")(Y.Params(P, eps=1e-3, act_q=bf16_round, fp8=fp8), x[i:i + 1])
+        store8 = {io.prefix: io.y_step for io in ios if io.y_e4m3}
+        rbq, rsq = Y.yolo26(80, "m")(Y.Params(P, eps=1e-3, act_q=bf16_round, fp8=fp8, store8=store8),
+                                     x[i:i + 1])
         qb, qs, _, _, _ = e2e_report(f"yolo26m {tag} bs64 image {i} vs the same-precision emulation",
                                      boxes[i:i + 1], scores[i:i + 1], rbq, rsq, S)
         if dtype == vrs.BF16:

@@ -455,6 +455,129 @@ def test_grouped_conv2d_fp8(case):
     assert e.value.code == -3
 
 
+def _e4m3_nhwc(a_nchw, step, pitch=None, c_off=0):
+    """NCHW float32 -> device uint8 [n, h, w, pitch] holding e4m3(a / step)
+    (round to nearest even, torch.float8_e4m3fn) in channels [c_off, c_off+c),
+    and the dequantised values it holds."""
+    import torch
+    n, c, h, w = a_nchw.shape
+    pitch = c if pitch is None else pitch
+    q = torch.from_numpy(np.ascontiguousarray(a_nchw.transpose(0, 2, 3, 1)) / np.float32(step)).to(
+        torch.float8_e4m3fn)
+    t = torch.zeros((n, h, w, pitch), dtype=torch.uint8, device="cuda")
+    t[..., c_off:c_off + c] = q.view(torch.uint8).to("cuda")
+    return t, (q.float().numpy() * np.float32(step)).transpose(0, 3, 1, 2).copy()
+
+
+def _from_e4m3_nhwc(t, step, c, c_off=0):
+    import torch
+    return (t[..., c_off:c_off + c].cpu().view(torch.float8_e4m3fn).float().numpy() * np.float32(step)).transpose(
+        0, 3, 1, 2)
+
+
+def e4m3_bracket(ref, step, tol=TOL[vrs.BF16], floor_frac=FLOOR[vrs.BF16]):
+    """The e4m3 outputs an fp8 conv may store for reference values ref: the
+    e4m3 rounding (on step, of the bfloat16 value) of something within the
+    single-kernel bar of ref, i.e. [Q(ref - t), Q(ref + t)] with
+    t = tol * max(|ref|, floor_frac * rms(ref)); Q is monotone."""
+    from oracle.yolo26 import e4m3_round
+    rms = float(np.sqrt(np.mean(np.asarray(ref, np.float64) ** 2)))
+    t = tol * np.maximum(np.abs(ref), floor_frac * rms)
+    q = lambda v: e4m3_round(bf16_round(np.asarray(v, np.float32)) / np.float32(step)) * np.float32(step)  # noqa: E731
+    return q(ref - t), q(ref + t)
+
+
+# (n, cin, h, w, cout, k, stride, residual, tile, e4m3 input, e4m3 output, e4m3 residual, channel offset)
+FP8_E4M3_CASES = [
+    (2, 64, 20, 18, 128, 3, 1, True, vrs.TILE_128x128, True, True, True, 16),
+    (2, 128, 16, 16, 64, 1, 1, False, vrs.TILE_64x256, True, True, False, 0),
+    (1, 128, 24, 20, 256, 3, 2, False, vrs.TILE_256x128, True, False, False, 32),
+    (1, 192, 12, 12, 128, 1, 1, True, vrs.TILE_128x256, False, True, True, 0),
+    (1, 256, 20, 20, 256, 3, 2, False, vrs.TILE_256x256, True, True, False, 0),
+    (2, 64, 10, 14, 256, 3, 1, True, vrs.TILE_256x256, True, True, True, 64),
+    (1, 128, 30, 30, 128, 3, 1, True, vrs.TILE_128x128, False, False, True, 0),
+]
+
+
+@pytest.mark.parametrize("case", FP8_E4M3_CASES)
+def test_conv2d_fp8_e4m3_activations(case):
+    """fp8 conv with e4m3 activations in memory: an e4m3 input on its step
+    (staged into LDS as read), an e4m3 output (the e4m3 rounding, on its
+    step, of the bf16 result) and an e4m3 residual, each alone and together,
+    on every fp8 tile, in views with a channel offset.  Against the oracle conv
+    of the same dequantised operands: a bf16 output to the bf16 bar, an e4m3
+    output inside the e4m3 bracket of that bar (e4m3_bracket)."""
+    import torch
+    n, cin, h, w, cout, k, s, with_res, tile, x8, y8, r8, off = case
+    rng = np.random.default_rng(71 + cin + cout)
+    x = bf16_round(rng.standard_normal((n, cin, h, w)).astype(np.float32) * 2.0)
+    wt = (rng.standard_normal((cout, cin, k, k)) * np.sqrt(2.0 / (cin * k * k))).astype(np.float32)
+    bn_s = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    in_scale = float(2.0 ** np.ceil(np.log2(np.abs(x).max() / 448.0)))
+    q, ws = vrs.pack_conv_weight_fp8(wt)
+    from oracle.yolo26 import fp8_conv_inputs
+    xq, wq = fp8_conv_inputs(x, wt, in_scale)
+    ho, wo = (h + 2 * (k // 2) - k) // s + 1, (w + 2 * (k // 2) - k) // s + 1
+    res = bf16_round(rng.standard_normal((n, cout, ho, wo)).astype(np.float32)) if with_res else None
+    res_step = 2.0 ** -5
+    if x8:
+        xt, xq2 = _e4m3_nhwc(x, in_scale, cin + off, off)
+        assert np.array_equal(xq2, xq)
+    else:
+        xt = to_nhwc(x, vrs.BF16, cin + off, off)
+    rt = None
+    if with_res:
+        if r8:
+            rt, res = _e4m3_nhwc(res, res_step, cout + off, off)
+        else:
+            rt = to_nhwc(res, vrs.BF16, cout + off, off)
+    ref = oracle.affine_act(oracle.conv2d(xq, wq, s, k // 2), bn_s, shift, 1)
+    if with_res:
+        ref = ref + res
+    out_step = float(2.0 ** np.ceil(np.log2(np.abs(ref).max() / 448.0)))
+    if y8:
+        yt = torch.full((n, ho, wo, cout + off), 0x55, dtype=torch.uint8, device="cuda")
+    else:
+        yt = torch.full((n, ho, wo, cout + off), 7.0, dtype=torch.bfloat16, device="cuda")
+    ctx().conv2d(vrs.nhwc(xt, cin, off), dev(q), dev((bn_s * ws * in_scale).astype(np.float32)), dev(shift),
+                 vrs.nhwc(yt, cout, off), k, s, 1, vrs.ACT_SILU, vrs.nhwc(rt, cout, off) if with_res else None,
+                 vrs.FP8, tile=tile, in_scale=in_scale, x_e4m3=x8, y_e4m3=y8, out_step=out_step if y8 else 0.0,
+                 res_e4m3=r8 and with_res, res_step=res_step if (r8 and with_res) else 0.0)
+    torch.cuda.synchronize()
+    if y8:
+        got = _from_e4m3_nhwc(yt, out_step, cout, off)
+        lo, hi = e4m3_bracket(ref, out_step)
+        bad = (got < lo) | (got > hi)
+        assert not bad.any(), (int(bad.sum()), got[bad][:4], ref[bad][:4])
+        assert torch.all(yt[..., :off] == 0x55)   # channels before the view untouched
+    else:
+        assert rel_err(from_nhwc(yt, cout, off), ref, FLOOR[vrs.BF16]) < TOL[vrs.BF16]
+
+
+def test_conv2d_fp8_e4m3_rejections():
+    import torch
+    x = torch.zeros((1, 4, 4, 72), dtype=torch.uint8, device="cuda")
+    y = torch.zeros((1, 4, 4, 64), dtype=torch.uint8, device="cuda")
+    w = torch.zeros(64 * 64, dtype=torch.uint8, device="cuda")
+    sc = torch.ones(64, device="cuda")
+    with pytest.raises(vrs.VrsError):   # e4m3 input view not 16-channel aligned
+        ctx().conv2d(vrs.nhwc(x, 64, 8), w, sc, sc, vrs.nhwc(y), 1, 1, 1, vrs.ACT_NONE, None, vrs.FP8,
+                     in_scale=1.0, x_e4m3=True)
+    x = torch.zeros((1, 4, 4, 64), dtype=torch.uint8, device="cuda")
+    with pytest.raises(vrs.VrsError):   # output step not a power of two
+        ctx().conv2d(vrs.nhwc(x), w, sc, sc, vrs.nhwc(y), 1, 1, 1, vrs.ACT_NONE, None, vrs.FP8, in_scale=1.0,
+                     x_e4m3=True, y_e4m3=True, out_step=0.3)
+    y2 = torch.zeros((1, 4, 4, 72), dtype=torch.uint8, device="cuda")
+    with pytest.raises(vrs.VrsError):   # e4m3 output view not 16-channel aligned
+        ctx().conv2d(vrs.nhwc(x), w, sc, sc, vrs.nhwc(y2, 64, 8), 1, 1, 1, vrs.ACT_NONE, None, vrs.FP8,
+                     in_scale=1.0, x_e4m3=True, y_e4m3=True, out_step=1.0)
+    xb = torch.zeros((1, 4, 4, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(vrs.VrsError):   # e4m3 activations on a bf16 conv
+        ctx().conv2d(vrs.nhwc(xb), w, sc, sc, vrs.nhwc(y), 1, 1, 1, vrs.ACT_NONE, None, vrs.BF16,
+                     x_e4m3=True)
+
+
 def test_conv2d_fp8_rejections():
     import torch
     x = torch.zeros((1, 4, 4, 32), dtype=torch.bfloat16, device="cuda")

@@ -80,12 +80,22 @@ def test_fp8_forced_mode_keeps_every_eligible_conv_on_fp8():
     m.forward(x)
     torch.cuda.synchronize()
     ios = [m.conv_io(i) for i in range(len(m.conv_info()))]
-    eligible = [io for io in ios if io.groups == 1 and not io.stem and io.up.data is None and io.cin % 64 == 0]
+    eligible = [io for io in ios if io.groups == 1 and not io.stem and io.cin % 64 == 0 and
+                (io.up.data is None or io.up.c % 64 == 0)]
     assert all(io.fp8 for io in eligible) and len(eligible) > 60
+    assert any(io.up.data is not None for io in eligible)   # the fused-upsample convs too
     plan = m.get_plan()
     # every eligible conv has an fp8 plan entry, the Detect output convs included
     assert sum(1 for p in plan if p & vrs.PLAN_FP8) == len(eligible)
     assert all(io.in_scale > 0 for io in eligible)
+    # e4m3 storage: inputs read as e4m3 use their buffer's step; buffers with
+    # a non-fp8 reader or writer (attention, SPPF, depthwise, the stem) stay bf16
+    x8 = [io for io in eligible if io.x_e4m3]
+    assert len(x8) > 30 and all(io.in_scale == io.x_step for io in x8)
+    assert sum(io.y_e4m3 for io in ios) > 30
+    for i, (pre, _, _) in enumerate(m.conv_info()):
+        if pre.endswith(("attn.qkv", "model.9.cv1", "model.16.cv2")) or ".one2one_cv3." in pre and pre.endswith(".0"):
+            assert not ios[i].y_e4m3, pre
 
 
 def test_conv_io_views():

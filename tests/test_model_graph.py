@@ -19,6 +19,7 @@ class Recorder(dict):
         self.act_q = lambda t: t
         self.fp8 = {}
         self.observe = None
+        self.store8 = {}
         self.used = set()
 
     def __getitem__(self, k):

@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <memory>
 #include <string>
 
@@ -29,6 +30,12 @@ struct V {  // channel slice of a model buffer
 struct Buf {
   int h = 0, w = 0, pitch = 0;
   void* dev = nullptr;
+  // VRS_FP8 models: stored as e4m3 on `step` (every reader and writer is an
+  // fp8 conv); buffers read together by one conv (input + fused-upsample
+  // source) share a step group
+  bool f8 = false;
+  int grp = -1;
+  float step = 0.f;
 };
 
 struct Param {
@@ -133,7 +140,7 @@ struct vrs_model {
   // absmax reduction in front of each fp8 conv (slot = conv index)
   bool calibrated = false;
   bool calib_mode = false;
-  unsigned* absmax = nullptr;
+  unsigned* absmax = nullptr;   // slots: convs, then buffers
 };
 
 namespace {
@@ -599,6 +606,95 @@ bool pair_fused(const vrs_model* m, size_t i) {
          !(m->convs[i].f8 && m->convs[i].run_f8);
 }
 
+// fp8 conv c: e4m3 input / output / residual flags and steps from the
+// buffers' storage plan (steps of 1 before calibration: timing only).
+void e4m3_flags(const vrs_model* m, const ConvStep& c, ConvSpec& cs) {
+  auto step = [&](int b) { return m->bufs[b].step > 0.f ? m->bufs[b].step : 1.f; };
+  cs.x_f8 = c.x.buf >= 0 && m->bufs[c.x.buf].f8;
+  cs.y_f8 = c.out_idx < 0 && c.y.buf >= 0 && m->bufs[c.y.buf].f8;
+  cs.res_f8 = c.has_res && m->bufs[c.res.buf].f8;
+  if (cs.y_f8) cs.out_step = step(c.y.buf);
+  if (cs.res_f8) cs.res_step = step(c.res.buf);
+}
+
+// VRS_FP8 models: the activation buffers stored as e4m3.  A buffer is when
+// every launch that writes it and every conv that reads it (input, residual
+// or fused-upsample source) is a conv running on the fp8 MFMA, each such
+// view 16-channel aligned, and something writes it; the input and the
+// fused-upsample source of one conv must agree (both e4m3, in one step group,
+// or both bfloat16).  Everything else -- the stem, depthwise convs, SPPF
+// pooling, attention, bf16 convs, model outputs -- keeps bfloat16 buffers.
+void plan_e4m3(vrs_model* m) {
+  const size_t nb = m->bufs.size();
+  for (Buf& b : m->bufs) {
+    b.f8 = false;
+    b.grp = -1;
+  }
+  if (m->dtype != VRS_FP8) return;
+  std::vector<char> ok(nb, 1), written(nb, 0);
+  auto al16 = [&](V v) { return v.c_off % 16 == 0 && v.c % 16 == 0 && m->bufs[v.buf].pitch % 16 == 0; };
+  auto no = [&](V v) { if (v.buf >= 0) ok[v.buf] = 0; };
+  for (const Step& st : m->steps) {
+    switch (st.type) {
+      case Step::CONV: {
+        const ConvStep& c = m->convs[st.conv];
+        const bool f = c.f8 && c.run_f8 && !c.stem && !pair_fused(m, st.conv);
+        if (pair_fused(m, st.conv)) {
+          no(c.y);
+          break;
+        }
+        for (const V* v : {&c.x, c.has_res ? &c.res : nullptr, c.has_up ? &c.up : nullptr})
+          if (v && v->buf >= 0 && (!f || !al16(*v))) ok[v->buf] = 0;
+        if (c.out_idx < 0 && c.y.buf >= 0) {
+          written[c.y.buf] = 1;
+          if (!f || !al16(c.y)) ok[c.y.buf] = 0;
+        }
+        break;
+      }
+      case Step::STEM: no(m->convs[st.conv].y); break;
+      case Step::PACK: no(st.b); break;
+      case Step::POOL: case Step::UNPACK: no(st.a); break;
+      case Step::UP: case Step::ATTN: no(st.a); no(st.b); break;
+    }
+  }
+  for (size_t b = 0; b < nb; ++b) m->bufs[b].f8 = ok[b] && written[b];
+  // an fp8 conv's input and fused-upsample source: both e4m3 or both bf16
+  for (bool changed = true; changed;) {
+    changed = false;
+    for (const ConvStep& c : m->convs)
+      if (c.f8 && c.run_f8 && c.has_up && m->bufs[c.x.buf].f8 != m->bufs[c.up.buf].f8) {
+        m->bufs[c.x.buf].f8 = m->bufs[c.up.buf].f8 = false;
+        changed = true;
+      }
+  }
+  // step groups: union of the two views of each fused-upsample conv
+  std::vector<int> parent(nb);
+  for (size_t b = 0; b < nb; ++b) parent[b] = (int)b;
+  std::function<int(int)> root = [&](int b) { return parent[b] == b ? b : parent[b] = root(parent[b]); };
+  for (const ConvStep& c : m->convs)
+    if (c.f8 && c.run_f8 && c.has_up && m->bufs[c.x.buf].f8) parent[root(c.x.buf)] = root(c.up.buf);
+  for (size_t b = 0; b < nb; ++b)
+    if (m->bufs[b].f8) m->bufs[b].grp = root((int)b);
+}
+
+// Calibration forward (bf16): after a step that writes into a buffer planned
+// as e4m3, max |x| of the written channels into the buffer's absmax slot.
+int calib_writes(vrs_model* m, const LaunchIO& sio, std::vector<Launch>& ls, std::vector<std::string>& labels,
+                 std::vector<LaunchIO>& io) {
+  if (!m->calib_mode) return VRS_OK;
+  for (const Access& w : sio.wr) {
+    if (w.res < 0 || !m->bufs[w.res].f8) continue;
+    vrs_nhwc v = view_of(m, V{w.res, w.c0, w.c1 - w.c0});
+    const size_t before = ls.size();
+    if (int rc = prep_absmax(m->ctx, v, m->absmax + m->convs.size() + w.res, ls)) return rc;
+    for (size_t i = before; i < ls.size(); ++i) {
+      labels.push_back("calib.buf" + std::to_string(w.res) + ":" + ls[i].name);
+      io.push_back(LaunchIO{{{w.res, w.c0, w.c1}}, {}});
+    }
+  }
+  return VRS_OK;
+}
+
 int prepare(vrs_model* m, const float* x, float* const* outs) {
   const int nout = (int)m->out_dims.size();
   std::vector<float*> o(outs, outs + nout);
@@ -684,6 +780,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
           cs.tile = c.tile8;
           w = c.w8;
           scale = c.scale8;
+          e4m3_flags(m, c, cs);
         }
         const size_t conv_first = ls.size();
         if (c.out_idx >= 0) {
@@ -711,6 +808,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         conv_launch[st.conv] = (int)ls.size() - 1;
         for (size_t i = conv_first; i < ls.size(); ++i) labels.push_back(label + ":" + ls[i].name);
         flush_io();
+        if ((rc = calib_writes(m, sio, ls, labels, io))) return rc;
         continue;
       }
       case Step::STEM: {
@@ -745,6 +843,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
     if (rc) return rc;
     for (size_t i = before; i < ls.size(); ++i) labels.push_back(label + ":" + ls[i].name);
     flush_io();
+    if ((rc = calib_writes(m, sio, ls, labels, io))) return rc;
   }
   m->launches = std::move(ls);
   m->labels = std::move(labels);
@@ -844,6 +943,7 @@ int autotune_tiles(vrs_model* m) {
     ConvSpec cs;
     cs.k = c.k; cs.stride = c.s; cs.dtype = dt; cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
     cs.in_scale = 1.f;  // timing only: values do not matter
+    if (pass) e4m3_flags(m, c, cs);   // the storage planned for the forced fp8 model
     float best = 1e30f;
     int best_tile = VRS_TILE_AUTO;
     for (int t : cand) {
@@ -997,8 +1097,8 @@ int finalize_upload(vrs_model* m) {
     c.scale = static_cast<float*>(p);
     if ((rc = dev_upload(m, shift.data(), shift.size() * 4, &p))) return rc;
     c.shift = static_cast<float*>(p);
-    // (a fused-upsample conv stays bfloat16: its kernels have no fp8 instance)
-    c.f8 = m->dtype == VRS_FP8 && !c.dw && !c.stem && !c.has_up && c.cin % 64 == 0 && cin_g == c.cin;
+    c.f8 = m->dtype == VRS_FP8 && !c.dw && !c.stem && c.cin % 64 == 0 && cin_g == c.cin &&
+           (!c.has_up || c.up.c % 64 == 0);
     if (c.f8) {  // e4m3 copy of the weights; the bf16 one serves calibration
       const int64_t qb = vrs_pack_conv_weight_fp8(nullptr, c.cout, cin_g, c.k, c.cin, nullptr, nullptr);
       if (qb < 0) return (int)qb;
@@ -1015,7 +1115,7 @@ int finalize_upload(vrs_model* m) {
   }
   if (m->dtype == VRS_FP8) {
     void* p;
-    VRS_HIP(hipMalloc(&p, m->convs.size() * sizeof(unsigned)));
+    VRS_HIP(hipMalloc(&p, (m->convs.size() + m->bufs.size()) * sizeof(unsigned)));
     m->allocs.push_back(p);
     m->absmax = static_cast<unsigned*>(p);
   }
@@ -1025,6 +1125,9 @@ int finalize_upload(vrs_model* m) {
 // A caller's tile plan (vrs_model_set_plan) instead of autotuning: every
 // entry is checked against the kernels built for its conv's shape.
 int apply_plan(vrs_model* m) {
+  // first the entries' kinds (which convs run on fp8 decides which buffers
+  // are e4m3), then each entry validated by preparing its launch with that
+  // storage
   for (size_t i = 0; i < m->convs.size(); ++i) {
     ConvStep& c = m->convs[i];
     const int32_t e = m->plan[i];
@@ -1037,26 +1140,11 @@ int apply_plan(vrs_model* m) {
     }
     if (f8 && !c.f8)
       return fail(VRS_EINVAL, "plan entry %zu (%s): fp8 requested for a conv that has no fp8 form", i, c.pre.c_str());
-    if (tile == VRS_TILE_STEM_PAIR) {
-      if (f8 || !pair_eligible(m, i))
-        return fail(VRS_EINVAL,
-                    "plan entry %zu (%s): the stem pair applies only to a bf16 3x3/s2 64->128 conv reading a "
-                    "64-channel stem's output alone (image width a multiple of 4)",
-                    i, c.pre.c_str());
-    } else if (tile != VRS_TILE_AUTO) {   // validate by preparing the launch
-      ConvSpec cs;
-      cs.k = c.k; cs.stride = c.s; cs.dtype = f8 ? VRS_FP8 : act_dt(m);
-      cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
-      cs.in_scale = 1.f;
-      cs.tile = tile;
-      // a Detect output conv is prepared against a stand-in output address
-      // (16-byte aligned, as every output tensor the model is given must be):
-      // preparing only builds the launch arguments, nothing is launched
-      std::vector<float*> probe(m->out_dims.size(), reinterpret_cast<float*>(uintptr_t{1} << 20));
-      std::vector<Launch> ls;
-      const int rc = prep_conv_step(m, c, cs, f8 ? c.w8 : c.w, f8 ? c.scale8 : c.scale, probe.data(), ls);
-      if (rc) return fail(rc, "plan entry %zu (%s): %s", i, c.pre.c_str(), vrs_last_error());
-    }
+    if (tile == VRS_TILE_STEM_PAIR && (f8 || !pair_eligible(m, i)))
+      return fail(VRS_EINVAL,
+                  "plan entry %zu (%s): the stem pair applies only to a bf16 3x3/s2 64->128 conv reading a "
+                  "64-channel stem's output alone (image width a multiple of 4)",
+                  i, c.pre.c_str());
     if (c.f8) {
       c.run_f8 = f8;
       if (f8) c.tile8 = tile;
@@ -1064,6 +1152,27 @@ int apply_plan(vrs_model* m) {
     } else {
       c.tile = tile;
     }
+  }
+  plan_e4m3(m);
+  for (size_t i = 0; i < m->convs.size(); ++i) {
+    const ConvStep& c = m->convs[i];
+    const int32_t e = m->plan[i];
+    const bool f8 = (e & VRS_PLAN_FP8) != 0;
+    const int tile = e & ~VRS_PLAN_FP8;
+    if (!tunable(c) || tile == VRS_TILE_STEM_PAIR || tile == VRS_TILE_AUTO) continue;
+    ConvSpec cs;   // validate by preparing the launch
+    cs.k = c.k; cs.stride = c.s; cs.dtype = f8 ? VRS_FP8 : act_dt(m);
+    cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
+    cs.in_scale = 1.f;
+    cs.tile = tile;
+    if (f8) e4m3_flags(m, c, cs);
+    // a Detect output conv is prepared against a stand-in output address
+    // (16-byte aligned, as every output tensor the model is given must be):
+    // preparing only builds the launch arguments, nothing is launched
+    std::vector<float*> probe(m->out_dims.size(), reinterpret_cast<float*>(uintptr_t{1} << 20));
+    std::vector<Launch> ls;
+    const int rc = prep_conv_step(m, c, cs, f8 ? c.w8 : c.w, f8 ? c.scale8 : c.scale, probe.data(), ls);
+    if (rc) return fail(rc, "plan entry %zu (%s): %s", i, c.pre.c_str(), vrs_last_error());
   }
   return VRS_OK;
 }
@@ -1174,12 +1283,20 @@ int vrs_model_finalize(vrs_model* m) {
   // leaves the model as it was (a retry folds and uploads again).
   const size_t first_alloc = m->allocs.size();
   int rc = finalize_upload(m);
+  // forced fp8: every eligible conv runs on fp8, so the e4m3 storage is known
+  // before the tiles are timed (they are timed on it)
+  if (!rc && m->plan.empty()) plan_e4m3(m);
   if (!rc) rc = m->plan.empty() ? (m->autotune ? autotune_tiles(m) : VRS_OK) : apply_plan(m);
+  if (!rc) plan_e4m3(m);
   if (rc) {
     const std::string err = vrs_last_error();
     for (size_t i = first_alloc; i < m->allocs.size(); ++i) (void)hipFree(m->allocs[i]);
     m->allocs.resize(first_alloc);
-    for (Buf& b : m->bufs) b.dev = nullptr;
+    for (Buf& b : m->bufs) {
+      b.dev = nullptr;
+      b.f8 = false;
+      b.grp = -1;
+    }
     for (ConvStep& c : m->convs) {
       c.w = c.w8 = nullptr;
       c.scale = c.shift = c.scale8 = nullptr;
@@ -1409,12 +1526,12 @@ int vrs_model_calibrate(vrs_model* m, const float* x, void* stream) {
     m->launches.clear();
     m->prep_x = nullptr;
     rc = prepare(m, x, outs.data());
-    if (!rc && hipMemsetAsync(m->absmax, 0, m->convs.size() * sizeof(unsigned), s) != hipSuccess)
+    if (!rc && hipMemsetAsync(m->absmax, 0, (m->convs.size() + m->bufs.size()) * sizeof(unsigned), s) != hipSuccess)
       rc = fail(VRS_EHIP, "vrs_model_calibrate: memset");
     for (size_t i = 0; !rc && i < m->launches.size(); ++i) rc = run(m->launches[i], s);
     if (!rc && hipStreamSynchronize(s) != hipSuccess) rc = fail(VRS_EHIP, "vrs_model_calibrate: sync");
   }
-  std::vector<unsigned> amax(m->convs.size());
+  std::vector<unsigned> amax(m->convs.size() + m->bufs.size());
   if (!rc && hipMemcpy(amax.data(), m->absmax, amax.size() * sizeof(unsigned), hipMemcpyDeviceToHost) != hipSuccess)
     rc = fail(VRS_EHIP, "vrs_model_calibrate: readback");
   for (float* p : outs) (void)hipFree(p);
@@ -1422,18 +1539,28 @@ int vrs_model_calibrate(vrs_model* m, const float* x, void* stream) {
   m->launches.clear();
   m->prep_x = nullptr;
   if (rc) return rc;
-  for (size_t i = 0; i < m->convs.size(); ++i) {
+  // smallest power of two >= a / 448 (1 for an all-zero tensor)
+  auto step_of = [](unsigned bits) {
+    float a;
+    memcpy(&a, &bits, 4);
+    if (!(a > 0.f) || !std::isfinite(a)) return 1.f;
+    int e;
+    const float f = std::frexp(a / 448.f, &e);
+    return std::ldexp(1.f, f == 0.5f ? e - 1 : e);
+  };
+  // e4m3 buffers: one step per group, from the largest value ever written
+  // into any of its buffers
+  const size_t nc = m->convs.size();
+  std::vector<unsigned> gmax(m->bufs.size(), 0u);
+  for (size_t b = 0; b < m->bufs.size(); ++b)
+    if (m->bufs[b].f8) gmax[m->bufs[b].grp] = std::max(gmax[m->bufs[b].grp], amax[nc + b]);   // non-negative floats
+  for (Buf& b : m->bufs) b.step = b.f8 ? step_of(gmax[b.grp]) : 0.f;
+  for (size_t i = 0; i < nc; ++i) {
     ConvStep& c = m->convs[i];
     if (!c.f8) continue;
-    float a;
-    memcpy(&a, &amax[i], 4);
-    // smallest power of two >= a / 448 (1 for an all-zero input)
-    float sc = 1.f;
-    if (a > 0.f && std::isfinite(a)) {
-      int e;
-      const float f = std::frexp(a / 448.f, &e);
-      sc = std::ldexp(1.f, f == 0.5f ? e - 1 : e);
-    }
+    // an e4m3 input is read on its buffer's step; a bf16 one is quantised on
+    // the step of the conv's own input
+    const float sc = m->bufs[c.x.buf].f8 ? m->bufs[c.x.buf].step : step_of(amax[i]);
     c.in_scale = sc;
     std::vector<float> s8(c.scale8_host);
     for (float& v : s8) v *= sc;
@@ -1487,6 +1614,16 @@ int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io) {
   io->out_sb = c.sb;
   io->out_sp = c.sp;
   io->out_sc = c.sc;
+  auto e4 = [&](const vrs_nhwc& v, V src, int32_t* flag, float* step) {
+    if (v.data && src.buf >= 0 && m->bufs[src.buf].f8) {
+      *flag = 1;
+      *step = m->bufs[src.buf].step;
+    }
+  };
+  e4(io->x, c.x, &io->x_e4m3, &io->x_step);
+  e4(io->y, c.y, &io->y_e4m3, &io->y_step);
+  if (c.has_res) e4(io->res, c.res, &io->res_e4m3, &io->res_step);
+  if (c.has_up) e4(io->up, c.up, &io->up_e4m3, &io->up_step);
   return VRS_OK;
 }
 

@@ -57,7 +57,14 @@ int vrs_conv2d(vrs_ctx* ctx, const vrs_conv_desc* d, const vrs_nhwc* x, const vo
   ConvSpec cs;
   cs.k = d->k; cs.stride = d->stride; cs.act = d->act; cs.dtype = d->dtype; cs.tile = d->tile;
   cs.in_scale = d->in_scale;
+  cs.x_f8 = d->x_e4m3 != 0;
+  cs.y_f8 = d->y_e4m3 != 0;
+  cs.res_f8 = d->res_e4m3 != 0;
+  cs.out_step = d->out_step;
+  cs.res_step = d->res_step;
   if (d->groups < 1) return fail(VRS_EINVAL, "vrs_conv2d: groups=%d", d->groups);
+  if ((cs.x_f8 || cs.y_f8 || cs.res_f8) && (d->groups != 1 || d->dtype != VRS_FP8))
+    return fail(VRS_EINVAL, "vrs_conv2d: e4m3 activations are for dense VRS_FP8 convs");
   if (d->groups > 1 && d->groups == x->c && d->groups == y->c) cs.depthwise = true;
   else cs.groups = d->groups;
   if (d->act != VRS_ACT_NONE && d->act != VRS_ACT_SILU) return fail(VRS_EINVAL, "vrs_conv2d: act %d", d->act);

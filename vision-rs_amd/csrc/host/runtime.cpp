@@ -56,6 +56,15 @@ int run(const Launch& l, hipStream_t s) {
 static const void* at(const vrs_nhwc& v, int dtype) {
   return static_cast<const char*>(v.data) + (int64_t)v.c_off * elt_size(dtype);
 }
+// a view of e4m3 bytes (fp8 convs with e4m3 activations in memory)
+static const void* at8(const vrs_nhwc& v) { return static_cast<const char*>(v.data) + v.c_off; }
+
+// power of two in [2^-100, 2^100] (an e4m3 activation step)
+static bool pow2_step(float s) {
+  int e = 0;
+  const float m = frexpf(s, &e);
+  return s > 0.f && m == 0.5f && s >= 1e-30f && s <= 1e30f;
+}
 
 static int check_view(const vrs_nhwc& v, const char* what, int align) {
   if (!v.data) return fail(VRS_EINVAL, "%s: null data", what);
@@ -107,23 +116,24 @@ static const TileInfo* tile_info(int code) {
 // up: the fused-upsample instance (_u), built for 128x128, 256x128, 128x256
 // and 256x256 in bf16 and 128x128 and 64x256 in float32, aligned and not
 // persistent
-static int tile_kernel(int code, int cin, int dtype, bool up, char* name, size_t n, int* bm, int* bn, int* threads) {
+static int tile_kernel(int code, int cin, int dtype, bool up, char* name, size_t n, int* bm, int* bn, int* threads,
+                       bool x8 = false, bool y8 = false) {
   if ((code & 0xff) == VRS_TILE_H3 || (code & 0xff) == VRS_TILE_W1_256 || (code & 0xff) == VRS_TILE_W1_128)
     return fail(VRS_EINVAL, "conv: the halo and weight-stationary tiles are prepared separately");
   const TileInfo* t = tile_info(code);
   if (!t) return fail(VRS_EINVAL, "conv: unknown tile code %d", code);
   if (up) {
-    const bool built = dtype == VRS_BF16 ? (t->code == VRS_TILE_128x128 || t->code == VRS_TILE_256x128 ||
-                                            t->code == VRS_TILE_128x256 || t->code == VRS_TILE_256x256)
-                                         : dtype == VRS_F32 && (t->code == VRS_TILE_128x128 || t->code == VRS_TILE_64x256);
+    const bool built = dtype != VRS_F32 ? (t->code == VRS_TILE_128x128 || t->code == VRS_TILE_256x128 ||
+                                           t->code == VRS_TILE_128x256 || t->code == VRS_TILE_256x256)
+                                        : (t->code == VRS_TILE_128x128 || t->code == VRS_TILE_64x256);
     if (!built || (code & VRS_TILE_PERSIST) || cin % 32 != 0)
       return fail(VRS_EUNSUPPORTED, "conv: no fused-upsample kernel for tile %s (dtype %d, Cin %d)", t->tag, dtype, cin);
   }
   if (dtype == VRS_FP8) {
     if (cin % 64 != 0) return fail(VRS_EUNSUPPORTED, "conv fp8: needs Cin %% 64 == 0 (Cin=%d)", cin);
-    if (t->code == VRS_TILE_32x256 || t->code == VRS_TILE_64x64)
-      return fail(VRS_EUNSUPPORTED, "conv fp8: tile %s not built", t->tag);
-    snprintf(name, n, "vrs_conv_fp8_%s_k64_a", t->tag);
+    if (t->code == VRS_TILE_32x256 || t->code == VRS_TILE_64x64 || (code & VRS_TILE_PERSIST))
+      return fail(VRS_EUNSUPPORTED, "conv fp8: tile %s%s not built", t->tag, (code & VRS_TILE_PERSIST) ? " persistent" : "");
+    snprintf(name, n, "vrs_conv_fp8_%s_k64_%c%s%s", t->tag, up ? 'u' : 'a', x8 ? "_x8" : "", y8 ? "_y8" : "");
     *bm = t->bm;
     *bn = t->bn;
     *threads = t->threads;
@@ -234,11 +244,21 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   int rc;
   const bool f8 = cs.dtype == VRS_FP8;
   if (!f8 && (rc = check_dtype(cs.dtype))) return rc;
+  if (!f8 && (cs.x_f8 || cs.y_f8 || cs.res_f8))
+    return fail(VRS_EINVAL, "conv: e4m3 activations need the fp8 dtype");
+  // bytes per element of the input (and fused-upsample source)
+  const int64_t xs = cs.x_f8 ? 1 : (int64_t)elt_size(cs.dtype);
   if (f8) {
-    int e = 0;
-    const float m = frexpf(cs.in_scale, &e);
-    if (!(cs.in_scale > 0.f) || m != 0.5f || cs.in_scale < 1e-30f || cs.in_scale > 1e30f)
+    if (!pow2_step(cs.in_scale))
       return fail(VRS_EINVAL, "conv fp8: in_scale %g must be a positive power of two", (double)cs.in_scale);
+    if (cs.y_f8 && !pow2_step(cs.out_step))
+      return fail(VRS_EINVAL, "conv fp8: out_step %g must be a positive power of two", (double)cs.out_step);
+    if (cs.y_f8 && a.stage != 1)
+      return fail(VRS_EUNSUPPORTED, "conv fp8: an e4m3 output must be an NHWC view with 16-channel aligned offset, "
+                  "pitch and count, under 2 GiB");
+    if (cs.res_f8 && a.stage != 1)
+      return fail(VRS_EUNSUPPORTED, "conv fp8: an e4m3 residual needs a staged output (16-byte aligned NHWC view)");
+    a.out_step = cs.y_f8 ? cs.out_step : 0.f;
     a.in_scale = cs.in_scale;
     // bfloat16 bits of 448 * in_scale (exact: 448 has 3 significant bits)
     uint32_t fb;
@@ -247,18 +267,18 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
     const uint32_t hb = fb >> 16;
     a.clamp_bits = hb | (hb << 16);
   }
-  if ((rc = check_view(x, "conv input", 8))) return rc;
+  if ((rc = check_view(x, "conv input", cs.x_f8 ? 16 : 8))) return rc;
   if (!w || !scale || !shift) return fail(VRS_EINVAL, "conv: null weight/scale/shift");
   if (cs.k < 1 || cs.k > 7 || cs.k % 2 == 0 || cs.stride < 1) return fail(VRS_EBADSHAPE, "conv: k=%d s=%d", cs.k, cs.stride);
   if (ho != out_size(x.h, cs.k, cs.stride) || wo != out_size(x.w, cs.k, cs.stride))
     return fail(VRS_EBADSHAPE, "conv: output %dx%d does not match input %dx%d k=%d s=%d", ho, wo, x.h, x.w, cs.k,
                 cs.stride);
-  a.x = at(x, cs.dtype);
+  a.x = cs.x_f8 ? at8(x) : at(x, cs.dtype);
   a.w = w;
   a.scale = scale;
   a.shift = shift;
   {  // raw-buffer extents (the kernels use 32-bit byte offsets)
-    const int64_t xb = ((int64_t)x.n * x.h * x.w * x.pitch - x.c_off) * (int64_t)elt_size(cs.dtype);
+    const int64_t xb = ((int64_t)x.n * x.h * x.w * x.pitch - x.c_off) * xs;
     const int64_t wb = (int64_t)cout * cs.k * cs.k * x.c * (f8 ? 1 : (int64_t)elt_size(cs.dtype));
     if (xb >= (1ll << 31) || wb >= (1ll << 31))
       return fail(VRS_EBADSHAPE, "conv: input buffer (%lld B) or weights (%lld B) exceed 2 GiB", (long long)xb,
@@ -268,14 +288,14 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   }
   if (cs.up) {  // channels [0, up->c) of the input are up(*cs.up), nearest 2x
     const vrs_nhwc& u = *cs.up;
-    if ((rc = check_view(u, "conv upsample source", 8))) return rc;
+    if ((rc = check_view(u, "conv upsample source", cs.x_f8 ? 16 : 8))) return rc;
     if (cs.k != 1 || cs.stride != 1 || u.n != x.n || 2 * u.h != x.h || 2 * u.w != x.w || u.c >= x.c || u.c % 64)
       return fail(VRS_EBADSHAPE, "conv: a fused upsample needs a 1x1 stride-1 conv, a half-size source and a "
                   "split at a multiple of 64 channels below Cin (source %dx%dx%d, input %dx%dx%d)", u.h, u.w, u.c,
                   x.h, x.w, x.c);
-    const int64_t ub = ((int64_t)u.n * u.h * u.w * u.pitch - u.c_off) * (int64_t)elt_size(cs.dtype);
+    const int64_t ub = ((int64_t)u.n * u.h * u.w * u.pitch - u.c_off) * xs;
     if (ub >= (1ll << 31)) return fail(VRS_EBADSHAPE, "conv: upsample source exceeds 2 GiB");
-    a.x2 = at(u, cs.dtype);
+    a.x2 = cs.x_f8 ? at8(u) : at(u, cs.dtype);
     a.x2_bytes = (int32_t)ub;
     a.c_split = u.c;
     a.H2 = u.h;
@@ -353,10 +373,12 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
     return VRS_OK;
   }
   const int tile = cs.tile ? cs.tile
-                            : f8 ? (cout <= 64 ? VRS_TILE_64x256 : VRS_TILE_128x128)
+                            : f8 ? (cout <= 64 && !cs.up ? VRS_TILE_64x256 : VRS_TILE_128x128)
                                  : cs.up ? VRS_TILE_128x128   // built in every fused-upsample dtype
                                          : auto_tile(cout, x.c, M, cs.dtype, ctx->num_cu);
-  if ((rc = tile_kernel(tile, x.c, cs.dtype, cs.up != nullptr, name, sizeof name, &bm, &bn, &threads))) return rc;
+  if ((rc = tile_kernel(tile, x.c, cs.dtype, cs.up != nullptr, name, sizeof name, &bm, &bn, &threads, cs.x_f8,
+                        cs.y_f8)))
+    return rc;
   a.tiles_m = (cout + bm - 1) / bm;
   a.tiles_n = (int32_t)((M + bn - 1) / bn);
   int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
@@ -376,8 +398,10 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
   const double kk = (double)cs.k * cs.k;
   const double flops = 2.0 * (double)M * cout * kk * cin;
   const double cin_up = cs.up ? (double)cs.up->c : 0.0;   // read at a quarter of the pixels
-  const double bytes = (double)x.n * x.h * x.w * (cin - 0.75 * cin_up) * es + (double)cout * kk * cin * (f8 ? 1.0 : es) +
-                       (double)M * cout * (a.y_f32 ? 4.0 : es) + (a.res ? (double)M * cout * es : 0.0) + 8.0 * cout;
+  const double bytes = (double)x.n * x.h * x.w * (cin - 0.75 * cin_up) * (double)xs +
+                       (double)cout * kk * cin * (f8 ? 1.0 : es) +
+                       (double)M * cout * (a.y_f32 ? 4.0 : cs.y_f8 ? 1.0 : es) +
+                       (a.res ? (double)M * cout * (cs.res_f8 ? 1.0 : es) : 0.0) + 8.0 * cout;
   // Partial last round of 256x256 tiles (one workgroup per CU): when the
   // tiles leave a last round at most half full, the full rounds run on the
   // 256x256 tile (persistent: one workgroup per CU looping over an equal
@@ -555,21 +579,29 @@ int prep_conv(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const void* w
     if ((rc = check_view(*res, "conv residual", 4))) return rc;
     if (res->n != y.n || res->h != y.h || res->w != y.w || res->c != y.c)
       return fail(VRS_EBADSHAPE, "conv: residual shape differs from output");
-    a.res = at(*res, cs.dtype);
+    if (cs.res_f8 && !pow2_step(cs.res_step))
+      return fail(VRS_EINVAL, "conv fp8: res_step %g must be a positive power of two", (double)cs.res_step);
+    a.res = cs.res_f8 ? at8(*res) : at(*res, cs.dtype);
     a.r_sb = (int64_t)res->h * res->w * res->pitch; a.r_sp = res->pitch; a.r_sc = 1;
-    const int64_t rb = ((int64_t)res->n * res->h * res->w * res->pitch - res->c_off) * (int64_t)elt_size(cs.dtype);
+    const int64_t rb = ((int64_t)res->n * res->h * res->w * res->pitch - res->c_off) *
+                       (cs.res_f8 ? 1 : (int64_t)elt_size(cs.dtype));
     a.res_bytes = rb < (1ll << 31) ? (int32_t)rb : -1;   // -1: too large for 32-bit buffer offsets
+    a.res_f8 = cs.res_f8 ? 1 : 0;
+    a.res_step = cs.res_f8 ? cs.res_step : 0.f;
+  } else if (cs.res_f8) {
+    return fail(VRS_EINVAL, "conv: e4m3 residual flag without a residual");
   }
-  a.y = const_cast<void*>(at(y, cs.dtype));
+  a.y = const_cast<void*>(cs.y_f8 ? at8(y) : at(y, cs.dtype));
   a.y_sb = (int64_t)y.h * y.w * y.pitch; a.y_sp = y.pitch; a.y_sc = 1;
   a.y_f32 = 0;
-  // 16-byte chunks of 8 (bf16) or 4 (f32) channels must be whole and aligned;
-  // the staged stores (and residual loads) address the views with 32-bit
-  // raw-buffer byte offsets: pixel m at m * pitch from the view's base
-  const int chunk = cs.dtype == VRS_F32 ? 4 : 8;
-  const int64_t yb = ((int64_t)y.n * y.h * y.w * y.pitch - y.c_off) * (int64_t)elt_size(cs.dtype);
+  // 16-byte chunks of 8 (bf16), 4 (f32) or 16 (e4m3) channels must be whole
+  // and aligned; the staged stores (and residual loads) address the views
+  // with 32-bit raw-buffer byte offsets: pixel m at m * pitch from the view's
+  // base
+  const int chunk = cs.y_f8 ? 16 : cs.dtype == VRS_F32 ? 4 : 8;
+  const int64_t yb = ((int64_t)y.n * y.h * y.w * y.pitch - y.c_off) * (cs.y_f8 ? 1 : (int64_t)elt_size(cs.dtype));
   a.y_bytes = yb < (1ll << 31) ? (int32_t)yb : 0;
-  a.stage = (y.c % 8 == 0 && y.c_off % chunk == 0 && y.pitch % chunk == 0 && a.y_bytes > 0 &&
+  a.stage = (y.c % chunk == 0 && y.c % 8 == 0 && y.c_off % chunk == 0 && y.pitch % chunk == 0 && a.y_bytes > 0 &&
              (!res || a.res_bytes >= 0)) ? 1 : 0;
   return prep_dense(ctx, cs, x, w, scale, shift, y.c, y.h, y.w, a, out);
 }

@@ -101,6 +101,11 @@ struct ConvSpec {
   int cin_real = 0;  // unpadded input channels for work accounting (0: the view's)
   int tile = VRS_TILE_AUTO;  // dense conv tile (VRS_TILE_*)
   float in_scale = 1.f;      // VRS_FP8: activation quantisation step (power of two)
+  // VRS_FP8 with e4m3 activations in memory: x (and the fused-upsample
+  // source) hold e4m3 bytes on in_scale; y is written as e4m3 on out_step;
+  // res holds e4m3 bytes on res_step
+  bool x_f8 = false, y_f8 = false, res_f8 = false;
+  float out_step = 0.f, res_step = 0.f;
   // fused nearest-2x upsample (1x1 stride-1 dense convs): input channels
   // [0, up->c) are read from this half-resolution view instead of x
   const vrs_nhwc* up = nullptr;

@@ -67,6 +67,13 @@ typedef struct {
    * logical / tiles_m); non-zero for the launch that takes the pixel tiles
    * left over by a larger tile's full rounds */
   int32_t n_tile0;
+  /* fp8 kernels with e4m3 activations in memory: the output's quantisation
+   * step (e4m3-output kernels: y = e4m3(clamp(out, +-448*out_step) /
+   * out_step)); a residual stored as e4m3 (res_f8 = 1) is read as
+   * e4m3 * res_step */
+  float out_step;
+  float res_step;
+  int32_t res_f8;
 } vrs_conv_args;
 
 /* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the

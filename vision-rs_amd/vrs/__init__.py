@@ -55,7 +55,9 @@ class Nhwc(C.Structure):
 
 class ConvDesc(C.Structure):
     _fields_ = [("k", C.c_int32), ("stride", C.c_int32), ("groups", C.c_int32), ("act", C.c_int32),
-                ("dtype", C.c_int32), ("tile", C.c_int32), ("in_scale", C.c_float)]
+                ("dtype", C.c_int32), ("tile", C.c_int32), ("in_scale", C.c_float),
+                ("x_e4m3", C.c_int32), ("y_e4m3", C.c_int32), ("res_e4m3", C.c_int32),
+                ("out_step", C.c_float), ("res_step", C.c_float)]
 
 
 class PsaDesc(C.Structure):
@@ -85,7 +87,9 @@ class ConvIo(C.Structure):
                 ("act", C.c_int32), ("plain", C.c_int32), ("stem", C.c_int32), ("fp8", C.c_int32),
                 ("in_scale", C.c_float), ("dtype", C.c_int32), ("cin", C.c_int32), ("cout", C.c_int32),
                 ("x", Nhwc), ("y", Nhwc), ("res", Nhwc), ("up", Nhwc), ("out_idx", C.c_int32),
-                ("out_off", C.c_int64), ("out_sb", C.c_int64), ("out_sp", C.c_int64), ("out_sc", C.c_int64)]
+                ("out_off", C.c_int64), ("out_sb", C.c_int64), ("out_sp", C.c_int64), ("out_sc", C.c_int64),
+                ("x_e4m3", C.c_int32), ("y_e4m3", C.c_int32), ("res_e4m3", C.c_int32), ("up_e4m3", C.c_int32),
+                ("x_step", C.c_float), ("y_step", C.c_float), ("res_step", C.c_float), ("up_step", C.c_float)]
 
 
 PLAN_FP8 = 0x10000
@@ -240,17 +244,20 @@ class Context:
 
     # ---- single ops --------------------------------------------------------
     def conv2d(self, x, w, scale, shift, y, k, stride=1, groups=1, act=ACT_SILU, res=None, dtype=BF16,
-               stream=None, tile=TILE_AUTO, in_scale=1.0):
+               stream=None, tile=TILE_AUTO, in_scale=1.0, x_e4m3=False, y_e4m3=False, out_step=0.0,
+               res_e4m3=False, res_step=0.0):
         """x, y, res: Nhwc views; w/scale/shift: device tensors.  FP8: w from
-        pack_conv_weight_fp8, scale including weight scale * in_scale."""
-        d = ConvDesc(k, stride, groups, act, dtype, tile, in_scale)
+        pack_conv_weight_fp8, scale including weight scale * in_scale; views of
+        uint8 tensors hold e4m3 activations when x_e4m3 / y_e4m3 / res_e4m3."""
+        d = ConvDesc(k, stride, groups, act, dtype, tile, in_scale, int(x_e4m3), int(y_e4m3), int(res_e4m3),
+                     out_step, res_step)
         check(lib().vrs_conv2d(self.handle, C.byref(d), C.byref(x), _ptr(w), _ptr(scale), _ptr(shift),
                                C.byref(res) if res is not None else None, C.byref(y), _stream(stream)))
 
     def conv_stem(self, x_nchw, w, scale, shift, y, act=ACT_SILU, dtype=BF16, stream=None):
         """model.0 (3x3 s2, 3 channels) from the NCHW float32 image into NHWC view y."""
         n, c, h, w_ = x_nchw.shape
-        d = ConvDesc(3, 2, 1, act, dtype, TILE_AUTO, 1.0)
+        d = ConvDesc(3, 2, 1, act, dtype, TILE_AUTO, 1.0, 0, 0, 0, 0.0, 0.0)
         check(lib().vrs_conv_stem(self.handle, C.byref(d), _ptr(x_nchw), n, c, h, w_, _ptr(w), _ptr(scale),
                                   _ptr(shift), C.byref(y), _stream(stream)))
 
@@ -260,8 +267,8 @@ class Context:
         float32 image into the 128-channel NHWC view y; w0 from pack_stem_weight, w1 from
         pack_conv_weight."""
         n, c, h, w_ = x_nchw.shape
-        d0 = ConvDesc(3, 2, 1, act, dtype, TILE_AUTO, 1.0)
-        d1 = ConvDesc(3, 2, 1, act, dtype, TILE_AUTO, 1.0)
+        d0 = ConvDesc(3, 2, 1, act, dtype, TILE_AUTO, 1.0, 0, 0, 0, 0.0, 0.0)
+        d1 = ConvDesc(3, 2, 1, act, dtype, TILE_AUTO, 1.0, 0, 0, 0, 0.0, 0.0)
         check(lib().vrs_conv_stem_pair(self.handle, C.byref(d0), C.byref(d1), _ptr(x_nchw), n, c, h, w_, _ptr(w0),
                                        _ptr(scale0), _ptr(shift0), _ptr(w1), _ptr(scale1), _ptr(shift1),
                                        C.byref(y), _stream(stream)))
