@@ -137,7 +137,9 @@ def save_plan(path, m, note):
 def traffic_pass(a, ctx, labels_out):
     """Workload for the two rocprofv3 --pmc passes: a 1 GiB copy (counter
     calibration), model build + tile autotuning, then two eager forwards; the
-    last forward's dispatches are the ones the summary reads."""
+    last forward's dispatches are the ones the summary reads.  --dtype fp8:
+    the forced fp8 model (every eligible conv on e4m3, its committed plan),
+    calibrated on the batch first."""
     import torch
     import vrs
     from vrs.synth import images, seeded_params
@@ -146,11 +148,12 @@ def traffic_pass(a, ctx, labels_out):
     dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    dt = vrs.BF16 if a.dtype == "bf16" else vrs.F32
+    dt = {"bf16": vrs.BF16, "f32": vrs.F32, "fp8": vrs.FP8}[a.dtype]
     m = vrs.Model(ctx, vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant=a.variant, one2one=True),
-                  a.batch, a.size, a.size, dt, 1e-3)
+                  a.batch, a.size, a.size, dt, 1e-3, autotune=2 if dt == vrs.FP8 else 1)
     # the committed tile plan, so each counter pass runs the kernels the bench line times
-    plan = None if a.autotune else load_plan(plan_path(a.variant, a.dtype, a.batch, a.size),
+    dname = "fp8_forced" if dt == vrs.FP8 else a.dtype
+    plan = None if a.autotune else load_plan(plan_path(a.variant, dname, a.batch, a.size),
                                               [pre for pre, _, _ in m.conv_info()])
     if plan is not None:
         m.set_plan(plan)
@@ -158,6 +161,8 @@ def traffic_pass(a, ctx, labels_out):
     m.load(seeded_params(m.params(), seed=0, bn="identity"))
     x = torch.from_numpy(images(a.batch, a.size, a.size, seed=0)).cuda()
     outs = m.alloc_outputs()
+    if dt == vrs.FP8:
+        m.calibrate(x)
     m.forward(x, outs)
     m.forward(x, outs)
     torch.cuda.synchronize()
@@ -316,22 +321,24 @@ def pmc_table(dirs, copy_bytes=2 ** 30):
     return "\n".join(out)
 
 
-def layers_summary(path, peak_tflops=PEAK_BF16_TFLOPS):
+def layers_summary(path, key="layer"):
     """Markdown table of the per-layer lines `bench.py --layers` writes to
-    stderr: each launch's time (HIP events around every launch of one
-    eager forward, averaged over 3), its algorithmic work and the fraction of
-    its bounding roofline (MFMA or HBM, whichever the work's arithmetic
-    intensity puts it under)."""
+    stderr (key "layer": the bf16 run; "layer8": the forced fp8 run): each
+    launch's time (HIP events around every launch of one eager forward,
+    averaged over 3), its algorithmic work and the fraction of its bounding
+    roofline (MFMA -- fp8 peak for the fp8 kernels, bf16 peak for the others
+    -- or HBM, whichever the work's arithmetic intensity puts it under)."""
     rows = []
     with open(path) as f:
         for line in f:
-            if line.startswith('{"layer"'):
+            if line.startswith('{"%s"' % key):
                 rows.append(json.loads(line))
-    ridge = peak_tflops * 1e12 / (PEAK_HBM_GBS * 1e9)
     out = ["| launch | kernel | us | GFLOP | MB | bound | achieved | roofline frac |", "|---|---|---|---|---|---|---|---|"]
     tot = ideal = 0.0
     for r in rows:
-        lab, sym = r["layer"].rsplit(":", 1)
+        lab, sym = r[key].rsplit(":", 1)
+        peak_tflops = PEAK_FP8_TFLOPS if "_fp8_" in sym else PEAK_BF16_TFLOPS
+        ridge = peak_tflops * 1e12 / (PEAK_HBM_GBS * 1e9)
         fl, mb, us = r["gflop"] * 1e9, r["mb"] * 1e6, r["us"]
         if fl > 0 and fl / max(mb, 1.0) > ridge:
             ach, bound, frac = f"{fl / us / 1e6:.0f} TFLOP/s", "mfma", fl / us / 1e6 / peak_tflops
@@ -340,8 +347,9 @@ def layers_summary(path, peak_tflops=PEAK_BF16_TFLOPS):
         tot += us
         ideal += max(fl / (peak_tflops * 1e12), mb / (PEAK_HBM_GBS * 1e9)) * 1e6
         out.append(f"| {lab} | {sym} | {us:.1f} | {r['gflop']:.2f} | {r['mb']:.1f} | {bound} | {ach} | {frac:.3f} |")
-    out += ["", f"{len(rows)} launches, {tot:.0f} us in sum (eager, one launch at a time; the hipGraph replay "
-                f"overlaps branches on 4 streams); at the MI355X peaks the same work needs {ideal:.0f} us."]
+    out += ["", f"{len(rows)} launches, {tot:.0f} us in sum (eager, one launch at a time; the hipGraph replay runs "
+                f"the same launches in order on one hardware queue); at the MI355X peaks the same work needs "
+                f"{ideal:.0f} us."]
     return "\n".join(out)
 
 
@@ -730,6 +738,8 @@ def main() -> int:
                          "SQ_VALU_MFMA_BUSY_CYCLES pass over the --traffic-pass workload")
     ap.add_argument("--layers-summary", metavar="STDERR_FILE",
                     help="instead (no GPU): per-layer roofline table from a --layers run's stderr")
+    ap.add_argument("--layers-key", default="layer",
+                    help="with --layers-summary: layer (the bf16 run) or layer8 (the forced fp8 run)")
     ap.add_argument("--trace-summary", nargs=2, metavar=("TRACE_DIR", "BENCH_JSON"),
                     help="instead (no GPU): per-kernel durations of a rocprofv3 --kernel-trace run of "
                          "bench.py --no-cpu --no-fp8 against its JSON line (pass the run's --steps)")
@@ -737,7 +747,7 @@ def main() -> int:
                     help="instead (no GPU): per-kernel medians of the counters in these --pmc passes")
     a = ap.parse_args()
     if a.layers_summary:
-        print(layers_summary(a.layers_summary))
+        print(layers_summary(a.layers_summary, a.layers_key))
         return 0
     if a.trace_summary:
         print(trace_summary(*a.trace_summary, steps=a.steps))
@@ -841,7 +851,11 @@ def main() -> int:
                               "fastest fp8 tile beats their fastest bf16 tile (per-layer plan); the rest bf16; "
                               "activations stored as e4m3 where every reader and writer is an fp8 conv, else bf16")
         m8.close()
-        m8, el8, ps8, _ = run(vrs.FP8, tune_mode=2)
+        m8, el8, ps8, ly8 = run(vrs.FP8, tune_mode=2)
+        if a.layers:
+            for r in ly8:
+                r = dict(r)
+                log(json.dumps({"layer8": r.pop("layer"), **r}))
         fp8_forced = fp8_summary(m8, el8, ps8,
                                  "every conv with Cin % 64 == 0 forced onto the fp8 MFMA (fastest fp8 tile per "
                                  "layer), the rest (stem, depthwise) bf16; activations stored as e4m3 where every "

@@ -367,8 +367,10 @@ int vrs_model_create(vrs_ctx* ctx, const vrs_block_desc* d, int32_t batch, int32
  * every dense conv is timed with each applicable VRS_TILE_* on the model's own
  * buffers and the fastest is kept; in a VRS_FP8 model each eligible conv also
  * keeps bf16 when its best bf16 tile is faster.  mode 2 (VRS_FP8 models):
- * only fp8 tiles are timed, every eligible conv runs on fp8.  mode 0: the
- * shape heuristic of VRS_TILE_AUTO. */
+ * only fp8 tiles are timed and every eligible conv runs on fp8, except the
+ * conv after a 64-channel stem when the stem pair (VRS_TILE_STEM_PAIR, a bf16
+ * kernel that never writes the stem's map) beats the stem plus that conv's
+ * best fp8 tile.  mode 0: the shape heuristic of VRS_TILE_AUTO. */
 int vrs_model_set_autotune(vrs_model* m, int32_t mode);
 /* Tile plan: one entry per conv (build order, vrs_model_num_convs): a
  * VRS_TILE_* code, OR VRS_PLAN_FP8 for a conv that runs on e4m3 (VRS_FP8

@@ -963,8 +963,12 @@ int autotune_tiles(vrs_model* m) {
    }
    if (rc) break;
    // the stem pair (this conv fused with the stem before it) against this
-   // conv's best bf16 tile plus the stem's own launch
-   if (pair_eligible(m, ci) && best_of[0] < 1e29f) {
+   // conv's best tile plus the stem's own launch (forced fp8: its best fp8
+   // tile -- the pair is a bf16 kernel that never writes the stem's map, and
+   // runs this conv on bf16 when it wins)
+   const bool forced = c.f8 && m->autotune == 2;
+   const float best_alone = forced ? best_of[1] : best_of[0];
+   if (pair_eligible(m, ci) && best_alone < 1e29f) {
      const ConvStep& s0 = m->convs[ci - 1];
      const size_t bytes = (size_t)m->batch * 3 * m->in_h * m->in_w * sizeof(float);
      if (!img) {
@@ -982,15 +986,15 @@ int autotune_tiles(vrs_model* m) {
                         view_of(m, c.y), lp) == VRS_OK) {
        float t0, tp;
        if ((rc = timed(l0, t0)) || (rc = timed(lp, tp))) break;
-       if (tp < 0.98f * (best_of[0] + t0)) {
+       if (tp < 0.98f * (best_alone + t0)) {
          c.tile = VRS_TILE_STEM_PAIR;
          best_of[0] = tp - t0;
        }
      }
    }
    // fp8 models: a layer whose bf16 tile is faster by 2% stays on bf16
-   // (unless fp8 is forced)
-   if (c.f8) c.run_f8 = m->autotune == 2 || !(best_of[0] < 0.98f * best_of[1]);
+   // (unless fp8 is forced; then only the conv fused into a stem pair does)
+   if (c.f8) c.run_f8 = forced ? c.tile != VRS_TILE_STEM_PAIR : !(best_of[0] < 0.98f * best_of[1]);
   }
   if (img) (void)hipFree(img);
   for (float* o : outs)
