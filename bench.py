@@ -302,9 +302,12 @@ def pmc_table(dirs, copy_bytes=2 ** 30):
     cal = {c: max(e.get(c, 0.0) for (n, _), e in med.items() if "copybuffer" in n.lower())
            for c in ("FETCH_SIZE", "WRITE_SIZE")}
     fac = {c: copy_bytes / 1024.0 / v if v else None for c, v in cal.items()}
+    known = {"GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES", "FETCH_SIZE", "WRITE_SIZE"}
+    extra = sorted({c for e in med.values() for c in e if not c.startswith("ns:") and c not in known})
     out = [f"Calibration (1 GiB device copy): FETCH_SIZE factor {fac['FETCH_SIZE'] or 0:.4f}, "
            f"WRITE_SIZE factor {fac['WRITE_SIZE'] or 0:.4f}.", "",
-           "| kernel | grid | us | MFMA busy % | HBM read MB | HBM write MB | HBM GB/s |", "|---|---|---|---|---|---|---|"]
+           "| kernel | grid | us | MFMA busy % | HBM read MB | HBM write MB | HBM GB/s |" +
+           "".join(f" {c} |" for c in extra), "|---|---|---|---|---|---|---|" + "---|" * len(extra)]
     for (name, grid), e in sorted(med.items()):
         if not name.startswith("vrs_"):
             continue
@@ -317,7 +320,8 @@ def pmc_table(dirs, copy_bytes=2 ** 30):
         wr = e["WRITE_SIZE"] * fac["WRITE_SIZE"] * 1024 / 1e6 if "WRITE_SIZE" in e and fac["WRITE_SIZE"] else None
         gbs = f"{(rd + wr) / us * 1e3:.0f}" if rd is not None and wr is not None and us else ""
         out.append(f"| {name} | {grid} | {us:.1f} | {busy} | {'' if rd is None else f'{rd:.2f}'} | "
-                   f"{'' if wr is None else f'{wr:.2f}'} | {gbs} |")
+                   f"{'' if wr is None else f'{wr:.2f}'} | {gbs} |" +
+                   "".join(f" {e[c]:.4g} |" if c in e else " |" for c in extra))
     return "\n".join(out)
 
 
