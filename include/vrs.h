@@ -431,10 +431,14 @@ int vrs_model_launch_work(const vrs_model* m, int32_t i, double* flops, double* 
 /* Run launches [first, first+count) of the prepared forward on `stream`
  * (per-kernel timing with events between launches). */
 int vrs_model_run_launches(vrs_model* m, int32_t first, int32_t count, void* stream);
-/* VRS_FP8 models: set the per-tensor activation scales of the fp8 convs from
- * one bfloat16 forward of `x` (same layout as vrs_model_forward): in_scale =
- * the smallest power of two >= max|input| / 448.  Required once before the
- * first fp8 forward/capture; synchronises `stream`. */
+/* VRS_FP8 models: set the activation steps from one bfloat16 forward of `x`
+ * (same layout as vrs_model_forward).  Buffers one conv reads together (its
+ * input and a fused-upsample source) form a step group; a group's step is the
+ * smallest power of two >= max|value| / 448 over every write into its
+ * buffers.  An fp8 conv's in_scale is its input's step; buffers stored as
+ * e4m3 (every writer and reader an fp8 conv) hold values on that step.
+ * Required once before the first fp8 forward/capture; synchronises
+ * `stream`. */
 int vrs_model_calibrate(vrs_model* m, const float* x, void* stream);
 /* Convs in build order: parameter prefix (e.g. "model.3"), whether it runs on
  * fp8 and its activation scale (0 before calibration). */

@@ -220,16 +220,6 @@ __device__ __forceinline__ uint32_t bf16x2_to_fp8x2(uint32_t v, uint32_t lim, fl
   return (uint32_t)(uint16_t)r[0];
 }
 
-// Four floats -> four e4m3 bytes (element 0 in the low byte): v / step
-// rounded to nearest even, step a power of two; |v| is clamped to 448 * step
-// first (the conversion does not saturate: past 448 it gives NaN).
-__device__ __forceinline__ uint32_t f32x4_to_fp8x4(float a, float b, float c, float d, float step) {
-  const float lim = 448.f * step;
-  auto cl = [lim](float v) { return __builtin_fminf(__builtin_fmaxf(v, -lim), lim); };
-  i16x2_t r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32((i16x2_t){0, 0}, cl(a), cl(b), step, false);
-  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, cl(c), cl(d), step, true);
-  return __builtin_bit_cast(uint32_t, r);
-}
 // Four e4m3 bytes (element 0 in the low byte) -> floats times step.
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void fp8x4_to_f32(uint32_t u, float step, float (&o)[4]) {
