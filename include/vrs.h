@@ -102,7 +102,10 @@ typedef struct {
  * workgroup keeps a 256- or 128-channel slice of the weights in LDS and
  * streams 64-pixel tiles of whole input pixel rows through it (Cin 384: as
  * two 192-channel halves).  In model plans, _128 also serves the
- * Detect head's channel-major float32 output convs with Cin 64 or 256. */
+ * Detect head's channel-major float32 output convs with Cin 64 or 256.
+ * VRS_FP8: _128 only, e4m3 weights in LDS and 128-pixel tiles, Cin 128, 192,
+ * 256, 384, 512 or 768, e4m3 or bf16 input and output, no residual; results
+ * bit-identical to the tiled fp8 kernels. */
 #define VRS_TILE_W1_256 8
 #define VRS_TILE_W1_128 9
 /* 64x64 tile (bf16, Cin % 32 == 0; 4 waves of 32x32): four times the
@@ -119,6 +122,10 @@ typedef struct {
  * Cin % step == 0, an even number of K steps, no residual, output channel
  * offset/pitch/count multiples of 8. */
 #define VRS_TILE_PERSIST 0x200
+/* OR VRS_TILE_K128 (VRS_FP8 only): 128-deep K steps, two fp8 MFMA k slices per
+ * LDS stage and barrier; tile 256x256 with an e4m3 input (x_e4m3), Cin % 128
+ * == 0, no fused upsample. */
+#define VRS_TILE_K128 0x400
 
 typedef struct {
   int32_t k;        /* square kernel size; padding = k/2 (blocks/conv.rs:36) */

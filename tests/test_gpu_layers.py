@@ -1,7 +1,8 @@
 """Layer by layer (teacher-forced) parity of the whole YOLO26m network at
 BASELINE config 5's full size (batch 64, 640x640), bf16 and fp8.
 
-The forward is replayed one kernel launch at a time.  Before each conv's
+The forward runs the committed tile plans (the bench line's kernels) and is
+replayed one kernel launch at a time.  Before each conv's
 launch its actual device input (and residual, and the half-size source of a
 fused upsample) is read back for images 0 and 31; after it, its output.  The
 oracle then recomputes that one conv from the device's own input, so every
@@ -194,6 +195,12 @@ def test_yolo26m_bs64_640_layer_by_layer(dtype):
     B, S = 64, 640
     desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="m", one2one=True)
     m = vrs.Model(ctx(), desc, B, S, S, dtype, 1e-3, autotune=2 if dtype == vrs.FP8 else 1)
+    # the committed tile plan: every kernel the bench line runs is the one checked here
+    import bench
+    plan = bench.load_plan(bench.plan_path("m", "fp8_forced" if dtype == vrs.FP8 else "bf16", B, S),
+                           [pre for pre, _, _ in m.conv_info()])
+    assert plan is not None, "committed plan missing or out of step with the model's convs"
+    m.set_plan(plan)
     P32 = seeded_params(m.params(), 0)
     P = {k: (bf16_round(v) if v.ndim == 4 else v) for k, v in P32.items()}
     x32 = np.random.default_rng(7).uniform(0, 1, (B, 3, S, S)).astype(np.float32)

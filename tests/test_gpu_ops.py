@@ -555,6 +555,125 @@ def test_conv2d_fp8_e4m3_activations(case):
         assert rel_err(from_nhwc(yt, cout, off), ref, FLOOR[vrs.BF16]) < TOL[vrs.BF16]
 
 
+# (n, cin, h, w, cout, e4m3 input, e4m3 output, channel offset, act)
+FP8_W1_CASES = [
+    (2, 128, 20, 18, 128, False, False, 0, vrs.ACT_SILU),
+    (1, 192, 16, 16, 256, False, True, 0, vrs.ACT_SILU),
+    (2, 256, 12, 11, 64, True, True, 16, vrs.ACT_SILU),
+    (1, 256, 9, 7, 128, False, False, 8, vrs.ACT_NONE),
+    (1, 384, 10, 13, 512, True, True, 0, vrs.ACT_SILU),
+    (1, 512, 9, 9, 192, True, False, 0, vrs.ACT_SILU),
+    (1, 512, 7, 9, 256, False, False, 0, vrs.ACT_SILU),
+    (1, 768, 8, 10, 512, True, True, 32, vrs.ACT_SILU),
+    (1, 768, 12, 12, 256, False, True, 0, vrs.ACT_NONE),
+]
+
+
+@pytest.mark.parametrize("case", FP8_W1_CASES)
+def test_conv2d_fp8_weight_stationary(case):
+    """The fp8 weight-stationary 1x1 kernel (VRS_TILE_W1_128 on VRS_FP8) on
+    every input width it is built for, with bf16 or e4m3 inputs and outputs,
+    ragged pixel counts, Cout below and above one 128-channel slice and channel
+    offsets: bit-identical to the tiled fp8 kernel (same e4m3 staging, k slices
+    in the same order, same output rounding), whose results the other fp8
+    tests hold to the oracle; and, on its own, within the bar of the oracle
+    conv of the same dequantised operands."""
+    import torch
+    n, cin, h, w, cout, x8, y8, off, act = case
+    rng = np.random.default_rng(91 + cin + cout)
+    x = bf16_round(rng.standard_normal((n, cin, h, w)).astype(np.float32) * 2.0)
+    wt = (rng.standard_normal((cout, cin, 1, 1)) * np.sqrt(2.0 / cin)).astype(np.float32)
+    bn_s = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    in_scale = float(2.0 ** np.ceil(np.log2(np.abs(x).max() / 448.0)))
+    q, ws = vrs.pack_conv_weight_fp8(wt)
+    from oracle.yolo26 import fp8_conv_inputs
+    xq, wq = fp8_conv_inputs(x, wt, in_scale)
+    if x8:
+        xt, _ = _e4m3_nhwc(x, in_scale, cin + off, off)
+    else:
+        xt = to_nhwc(x, vrs.BF16, cin + off, off)
+    ref = oracle.affine_act(oracle.conv2d(xq, wq, 1, 0), bn_s, shift, act)
+    out_step = float(2.0 ** np.ceil(np.log2(np.abs(ref).max() / 448.0)))
+    outs = {}
+    for tile in (vrs.TILE_128x128, vrs.TILE_W1_128):
+        if y8:
+            yt = torch.full((n, h, w, cout + off), 0x55, dtype=torch.uint8, device="cuda")
+        else:
+            yt = torch.full((n, h, w, cout + off), 7.0, dtype=torch.bfloat16, device="cuda")
+        ctx().conv2d(vrs.nhwc(xt, cin, off), dev(q), dev((bn_s * ws * in_scale).astype(np.float32)), dev(shift),
+                     vrs.nhwc(yt, cout, off), 1, 1, 1, act, None, vrs.FP8, tile=tile, in_scale=in_scale, x_e4m3=x8,
+                     y_e4m3=y8, out_step=out_step if y8 else 0.0)
+        torch.cuda.synchronize()
+        outs[tile] = yt
+    a, b = outs[vrs.TILE_128x128], outs[vrs.TILE_W1_128]
+    if y8:
+        assert torch.equal(a, b), int((a != b).sum())
+        got = _from_e4m3_nhwc(b, out_step, cout, off)
+        lo, hi = e4m3_bracket(ref, out_step)
+        assert not ((got < lo) | (got > hi)).any()
+    else:
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), int((a != b).sum())
+        assert rel_err(from_nhwc(b, cout, off), ref, FLOOR[vrs.BF16]) < TOL[vrs.BF16]
+
+
+def test_conv2d_fp8_weight_stationary_rejections():
+    """Shapes the fp8 weight-stationary kernel is not built for fail to prepare
+    with VRS_EUNSUPPORTED (the autotuner then skips it)."""
+    import torch
+    sc = torch.ones(128, device="cuda")
+    for cin, k, with_res in ((64, 1, False), (320, 1, False), (128, 3, False), (128, 1, True)):
+        x = torch.zeros((1, 8, 8, cin), dtype=torch.bfloat16, device="cuda")
+        y = torch.zeros((1, 8, 8, 128), dtype=torch.bfloat16, device="cuda")
+        w = torch.zeros(128 * cin * k * k, dtype=torch.uint8, device="cuda")
+        with pytest.raises(vrs.VrsError) as e:
+            ctx().conv2d(vrs.nhwc(x), w, sc, sc, vrs.nhwc(y), k, 1, 1, vrs.ACT_NONE,
+                         vrs.nhwc(y) if with_res else None, vrs.FP8, tile=vrs.TILE_W1_128, in_scale=1.0)
+        assert e.value.code == -3, (cin, k, with_res)
+
+
+# (n, cin, h, w, cout, k, stride)
+FP8_K128_CASES = [(1, 256, 20, 20, 256, 3, 2), (2, 128, 10, 12, 512, 3, 1), (1, 384, 9, 11, 256, 1, 1)]
+
+
+@pytest.mark.parametrize("case", FP8_K128_CASES)
+def test_conv2d_fp8_k128(case):
+    """128-deep K steps on the fp8 256x256 tile (VRS_TILE_K128, e4m3 input):
+    within the bar of the oracle conv of the same dequantised operands, and on
+    a 1x1 conv (where the 64- and 128-deep orders visit the channels alike)
+    bit-identical to the 64-deep tile; a bf16 input is refused."""
+    import torch
+    n, cin, h, w, cout, k, s = case
+    rng = np.random.default_rng(13 + cin + cout)
+    x = bf16_round(rng.standard_normal((n, cin, h, w)).astype(np.float32) * 2.0)
+    wt = (rng.standard_normal((cout, cin, k, k)) * np.sqrt(2.0 / (cin * k * k))).astype(np.float32)
+    bn_s = rng.uniform(0.5, 1.5, cout).astype(np.float32)
+    shift = rng.normal(0, 0.2, cout).astype(np.float32)
+    in_scale = float(2.0 ** np.ceil(np.log2(np.abs(x).max() / 448.0)))
+    q, ws = vrs.pack_conv_weight_fp8(wt)
+    from oracle.yolo26 import fp8_conv_inputs
+    xq, wq = fp8_conv_inputs(x, wt, in_scale)
+    xt, _ = _e4m3_nhwc(x, in_scale)
+    ho, wo = (h + 2 * (k // 2) - k) // s + 1, (w + 2 * (k // 2) - k) // s + 1
+    ref = oracle.affine_act(oracle.conv2d(xq, wq, s, k // 2), bn_s, shift, 1)
+    outs = {}
+    for tile in (vrs.TILE_256x256, vrs.TILE_256x256 | vrs.TILE_K128):
+        yt = torch.full((n, ho, wo, cout), 7.0, dtype=torch.bfloat16, device="cuda")
+        ctx().conv2d(vrs.nhwc(xt), dev(q), dev((bn_s * ws * in_scale).astype(np.float32)), dev(shift), vrs.nhwc(yt),
+                     k, s, 1, vrs.ACT_SILU, None, vrs.FP8, tile=tile, in_scale=in_scale, x_e4m3=True)
+        torch.cuda.synchronize()
+        outs[tile] = yt
+        assert rel_err(from_nhwc(yt), ref, FLOOR[vrs.BF16]) < TOL[vrs.BF16], hex(tile)
+    if k == 1:
+        a, b = outs.values()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    xb = to_nhwc(x, vrs.BF16)
+    with pytest.raises(vrs.VrsError) as e:
+        ctx().conv2d(vrs.nhwc(xb), dev(q), dev(bn_s), dev(shift), vrs.nhwc(outs[vrs.TILE_256x256]), k, s, 1,
+                     vrs.ACT_SILU, None, vrs.FP8, tile=vrs.TILE_256x256 | vrs.TILE_K128, in_scale=in_scale)
+    assert e.value.code == -3
+
+
 def test_conv2d_fp8_e4m3_rejections():
     import torch
     x = torch.zeros((1, 4, 4, 72), dtype=torch.uint8, device="cuda")

@@ -1292,6 +1292,14 @@ int vrs_model_finalize(vrs_model* m) {
   if (!rc && m->plan.empty()) plan_e4m3(m);
   if (!rc) rc = m->plan.empty() ? (m->autotune ? autotune_tiles(m) : VRS_OK) : apply_plan(m);
   if (!rc) plan_e4m3(m);
+  // The storage is final only now: the tiles were timed on the storage of an
+  // all-fp8 model, and a buffer whose reader or writer then chose bfloat16
+  // stays bfloat16, so an fp8 conv reading it drops what needs an e4m3 input
+  // (128-deep steps; the 64-deep tile takes either input).
+  if (!rc && m->plan.empty())
+    for (ConvStep& c : m->convs)
+      if (c.f8 && c.run_f8 && (c.tile8 & VRS_TILE_K128) && !(c.x.buf >= 0 && m->bufs[c.x.buf].f8))
+        c.tile8 &= ~VRS_TILE_K128;
   if (rc) {
     const std::string err = vrs_last_error();
     for (size_t i = first_alloc; i < m->allocs.size(); ++i) (void)hipFree(m->allocs[i]);

@@ -129,11 +129,17 @@ static int tile_kernel(int code, int cin, int dtype, bool up, char* name, size_t
     if (!built || (code & VRS_TILE_PERSIST) || cin % 32 != 0)
       return fail(VRS_EUNSUPPORTED, "conv: no fused-upsample kernel for tile %s (dtype %d, Cin %d)", t->tag, dtype, cin);
   }
+  const bool k128 = (code & VRS_TILE_K128) != 0;
+  if (k128 && dtype != VRS_FP8) return fail(VRS_EUNSUPPORTED, "conv: 128-deep steps are built for fp8 only");
   if (dtype == VRS_FP8) {
     if (cin % 64 != 0) return fail(VRS_EUNSUPPORTED, "conv fp8: needs Cin %% 64 == 0 (Cin=%d)", cin);
     if (t->code == VRS_TILE_32x256 || t->code == VRS_TILE_64x64 || (code & VRS_TILE_PERSIST))
       return fail(VRS_EUNSUPPORTED, "conv fp8: tile %s%s not built", t->tag, (code & VRS_TILE_PERSIST) ? " persistent" : "");
-    snprintf(name, n, "vrs_conv_fp8_%s_k64_%c%s%s", t->tag, up ? 'u' : 'a', x8 ? "_x8" : "", y8 ? "_y8" : "");
+    if (k128 && (cin % 128 != 0 || up || t->code != VRS_TILE_256x256 || !x8))
+      return fail(VRS_EUNSUPPORTED, "conv fp8: 128-deep steps need tile 256x256, an e4m3 input, Cin %% 128 == 0 "
+                  "and no fused upsample (tile %s, Cin %d)", t->tag, cin);
+    snprintf(name, n, "vrs_conv_fp8_%s_k%d_%c%s%s", t->tag, k128 ? 128 : 64, up ? 'u' : 'a', x8 ? "_x8" : "",
+             y8 ? "_y8" : "");
     *bm = t->bm;
     *bn = t->bn;
     *threads = t->threads;
@@ -195,6 +201,11 @@ static int h3_strip_width(int w) {
   return 32;
 }
 
+// Input widths the fp8 weight-stationary 1x1 kernel is built for.
+static bool w1_fp8_cin(int cin) {
+  return cin == 128 || cin == 192 || cin == 256 || cin == 384 || cin == 512 || cin == 768;
+}
+
 std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int stride, int w, int64_t m,
                                       int num_cu) {
   std::vector<int> c;
@@ -210,6 +221,9 @@ std::vector<int> conv_tile_candidates(int cout, int cin, int dtype, int k, int s
     if (cout > 128) c.push_back(VRS_TILE_256x128);
     if (cout <= 128) c.push_back(VRS_TILE_128x256);
     if (cout >= 256) c.push_back(VRS_TILE_256x256);
+    // 128-deep steps (e4m3 inputs only: a bf16-input conv fails to prepare it)
+    if (cin % 128 == 0 && cout >= 256) c.push_back(VRS_TILE_256x256 | VRS_TILE_K128);
+    if (k == 1 && stride == 1 && w > 0 && w1_fp8_cin(cin)) c.push_back(VRS_TILE_W1_128);
     return c;
   }
   const bool g = cin % 32 != 0;
@@ -339,6 +353,29 @@ static int prep_dense(vrs_ctx* ctx, const ConvSpec& cs, const vrs_nhwc& x, const
     out.back().flops = 2.0 * (double)M * cout * 9.0 * (cs.cin_real > 0 ? cs.cin_real : x.c);
     out.back().bytes = (double)x.n * x.h * x.w * x.c * 2.0 + (double)cout * 9.0 * x.c * 2.0 + (double)M * cout * 2.0 +
                        (a.res ? (double)M * cout * 2.0 : 0.0) + 8.0 * cout;
+    return VRS_OK;
+  }
+  if (f8 && ((cs.tile & 0xff) == VRS_TILE_W1_256 || (cs.tile & 0xff) == VRS_TILE_W1_128)) {
+    // fp8 weight-stationary 1x1 kernel (conv1w8.hip): a 128-channel slice of
+    // e4m3 weights in LDS, 128-pixel tiles
+    if ((cs.tile & 0xff) != VRS_TILE_W1_128 || (cs.tile & ~0xff) || !w1_fp8_cin(x.c) || cs.k != 1 ||
+        cs.stride != 1 || cs.up)
+      return fail(VRS_EUNSUPPORTED, "conv fp8: the weight-stationary tile is the 128-channel one, for k=1, stride 1, "
+                  "no fused upsample and Cin 128, 192, 256, 384, 512 or 768 (k=%d s=%d Cin=%d)", cs.k, cs.stride, x.c);
+    if (a.res || a.stage != 1 || a.y_f32)
+      return fail(VRS_EUNSUPPORTED, "conv fp8: the weight-stationary tile takes no residual and stores aligned "
+                  "chunks of an NHWC view under 2 GiB");
+    a.tiles_m = (cout + 127) / 128;
+    a.tiles_n = (int32_t)((M + 127) / 128);
+    snprintf(name, sizeof name, "vrs_conv1w_fp8_128_c%d%s%s", x.c, cs.x_f8 ? "_x8" : "", cs.y_f8 ? "_y8" : "");
+    hipFunction_t f;
+    if ((rc = get_fn(ctx, name, &f))) return rc;
+    const int64_t resident = (int64_t)resident_wgs(f, 512) * (ctx->num_cu > 0 ? ctx->num_cu : 256);
+    const int64_t streams = std::max<int64_t>(1, std::min<int64_t>(resident / a.tiles_m, a.tiles_n));
+    out.push_back(make_launch(name, f, dim3((unsigned)(streams * a.tiles_m)), dim3(512), 0, a));
+    out.back().flops = 2.0 * (double)M * cout * (cs.cin_real > 0 ? cs.cin_real : x.c);
+    out.back().bytes = (double)M * x.c * (double)xs + (double)cout * x.c + (double)M * cout * (cs.y_f8 ? 1.0 : 2.0) +
+                       8.0 * cout;
     return VRS_OK;
   }
   if ((cs.tile & 0xff) == VRS_TILE_W1_256 || (cs.tile & 0xff) == VRS_TILE_W1_128) {

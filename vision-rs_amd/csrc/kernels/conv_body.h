@@ -65,7 +65,7 @@ template <typename T, int BM, int BN, int BK, int WGM, int WGN, bool ALIGNED, bo
 __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   using E = Elt<T>;
   using G = typename E::group;
-  static_assert(!F8 || (sizeof(T) == 2 && BK == 64 && ALIGNED), "fp8: bf16 activations, 64-deep steps");
+  static_assert(!F8 || (sizeof(T) == 2 && (BK == 64 || BK == 128) && ALIGNED), "fp8: 64- or 128-deep steps");
   static_assert(F8 || (!XF8 && !YF8), "e4m3 activations only on the fp8 tiles");
   // LDS rows of BK + 8 elements: the 32 rows a half-wave reads with
   // ds_read_b128 (row stride 144 B for BK=64 bf16) start on distinct 4-bank
@@ -86,7 +86,8 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
   constexpr int CEB = XF8 ? 16 : 8;          // activation elements per chunk
   constexpr int XS = XF8 ? 1 : (int)sizeof(T);   // bytes per activation element
   constexpr int AEL = F8 ? 16 : 8;           // weight elements per chunk
-  constexpr int LDKB = BK + 16;              // F8: LDS row stride in bytes (80: conflict-free)
+  constexpr int LDKB = BK + 16;              // F8: LDS row stride in bytes (80 or 144: the 16 rows a
+                                             // quarter-wave reads start on distinct 4-bank groups)
   constexpr int NT = 64 * WGM * WGN;         // threads per workgroup
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int TM = WTM / 32, TN = WTN / 32;   // 32x32 MFMA tiles per wave
@@ -380,21 +381,26 @@ __device__ __forceinline__ void conv_body(const vrs_conv_args& a) {
         const unsigned char* sA = reinterpret_cast<const unsigned char*>(sbuf(cur));
         const unsigned char* sB = sA + BM * LDKB;
         const int fk = (lane >> 5) * 32;
-        i32x8_t fa[TM], fb[TN];
         auto ld32 = [&](const unsigned char* p) {
           const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(p);
           const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(p + 16);
           return (i32x8_t){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
         };
+        // one 64-deep k slice per fp8 MFMA: fragment bytes [kk*64, kk*64+64)
+        // of each staged row
 #pragma unroll
-        for (int i = 0; i < TM; ++i) fa[i] = ld32(sA + (wm * WTM + i * 32 + frag_row) * LDKB + fk);
+        for (int kk = 0; kk < BK / 64; ++kk) {
+          i32x8_t fa[TM], fb[TN];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) fb[j] = ld32(sB + (wn * WTN + j * 32 + frag_row) * LDKB + fk);
+          for (int i = 0; i < TM; ++i) fa[i] = ld32(sA + (wm * WTM + i * 32 + frag_row) * LDKB + kk * 64 + fk);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+          for (int j = 0; j < TN; ++j) fb[j] = ld32(sB + (wn * WTN + j * 32 + frag_row) * LDKB + kk * 64 + fk);
 #pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32_fp8_k64(fa[i], fb[j], acc[i][j]);
-        pipe_schedule<TM * TN, 2 * (TM + TN), TM * TN, A_IT + B_IT>();
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma32_fp8_k64(fa[i], fb[j], acc[i][j]);
+        }
+        pipe_schedule<BK / 64 * TM * TN, 2 * (TM + TN), TM * TN, A_IT + B_IT>();
         __syncthreads();
         return;
       }

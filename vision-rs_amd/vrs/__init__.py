@@ -32,6 +32,7 @@ CONV_BN_SILU, CONV_BN, CONV_PLAIN = 0, 1, 2
 TILE_AUTO, TILE_128x128, TILE_256x128, TILE_128x256, TILE_64x256, TILE_32x256, TILE_256x256, TILE_K32 = (
     0, 1, 2, 3, 4, 5, 6, 0x100)
 TILE_PERSIST = 0x200
+TILE_K128 = 0x400   # fp8: 128-deep K steps (256x256 with e4m3 input, Cin % 128 == 0)
 TILE_H3 = 7   # halo-tiled 3x3 stride-1 kernel (bf16)
 TILE_W1_256 = 8   # weight-stationary 1x1 kernels (bf16): 256- or 128-channel weight slice in LDS
 TILE_W1_128 = 9
