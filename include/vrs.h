@@ -115,6 +115,12 @@ typedef struct {
  * BN + SiLU, bf16; it must be the stem output's only reader) runs fused with
  * the stem as one vrs_conv_stem_pair launch. */
 #define VRS_TILE_STEM_PAIR 11
+/* Model plans only: the second conv of a bottleneck (3x3 -> 3x3, bf16 model,
+ * the shapes vrs_conv_bottleneck_pair is built for; the first conv's output
+ * read by it alone) runs fused with the conv before it as one
+ * vrs_conv_bottleneck_pair launch; the first conv then has no launch and no
+ * output of its own. */
+#define VRS_TILE_BPAIR 12
 #define VRS_TILE_K32 0x100
 /* OR VRS_TILE_PERSIST: persistent grid (resident workgroups loop over the
  * tiles with one continuous load stream, so a tile's epilogue overlaps the
@@ -215,6 +221,23 @@ int vrs_conv_stem_pair(vrs_ctx* ctx, const vrs_conv_desc* d0, const vrs_conv_des
                        int32_t n, int32_t c, int32_t h, int32_t w, const void* w0_packed, const float* scale0,
                        const float* shift0, const void* w1_packed, const float* scale1, const float* shift1,
                        const vrs_nhwc* y, void* stream);
+
+/* A bottleneck's two convs in one kernel: bottleneck(c, c, shortcut, e)
+ * (blocks/bottleneck.rs:37-63) records conv(c, c_h, 3, 1) then conv(c_h, c,
+ * 3, 1) (blocks/conv.rs:31-46) and, with the shortcut, adds the block input:
+ *   y = bf16(silu(scale2 * conv3x3(m, w2) + shift2) + res),
+ *   m = bf16(silu(scale1 * conv3x3(x, w1) + shift1))
+ * with the same results as two vrs_conv2d calls on the halo 3x3 tile
+ * (VRS_TILE_H3); the middle map m never goes to memory.  bf16, SiLU on both,
+ * 3x3 stride 1, built for c = 64, c_hidden = 32 (YOLO26m's P2 C3k2 block);
+ * w1 [c_hidden][3][3][c] and w2 [c][3][3][c_hidden] from
+ * vrs_pack_conv_weight; res optional (NULL: no shortcut), shaped as y; x, y,
+ * res: 8-channel aligned views under 2 GiB.  Other shapes:
+ * VRS_EUNSUPPORTED. */
+int vrs_conv_bottleneck_pair(vrs_ctx* ctx, const vrs_conv_desc* d1, const vrs_conv_desc* d2, const vrs_nhwc* x,
+                             const void* w1_packed, const float* scale1, const float* shift1, int32_t c_hidden,
+                             const void* w2_packed, const float* scale2, const float* shift2, const vrs_nhwc* res,
+                             const vrs_nhwc* y, void* stream);
 
 /* NCHW float32 -> NHWC dtype, zero-padding channels C..y->c-1 (C <= y->c < C+8). */
 int vrs_pack_input(vrs_ctx* ctx, const float* x_nchw, int32_t n, int32_t c, int32_t h, int32_t w,
@@ -461,7 +484,10 @@ int vrs_model_conv_info(const vrs_model* m, int32_t i, const char** prefix, int3
  * (b, p, co) at output[out_idx] + out_off + b*out_sb + p*out_sp + co*out_sc).
  * A stem pair (VRS_TILE_STEM_PAIR): the stem has no launch (-1) and no y; the
  * conv after it has stem = 2 and no x (its input is the stem of the model
- * input, computed on chip). */
+ * input, computed on chip).  A bottleneck pair (VRS_TILE_BPAIR): the first
+ * conv has no launch and no y; the second has fused_in = 1 and no x (its
+ * input is the first conv's output, computed on chip from the first conv's
+ * x). */
 typedef struct {
   int32_t launch;          /* index among vrs_model_launch_name's launches of the conv's
                               last launch (its output is complete after it; a
@@ -483,6 +509,7 @@ typedef struct {
    * channel, value = e4m3 * step; the others hold dtype elements) */
   int32_t x_e4m3, y_e4m3, res_e4m3, up_e4m3;
   float x_step, y_step, res_step, up_step;
+  int32_t fused_in;        /* 1: the input is the conv before it, computed inside this launch */
 } vrs_conv_io;
 int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io);
 int vrs_model_destroy(vrs_model* m);

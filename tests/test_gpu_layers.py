@@ -2,7 +2,9 @@
 BASELINE config 5's full size (batch 64, 640x640), bf16 and fp8.
 
 The forward runs the committed tile plans (the bench line's kernels) and is
-replayed one kernel launch at a time.  Before each conv's
+replayed one kernel launch at a time (a fused pair -- the stem pair, a
+bottleneck pair -- is one launch: its second conv is checked on the first
+conv's output recomputed by the oracle).  Before each conv's
 launch its actual device input (and residual, and the half-size source of a
 fused upsample) is read back for images 0 and 31; after it, its output.  The
 oracle then recomputes that one conv from the device's own input, so every
@@ -233,6 +235,10 @@ def test_yolo26m_bs64_640_layer_by_layer(dtype):
         if io is not None:
             if io.stem == 2:   # stem pair: the input is the stem of the image, computed on chip
                 xin = bf16_round(conv_reference(ios[io.index - 1], P, 1e-3, x[list(IMAGES)], None))
+            elif io.fused_in:   # bottleneck pair: the input is the conv before it, computed on chip
+                prev = ios[io.index - 1]
+                xprev = read_view(prev.x, prev.dtype, IMAGES, prev.x_e4m3, prev.x_step)
+                xin = bf16_round(conv_reference(prev, P, 1e-3, xprev, None))
             elif io.stem:
                 xin = x[list(IMAGES)]
             else:

@@ -215,6 +215,80 @@ def test_conv2d_halo3(case):
         assert torch.all(rest == 7.0)
 
 
+# (n, h, w, residual, input/output channel layout: (buffer pitch, x offset, y offset) or None)
+BPAIR_CASES = [
+    (2, 16, 32, True, None),
+    (1, 20, 40, True, (192, 64, 128)),   # partial strip and run; C2f-style views of one buffer
+    (2, 9, 13, False, None),             # smaller than one run
+    (1, 48, 96, True, (128, 0, 64)),
+]
+
+
+@pytest.mark.parametrize("case", BPAIR_CASES)
+def test_conv_bottleneck_pair(case):
+    """vrs_conv_bottleneck_pair (3x3 64 -> 32 -> 3x3 32 -> 64, SiLU, optional
+    residual) equals, bit for bit, the two halo-kernel launches it replaces
+    (the middle map written to memory in between), and is within the bf16 bar
+    of the oracle bottleneck (the middle map rounded to bf16 where the GPU
+    rounds it); bytes outside the output view untouched."""
+    import torch
+    n, h, w, with_res, lay = case
+    C, CH = 64, 32
+    rng = np.random.default_rng(h * 31 + w)
+    x = bf16_round(rng.standard_normal((n, C, h, w)).astype(np.float32))
+    w1 = bf16_round((rng.standard_normal((CH, C, 3, 3)) * np.sqrt(2.0 / (C * 9))).astype(np.float32))
+    w2 = bf16_round((rng.standard_normal((C, CH, 3, 3)) * np.sqrt(2.0 / (CH * 9))).astype(np.float32))
+    s1, b1 = rng.uniform(0.5, 1.5, CH).astype(np.float32), rng.normal(0, 0.2, CH).astype(np.float32)
+    s2, b2 = rng.uniform(0.5, 1.5, C).astype(np.float32), rng.normal(0, 0.2, C).astype(np.float32)
+    mid = bf16_round(oracle.affine_act(oracle.conv2d(x, w1, 1, 1), s1, s1 * 0 + b1, 1))
+    ref = oracle.affine_act(oracle.conv2d(mid, w2, 1, 1), s2, b2, 1) + (x if with_res else 0)
+    pitch, xo, yo = lay or (C, 0, 0)
+    if lay:   # input, residual and output as channel slices of one buffer (as in C2f)
+        buf = torch.full((n, h, w, pitch), 7.0, dtype=torch.bfloat16, device="cuda")
+        buf[..., xo:xo + C] = to_nhwc(x, vrs.BF16)
+        xv, yv = vrs.nhwc(buf, C, xo), vrs.nhwc(buf, C, yo)
+        outs = [buf]
+    else:
+        xt = to_nhwc(x, vrs.BF16)
+        yt = torch.full((n, h, w, C), 7.0, dtype=torch.bfloat16, device="cuda")
+        xv, yv = vrs.nhwc(xt), vrs.nhwc(yt)
+        outs = [yt]
+    wd1, wd2 = dev(vrs.pack_conv_weight(w1, 1, C, vrs.BF16)), dev(vrs.pack_conv_weight(w2, 1, CH, vrs.BF16))
+    ctx().conv_bottleneck_pair(xv, wd1, dev(s1), dev(b1), CH, wd2, dev(s2), dev(b2), yv,
+                               res=xv if with_res else None)
+    torch.cuda.synchronize()
+    fused = outs[0].clone()
+    # the same two convs on the halo kernel, the middle map in memory
+    mt = torch.zeros((n, h, w, CH), dtype=torch.bfloat16, device="cuda")
+    ctx().conv2d(xv, wd1, dev(s1), dev(b1), vrs.nhwc(mt), 3, 1, 1, vrs.ACT_SILU, None, vrs.BF16, tile=vrs.TILE_H3)
+    if lay:
+        buf[..., yo:yo + C] = 7.0
+    else:
+        yt.fill_(7.0)
+    ctx().conv2d(vrs.nhwc(mt), wd2, dev(s2), dev(b2), yv, 3, 1, 1, vrs.ACT_SILU, xv if with_res else None, vrs.BF16,
+                 tile=vrs.TILE_H3)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), outs[0].view(torch.int16)), int((fused != outs[0]).sum())
+    got = from_nhwc(fused, C, yo)
+    assert rel_err(got, ref, FLOOR[vrs.BF16]) < TOL[vrs.BF16]
+    if lay:   # channels outside the output slice (including the input slice) untouched
+        keep = [c for c in range(pitch) if not yo <= c < yo + C]
+        assert torch.equal(fused[..., keep], outs[0][..., keep])
+
+
+def test_conv_bottleneck_pair_rejections():
+    """Shapes and types the fused pair is not built for: VRS_EUNSUPPORTED."""
+    import torch
+    for C, CH, dtype in ((64, 64, vrs.BF16), (128, 64, vrs.BF16), (64, 32, vrs.F32)):
+        x = torch.zeros((1, 8, 8, C), dtype=tdtype(dtype), device="cuda")
+        y = torch.zeros((1, 8, 8, C), dtype=tdtype(dtype), device="cuda")
+        w1 = torch.zeros(CH * 9 * C, dtype=tdtype(dtype), device="cuda")
+        s = torch.ones(C, device="cuda")
+        with pytest.raises(vrs.VrsError) as e:
+            ctx().conv_bottleneck_pair(vrs.nhwc(x), w1, s, s, CH, w1, s, s, vrs.nhwc(y), dtype=dtype)
+        assert e.value.code == -3, (C, CH, dtype)
+
+
 def test_conv2d_halo3_rejections():
     import torch
     s = torch.ones(64, device="cuda")

@@ -224,6 +224,57 @@ def test_stem_pair_plan():
         mn.load(_params(mn))
 
 
+def test_bottleneck_pair_plan():
+    """VRS_TILE_BPAIR on model.2.m.0.cv2 (YOLO26m's 64 -> 32 -> 64 bottleneck
+    at stride 4): one launch replaces model.2.m.0.cv1 + cv2, bit-identical to
+    both convs on the halo kernel (the same K order and rounding); conv_io
+    reports cv1 as launch-less and without output, cv2 as fused_in without
+    input.  The entry is refused on a conv that is not a bottleneck's second
+    3x3 and on a bottleneck of other widths (YOLO26n's 16 -> 8 -> 16)."""
+    import torch
+    B, S = 2, 192
+    names = [pre for pre, _, _ in _yolo(B, S, vrs.BF16, autotune=False).conv_info()]
+    i1, i2 = names.index("model.2.m.0.cv1"), names.index("model.2.m.0.cv2")
+    x = dev(np.random.default_rng(5).uniform(0, 1, (B, 3, S, S)).astype(np.float32))
+    outs = {}
+    for tile in (vrs.TILE_BPAIR, vrs.TILE_H3):
+        plan = [0] * len(names)
+        plan[i1] = vrs.TILE_H3
+        plan[i2] = tile
+        m = _yolo(B, S, vrs.BF16, autotune=False)
+        m.set_plan(plan)
+        m.load(_params(m))
+        outs[tile] = [o.clone() for o in m.forward(x)]
+        torch.cuda.synchronize()
+        launches = m.launch_names()
+        io1, io2 = m.conv_io(i1), m.conv_io(i2)
+        if tile == vrs.TILE_BPAIR:
+            assert m.get_plan()[i2] == vrs.TILE_BPAIR
+            assert io1.launch == -1 and io1.y.data is None and io1.x.data is not None
+            assert io2.fused_in == 1 and io2.x.data is None and io2.y.data is not None
+            assert launches[io2.launch] == "model.2.m.0.cv2:vrs_bpair_bf16_c64_h32_w32"
+            assert not any(l.startswith("model.2.m.0.cv1:") for l in launches)
+        else:
+            assert io1.launch >= 0 and io2.fused_in == 0
+    for a, b in zip(outs[vrs.TILE_BPAIR], outs[vrs.TILE_H3]):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    for nm in ("model.2.m.0.cv1", "model.3", "model.6.m.0.m.0.cv2"):
+        m = _yolo(1, 128, vrs.BF16, autotune=False)
+        bad = [0] * len(names)
+        bad[names.index(nm)] = vrs.TILE_BPAIR
+        m.set_plan(bad)
+        with pytest.raises(vrs.VrsError):
+            m.load(_params(m))
+    dn = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="n", one2one=True)
+    mn = vrs.Model(ctx(), dn, 1, 128, 128, vrs.BF16, 1e-3, autotune=False)
+    names_n = [pre for pre, _, _ in mn.conv_info()]
+    bad = [0] * len(names_n)
+    bad[names_n.index("model.2.m.0.cv2")] = vrs.TILE_BPAIR
+    mn.set_plan(bad)
+    with pytest.raises(vrs.VrsError):
+        mn.load(_params(mn))
+
+
 def test_head_outputs_on_the_weight_stationary_tile():
     """The Detect head's channel-major float32 output convs (box 64 -> 4,
     class 256 -> 80, plain convs with bias) on the weight-stationary 1x1 tile

@@ -606,6 +606,54 @@ bool pair_fused(const vrs_model* m, size_t i) {
          !(m->convs[i].f8 && m->convs[i].run_f8);
 }
 
+// Conv i as the second conv of a bottleneck pair (vrs_conv_bottleneck_pair):
+// conv i-1 and conv i are 3x3 stride-1 BN + SiLU convs of a bf16 model in the
+// shapes the fused kernel is built for, conv i reads exactly conv i-1's
+// output, which nothing else reads or writes, and conv i's output overlaps
+// neither conv i-1's input nor its own residual (the fused kernel reads those
+// while other workgroups write the output).
+bool bpair_eligible(const vrs_model* m, size_t i) {
+  if (i == 0 || i >= m->convs.size() || m->dtype != VRS_BF16) return false;
+  const ConvStep& a = m->convs[i - 1];
+  const ConvStep& c = m->convs[i];
+  auto plain3 = [](const ConvStep& s) {
+    return !s.stem && !s.dw && s.groups <= 1 && s.k == 3 && s.s == 1 && s.kind == CK_BN_SILU && !s.has_up &&
+           s.out_idx < 0 && s.x.buf >= 0 && s.y.buf >= 0 && s.cin_real == s.cin;
+  };
+  if (!plain3(a) || !plain3(c) || a.has_res) return false;
+  if (c.x.buf != a.y.buf || c.x.c_off != a.y.c_off || c.x.c != a.y.c) return false;
+  if (bpair_check(VRS_BF16, VRS_ACT_SILU, VRS_ACT_SILU, a.cin, a.cout, c.cout) != VRS_OK) {
+    (void)vrs_last_error();
+    return false;
+  }
+  auto overlap = [](V p, V q) { return p.buf == q.buf && p.c_off < q.c_off + q.c && q.c_off < p.c_off + p.c; };
+  if (overlap(c.y, a.x) || (c.has_res && overlap(c.y, c.res))) return false;
+  const int bb = a.y.buf;
+  for (size_t k = 0; k < m->convs.size(); ++k) {
+    const ConvStep& o = m->convs[k];
+    if (k != i && (o.x.buf == bb || (o.has_res && o.res.buf == bb) || (o.has_up && o.up.buf == bb))) return false;
+    if (k != i - 1 && o.y.buf == bb) return false;
+  }
+  for (const Step& st : m->steps)
+    if (st.type != Step::CONV && (st.a.buf == bb || st.b.buf == bb)) return false;
+  return true;
+}
+
+// conv i runs as the second conv of a bottleneck pair in this forward
+bool bpair_fused(const vrs_model* m, size_t i) {
+  return !m->calib_mode && i < m->convs.size() && m->convs[i].tile == VRS_TILE_BPAIR;
+}
+
+// the launch of a bottleneck pair ending at conv i
+int prep_bpair_step(const vrs_model* m, size_t i, std::vector<Launch>& ls) {
+  const ConvStep& a = m->convs[i - 1];
+  const ConvStep& c = m->convs[i];
+  vrs_nhwc r;
+  if (c.has_res) r = view_of(m, c.res);
+  return prep_bpair(m->ctx, view_of(m, a.x), a.w, a.scale, a.shift, a.cout, c.w, c.scale, c.shift,
+                    c.has_res ? &r : nullptr, view_of(m, c.y), ls);
+}
+
 // fp8 conv c: e4m3 input / output / residual flags and steps from the
 // buffers' storage plan (steps of 1 before calibration: timing only).
 void e4m3_flags(const vrs_model* m, const ConvStep& c, ConvSpec& cs) {
@@ -719,6 +767,12 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
           sio.wr = {acc(c.y)};
           break;
         }
+        if (bpair_fused(m, st.conv)) {   // reads the first conv's input through it
+          sio.rd = {acc(m->convs[st.conv - 1].x)};
+          if (c.has_res) sio.rd.push_back(acc(c.res));
+          sio.wr = {acc(c.y)};
+          break;
+        }
         sio.rd = {acc(c.x)};
         if (c.has_res) sio.rd.push_back(acc(c.res));
         if (c.has_up) sio.rd.push_back(acc(c.up));
@@ -745,6 +799,13 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
           conv_launch[st.conv] = (int)ls.size();
           rc = prep_stem_pair(m->ctx, x, m->batch, m->in_h, m->in_w, s0.w, s0.scale, s0.shift, c.w, c.scale,
                               c.shift, view_of(m, c.y), ls);
+          label = c.pre;
+          break;
+        }
+        if (bpair_fused(m, st.conv + 1)) continue;   // computed inside the next conv's launch
+        if (bpair_fused(m, st.conv)) {
+          conv_launch[st.conv] = (int)ls.size();
+          rc = prep_bpair_step(m, st.conv, ls);
           label = c.pre;
           break;
         }
@@ -916,6 +977,7 @@ int autotune_tiles(vrs_model* m) {
     return VRS_OK;
   };
   float* img = nullptr;   // a zero image for timing the stem pair (values do not matter)
+  std::vector<float> best_bf16(m->convs.size(), 1e30f);   // each conv's fastest bf16 tile
   // scratch float32 outputs for timing the Detect output convs
   std::vector<float*> outs(m->out_dims.size(), nullptr);
   for (size_t ci = 0; ci < m->convs.size() && !rc; ++ci) {
@@ -990,6 +1052,21 @@ int autotune_tiles(vrs_model* m) {
          c.tile = VRS_TILE_STEM_PAIR;
          best_of[0] = tp - t0;
        }
+     }
+   }
+   // a bottleneck pair (this conv fused with the 3x3 conv before it, which
+   // is not itself the second conv of a pair) against the two on their own
+   // fastest tiles
+   best_bf16[ci] = best_of[0];
+   if (bpair_eligible(m, ci) && m->convs[ci - 1].tile != VRS_TILE_BPAIR && best_of[0] < 1e29f &&
+       best_bf16[ci - 1] < 1e29f) {
+     std::vector<Launch> lp;
+     if (prep_bpair_step(m, ci, lp) == VRS_OK) {
+       float tp;
+       if ((rc = timed(lp, tp))) break;
+       if (tp < 0.98f * (best_of[0] + best_bf16[ci - 1])) c.tile = VRS_TILE_BPAIR;
+     } else {
+       (void)vrs_last_error();
      }
    }
    // fp8 models: a layer whose bf16 tile is faster by 2% stays on bf16
@@ -1149,6 +1226,13 @@ int apply_plan(vrs_model* m) {
                   "plan entry %zu (%s): the stem pair applies only to a bf16 3x3/s2 64->128 conv reading a "
                   "64-channel stem's output alone (image width a multiple of 4)",
                   i, c.pre.c_str());
+    if (tile == VRS_TILE_BPAIR &&
+        (f8 || !bpair_eligible(m, i) || (m->plan[i - 1] & ~VRS_PLAN_FP8) == VRS_TILE_BPAIR))
+      return fail(VRS_EINVAL,
+                  "plan entry %zu (%s): the bottleneck pair applies only to the second 3x3 conv of a bf16 "
+                  "bottleneck in the shapes vrs_conv_bottleneck_pair is built for, reading the first conv's output "
+                  "alone, whose first conv is not itself fused as a second conv",
+                  i, c.pre.c_str());
     if (c.f8) {
       c.run_f8 = f8;
       if (f8) c.tile8 = tile;
@@ -1164,6 +1248,12 @@ int apply_plan(vrs_model* m) {
     const bool f8 = (e & VRS_PLAN_FP8) != 0;
     const int tile = e & ~VRS_PLAN_FP8;
     if (!tunable(c) || tile == VRS_TILE_STEM_PAIR || tile == VRS_TILE_AUTO) continue;
+    if (tile == VRS_TILE_BPAIR) {   // validate by preparing the fused launch (nothing is launched)
+      std::vector<Launch> ls;
+      if (const int rc = prep_bpair_step(m, i, ls)) return fail(rc, "plan entry %zu (%s): %s", i, c.pre.c_str(),
+                                                                 vrs_last_error());
+      continue;
+    }
     ConvSpec cs;   // validate by preparing the launch
     cs.k = c.k; cs.stride = c.s; cs.dtype = f8 ? VRS_FP8 : act_dt(m);
     cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
@@ -1323,9 +1413,10 @@ int vrs_model_finalize(vrs_model* m) {
   // largest activation: 839 MB for YOLO26m at batch 64, 640x640).  Release
   // it, unless the model is fp8, whose calibration forward runs the stem on
   // its own.
+  // The middle map of a fused bottleneck pair is never written either.
   if (m->dtype != VRS_FP8)
     for (size_t i = 1; i < m->convs.size(); ++i) {
-      if (m->convs[i].tile != VRS_TILE_STEM_PAIR || !pair_eligible(m, i)) continue;
+      if (!(m->convs[i].tile == VRS_TILE_STEM_PAIR && pair_eligible(m, i)) && !bpair_fused(m, i)) continue;
       Buf& b = m->bufs[m->convs[i - 1].y.buf];
       auto it = std::find(m->allocs.begin(), m->allocs.end(), b.dev);
       if (b.dev && it != m->allocs.end()) {
@@ -1610,14 +1701,18 @@ int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io) {
   io->plain = c.kind == CK_PLAIN;
   // a stem pair: the stem has no launch and no output of its own; the conv
   // after it reads the model input (stem = 2)
-  const bool fused_out = c.stem && pair_fused(m, i + 1), fused_in = pair_fused(m, i);
+  // a bottleneck pair: the first conv has no launch and no output; the second
+  // reads the first conv's input through it (fused_in, no x)
+  const bool bp_out = bpair_fused(m, i + 1), bp_in = bpair_fused(m, i);
+  const bool fused_out = (c.stem && pair_fused(m, i + 1)) || bp_out, fused_in = pair_fused(m, i);
   io->stem = fused_in ? 2 : c.stem;
+  io->fused_in = fused_in || bp_in ? 1 : 0;
   io->fp8 = c.f8 && c.run_f8;
   io->in_scale = c.in_scale;
   io->dtype = act_dt(m);
   io->cin = c.cin_real;
   io->cout = c.cout;
-  if (!c.stem && !fused_in) io->x = view_of(m, c.x);
+  if (!c.stem && !fused_in && !bp_in) io->x = view_of(m, c.x);
   if (c.out_idx < 0 && c.y.buf >= 0 && !fused_out) io->y = view_of(m, c.y);
   if (c.has_res) io->res = view_of(m, c.res);
   if (c.has_up) io->up = view_of(m, c.up);

@@ -918,6 +918,61 @@ int prep_stem_pair(vrs_ctx* ctx, const float* x, int n, int h, int w, const void
   return VRS_OK;
 }
 
+// Bottleneck pair (bpair.hip): the channel counts it is built for.
+int bpair_check(int dtype, int act1, int act2, int cin, int ch, int cout) {
+  if (dtype != VRS_BF16) return fail(VRS_EUNSUPPORTED, "bottleneck pair: bf16 only");
+  if (act1 != VRS_ACT_SILU || act2 != VRS_ACT_SILU)
+    return fail(VRS_EUNSUPPORTED, "bottleneck pair: BN + SiLU on both convs only");
+  if (cin != 64 || ch != 32 || cout != 64)
+    return fail(VRS_EUNSUPPORTED, "bottleneck pair: built for 64 -> 32 -> 64 channels (got %d -> %d -> %d)", cin, ch,
+                cout);
+  return VRS_OK;
+}
+
+int prep_bpair(vrs_ctx* ctx, const vrs_nhwc& x, const void* w1, const float* s1, const float* b1, int ch,
+               const void* w2, const float* s2, const float* b2, const vrs_nhwc* res, const vrs_nhwc& y,
+               std::vector<Launch>& ls) {
+  int rc;
+  if ((rc = bpair_check(VRS_BF16, VRS_ACT_SILU, VRS_ACT_SILU, x.c, ch, y.c))) return rc;
+  if (!w1 || !s1 || !b1 || !w2 || !s2 || !b2) return fail(VRS_EINVAL, "bottleneck pair: null weight/scale/shift");
+  if ((rc = check_view(x, "bottleneck pair input", 8)) || (rc = check_view(y, "bottleneck pair output", 8)) ||
+      (res && (rc = check_view(*res, "bottleneck pair residual", 8))))
+    return rc;
+  if (y.n != x.n || y.h != x.h || y.w != x.w)
+    return fail(VRS_EBADSHAPE, "bottleneck pair: output %dx%dx%d for input %dx%dx%d (3x3 stride 1 keeps the size)",
+                y.n, y.h, y.w, x.n, x.h, x.w);
+  if (res && (res->n != y.n || res->h != y.h || res->w != y.w || res->c != y.c))
+    return fail(VRS_EBADSHAPE, "bottleneck pair: residual shape differs from the output");
+  auto extent = [](const vrs_nhwc& v) { return ((int64_t)v.n * v.h * v.w * v.pitch - v.c_off) * 2; };
+  const int64_t xb = extent(x), yb = extent(y), rb = res ? extent(*res) : 0;
+  if (xb >= (1ll << 31) || yb >= (1ll << 31) || rb >= (1ll << 31))
+    return fail(VRS_EBADSHAPE, "bottleneck pair: views must be under 2 GiB (32-bit buffer offsets)");
+  vrs_bpair_args a{};
+  a.x = at(x, VRS_BF16);
+  a.w1 = w1; a.s1 = s1; a.b1 = b1;
+  a.w2 = w2; a.s2 = s2; a.b2 = b2;
+  a.res = res ? at(*res, VRS_BF16) : nullptr;
+  a.y = const_cast<void*>(at(y, VRS_BF16));
+  a.N = x.n; a.H = x.h; a.W = x.w;
+  a.x_pitch = x.pitch; a.y_pitch = y.pitch; a.r_pitch = res ? res->pitch : 0;
+  a.strips = (x.w + 31) / 32;   // 32-pixel strips, runs of 8 rows (256 output pixels)
+  a.runs = (x.h + 7) / 8;
+  a.x_bytes = (int32_t)xb; a.y_bytes = (int32_t)yb; a.res_bytes = (int32_t)rb;
+  a.w1_bytes = ch * 9 * x.c * 2;
+  a.w2_bytes = y.c * 9 * ch * 2;
+  const int64_t blocks = (int64_t)x.n * a.strips * a.runs;
+  if (blocks >= (1ll << 31)) return fail(VRS_EBADSHAPE, "bottleneck pair: grid too large");
+  const char* name = "vrs_bpair_bf16_c64_h32_w32";
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  ls.push_back(make_launch(name, f, dim3((unsigned)blocks), dim3(256), 0, a));
+  const double M = (double)x.n * x.h * x.w;
+  ls.back().flops = 2.0 * M * 9.0 * ((double)x.c * ch + (double)ch * y.c);
+  ls.back().bytes = M * x.c * 2.0 + M * y.c * 2.0 + (res ? M * y.c * 2.0 : 0.0) + 2.0 * 9.0 * x.c * ch * 2.0 +
+                    8.0 * (ch + y.c);
+  return VRS_OK;
+}
+
 }  // namespace vrs
 
 using namespace vrs;

@@ -121,6 +121,13 @@ int stem_pair_check(int dtype, int act0, int act1, int h, int w);
 int prep_stem_pair(vrs_ctx* ctx, const float* x, int n, int h, int w, const void* w0, const float* scale0,
                    const float* shift0, const void* w1, const float* scale1, const float* shift1, const vrs_nhwc& y,
                    std::vector<Launch>& ls);
+// bottleneck pair (3x3 -> 3x3 + residual, bf16, SiLU on both) in one kernel:
+// x the block input (C channels), w1 [ch][3][3][C], w2 [C][3][3][ch], res
+// optional, y (C channels); bpair_check: the channel counts built
+int bpair_check(int dtype, int act1, int act2, int cin, int ch, int cout);
+int prep_bpair(vrs_ctx* ctx, const vrs_nhwc& x, const void* w1, const float* s1, const float* b1, int ch,
+               const void* w2, const float* s2, const float* b2, const vrs_nhwc* res, const vrs_nhwc& y,
+               std::vector<Launch>& ls);
 // max |x| of a bfloat16 NHWC view into *out (float bits; caller zeroes it)
 int prep_absmax(vrs_ctx* ctx, const vrs_nhwc& x, unsigned* out, std::vector<Launch>& ls);
 // float -> e4m3 (OCP, max 448) with round-to-nearest-even; |v| > 448 saturates

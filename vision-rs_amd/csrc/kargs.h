@@ -76,6 +76,28 @@ typedef struct {
   int32_t res_f8;
 } vrs_conv_args;
 
+/* Fused bottleneck pair (bf16): y = act2(s2 * conv3x3(w2, act1(s1 * conv3x3(w1,
+ * x) + b1)) + b2) + res, both convs 3x3 stride 1 pad 1 with SiLU, the middle
+ * map never leaving the workgroup.  x, y, res: NHWC views of N x H x W pixels
+ * (pointers at their first channel, pitches in elements, bytes readable from
+ * the pointer < 2^31); w1 [CH][3][3][C], w2 [C][3][3][CH] in bf16.  The grid
+ * is N x strips x runs: strips of TW columns, runs of 256 / TW rows. */
+typedef struct {
+  const void* x;
+  const void* w1;
+  const float* s1;
+  const float* b1;
+  const void* w2;
+  const float* s2;
+  const float* b2;
+  const void* res;   /* null: no residual */
+  void* y;
+  int32_t N, H, W;
+  int32_t x_pitch, y_pitch, r_pitch;
+  int32_t strips, runs;
+  int32_t x_bytes, y_bytes, res_bytes, w1_bytes, w2_bytes;
+} vrs_bpair_args;
+
 /* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the
  * element type. */
 typedef struct {

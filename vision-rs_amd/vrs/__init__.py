@@ -38,6 +38,7 @@ TILE_W1_256 = 8   # weight-stationary 1x1 kernels (bf16): 256- or 128-channel we
 TILE_W1_128 = 9
 TILE_64x64 = 10   # bf16: small maps (four times the workgroups of 128x128)
 TILE_STEM_PAIR = 11   # model plans: the conv after a 64-channel stem, fused with it (bf16)
+TILE_BPAIR = 12   # model plans: a bottleneck's second 3x3 conv, fused with the first (bf16)
 
 ERRORS = {-1: "EINVAL", -2: "EBADSHAPE", -3: "EUNSUPPORTED", -4: "ENOMODULE", -5: "EHIP", -6: "ENOTFOUND",
           -7: "ESTATE"}
@@ -90,7 +91,8 @@ class ConvIo(C.Structure):
                 ("x", Nhwc), ("y", Nhwc), ("res", Nhwc), ("up", Nhwc), ("out_idx", C.c_int32),
                 ("out_off", C.c_int64), ("out_sb", C.c_int64), ("out_sp", C.c_int64), ("out_sc", C.c_int64),
                 ("x_e4m3", C.c_int32), ("y_e4m3", C.c_int32), ("res_e4m3", C.c_int32), ("up_e4m3", C.c_int32),
-                ("x_step", C.c_float), ("y_step", C.c_float), ("res_step", C.c_float), ("up_step", C.c_float)]
+                ("x_step", C.c_float), ("y_step", C.c_float), ("res_step", C.c_float), ("up_step", C.c_float),
+                ("fused_in", C.c_int32)]
 
 
 PLAN_FP8 = 0x10000
@@ -110,6 +112,8 @@ SIGNATURES = {
     "vrs_conv_stem": (C.c_int, [_vp, _P(ConvDesc), _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _P(Nhwc), _vp]),
     "vrs_conv_stem_pair": (C.c_int, [_vp, _P(ConvDesc), _P(ConvDesc), _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp,
                                      _vp, _vp, _vp, _P(Nhwc), _vp]),
+    "vrs_conv_bottleneck_pair": (C.c_int, [_vp, _P(ConvDesc), _P(ConvDesc), _P(Nhwc), _vp, _vp, _vp, _i32, _vp, _vp,
+                                           _vp, _P(Nhwc), _P(Nhwc), _vp]),
     "vrs_bn_fold": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _i32, _vp, _vp]),
     "vrs_pack_input": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _P(Nhwc), _i32, _vp]),
     "vrs_unpack_output": (C.c_int, [_vp, _P(Nhwc), _i32, _vp, _vp]),
@@ -273,6 +277,17 @@ class Context:
         check(lib().vrs_conv_stem_pair(self.handle, C.byref(d0), C.byref(d1), _ptr(x_nchw), n, c, h, w_, _ptr(w0),
                                        _ptr(scale0), _ptr(shift0), _ptr(w1), _ptr(scale1), _ptr(shift1),
                                        C.byref(y), _stream(stream)))
+
+    def conv_bottleneck_pair(self, x, w1, scale1, shift1, c_hidden, w2, scale2, shift2, y, res=None, dtype=BF16,
+                             stream=None):
+        """A bottleneck's 3x3 -> 3x3 (+ residual res) in one kernel: x, y, res Nhwc
+        views; w1 / w2 from pack_conv_weight ([c_hidden][3][3][c], [c][3][3][c_hidden])."""
+        d1 = ConvDesc(3, 1, 1, ACT_SILU, dtype, TILE_AUTO, 1.0, 0, 0, 0, 0.0, 0.0)
+        d2 = ConvDesc(3, 1, 1, ACT_SILU, dtype, TILE_AUTO, 1.0, 0, 0, 0, 0.0, 0.0)
+        check(lib().vrs_conv_bottleneck_pair(self.handle, C.byref(d1), C.byref(d2), C.byref(x), _ptr(w1),
+                                             _ptr(scale1), _ptr(shift1), c_hidden, _ptr(w2), _ptr(scale2),
+                                             _ptr(shift2), C.byref(res) if res is not None else None, C.byref(y),
+                                             _stream(stream)))
 
     def pack_input(self, x_nchw, y, dtype, stream=None):
         n, c, h, w = x_nchw.shape
