@@ -720,8 +720,9 @@ def main() -> int:
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "f32", "fp8"])
     ap.add_argument("--no-fp8", action="store_true", help="skip the fp8 second run (BASELINE config 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
-    ap.add_argument("--streams", type=int, default=4,
-                    help="streams the graph capture spreads independent launches over (1 = serial)")
+    ap.add_argument("--streams", type=int, default=1,
+                    help="streams the graph capture spreads independent launches over (1 = serial, one graph; "
+                         "more: one graph per segment between cross-stream waits, replayed on that many streams)")
     ap.add_argument("--layers", action="store_true", help="also print the per-layer table to stderr")
     ap.add_argument("--autotune", action="store_true",
                     help="autotune the tiles instead of loading the committed plan (vision-rs_amd/plans/)")
@@ -916,8 +917,9 @@ def main() -> int:
         "dtype": a.dtype, "data": "synthetic",
         "config": {"workload": f"YOLO26{a.variant} end-to-end forward {a.size}x{a.size} batch {a.batch}",
                    "batch": a.batch, "size": a.size, "variant": a.variant, "classes": 80,
-                   "weights": "seeded Kaiming-normal, identity BN folded", "graph": f"hipGraph replay (captured over {a.streams} streams; the replay's dispatches "
-                            "run in order on one hardware queue, so independent branches do not overlap)",
+                   "weights": "seeded Kaiming-normal, identity BN folded", "graph": ("hipGraph replay: one graph, its dispatches in order on one hardware queue" if a.streams == 1
+                             else f"hipGraph replay over {a.streams} streams: one graph per segment between "
+                                  "cross-stream waits, independent branches on separate streams"),
                    "forward_tflop": round(total_flops / 1e12, 3),
                    "achieved_tflops_e2e": round(total_flops / (ms / 1e3) / 1e12, 1),
                    "tile_plans": plans_used},

@@ -185,12 +185,13 @@ def test_yolo26_weights_from_safetensors(dtype, tmp_path):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("streams", [1, 4])
+@pytest.mark.parametrize("streams", [1, 2, 4, 8])
 def test_yolo26m_graph_replay_matches_eager(streams):
-    """The captured graph (launches spread over `streams` streams with
-    buffer-conflict dependencies) replayed three times, with eager work and
-    synchronisation between the replays, gives bit for bit the eager forward
-    on every replay."""
+    """The captured forward (launches spread over `streams` streams with
+    buffer-conflict dependencies, one graph per segment between cross-stream
+    waits, the segments replayed on the model's streams) replayed three
+    times, with eager work and synchronisation between the replays, gives bit
+    for bit the eager forward on every replay; one stream is one graph."""
     import torch
     x = np.random.default_rng(4).uniform(0, 1, (2, 3, 320, 320)).astype(np.float32)
     desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="m", one2one=True)
@@ -203,6 +204,9 @@ def test_yolo26m_graph_replay_matches_eager(streams):
     outs = m.alloc_outputs()
     st = torch.cuda.Stream()
     m.capture(xd, outs, st.cuda_stream)
+    nseg = m.num_graph_segments()
+    print(f"{streams} streams: {nseg} graph segments for {len(m.launch_names())} launches")
+    assert nseg == 1 if streams == 1 else nseg > 1
     for rep in range(3):
         for o in outs:
             o.fill_(float("nan"))

@@ -129,13 +129,25 @@ struct vrs_model {
   std::vector<std::string> labels;
   std::vector<LaunchIO> io;      // per launch: what it reads and writes
   std::vector<int> conv_launch;  // per conv: index of its kernel launch (-1: none)
-  int streams = 4;               // capture concurrency (1 = one serial chain)
+  int streams = 1;               // capture concurrency (1 = one serial chain, one graph)
   std::vector<hipStream_t> side; // extra capture streams (default priority)
-  std::vector<hipEvent_t> evs;   // capture-time dependency events
   const float* prep_x = nullptr;
   std::vector<float*> prep_outs;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
+  // the captured forward: one graph per segment -- a run of consecutive
+  // launches of one capture stream between cross-stream waits -- replayed on
+  // that stream (graphs on different streams run concurrently; the launches
+  // of one graph run in order on one hardware queue)
+  struct Seg {
+    int stream = 0;
+    std::vector<int> waits;   // segments whose end this one waits for (other streams)
+    bool recorded = false;    // another stream waits for this segment's end
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    hipEvent_t done = nullptr;
+  };
+  std::vector<Seg> segs;
+  int seg_streams = 1;          // streams the segments use
+  std::vector<hipEvent_t> join_evs;   // fork (0) and one join event per side stream
   // fp8: calibrated scales; calib_mode runs every conv on bf16 with an
   // absmax reduction in front of each fp8 conv (slot = conv index)
   bool calibrated = false;
@@ -149,6 +161,17 @@ std::string J(const std::string& pre, const std::string& n) { return pre.empty()
 
 // element type of activations and of every non-fp8 kernel
 int act_dt(const vrs_model* m) { return m->dtype == VRS_FP8 ? VRS_BF16 : m->dtype; }
+
+// release the captured segment graphs (a later capture rebuilds them)
+void drop_graphs(vrs_model* m) {
+  for (auto& g : m->segs) {
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    if (g.graph) (void)hipGraphDestroy(g.graph);
+    if (g.done) (void)hipEventDestroy(g.done);
+  }
+  m->segs.clear();
+  m->seg_streams = 1;
+}
 
 class Builder {
  public:
@@ -1492,29 +1515,18 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
   if (!m->finalized) return fail(VRS_ESTATE, "vrs_model_capture: call vrs_model_finalize first");
   int rc = prepare(m, x, outputs);
   if (rc) return rc;
-  if (m->exec) { (void)hipGraphExecDestroy(m->exec); m->exec = nullptr; }
-  if (m->graph) { (void)hipGraphDestroy(m->graph); m->graph = nullptr; }
+  drop_graphs(m);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Concurrency: the launches go to up to m->streams streams of the capture,
-  // each waiting (through events) only for the earlier launches whose
-  // accesses conflict with its own -- a write against any overlapping read
-  // or write of the same buffer and channel range.  Independent branches
-  // (the Detect head's six chains, slices of one concat buffer) then become
-  // parallel graph branches.
+  // Concurrency: the launches go to up to m->streams streams, each waiting
+  // only for the earlier launches whose accesses conflict with its own -- a
+  // write against any overlapping read or write of the same buffer and
+  // channel range.  A stream's launches between two cross-stream waits form
+  // a segment, captured as a graph of its own: independent branches (the
+  // Detect head's chains, the P3 head beside the neck's bottom-up layers)
+  // are graphs on different streams and run concurrently at replay, while
+  // the launches of one segment keep the graph's back-to-back dispatch.
   const int n = (int)m->launches.size();
   const int K = std::max(1, std::min(m->streams, 8));
-  while ((int)m->side.size() < K - 1) {
-    hipStream_t t;
-    VRS_HIP(hipStreamCreateWithFlags(&t, hipStreamNonBlocking));
-    m->side.push_back(t);
-  }
-  while ((int)m->evs.size() < n + K) {
-    hipEvent_t e;
-    VRS_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-    m->evs.push_back(e);
-  }
-  std::vector<hipStream_t> ss(1, s);
-  for (int k = 0; k < K - 1; ++k) ss.push_back(m->side[k]);
   auto conflict = [](const LaunchIO& a, const LaunchIO& b) {   // a after b
     auto ov = [](const Access& x, const Access& y) { return x.res == y.res && x.c0 < y.c1 && y.c0 < x.c1; };
     for (const Access& w : a.wr) {
@@ -1525,47 +1537,87 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
       for (const Access& w : b.wr) if (ov(r, w)) return true;
     return false;
   };
-  VRS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-  auto abort_capture = [&](int code) {
-    hipGraph_t g = nullptr;
-    (void)hipStreamEndCapture(s, &g);
-    if (g) (void)hipGraphDestroy(g);
-    return code;
-  };
-  hipEvent_t fork = m->evs[n];
-  if (hipEventRecord(fork, s) != hipSuccess) return abort_capture(fail(VRS_EHIP, "capture: fork event"));
-  for (int k = 1; k < K; ++k)
-    if (hipStreamWaitEvent(ss[k], fork, 0) != hipSuccess) return abort_capture(fail(VRS_EHIP, "capture: fork wait"));
+  // stream of each launch and the cross-stream waits it needs
   std::vector<int> stream_of(n, 0), last(K, -1);
+  std::vector<std::vector<int>> in_waits(n);
+  std::vector<char> waited_on(n, 0);
   std::vector<std::vector<int>> waited(K, std::vector<int>(K, -1));   // [s][t]: launches of t that s has waited for
   for (int i = 0; i < n; ++i) {
     std::vector<int> deps;
     for (int j = 0; j < i; ++j)
       if (conflict(m->io[i], m->io[j])) deps.push_back(j);
-    int st = 0;
-    if (!deps.empty()) {
-      st = stream_of[deps.back()];
-    } else {
+    // continue a stream whose last launch is one of the dependencies (the
+    // latest such); a launch none of whose dependencies ends a stream -- a
+    // sibling branch -- starts on the least recently used stream
+    int st = -1;
+    for (int k = 0; k < K; ++k)
+      if (last[k] >= 0 && std::binary_search(deps.begin(), deps.end(), last[k]) && (st < 0 || last[k] > last[st]))
+        st = k;
+    if (st < 0) {
+      st = 0;
       for (int k = 1; k < K; ++k) if (last[k] < last[st]) st = k;
     }
     for (int j : deps) {
       const int t = stream_of[j];
       if (t == st || waited[st][t] >= j) continue;
-      if (hipStreamWaitEvent(ss[st], m->evs[j], 0) != hipSuccess)
-        return abort_capture(fail(VRS_EHIP, "capture: dependency wait"));
+      in_waits[i].push_back(j);
+      waited_on[j] = 1;
       waited[st][t] = j;
     }
-    if ((rc = run(m->launches[i], ss[st]))) return abort_capture(rc);
-    if (hipEventRecord(m->evs[i], ss[st]) != hipSuccess) return abort_capture(fail(VRS_EHIP, "capture: event"));
     stream_of[i] = st;
     last[st] = i;
   }
-  for (int k = 1; k < K; ++k) {   // join every side stream back into the origin
-    if (hipEventRecord(m->evs[n + k], ss[k]) != hipSuccess || hipStreamWaitEvent(s, m->evs[n + k], 0) != hipSuccess)
-      return abort_capture(fail(VRS_EHIP, "capture: join"));
+  // segments: a launch with a cross-stream wait starts one, a launch another
+  // stream waits for ends one
+  std::vector<int> seg_of(n, -1), open(K, -1);
+  std::vector<std::vector<int>> seg_launches;
+  for (int i = 0; i < n; ++i) {
+    const int st = stream_of[i];
+    if (open[st] < 0 || !in_waits[i].empty()) {
+      open[st] = (int)m->segs.size();
+      m->segs.emplace_back();
+      m->segs.back().stream = st;
+      seg_launches.emplace_back();
+      for (int j : in_waits[i]) m->segs.back().waits.push_back(seg_of[j]);
+    }
+    seg_of[i] = open[st];
+    seg_launches[open[st]].push_back(i);
+    if (waited_on[i]) {
+      m->segs[open[st]].recorded = true;
+      open[st] = -1;
+    }
   }
-  VRS_HIP(hipStreamEndCapture(s, &m->graph));
-  VRS_HIP(hipGraphInstantiate(&m->exec, m->graph, nullptr, nullptr, 0));
+  int used = 1;
+  for (const auto& g : m->segs) used = std::max(used, g.stream + 1);
+  while ((int)m->side.size() < used - 1) {
+    hipStream_t t;
+    VRS_HIP(hipStreamCreateWithFlags(&t, hipStreamNonBlocking));
+    m->side.push_back(t);
+  }
+  while ((int)m->join_evs.size() < used) {   // fork + one join per side stream
+    hipEvent_t e;
+    VRS_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    m->join_evs.push_back(e);
+  }
+  m->seg_streams = used;
+  for (size_t g = 0; g < m->segs.size(); ++g) {
+    vrs_model::Seg& sg = m->segs[g];
+    if (sg.recorded) VRS_HIP(hipEventCreateWithFlags(&sg.done, hipEventDisableTiming));
+    VRS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    for (int i : seg_launches[g])
+      if ((rc = run(m->launches[i], s))) {
+        hipGraph_t gr = nullptr;
+        (void)hipStreamEndCapture(s, &gr);
+        if (gr) (void)hipGraphDestroy(gr);
+        drop_graphs(m);
+        return rc;
+      }
+    if (hipStreamEndCapture(s, &sg.graph) != hipSuccess ||
+        hipGraphInstantiate(&sg.exec, sg.graph, nullptr, nullptr, 0) != hipSuccess) {
+      drop_graphs(m);
+      return fail(VRS_EHIP, "capture: segment %zu", g);
+    }
+  }
   return VRS_OK;
 }
 
@@ -1578,10 +1630,29 @@ int vrs_model_set_streams(vrs_model* m, int32_t streams) {
 
 int vrs_model_replay(vrs_model* m, void* stream) {
   if (!m) return fail(VRS_EINVAL, "null model");
-  if (!m->exec) return fail(VRS_ESTATE, "vrs_model_replay: no captured graph");
-  VRS_HIP(hipGraphLaunch(m->exec, static_cast<hipStream_t>(stream)));
+  if (m->segs.empty()) return fail(VRS_ESTATE, "vrs_model_replay: no captured graph");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  std::vector<hipStream_t> ss(1, s);
+  for (int k = 1; k < m->seg_streams; ++k) ss.push_back(m->side[k - 1]);
+  // the side streams start after what the caller's stream holds (fork) and
+  // the caller's stream continues after all of them (join)
+  if (m->seg_streams > 1) {
+    VRS_HIP(hipEventRecord(m->join_evs[0], s));
+    for (int k = 1; k < m->seg_streams; ++k) VRS_HIP(hipStreamWaitEvent(ss[k], m->join_evs[0], 0));
+  }
+  for (const auto& g : m->segs) {
+    for (int w : g.waits) VRS_HIP(hipStreamWaitEvent(ss[g.stream], m->segs[w].done, 0));
+    VRS_HIP(hipGraphLaunch(g.exec, ss[g.stream]));
+    if (g.recorded) VRS_HIP(hipEventRecord(g.done, ss[g.stream]));
+  }
+  for (int k = 1; k < m->seg_streams; ++k) {
+    VRS_HIP(hipEventRecord(m->join_evs[k], ss[k]));
+    VRS_HIP(hipStreamWaitEvent(s, m->join_evs[k], 0));
+  }
   return VRS_OK;
 }
+
+int vrs_model_num_graph_segments(const vrs_model* m) { return m ? (int)m->segs.size() : 0; }
 
 int vrs_model_num_launches(const vrs_model* m) { return m ? (int)m->launches.size() : 0; }
 
@@ -1669,8 +1740,7 @@ int vrs_model_calibrate(vrs_model* m, const float* x, void* stream) {
     for (float& v : s8) v *= sc;
     VRS_HIP(hipMemcpy(c.scale8, s8.data(), s8.size() * 4, hipMemcpyHostToDevice));
   }
-  if (m->exec) { (void)hipGraphExecDestroy(m->exec); m->exec = nullptr; }
-  if (m->graph) { (void)hipGraphDestroy(m->graph); m->graph = nullptr; }
+  drop_graphs(m);
   m->calibrated = true;
   return VRS_OK;
 }
@@ -1736,9 +1806,8 @@ int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io) {
 
 int vrs_model_destroy(vrs_model* m) {
   if (!m) return VRS_OK;
-  if (m->exec) (void)hipGraphExecDestroy(m->exec);
-  if (m->graph) (void)hipGraphDestroy(m->graph);
-  for (hipEvent_t e : m->evs) (void)hipEventDestroy(e);
+  drop_graphs(m);
+  for (hipEvent_t e : m->join_evs) (void)hipEventDestroy(e);
   for (hipStream_t t : m->side) (void)hipStreamDestroy(t);
   for (void* p : m->allocs) (void)hipFree(p);
   delete m;
