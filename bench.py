@@ -491,14 +491,37 @@ def yolo26n_latency(ctx, iters=200):
             "note": "context only: the reference's one published configuration, not BASELINE's metric"}
 
 
-def _time_launches(fn, n_sets, iters=20, warmup=3):
-    """Average GPU time of fn(set_index) (one kernel launch each), measured with
-    events around every launch on the current stream."""
+def _time_launches(fn, n_sets, iters=20, warmup=3, queued=False):
+    """Average GPU time of fn(set_index) (one kernel launch each) on the current
+    stream.  queued=False: events around every launch.  queued=True (calls
+    that only enqueue GPU work): the launches are queued behind a GPU spin
+    longer than the host takes to issue them, then run back to back between
+    one event pair -- the GPU never waits for the host and no event sits
+    between two launches (per-launch event pairs add ~2 us to each)."""
     import torch
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         fn(i % n_sets)
     torch.cuda.synchronize()
+    if queued:
+        t0 = time.perf_counter()
+        for i in range(3):
+            fn(i % n_sets)
+        issue_s = (time.perf_counter() - t0) / 3   # host time to issue one call
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        torch.cuda._sleep(1 << 20)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        spin_s = e0.elapsed_time(e1) / 1e3 / (1 << 20)   # seconds per spin cycle
+        torch.cuda._sleep(int(min(2 * iters * issue_s + 1e-3, 0.5) / spin_s))
+        e0.record(stream)
+        for i in range(iters):
+            fn(i % n_sets)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters  # ms
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
     for i, (e0, e1) in enumerate(evs):
         e0.record(stream)
@@ -566,7 +589,7 @@ def micro(ctx, emit, cpu=True):
             try:
                 f = lambda i, t=tile: ctx.conv2d(vrs.nhwc(xs[i]), wp, sc, sh, vrs.nhwc(ys[i]), k, s, 1, vrs.ACT_SILU,
                                                   None, vrs.BF16, tile=t)
-                ms = _time_launches(f, n_sets)
+                ms = _time_launches(f, n_sets, queued=True)
             except vrs.VrsError:
                 continue
             if best is None or ms < best[1]:
@@ -598,7 +621,7 @@ def micro(ctx, emit, cpu=True):
               for _ in range(n_sets)]
         ys = [torch.empty(bb, hw, hw, C, dtype=torch.bfloat16, device=dev) for _ in range(n_sets)]
         ms = _time_launches(lambda i: ctx.conv2d(vrs.nhwc(xs[i]), wp, sc, sh, vrs.nhwc(ys[i]), 3, 1, C,
-                                                 vrs.ACT_SILU, None, vrs.BF16), n_sets, iters=60)
+                                                 vrs.ACT_SILU, None, vrs.BF16), n_sets, iters=60, queued=True)
         line = {"config": name, "batch": bb, "us": round(ms * 1e3, 2), "mb": round(nb / 1e6, 2),
                 "gbs": round(nb / ms / 1e6, 1), "frac_hbm": round(nb / ms / 1e6 / PEAK_HBM_GBS, 4),
                 "buffer_sets": n_sets}
@@ -625,8 +648,9 @@ def micro(ctx, emit, cpu=True):
     names = m.launch_names()
     work = m.launch_work()
     ai = [i for i, n in enumerate(names) if "psa_attn" in n][0]
-    ms_core = _time_launches(lambda i: m.run_launches(ai, 1), 1, iters=50)
-    ms_blk = _time_launches(lambda i: m.run_launches(1, len(names) - 2), 1, iters=20)  # qkv..proj, no pack/unpack
+    ms_core = _time_launches(lambda i: m.run_launches(ai, 1), 1, iters=50, queued=True)
+    ms_blk = _time_launches(lambda i: m.run_launches(1, len(names) - 2), 1, iters=20,  # qkv..proj, no pack/unpack
+                            queued=True)
     core_fl = work[ai][0]
     blk_fl = sum(w[0] for w in work[1:len(names) - 1])
     line = {"config": "c2 psa attention B32 256ch 20x20 4 heads", "core_us": round(ms_core * 1e3, 2),
@@ -652,7 +676,7 @@ def micro(ctx, emit, cpu=True):
     off = torch.randn(Bq, Q, Hh, L, Pp, 2, device=dev) * 0.05
     attw = torch.softmax(torch.randn(Bq, Q, Hh, L * Pp, device=dev), -1).reshape(Bq, Q, Hh, L, Pp).contiguous()
     out = torch.empty(Bq, Q, Hh * 32, device=dev)
-    ms = _time_launches(lambda i: ctx.msda(vals[i], shapes, ref, off, attw, out), n_sets, iters=60)
+    ms = _time_launches(lambda i: ctx.msda(vals[i], shapes, ref, off, attw, out), n_sets, iters=60, queued=True)
     comp = vbytes + ref.numel() * 4 + off.numel() * 4 + attw.numel() * 4 + out.numel() * 4
     issued = Bq * Q * Hh * L * Pp * 4 * 32 * 4
     line = {"config": "c4 msda B8 Q300 8h 4L 4P fp32", "us": round(ms * 1e3, 2),
