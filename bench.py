@@ -423,8 +423,8 @@ def cpu_model():
 
 def cpu_baseline(variant, size, batch, P, max_images=64):
     """CPU oracle (float32, OpenMP over the host's cores): one warm forward of
-    the whole workload batch (one warm iteration at bs64), capped
-    at max_images."""
+    the whole workload batch (the CPU baseline is one warm iteration at bs64),
+    capped at max_images."""
     import oracle
     from oracle import yolo26 as Y
     from vrs.synth import images
@@ -753,7 +753,7 @@ def main() -> int:
     ap.add_argument("--save-plans", action="store_true",
                     help="write the tile plans this run used to vision-rs_amd/plans/ (or --plan-dir)")
     ap.add_argument("--plan-dir", default=None,
-                    help="directory --save-plans writes to (e.g. gpurun_out/plans on a remote box)")
+                    help="directory --save-plans writes to (e.g. a scratch folder on a remote box)")
     ap.add_argument("--no-micro", action="store_true",
                     help="skip the isolated BASELINE configs 2-4 in the default line's `micro` object")
     ap.add_argument("--micro", action="store_true",

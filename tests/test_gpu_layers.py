@@ -16,8 +16,8 @@ layers:
 * fp8 (every eligible conv forced onto the e4m3 MFMA, as the bench's forced
   fp8 line runs): the oracle conv on the same dequantised e4m3 operands --
   the input quantised with the layer's calibrated power-of-two step, the
-  weights per output channel on max|w|/448 ("the CPU path uses
-  the same dequantized weights and activation scales").
+  weights per output channel on max|w|/448 (the fp8 configuration's CPU
+  check uses the same dequantised weights and activation scales).
 
 The end-to-end outputs of the same run are then compared with the plain
 float32 oracle (the reference CPU path on the unrounded weights and input):
