@@ -187,11 +187,12 @@ def test_yolo26_weights_from_safetensors(dtype, tmp_path):
 
 @pytest.mark.parametrize("streams", [1, 2, 4, 8])
 def test_yolo26m_graph_replay_matches_eager(streams):
-    """The captured forward (launches spread over `streams` streams with
-    buffer-conflict dependencies, one graph per segment between cross-stream
-    waits, the segments replayed on the model's streams) replayed three
-    times, with eager work and synchronisation between the replays, gives bit
-    for bit the eager forward on every replay; one stream is one graph."""
+    """The captured forward (the Detect head's six chains spread over
+    `streams` streams with buffer-conflict dependencies, one graph per
+    segment between cross-stream waits, the segments replayed on the model's
+    streams) replayed three times, with eager work and synchronisation
+    between the replays, gives bit for bit the eager forward on every replay;
+    one stream is one graph."""
     import torch
     x = np.random.default_rng(4).uniform(0, 1, (2, 3, 320, 320)).astype(np.float32)
     desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="m", one2one=True)

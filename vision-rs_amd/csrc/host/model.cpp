@@ -101,6 +101,11 @@ struct Step {
   // model input (a multi-input block's tensors lie back to back)
   int in_c = 0, in_h = 0, in_w = 0;
   int64_t in_off = 0;
+  // independent chain this step belongs to (-1: the network's trunk): the
+  // Detect head's six chains (box and class branch of each scale) read the
+  // neck and write only their slices of the outputs, so a captured forward
+  // may run them on streams of their own
+  int branch = -1;
 };
 
 }  // namespace
@@ -127,9 +132,10 @@ struct vrs_model {
   // prepared launches for the last (x, outputs) pointers
   std::vector<Launch> launches;
   std::vector<std::string> labels;
+  std::vector<int> branch;       // per launch: its step's chain tag (-1: trunk)
   std::vector<LaunchIO> io;      // per launch: what it reads and writes
   std::vector<int> conv_launch;  // per conv: index of its kernel launch (-1: none)
-  int streams = 1;               // capture concurrency (1 = one serial chain, one graph)
+  int streams = 7;               // capture concurrency: the trunk plus one stream per Detect chain
   std::vector<hipStream_t> side; // extra capture streams (default priority)
   const float* prep_x = nullptr;
   std::vector<float*> prep_outs;
@@ -287,6 +293,7 @@ class Builder {
     const int pe = conv_common(J(pre, "pe"), slice(qkv, 0, c), c, 3, 1, CK_BN, true);
     Step st;
     st.type = Step::ATTN; st.conv = pe; st.a = qkv; st.b = att; st.heads = heads;
+    st.branch = branch_;
     m_->steps.push_back(st);
     conv(J(pre, "proj"), att, y, 1, 1, CK_BN, res);
   }
@@ -332,6 +339,7 @@ class Builder {
     conv(J(pre, "cv1"), x, slice(cat, 0, c), 1, 1, CK_BN);
     Step st;
     st.type = Step::POOL; st.a = cat;
+    st.branch = branch_;
     m_->steps.push_back(st);
     const bool add = shortcut && c_in == c_out;
     conv(J(pre, "cv2"), cat, y, 1, 1, CK_BN_SILU, add ? &x : nullptr);
@@ -340,6 +348,7 @@ class Builder {
   void upsample(V x, V y) {
     Step st;
     st.type = Step::UP; st.a = x; st.b = y;
+    st.branch = branch_;
     m_->steps.push_back(st);
   }
 
@@ -355,6 +364,7 @@ class Builder {
       const V x = feats[i];
       const int64_t as = (int64_t)H(x) * W(x);
       const std::string q = J(pre, p2 + "." + std::to_string(i));
+      branch_ = i;   // box chain of scale i
       V t1 = alloc(H(x), W(x), c2), t2 = alloc(H(x), W(x), c2);
       conv(J(q, "0"), x, t1, 3, 1, CK_BN_SILU);
       conv(J(q, "1"), t1, t2, 3, 1, CK_BN_SILU);
@@ -366,6 +376,7 @@ class Builder {
       const V x = feats[i];
       const int64_t as = (int64_t)H(x) * W(x);
       const std::string q = J(pre, p3 + "." + std::to_string(i));
+      branch_ = 3 + i;   // class chain of scale i
       V d1 = alloc(H(x), W(x), chs[i]), p1 = alloc(H(x), W(x), c3);
       V d2 = alloc(H(x), W(x), c3), pw = alloc(H(x), W(x), c3);
       dwconv(J(q, "0.0"), x, d1, 3, 1, CK_BN_SILU);
@@ -375,6 +386,7 @@ class Builder {
       conv_flat(J(q, "2"), pw, nc, 1, CK_PLAIN, 1, (int64_t)nc * base, (int64_t)nc * A, 1, as);
       base += as;
     }
+    branch_ = -1;
     m_->out_dims = {{m_->batch, (int32_t)(4 * A)}, {m_->batch, (int32_t)(nc * A)}};
   }
 
@@ -385,6 +397,7 @@ class Builder {
     m_->convs[i].stem = true;
     Step st;
     st.type = Step::STEM; st.conv = i;
+    st.branch = branch_;
     m_->steps.push_back(st);
   }
 
@@ -397,6 +410,7 @@ class Builder {
     Step st;
     st.type = Step::PACK; st.b = in;
     st.in_c = c_real; st.in_h = h; st.in_w = w; st.in_off = off;
+    st.branch = branch_;
     m_->steps.push_back(st);
     return in;
   }
@@ -404,6 +418,7 @@ class Builder {
   void output(V y) {
     Step st;
     st.type = Step::UNPACK; st.a = y; st.out_idx = (int)m_->out_dims.size();
+    st.branch = branch_;
     m_->steps.push_back(st);
     m_->out_dims.push_back({m_->batch, y.c, H(y), W(y)});
   }
@@ -418,10 +433,12 @@ class Builder {
   void push_conv(int i) {
     Step st;
     st.type = Step::CONV; st.conv = i;
+    st.branch = branch_;
     m_->steps.push_back(st);
   }
   vrs_model* m_;
   std::unordered_map<int, int> real_c_;  // input buffer -> unpadded channels
+  int branch_ = -1;                      // chain tag of the steps being added
 };
 
 int round_half_away(float v) { return (int)std::floor(v + 0.5f); }
@@ -772,6 +789,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
   if (!m->launches.empty() && m->prep_x == x && m->prep_outs == o) return VRS_OK;
   std::vector<Launch> ls;
   std::vector<std::string> labels;
+  std::vector<int> branch;
   std::vector<LaunchIO> io;
   std::vector<int> conv_launch(m->convs.size(), -1);
   int rc = VRS_OK;
@@ -928,9 +946,11 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
     for (size_t i = before; i < ls.size(); ++i) labels.push_back(label + ":" + ls[i].name);
     flush_io();
     if ((rc = calib_writes(m, sio, ls, labels, io))) return rc;
+    branch.resize(labels.size(), st.branch);
   }
   m->launches = std::move(ls);
   m->labels = std::move(labels);
+  m->branch = std::move(branch);
   m->io = std::move(io);
   m->conv_launch = std::move(conv_launch);
   m->prep_x = x;
@@ -1517,14 +1537,22 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
   if (rc) return rc;
   drop_graphs(m);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Concurrency: the launches go to up to m->streams streams, each waiting
-  // only for the earlier launches whose accesses conflict with its own -- a
-  // write against any overlapping read or write of the same buffer and
-  // channel range.  A stream's launches between two cross-stream waits form
-  // a segment, captured as a graph of its own: independent branches (the
-  // Detect head's chains, the P3 head beside the neck's bottom-up layers)
-  // are graphs on different streams and run concurrently at replay, while
-  // the launches of one segment keep the graph's back-to-back dispatch.
+  // Concurrency: with m->streams > 1 the Detect head's chains (steps tagged
+  // with a branch) may leave the caller's stream, which every other launch
+  // keeps.  A chain launch continues the stream whose latest launch it
+  // depends on, else (a chain starting beside others) takes the least
+  // recently used stream, so the first chain to fork from the trunk stays
+  // on it and its siblings go to side streams.  Each launch waits only for
+  // the earlier launches whose accesses conflict with its own -- a write
+  // against any overlapping read or write of the same buffer and channel
+  // range.  A stream's launches between two cross-stream waits form a
+  // segment, captured as a graph of its own, so the head's chains (the P3
+  // ones beside the neck's bottom-up layers) run concurrently at replay
+  // while the trunk keeps one graph's back-to-back dispatch between the
+  // points the chains fork from.  (Measured: forking every sibling branch
+  // of the trunk as well is slower -- many segments, whose boundary waits
+  // cost what the overlap gains -- and so is sending every chain to a side
+  // stream, which adds a fork and a join per chain.)
   const int n = (int)m->launches.size();
   const int K = std::max(1, std::min(m->streams, 8));
   auto conflict = [](const LaunchIO& a, const LaunchIO& b) {   // a after b
@@ -1546,16 +1574,19 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
     std::vector<int> deps;
     for (int j = 0; j < i; ++j)
       if (conflict(m->io[i], m->io[j])) deps.push_back(j);
-    // continue a stream whose last launch is one of the dependencies (the
-    // latest such); a launch none of whose dependencies ends a stream -- a
-    // sibling branch -- starts on the least recently used stream
-    int st = -1;
-    for (int k = 0; k < K; ++k)
-      if (last[k] >= 0 && std::binary_search(deps.begin(), deps.end(), last[k]) && (st < 0 || last[k] > last[st]))
-        st = k;
-    if (st < 0) {
-      st = 0;
-      for (int k = 1; k < K; ++k) if (last[k] < last[st]) st = k;
+    // a chain launch continues the stream whose last launch is one of its
+    // dependencies (the latest such) or, starting a chain beside others,
+    // takes the least recently used stream; trunk launches stay on stream 0
+    int st = 0;
+    if (K > 1 && m->branch[i] >= 0) {
+      st = -1;
+      for (int k = 0; k < K; ++k)
+        if (last[k] >= 0 && std::binary_search(deps.begin(), deps.end(), last[k]) && (st < 0 || last[k] > last[st]))
+          st = k;
+      if (st < 0) {
+        st = 0;
+        for (int k = 1; k < K; ++k) if (last[k] < last[st]) st = k;
+      }
     }
     for (int j : deps) {
       const int t = stream_of[j];
