@@ -363,7 +363,7 @@ def trace_summary(trace_dir, bench_json, steps, profile_iters=PROFILE_ITERS * PR
     the last profile_iters x launches dispatches of each kernel are bench.py's
     per-kernel profile (kernel_profile: the source of `kernels` and
     `roofline.avg_launch_us`), the steps x launches before them the timed
-    hipGraph replays (the Detect head's chains on side streams beside the trunk)."""
+    hipGraph replays (the Detect head's chains as parallel branches beside the trunk)."""
     import csv
     import glob
     with open(bench_json) as f:
@@ -744,9 +744,9 @@ def main() -> int:
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "f32", "fp8"])
     ap.add_argument("--no-fp8", action="store_true", help="skip the fp8 second run (BASELINE config 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
-    ap.add_argument("--streams", type=int, default=7,
-                    help="capture streams: the trunk plus side streams for the Detect head's six chains (1 = "
-                         "serial, one graph; more: one graph per segment between cross-stream waits)")
+    ap.add_argument("--streams", type=int, default=3,
+                    help="capture streams: the trunk plus side streams for the Detect head's six chains, all in "
+                         "one graph whose parallel branches replay on parallel hardware queues (1 = serial)")
     ap.add_argument("--layers", action="store_true", help="also print the per-layer table to stderr")
     ap.add_argument("--autotune", action="store_true",
                     help="autotune the tiles instead of loading the committed plan (vision-rs_amd/plans/)")
@@ -942,9 +942,8 @@ def main() -> int:
         "config": {"workload": f"YOLO26{a.variant} end-to-end forward {a.size}x{a.size} batch {a.batch}",
                    "batch": a.batch, "size": a.size, "variant": a.variant, "classes": 80,
                    "weights": "seeded Kaiming-normal, identity BN folded", "graph": ("hipGraph replay: one graph, its dispatches in order on one hardware queue" if a.streams == 1
-                             else f"hipGraph replay over {a.streams} streams: the Detect head's six chains on "
-                                  "side streams beside the trunk, one graph per segment between cross-stream "
-                                  "waits"),
+                             else f"hipGraph replay: one graph captured over {a.streams} streams, the Detect "
+                                  "head's six chains as parallel branches beside the trunk"),
                    "forward_tflop": round(total_flops / 1e12, 3),
                    "achieved_tflops_e2e": round(total_flops / (ms / 1e3) / 1e12, 1),
                    "tile_plans": plans_used},

@@ -446,21 +446,21 @@ int vrs_model_forward(vrs_model* m, const float* x, float* const* outputs, void*
 int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void* stream);
 int vrs_model_replay(vrs_model* m, void* stream);
 /* Capture concurrency (no counterpart in the reference, whose graphs run on
- * one stream): with streams > 1 (1..8, default 7) vrs_model_capture puts the
+ * one stream): with streams > 1 (1..8, default 3) vrs_model_capture puts the
  * Detect head's six independent chains (box and class branch of each scale)
  * beside the trunk: a chain launch continues the stream whose latest launch
  * it depends on, else takes the least recently used of the caller's stream
  * and the model's streams - 1 side streams (default priority); every other
  * launch stays on the caller's stream.  Each launch waits only for earlier
- * launches that touch overlapping buffer channels.  A stream's launches between two cross-stream waits are
- * captured as one graph (a segment); vrs_model_replay launches the segments
- * with event waits only at the segment boundaries, so the chains run beside
- * each other and beside the neck's remaining layers, and the caller's stream
- * continues after all of them.  1 = one serial chain (a single graph).
- * Models without a Detect head capture one graph whatever the setting. */
+ * launches that touch overlapping buffer channels.  All streams are captured
+ * into the one graph (cross-stream waits as graph edges), whose parallel
+ * branches the runtime replays on parallel hardware queues; the caller's
+ * stream continues after all of them.  1 = one serial chain.  Models without
+ * a Detect head capture one chain whatever the setting. */
 int vrs_model_set_streams(vrs_model* m, int32_t streams);
-/* Graphs the last vrs_model_capture built (segments; 0 before a capture). */
-int vrs_model_num_graph_segments(const vrs_model* m);
+/* Streams the last vrs_model_capture used (1 = a serial graph; 0 before a
+ * capture). */
+int vrs_model_num_capture_streams(const vrs_model* m);
 /* Number of kernel launches in one forward and their "layer:kernel" names
  * (valid after the first vrs_model_forward / vrs_model_capture). */
 int vrs_model_num_launches(const vrs_model* m);

@@ -185,36 +185,42 @@ def test_yolo26_weights_from_safetensors(dtype, tmp_path):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("streams", [1, 2, 4, 8])
+@pytest.mark.parametrize("streams", [1, 2, 3, 8])
 def test_yolo26m_graph_replay_matches_eager(streams):
     """The captured forward (the Detect head's six chains spread over
-    `streams` streams with buffer-conflict dependencies, one graph per
-    segment between cross-stream waits, the segments replayed on the model's
-    streams) replayed three times, with eager work and synchronisation
-    between the replays, gives bit for bit the eager forward on every replay;
-    one stream is one graph."""
+    `streams` capture streams with buffer-conflict dependencies, all in one
+    graph) replayed eight times, each time on a different one of four inputs
+    written into the captured input buffer and with eager work and
+    synchronisation between the replays, gives bit for bit the eager forward
+    of that input: a missing cross-stream dependency would let a branch read
+    the previous replay's activations."""
     import torch
-    x = np.random.default_rng(4).uniform(0, 1, (2, 3, 320, 320)).astype(np.float32)
+    xs = [np.random.default_rng(4 + k).uniform(0, 1, (2, 3, 320, 320)).astype(np.float32) for k in range(4)]
     desc = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="m", one2one=True)
     m = vrs.Model(ctx(), desc, 2, 320, 320, vrs.BF16, 1e-3)
     m.load(_yolo_params(m, bn="random", bf16=True))
     m.set_streams(streams)
-    xd = dev(x)
-    ref = [o.clone() for o in m.forward(xd)]
+    xd = torch.empty(2, 3, 320, 320, device="cuda")
+    refs = []
+    for x in xs:
+        xd.copy_(torch.from_numpy(x))
+        refs.append([o.clone() for o in m.forward(xd)])
     torch.cuda.synchronize()
     outs = m.alloc_outputs()
     st = torch.cuda.Stream()
     m.capture(xd, outs, st.cuda_stream)
-    nseg = m.num_graph_segments()
-    print(f"{streams} streams: {nseg} graph segments for {len(m.launch_names())} launches")
-    assert nseg == 1 if streams == 1 else nseg > 1
-    for rep in range(3):
+    used = m.num_capture_streams()
+    print(f"{streams} streams requested: the capture used {used} for {len(m.launch_names())} launches")
+    assert used == 1 if streams == 1 else 1 < used <= streams
+    for rep in range(8):
+        k = rep % 4
+        xd.copy_(torch.from_numpy(xs[k]))
         for o in outs:
             o.fill_(float("nan"))
         torch.cuda.synchronize()
         m.replay(st.cuda_stream)
         st.synchronize()
-        for a, b in zip(outs, ref):
+        for a, b in zip(outs, refs[k]):
             assert torch.equal(a.view(torch.int32), b.view(torch.int32)), (rep, streams)
         junk = torch.randn(1 << 20, device="cuda") * 2   # eager work between replays
         torch.cuda.synchronize()

@@ -135,25 +135,16 @@ struct vrs_model {
   std::vector<int> branch;       // per launch: its step's chain tag (-1: trunk)
   std::vector<LaunchIO> io;      // per launch: what it reads and writes
   std::vector<int> conv_launch;  // per conv: index of its kernel launch (-1: none)
-  int streams = 7;               // capture concurrency: the trunk plus one stream per Detect chain
+  int streams = 3;               // capture concurrency: the trunk plus side streams for the Detect chains
   std::vector<hipStream_t> side; // extra capture streams (default priority)
   const float* prep_x = nullptr;
   std::vector<float*> prep_outs;
-  // the captured forward: one graph per segment -- a run of consecutive
-  // launches of one capture stream between cross-stream waits -- replayed on
-  // that stream (graphs on different streams run concurrently; the launches
-  // of one graph run in order on one hardware queue)
-  struct Seg {
-    int stream = 0;
-    std::vector<int> waits;   // segments whose end this one waits for (other streams)
-    bool recorded = false;    // another stream waits for this segment's end
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
-    hipEvent_t done = nullptr;
-  };
-  std::vector<Seg> segs;
-  int seg_streams = 1;          // streams the segments use
-  std::vector<hipEvent_t> join_evs;   // fork (0) and one join event per side stream
+  // the captured forward: one graph; with several capture streams its
+  // launches form parallel branches joined by the captured cross-stream
+  // waits, which the runtime replays on parallel hardware queues
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int capture_streams = 0;       // streams the last capture used
   // fp8: calibrated scales; calib_mode runs every conv on bf16 with an
   // absmax reduction in front of each fp8 conv (slot = conv index)
   bool calibrated = false;
@@ -168,15 +159,12 @@ std::string J(const std::string& pre, const std::string& n) { return pre.empty()
 // element type of activations and of every non-fp8 kernel
 int act_dt(const vrs_model* m) { return m->dtype == VRS_FP8 ? VRS_BF16 : m->dtype; }
 
-// release the captured segment graphs (a later capture rebuilds them)
+// release the captured graph (a later capture rebuilds it)
 void drop_graphs(vrs_model* m) {
-  for (auto& g : m->segs) {
-    if (g.exec) (void)hipGraphExecDestroy(g.exec);
-    if (g.graph) (void)hipGraphDestroy(g.graph);
-    if (g.done) (void)hipEventDestroy(g.done);
-  }
-  m->segs.clear();
-  m->seg_streams = 1;
+  if (m->exec) (void)hipGraphExecDestroy(m->exec);
+  if (m->graph) (void)hipGraphDestroy(m->graph);
+  m->exec = nullptr;
+  m->graph = nullptr;
 }
 
 class Builder {
@@ -1541,18 +1529,19 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
   // with a branch) may leave the caller's stream, which every other launch
   // keeps.  A chain launch continues the stream whose latest launch it
   // depends on, else (a chain starting beside others) takes the least
-  // recently used stream, so the first chain to fork from the trunk stays
-  // on it and its siblings go to side streams.  Each launch waits only for
-  // the earlier launches whose accesses conflict with its own -- a write
-  // against any overlapping read or write of the same buffer and channel
-  // range.  A stream's launches between two cross-stream waits form a
-  // segment, captured as a graph of its own, so the head's chains (the P3
-  // ones beside the neck's bottom-up layers) run concurrently at replay
-  // while the trunk keeps one graph's back-to-back dispatch between the
-  // points the chains fork from.  (Measured: forking every sibling branch
-  // of the trunk as well is slower -- many segments, whose boundary waits
-  // cost what the overlap gains -- and so is sending every chain to a side
-  // stream, which adds a fork and a join per chain.)
+  // recently used stream.  Each launch waits only for the earlier launches
+  // whose accesses conflict with its own -- a write against any overlapping
+  // read or write of the same buffer and channel range.  All streams are
+  // captured into one graph: the side streams join the capture through an
+  // event recorded on the caller's stream, every cross-stream wait is a
+  // captured event edge, and the side streams rejoin it before the capture
+  // ends, so the graph holds the chains as parallel branches, which the
+  // runtime replays on parallel hardware queues.  (Measured against the
+  // alternatives: one graph per run of launches between cross-stream waits,
+  // replayed on the model's streams, paid ~14 us at every graph boundary on
+  // the trunk and ~50 us per replay for the fork and join; forking every
+  // sibling branch of the trunk as well, and sending every chain to a side
+  // stream of its own, were slower still.)
   const int n = (int)m->launches.size();
   const int K = std::max(1, std::min(m->streams, 8));
   auto conflict = [](const LaunchIO& a, const LaunchIO& b) {   // a after b
@@ -1574,9 +1563,6 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
     std::vector<int> deps;
     for (int j = 0; j < i; ++j)
       if (conflict(m->io[i], m->io[j])) deps.push_back(j);
-    // a chain launch continues the stream whose last launch is one of its
-    // dependencies (the latest such) or, starting a chain beside others,
-    // takes the least recently used stream; trunk launches stay on stream 0
     int st = 0;
     if (K > 1 && m->branch[i] >= 0) {
       st = -1;
@@ -1598,57 +1584,72 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
     stream_of[i] = st;
     last[st] = i;
   }
-  // segments: a launch with a cross-stream wait starts one, a launch another
-  // stream waits for ends one
-  std::vector<int> seg_of(n, -1), open(K, -1);
-  std::vector<std::vector<int>> seg_launches;
-  for (int i = 0; i < n; ++i) {
-    const int st = stream_of[i];
-    if (open[st] < 0 || !in_waits[i].empty()) {
-      open[st] = (int)m->segs.size();
-      m->segs.emplace_back();
-      m->segs.back().stream = st;
-      seg_launches.emplace_back();
-      for (int j : in_waits[i]) m->segs.back().waits.push_back(seg_of[j]);
-    }
-    seg_of[i] = open[st];
-    seg_launches[open[st]].push_back(i);
-    if (waited_on[i]) {
-      m->segs[open[st]].recorded = true;
-      open[st] = -1;
-    }
-  }
   int used = 1;
-  for (const auto& g : m->segs) used = std::max(used, g.stream + 1);
+  for (int i = 0; i < n; ++i) used = std::max(used, stream_of[i] + 1);
   while ((int)m->side.size() < used - 1) {
     hipStream_t t;
     VRS_HIP(hipStreamCreateWithFlags(&t, hipStreamNonBlocking));
     m->side.push_back(t);
   }
-  while ((int)m->join_evs.size() < used) {   // fork + one join per side stream
-    hipEvent_t e;
-    VRS_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-    m->join_evs.push_back(e);
+  std::vector<hipStream_t> ss(1, s);
+  for (int k = 1; k < used; ++k) ss.push_back(m->side[k - 1]);
+  // capture-time events (edges of the graph, not needed after it is built):
+  // the fork, one per launch another stream waits for, one join per side stream
+  std::vector<hipEvent_t> evs;
+  auto new_ev = [&](hipEvent_t& e) {
+    const hipError_t r = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+    if (r == hipSuccess) evs.push_back(e);
+    return r;
+  };
+  auto free_evs = [&]() {
+    for (hipEvent_t e : evs) (void)hipEventDestroy(e);
+  };
+  hipEvent_t fork = nullptr;
+  std::vector<hipEvent_t> rec(n, nullptr), join(used, nullptr);
+  bool ok = new_ev(fork) == hipSuccess;
+  for (int i = 0; ok && i < n; ++i) if (waited_on[i]) ok = new_ev(rec[i]) == hipSuccess;
+  for (int k = 1; ok && k < used; ++k) ok = new_ev(join[k]) == hipSuccess;
+  if (!ok) {
+    free_evs();
+    return fail(VRS_EHIP, "vrs_model_capture: event creation failed");
   }
-  m->seg_streams = used;
-  for (size_t g = 0; g < m->segs.size(); ++g) {
-    vrs_model::Seg& sg = m->segs[g];
-    if (sg.recorded) VRS_HIP(hipEventCreateWithFlags(&sg.done, hipEventDisableTiming));
-    VRS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    for (int i : seg_launches[g])
-      if ((rc = run(m->launches[i], s))) {
-        hipGraph_t gr = nullptr;
-        (void)hipStreamEndCapture(s, &gr);
-        if (gr) (void)hipGraphDestroy(gr);
-        drop_graphs(m);
-        return rc;
-      }
-    if (hipStreamEndCapture(s, &sg.graph) != hipSuccess ||
-        hipGraphInstantiate(&sg.exec, sg.graph, nullptr, nullptr, 0) != hipSuccess) {
-      drop_graphs(m);
-      return fail(VRS_EHIP, "capture: segment %zu", g);
-    }
+  if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    free_evs();
+    return fail(VRS_EHIP, "vrs_model_capture: hipStreamBeginCapture failed");
   }
+  const char* what = nullptr;
+  if (used > 1) {
+    if (hipEventRecord(fork, s) != hipSuccess) what = "fork";
+    for (int k = 1; !what && k < used; ++k)
+      if (hipStreamWaitEvent(ss[k], fork, 0) != hipSuccess) what = "fork";
+  }
+  for (int i = 0; !what && !rc && i < n; ++i) {
+    const hipStream_t t = ss[stream_of[i]];
+    for (int j : in_waits[i])
+      if (hipStreamWaitEvent(t, rec[j], 0) != hipSuccess) what = "cross-stream wait";
+    if (what || (rc = run(m->launches[i], t))) break;
+    if (waited_on[i] && hipEventRecord(rec[i], t) != hipSuccess) what = "event record";
+  }
+  // the side streams rejoin the capture in every case, so that it can end
+  for (int k = 1; k < used; ++k) {
+    (void)hipEventRecord(join[k], ss[k]);
+    (void)hipStreamWaitEvent(s, join[k], 0);
+  }
+  hipGraph_t gr = nullptr;
+  const hipError_t end = hipStreamEndCapture(s, &gr);
+  free_evs();
+  if (rc || what || end != hipSuccess || !gr) {
+    if (gr) (void)hipGraphDestroy(gr);
+    if (rc) return rc;
+    return fail(VRS_EHIP, "vrs_model_capture: %s", what ? what : "capture did not end");
+  }
+  if (hipGraphInstantiate(&m->exec, gr, nullptr, nullptr, 0) != hipSuccess) {
+    (void)hipGraphDestroy(gr);
+    m->exec = nullptr;
+    return fail(VRS_EHIP, "vrs_model_capture: graph instantiation failed");
+  }
+  m->graph = gr;
+  m->capture_streams = used;
   return VRS_OK;
 }
 
@@ -1661,29 +1662,12 @@ int vrs_model_set_streams(vrs_model* m, int32_t streams) {
 
 int vrs_model_replay(vrs_model* m, void* stream) {
   if (!m) return fail(VRS_EINVAL, "null model");
-  if (m->segs.empty()) return fail(VRS_ESTATE, "vrs_model_replay: no captured graph");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  std::vector<hipStream_t> ss(1, s);
-  for (int k = 1; k < m->seg_streams; ++k) ss.push_back(m->side[k - 1]);
-  // the side streams start after what the caller's stream holds (fork) and
-  // the caller's stream continues after all of them (join)
-  if (m->seg_streams > 1) {
-    VRS_HIP(hipEventRecord(m->join_evs[0], s));
-    for (int k = 1; k < m->seg_streams; ++k) VRS_HIP(hipStreamWaitEvent(ss[k], m->join_evs[0], 0));
-  }
-  for (const auto& g : m->segs) {
-    for (int w : g.waits) VRS_HIP(hipStreamWaitEvent(ss[g.stream], m->segs[w].done, 0));
-    VRS_HIP(hipGraphLaunch(g.exec, ss[g.stream]));
-    if (g.recorded) VRS_HIP(hipEventRecord(g.done, ss[g.stream]));
-  }
-  for (int k = 1; k < m->seg_streams; ++k) {
-    VRS_HIP(hipEventRecord(m->join_evs[k], ss[k]));
-    VRS_HIP(hipStreamWaitEvent(s, m->join_evs[k], 0));
-  }
+  if (!m->exec) return fail(VRS_ESTATE, "vrs_model_replay: no captured graph");
+  VRS_HIP(hipGraphLaunch(m->exec, static_cast<hipStream_t>(stream)));
   return VRS_OK;
 }
 
-int vrs_model_num_graph_segments(const vrs_model* m) { return m ? (int)m->segs.size() : 0; }
+int vrs_model_num_capture_streams(const vrs_model* m) { return m && m->exec ? m->capture_streams : 0; }
 
 int vrs_model_num_launches(const vrs_model* m) { return m ? (int)m->launches.size() : 0; }
 
@@ -1838,7 +1822,6 @@ int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io) {
 int vrs_model_destroy(vrs_model* m) {
   if (!m) return VRS_OK;
   drop_graphs(m);
-  for (hipEvent_t e : m->join_evs) (void)hipEventDestroy(e);
   for (hipStream_t t : m->side) (void)hipStreamDestroy(t);
   for (void* p : m->allocs) (void)hipFree(p);
   delete m;

@@ -140,7 +140,7 @@ SIGNATURES = {
     "vrs_model_capture": (C.c_int, [_vp, _vp, _P(_vp), _vp]),
     "vrs_model_replay": (C.c_int, [_vp, _vp]),
     "vrs_model_set_streams": (C.c_int, [_vp, _i32]),
-    "vrs_model_num_graph_segments": (C.c_int, [_vp]),
+    "vrs_model_num_capture_streams": (C.c_int, [_vp]),
     "vrs_model_num_launches": (C.c_int, [_vp]),
     "vrs_model_launch_name": (C.c_char_p, [_vp, _i32]),
     "vrs_model_launch_work": (C.c_int, [_vp, _i32, _P(C.c_double), _P(C.c_double)]),
@@ -527,8 +527,8 @@ class Model:
     def set_streams(self, n):
         check(lib().vrs_model_set_streams(self.handle, n))
 
-    def num_graph_segments(self):
-        return lib().vrs_model_num_graph_segments(self.handle)
+    def num_capture_streams(self):
+        return lib().vrs_model_num_capture_streams(self.handle)
 
     def launch_names(self):
         n = lib().vrs_model_num_launches(self.handle)
