@@ -145,6 +145,7 @@ struct vrs_model {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   int capture_streams = 0;       // streams the last capture used
+  std::vector<hipEvent_t> cap_evs;   // the events the capture recorded and waited for
   // fp8: calibrated scales; calib_mode runs every conv on bf16 with an
   // absmax reduction in front of each fp8 conv (slot = conv index)
   bool calibrated = false;
@@ -161,10 +162,18 @@ int act_dt(const vrs_model* m) { return m->dtype == VRS_FP8 ? VRS_BF16 : m->dtyp
 
 // release the captured graph (a later capture rebuilds it)
 void drop_graphs(vrs_model* m) {
-  if (m->exec) (void)hipGraphExecDestroy(m->exec);
+  if (m->exec) {
+    // a replay may still run; the graph and the events it was captured
+    // from are released only after it
+    (void)hipDeviceSynchronize();
+    (void)hipGraphExecDestroy(m->exec);
+  }
   if (m->graph) (void)hipGraphDestroy(m->graph);
   m->exec = nullptr;
   m->graph = nullptr;
+  // the runtime's graph may refer to the capture's events: they go after it
+  for (hipEvent_t e : m->cap_evs) (void)hipEventDestroy(e);
+  m->cap_evs.clear();
 }
 
 class Builder {
@@ -1593,9 +1602,10 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
   }
   std::vector<hipStream_t> ss(1, s);
   for (int k = 1; k < used; ++k) ss.push_back(m->side[k - 1]);
-  // capture-time events (edges of the graph, not needed after it is built):
-  // the fork, one per launch another stream waits for, one join per side stream
-  std::vector<hipEvent_t> evs;
+  // capture events: the fork, one per launch another stream waits for, one
+  // join per side stream; they become the graph's cross-stream edges and are
+  // kept as long as the graph (drop_graphs releases them after it)
+  std::vector<hipEvent_t>& evs = m->cap_evs;
   auto new_ev = [&](hipEvent_t& e) {
     const hipError_t r = hipEventCreateWithFlags(&e, hipEventDisableTiming);
     if (r == hipSuccess) evs.push_back(e);
@@ -1603,6 +1613,7 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
   };
   auto free_evs = [&]() {
     for (hipEvent_t e : evs) (void)hipEventDestroy(e);
+    evs.clear();
   };
   hipEvent_t fork = nullptr;
   std::vector<hipEvent_t> rec(n, nullptr), join(used, nullptr);
@@ -1637,15 +1648,16 @@ int vrs_model_capture(vrs_model* m, const float* x, float* const* outputs, void*
   }
   hipGraph_t gr = nullptr;
   const hipError_t end = hipStreamEndCapture(s, &gr);
-  free_evs();
   if (rc || what || end != hipSuccess || !gr) {
     if (gr) (void)hipGraphDestroy(gr);
+    free_evs();
     if (rc) return rc;
     return fail(VRS_EHIP, "vrs_model_capture: %s", what ? what : "capture did not end");
   }
   if (hipGraphInstantiate(&m->exec, gr, nullptr, nullptr, 0) != hipSuccess) {
     (void)hipGraphDestroy(gr);
     m->exec = nullptr;
+    free_evs();
     return fail(VRS_EHIP, "vrs_model_capture: graph instantiation failed");
   }
   m->graph = gr;
