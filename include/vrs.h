@@ -121,6 +121,13 @@ typedef struct {
  * vrs_conv_bottleneck_pair launch; the first conv then has no launch and no
  * output of its own. */
 #define VRS_TILE_BPAIR 12
+/* Model plans only: a flat float32 output conv (conv_plain, 1x1, the Detect
+ * class logits) whose input is the output of the 1x1 BN + SiLU conv before
+ * it (bf16 model, the shapes vrs_conv_pointwise_pair is built for, that
+ * output read by it alone) runs fused with that conv as one
+ * vrs_conv_pointwise_pair launch; the first conv then has no launch and no
+ * output of its own. */
+#define VRS_TILE_PWPAIR 13
 #define VRS_TILE_K32 0x100
 /* OR VRS_TILE_PERSIST: persistent grid (resident workgroups loop over the
  * tiles with one continuous load stream, so a tile's epilogue overlaps the
@@ -238,6 +245,23 @@ int vrs_conv_bottleneck_pair(vrs_ctx* ctx, const vrs_conv_desc* d1, const vrs_co
                              const void* w1_packed, const float* scale1, const float* shift1, int32_t c_hidden,
                              const void* w2_packed, const float* scale2, const float* shift2, const vrs_nhwc* res,
                              const vrs_nhwc* y, void* stream);
+
+/* The last two convs of a Detect class branch in one kernel: the branch
+ * (blocks/detect.rs:117-155) records conv(c, c3, 1, 1) (blocks/conv.rs:31-46)
+ * then conv_plain(c3, nc, 1) (blocks/conv.rs:90-99) writing the class logits:
+ *   y[b*sb + p*sp + co*sc] = scale2[co] * (w2 . m)[co] + shift2[co],
+ *   m = bf16(silu(scale1 * (w1 . x) + shift1))
+ * with the same results as the two convs launched separately (the second
+ * on a flat float32 output, as vrs_model_forward runs the Detect head); the
+ * map m never goes to memory.  bf16, 1x1 stride 1, SiLU on the first conv
+ * and none on the second, built for x->c = c_mid = 256 and 1 <= nc <= 96;
+ * w1 [c_mid][256], w2 [nc][c_mid] from vrs_pack_conv_weight; x an 8-channel
+ * aligned view and the output under 2 GiB.  Other shapes: VRS_EUNSUPPORTED.
+ * No counterpart in the reference's API (it records the two convs). */
+int vrs_conv_pointwise_pair(vrs_ctx* ctx, const vrs_conv_desc* d1, const vrs_conv_desc* d2, const vrs_nhwc* x,
+                            const void* w1_packed, const float* scale1, const float* shift1, int32_t c_mid,
+                            const void* w2_packed, const float* scale2, const float* shift2, int32_t nc, float* y,
+                            int64_t sb, int64_t sp, int64_t sc, void* stream);
 
 /* NCHW float32 -> NHWC dtype, zero-padding channels C..y->c-1 (C <= y->c < C+8). */
 int vrs_pack_input(vrs_ctx* ctx, const float* x_nchw, int32_t n, int32_t c, int32_t h, int32_t w,

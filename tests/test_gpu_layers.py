@@ -235,7 +235,7 @@ def test_yolo26m_bs64_640_layer_by_layer(dtype):
         if io is not None:
             if io.stem == 2:   # stem pair: the input is the stem of the image, computed on chip
                 xin = bf16_round(conv_reference(ios[io.index - 1], P, 1e-3, x[list(IMAGES)], None))
-            elif io.fused_in:   # bottleneck pair: the input is the conv before it, computed on chip
+            elif io.fused_in:   # a fused pair: the input is the conv before it, computed on chip
                 prev = ios[io.index - 1]
                 xprev = read_view(prev.x, prev.dtype, IMAGES, prev.x_e4m3, prev.x_step)
                 xin = bf16_round(conv_reference(prev, P, 1e-3, xprev, None))

@@ -289,6 +289,57 @@ def test_conv_bottleneck_pair_rejections():
         assert e.value.code == -3, (C, CH, dtype)
 
 
+@pytest.mark.parametrize("case", [(2, 24, 24, 80, None), (2, 12, 12, 96, (320, 64)), (3, 6, 6, 5, None),
+                                  (1, 80, 80, 80, None)])
+def test_conv_pointwise_pair(case):
+    """vrs_conv_pointwise_pair (1x1 256 -> 256 BN + SiLU, then a plain 1x1
+    256 -> nc into a channel-major float32 output at y[b*sb + p + co*sc]) is
+    within the bf16 bar of the oracle's two convs (the middle map rounded to
+    bf16 where the GPU rounds it), over pixel tiles that cross image
+    boundaries (HW not a multiple of 64), an input that is a channel slice of
+    a wider buffer, and nc up to 96; float32 words outside the written slices
+    are untouched."""
+    import torch
+    n, h, w, nc, lay = case
+    C = CM = 256
+    rng = np.random.default_rng(h * 7 + nc)
+    x = bf16_round(rng.standard_normal((n, C, h, w)).astype(np.float32))
+    w1 = bf16_round((rng.standard_normal((CM, C, 1, 1)) * np.sqrt(2.0 / C)).astype(np.float32))
+    w2 = bf16_round((rng.standard_normal((nc, CM, 1, 1)) * np.sqrt(1.0 / CM)).astype(np.float32))
+    s1, b1 = rng.uniform(0.5, 1.5, CM).astype(np.float32), rng.normal(0, 0.2, CM).astype(np.float32)
+    s2, b2 = np.ones(nc, np.float32), rng.normal(0, 0.5, nc).astype(np.float32)
+    mid = bf16_round(oracle.affine_act(oracle.conv2d(x, w1, 1, 0), s1, b1, 1))
+    ref = oracle.affine_act(oracle.conv2d(mid, w2, 1, 0), s2, b2, 0)   # [n, nc, h, w]
+    pitch, xo = lay or (C, 0)
+    buf = torch.full((n, h, w, pitch), 3.0, dtype=torch.bfloat16, device="cuda")
+    buf[..., xo:xo + C] = to_nhwc(x, vrs.BF16)
+    xv = vrs.nhwc(buf, C, xo)
+    hw = h * w
+    off, sb = 7, nc * hw + 13   # a slice of a wider float32 row per image, as the Detect scales share one
+    y = torch.full((n * sb,), -5.0, dtype=torch.float32, device="cuda")
+    wd1, wd2 = dev(vrs.pack_conv_weight(w1, 1, C, vrs.BF16)), dev(vrs.pack_conv_weight(w2, 1, CM, vrs.BF16))
+    ctx().conv_pointwise_pair(xv, wd1, dev(s1), dev(b1), CM, wd2, dev(s2), dev(b2), nc, y[off:], sb, 1, hw)
+    torch.cuda.synchronize()
+    yh = y.cpu().numpy().reshape(n, sb)
+    got = yh[:, off:off + nc * hw].reshape(n, nc, h, w)
+    assert rel_err(got, ref, FLOOR[vrs.BF16]) < TOL[vrs.BF16]
+    untouched = np.concatenate([yh[:, :off].ravel(), yh[:, off + nc * hw:].ravel()])
+    assert np.all(untouched == -5.0)
+
+
+def test_conv_pointwise_pair_rejections():
+    """Shapes and types the fused pair is not built for: VRS_EUNSUPPORTED."""
+    import torch
+    for C, CM, nc in ((128, 256, 80), (256, 128, 80), (256, 256, 97)):
+        x = torch.zeros((1, 8, 8, C), dtype=torch.bfloat16, device="cuda")
+        w = torch.zeros(256 * 256, dtype=torch.bfloat16, device="cuda")
+        s = torch.ones(256, device="cuda")
+        y = torch.zeros(nc * 64, device="cuda")
+        with pytest.raises(vrs.VrsError) as e:
+            ctx().conv_pointwise_pair(vrs.nhwc(x), w, s, s, CM, w, s, s, nc, y, nc * 64, 1, 64)
+        assert e.value.code == -3, (C, CM, nc)
+
+
 def test_conv2d_halo3_rejections():
     import torch
     s = torch.ones(64, device="cuda")

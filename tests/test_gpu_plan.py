@@ -338,3 +338,59 @@ def test_fused_upsample_on_the_256x256_tile():
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_pointwise_pair_plan():
+    """VRS_TILE_PWPAIR on the three Detect class output convs
+    (model.23.one2one_cv3.{0,1,2}.2): one launch each replaces the 1x1
+    256 -> 256 conv before it and the 256 -> 80 logits conv, bit-identical
+    to the two launches (the same K order and rounding) at batch 2, where
+    the 64-pixel tiles of the 12x12 and 6x6 maps cross image boundaries;
+    conv_io reports the first conv as launch-less and without output, the
+    second as fused_in without input.  The entry is refused on the box
+    output convs (a 3x3 before them) and on YOLO26n (64 -> 80 class
+    channels)."""
+    import torch
+    B, S = 2, 192
+    names = [pre for pre, _, _ in _yolo(B, S, vrs.BF16, autotune=False).conv_info()]
+    pairs = [(names.index(f"model.23.one2one_cv3.{i}.1.1"), names.index(f"model.23.one2one_cv3.{i}.2"))
+             for i in range(3)]
+    x = dev(np.random.default_rng(6).uniform(0, 1, (B, 3, S, S)).astype(np.float32))
+    outs = {}
+    for tile in (vrs.TILE_PWPAIR, 0):
+        plan = [0] * len(names)
+        for _, i2 in pairs:
+            plan[i2] = tile
+        m = _yolo(B, S, vrs.BF16, autotune=False)
+        m.set_plan(plan)
+        m.load(_params(m))
+        outs[tile] = [o.clone() for o in m.forward(x)]
+        torch.cuda.synchronize()
+        launches = m.launch_names()
+        for i1, i2 in pairs:
+            io1, io2 = m.conv_io(i1), m.conv_io(i2)
+            if tile == vrs.TILE_PWPAIR:
+                assert m.get_plan()[i2] == vrs.TILE_PWPAIR
+                assert io1.launch == -1 and io1.y.data is None and io1.x.data is not None
+                assert io2.fused_in == 1 and io2.x.data is None and io2.out_idx == 1
+                assert launches[io2.launch] == f"{names[i2]}:vrs_pwpair_bf16_c256_m256"
+                assert not any(l.startswith(names[i1] + ":") for l in launches)
+            else:
+                assert io1.launch >= 0 and io2.fused_in == 0
+    for a, b in zip(outs[vrs.TILE_PWPAIR], outs[0]):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    for nm in ("model.23.one2one_cv2.0.2", "model.23.one2one_cv3.0.1.1"):
+        m = _yolo(1, 128, vrs.BF16, autotune=False)
+        bad = [0] * len(names)
+        bad[names.index(nm)] = vrs.TILE_PWPAIR
+        m.set_plan(bad)
+        with pytest.raises(vrs.VrsError):
+            m.load(_params(m))
+    dn = vrs.block(vrs.BLOCK_YOLO26, 3, nc=80, variant="n", one2one=True)
+    mn = vrs.Model(ctx(), dn, 1, 128, 128, vrs.BF16, 1e-3, autotune=False)
+    names_n = [pre for pre, _, _ in mn.conv_info()]
+    bad = [0] * len(names_n)
+    bad[names_n.index("model.23.one2one_cv3.0.2")] = vrs.TILE_PWPAIR
+    mn.set_plan(bad)
+    with pytest.raises(vrs.VrsError):
+        mn.load(_params(mn))

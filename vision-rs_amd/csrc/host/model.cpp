@@ -691,6 +691,49 @@ int prep_bpair_step(const vrs_model* m, size_t i, std::vector<Launch>& ls) {
                     c.has_res ? &r : nullptr, view_of(m, c.y), ls);
 }
 
+// Conv i (a Detect class output: 1x1 plain conv into a float32 flat output)
+// can run fused with the 1x1 BN + SiLU conv before it as one pointwise pair:
+// bf16 model, shapes the pair is built for, conv i's input exactly conv
+// i-1's output, which nothing else reads or writes.
+bool pwpair_eligible(const vrs_model* m, size_t i) {
+  if (i == 0 || i >= m->convs.size() || m->dtype != VRS_BF16) return false;
+  const ConvStep& a = m->convs[i - 1];
+  const ConvStep& c = m->convs[i];
+  auto plain1 = [](const ConvStep& s) {
+    return !s.stem && !s.dw && s.groups <= 1 && s.k == 1 && s.s == 1 && !s.has_up && !s.has_res && s.x.buf >= 0 &&
+           s.cin_real == s.cin;
+  };
+  if (!plain1(a) || !plain1(c) || a.kind != CK_BN_SILU || c.kind != CK_PLAIN) return false;
+  if (a.out_idx >= 0 || a.y.buf < 0 || c.out_idx < 0 || c.sp < 1 || c.sc < 1) return false;
+  if (c.x.buf != a.y.buf || c.x.c_off != a.y.c_off || c.x.c != a.y.c) return false;
+  if (pwpair_check(VRS_BF16, VRS_ACT_SILU, VRS_ACT_NONE, a.cin, a.cout, c.cout) != VRS_OK) {
+    (void)vrs_last_error();
+    return false;
+  }
+  const int bb = a.y.buf;
+  for (size_t k = 0; k < m->convs.size(); ++k) {
+    const ConvStep& o = m->convs[k];
+    if (k != i && (o.x.buf == bb || (o.has_res && o.res.buf == bb) || (o.has_up && o.up.buf == bb))) return false;
+    if (k != i - 1 && o.y.buf == bb) return false;
+  }
+  for (const Step& st : m->steps)
+    if (st.type != Step::CONV && (st.a.buf == bb || st.b.buf == bb)) return false;
+  return true;
+}
+
+// conv i runs as the second conv of a pointwise pair in this forward
+bool pwpair_fused(const vrs_model* m, size_t i) {
+  return !m->calib_mode && i < m->convs.size() && m->convs[i].tile == VRS_TILE_PWPAIR;
+}
+
+// the launch of a pointwise pair ending at conv i, into outs[c.out_idx]
+int prep_pwpair_step(const vrs_model* m, size_t i, float* const* outs, std::vector<Launch>& ls) {
+  const ConvStep& a = m->convs[i - 1];
+  const ConvStep& c = m->convs[i];
+  return prep_pwpair(m->ctx, view_of(m, a.x), a.w, a.scale, a.shift, a.cout, c.w, c.scale, c.shift, c.cout,
+                     outs[c.out_idx] + c.out_off, c.sb, c.sp, c.sc, ls);
+}
+
 // fp8 conv c: e4m3 input / output / residual flags and steps from the
 // buffers' storage plan (steps of 1 before calibration: timing only).
 void e4m3_flags(const vrs_model* m, const ConvStep& c, ConvSpec& cs) {
@@ -792,6 +835,16 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
   int rc = VRS_OK;
   auto acc = [](V v) { return Access{v.buf, v.c_off, v.c_off + v.c}; };
   constexpr int kAll = 1 << 30;
+  // a flat output conv writes [off, off + extent) of every batch row of its
+  // output (the Detect scales' slices are disjoint); the whole output when
+  // that range could reach the next row
+  auto flat_acc = [&](const ConvStep& c) {
+    const Buf& xb = m->bufs[c.x.buf];
+    const int64_t ho = (xb.h + 2 * (c.k / 2) - c.k) / c.s + 1, wo = (xb.w + 2 * (c.k / 2) - c.k) / c.s + 1;
+    const int64_t end = c.out_off + (ho * wo - 1) * c.sp + (int64_t)(c.cout - 1) * c.sc + 1;
+    if (c.out_off < 0 || c.sp < 1 || c.sc < 1 || end > c.sb || end >= kAll) return Access{kResOut - c.out_idx, 0, kAll};
+    return Access{kResOut - c.out_idx, (int)c.out_off, (int)end};
+  };
   for (const Step& st : m->steps) {
     const size_t before = ls.size();
     std::string label;
@@ -811,10 +864,10 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
           sio.wr = {acc(c.y)};
           break;
         }
-        sio.rd = {acc(c.x)};
+        sio.rd = {acc(pwpair_fused(m, st.conv) ? m->convs[st.conv - 1].x : c.x)};
         if (c.has_res) sio.rd.push_back(acc(c.res));
         if (c.has_up) sio.rd.push_back(acc(c.up));
-        if (c.out_idx >= 0) sio.wr = {{kResOut - c.out_idx, 0, kAll}};
+        if (c.out_idx >= 0) sio.wr = {flat_acc(c)};
         else sio.wr = {acc(c.y)};
         break;
       }
@@ -840,10 +893,16 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
           label = c.pre;
           break;
         }
-        if (bpair_fused(m, st.conv + 1)) continue;   // computed inside the next conv's launch
+        if (bpair_fused(m, st.conv + 1) || pwpair_fused(m, st.conv + 1)) continue;   // inside the next conv's launch
         if (bpair_fused(m, st.conv)) {
           conv_launch[st.conv] = (int)ls.size();
           rc = prep_bpair_step(m, st.conv, ls);
+          label = c.pre;
+          break;
+        }
+        if (pwpair_fused(m, st.conv)) {
+          conv_launch[st.conv] = (int)ls.size();
+          rc = prep_pwpair_step(m, st.conv, o.data(), ls);
           label = c.pre;
           break;
         }
@@ -852,7 +911,7 @@ int prepare(vrs_model* m, const float* x, float* const* outs) {
         cs.groups = c.groups;
         cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
         cs.cin_real = c.cin_real != c.cin ? c.cin_real : 0;
-        cs.tile = c.tile == VRS_TILE_STEM_PAIR ? VRS_TILE_AUTO : c.tile;   // unfused: fp8 calibration
+        cs.tile = c.tile == VRS_TILE_STEM_PAIR || c.tile == VRS_TILE_PWPAIR ? VRS_TILE_AUTO : c.tile;   // unfused
         vrs_nhwc upv;
         if (c.has_up) {
           upv = view_of(m, c.up);
@@ -1109,6 +1168,18 @@ int autotune_tiles(vrs_model* m) {
        (void)vrs_last_error();
      }
    }
+   // a pointwise pair (this Detect class output conv fused with the 1x1 conv
+   // before it) against the two on their own fastest tiles
+   if (pwpair_eligible(m, ci) && best_of[0] < 1e29f && best_bf16[ci - 1] < 1e29f && outs[c.out_idx]) {
+     std::vector<Launch> lp;
+     if (prep_pwpair_step(m, ci, outs.data(), lp) == VRS_OK) {
+       float tp;
+       if ((rc = timed(lp, tp))) break;
+       if (tp < 0.98f * (best_of[0] + best_bf16[ci - 1])) c.tile = VRS_TILE_PWPAIR;
+     } else {
+       (void)vrs_last_error();
+     }
+   }
    // fp8 models: a layer whose bf16 tile is faster by 2% stays on bf16
    // (unless fp8 is forced; then only the conv fused into a stem pair does)
    if (c.f8) c.run_f8 = forced ? c.tile != VRS_TILE_STEM_PAIR : !(best_of[0] < 0.98f * best_of[1]);
@@ -1273,6 +1344,11 @@ int apply_plan(vrs_model* m) {
                   "bottleneck in the shapes vrs_conv_bottleneck_pair is built for, reading the first conv's output "
                   "alone, whose first conv is not itself fused as a second conv",
                   i, c.pre.c_str());
+    if (tile == VRS_TILE_PWPAIR && (f8 || !pwpair_eligible(m, i)))
+      return fail(VRS_EINVAL,
+                  "plan entry %zu (%s): the pointwise pair applies only to a bf16 Detect class output conv in the "
+                  "shapes vrs_conv_pointwise_pair is built for, reading the 1x1 conv before it alone",
+                  i, c.pre.c_str());
     if (c.f8) {
       c.run_f8 = f8;
       if (f8) c.tile8 = tile;
@@ -1294,16 +1370,22 @@ int apply_plan(vrs_model* m) {
                                                                  vrs_last_error());
       continue;
     }
+    // a Detect output conv is prepared against a stand-in output address
+    // (16-byte aligned, as every output tensor the model is given must be):
+    // preparing only builds the launch arguments, nothing is launched
+    std::vector<float*> probe(m->out_dims.size(), reinterpret_cast<float*>(uintptr_t{1} << 20));
+    if (tile == VRS_TILE_PWPAIR) {
+      std::vector<Launch> ls;
+      if (const int rc = prep_pwpair_step(m, i, probe.data(), ls))
+        return fail(rc, "plan entry %zu (%s): %s", i, c.pre.c_str(), vrs_last_error());
+      continue;
+    }
     ConvSpec cs;   // validate by preparing the launch
     cs.k = c.k; cs.stride = c.s; cs.dtype = f8 ? VRS_FP8 : act_dt(m);
     cs.act = c.kind == CK_BN_SILU ? VRS_ACT_SILU : VRS_ACT_NONE;
     cs.in_scale = 1.f;
     cs.tile = tile;
     if (f8) e4m3_flags(m, c, cs);
-    // a Detect output conv is prepared against a stand-in output address
-    // (16-byte aligned, as every output tensor the model is given must be):
-    // preparing only builds the launch arguments, nothing is launched
-    std::vector<float*> probe(m->out_dims.size(), reinterpret_cast<float*>(uintptr_t{1} << 20));
     std::vector<Launch> ls;
     const int rc = prep_conv_step(m, c, cs, f8 ? c.w8 : c.w, f8 ? c.scale8 : c.scale, probe.data(), ls);
     if (rc) return fail(rc, "plan entry %zu (%s): %s", i, c.pre.c_str(), vrs_last_error());
@@ -1453,10 +1535,13 @@ int vrs_model_finalize(vrs_model* m) {
   // largest activation: 839 MB for YOLO26m at batch 64, 640x640).  Release
   // it, unless the model is fp8, whose calibration forward runs the stem on
   // its own.
-  // The middle map of a fused bottleneck pair is never written either.
+  // The middle map of a fused bottleneck or pointwise pair is never written
+  // either.
   if (m->dtype != VRS_FP8)
     for (size_t i = 1; i < m->convs.size(); ++i) {
-      if (!(m->convs[i].tile == VRS_TILE_STEM_PAIR && pair_eligible(m, i)) && !bpair_fused(m, i)) continue;
+      if (!(m->convs[i].tile == VRS_TILE_STEM_PAIR && pair_eligible(m, i)) && !bpair_fused(m, i) &&
+          !pwpair_fused(m, i))
+        continue;
       Buf& b = m->bufs[m->convs[i - 1].y.buf];
       auto it = std::find(m->allocs.begin(), m->allocs.end(), b.dev);
       if (b.dev && it != m->allocs.end()) {
@@ -1800,7 +1885,9 @@ int vrs_model_conv_io(const vrs_model* m, int32_t i, vrs_conv_io* io) {
   // after it reads the model input (stem = 2)
   // a bottleneck pair: the first conv has no launch and no output; the second
   // reads the first conv's input through it (fused_in, no x)
-  const bool bp_out = bpair_fused(m, i + 1), bp_in = bpair_fused(m, i);
+  // a pointwise pair likewise (the second conv writes a Detect output)
+  const bool bp_out = bpair_fused(m, i + 1) || pwpair_fused(m, i + 1);
+  const bool bp_in = bpair_fused(m, i) || pwpair_fused(m, i);
   const bool fused_out = (c.stem && pair_fused(m, i + 1)) || bp_out, fused_in = pair_fused(m, i);
   io->stem = fused_in ? 2 : c.stem;
   io->fused_in = fused_in || bp_in ? 1 : 0;

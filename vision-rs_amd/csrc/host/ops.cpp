@@ -196,6 +196,23 @@ int vrs_conv_bottleneck_pair(vrs_ctx* ctx, const vrs_conv_desc* d1, const vrs_co
   return rc ? rc : run_all(ls, stream);
 }
 
+int vrs_conv_pointwise_pair(vrs_ctx* ctx, const vrs_conv_desc* d1, const vrs_conv_desc* d2, const vrs_nhwc* x,
+                            const void* w1, const float* scale1, const float* shift1, int32_t c_mid, const void* w2,
+                            const float* scale2, const float* shift2, int32_t nc, float* y, int64_t sb, int64_t sp,
+                            int64_t sc, void* stream) {
+  if (!ctx || !d1 || !d2 || !x || !y) return fail(VRS_EINVAL, "vrs_conv_pointwise_pair: null argument");
+  if (d1->k != 1 || d1->stride != 1 || d1->groups != 1 || d2->k != 1 || d2->stride != 1 || d2->groups != 1)
+    return fail(VRS_EUNSUPPORTED, "vrs_conv_pointwise_pair: two 1x1 stride-1 dense convs only");
+  if (d1->dtype != d2->dtype) return fail(VRS_EINVAL, "vrs_conv_pointwise_pair: the two convs' dtypes differ");
+  if (d1->x_e4m3 || d1->y_e4m3 || d1->res_e4m3 || d2->x_e4m3 || d2->y_e4m3 || d2->res_e4m3)
+    return fail(VRS_EINVAL, "vrs_conv_pointwise_pair: e4m3 activations need the fp8 convs");
+  int rc = pwpair_check(d1->dtype, d1->act, d2->act, x->c, c_mid, nc);
+  if (rc) return rc;
+  std::vector<Launch> ls;
+  rc = prep_pwpair(ctx, *x, w1, scale1, shift1, c_mid, w2, scale2, shift2, nc, y, sb, sp, sc, ls);
+  return rc ? rc : run_all(ls, stream);
+}
+
 int vrs_bn_fold(const float* gamma, const float* beta, const float* mean, const float* var, float eps, int32_t c,
                 float* scale, float* shift) {
   if (!gamma || !beta || !mean || !var || !scale || !shift || c <= 0) return fail(VRS_EINVAL, "vrs_bn_fold: bad args");

@@ -973,6 +973,47 @@ int prep_bpair(vrs_ctx* ctx, const vrs_nhwc& x, const void* w1, const float* s1,
   return VRS_OK;
 }
 
+// Pointwise pair (pwpair.hip): the shapes it is built for.
+int pwpair_check(int dtype, int act1, int act2, int cin, int cm, int nc) {
+  if (dtype != VRS_BF16) return fail(VRS_EUNSUPPORTED, "pointwise pair: bf16 only");
+  if (act1 != VRS_ACT_SILU || act2 != VRS_ACT_NONE)
+    return fail(VRS_EUNSUPPORTED, "pointwise pair: BN + SiLU on the first conv, none on the second");
+  if (cin != 256 || cm != 256 || nc < 1 || nc > 96)
+    return fail(VRS_EUNSUPPORTED, "pointwise pair: built for 256 -> 256 -> (1..96) channels (got %d -> %d -> %d)",
+                cin, cm, nc);
+  return VRS_OK;
+}
+
+int prep_pwpair(vrs_ctx* ctx, const vrs_nhwc& x, const void* w1, const float* s1, const float* b1, int cm,
+                const void* w2, const float* s2, const float* b2, int nc, float* y, int64_t sb, int64_t sp,
+                int64_t sc, std::vector<Launch>& ls) {
+  int rc;
+  if ((rc = pwpair_check(VRS_BF16, VRS_ACT_SILU, VRS_ACT_NONE, x.c, cm, nc))) return rc;
+  if (!w1 || !s1 || !b1 || !w2 || !s2 || !b2 || !y) return fail(VRS_EINVAL, "pointwise pair: null pointer");
+  if ((rc = check_view(x, "pointwise pair input", 8))) return rc;
+  const int64_t M = (int64_t)x.n * x.h * x.w, hw = (int64_t)x.h * x.w;
+  const int64_t xb = (M * x.pitch - x.c_off) * 2;
+  if (sb < 0 || sp < 1 || sc < 1) return fail(VRS_EBADSHAPE, "pointwise pair: output strides must be positive");
+  const int64_t last = (x.n - 1) * sb + (hw - 1) * sp + (int64_t)(nc - 1) * sc + 1;
+  if (M >= (1ll << 31) || xb >= (1ll << 31) || last * 4 >= (1ll << 31))
+    return fail(VRS_EBADSHAPE, "pointwise pair: input and output must be under 2 GiB (32-bit buffer offsets)");
+  vrs_pwpair_args a{};
+  a.x = at(x, VRS_BF16);
+  a.w1 = w1; a.s1 = s1; a.b1 = b1;
+  a.w2 = w2; a.s2 = s2; a.b2 = b2;
+  a.y = y;
+  a.y_sb = sb; a.y_sp = sp; a.y_sc = sc;
+  a.M = (int32_t)M; a.HW = (int32_t)hw; a.NC = nc;
+  a.x_pitch = x.pitch; a.x_bytes = (int32_t)xb; a.y_bytes = (int32_t)(last * 4);
+  const char* name = "vrs_pwpair_bf16_c256_m256";
+  hipFunction_t f;
+  if ((rc = get_fn(ctx, name, &f))) return rc;
+  ls.push_back(make_launch(name, f, dim3((unsigned)((M + 63) / 64)), dim3(256), 0, a));
+  ls.back().flops = 2.0 * M * ((double)x.c * cm + (double)cm * nc);
+  ls.back().bytes = M * x.c * 2.0 + M * nc * 4.0 + ((double)cm * x.c + (double)nc * cm) * 2.0 + 8.0 * (cm + nc);
+  return VRS_OK;
+}
+
 }  // namespace vrs
 
 using namespace vrs;

@@ -125,6 +125,12 @@ int prep_stem_pair(vrs_ctx* ctx, const float* x, int n, int h, int w, const void
 // x the block input (C channels), w1 [ch][3][3][C], w2 [C][3][3][ch], res
 // optional, y (C channels); bpair_check: the channel counts built
 int bpair_check(int dtype, int act1, int act2, int cin, int ch, int cout);
+// Pointwise pair (pwpair.hip): 1x1 BN+SiLU conv cin -> cm, then a plain 1x1
+// cm -> nc into a float32 flat output y[b*sb + p*sp + c*sc].
+int pwpair_check(int dtype, int act1, int act2, int cin, int cm, int nc);
+int prep_pwpair(vrs_ctx* ctx, const vrs_nhwc& x, const void* w1, const float* s1, const float* b1, int cm,
+                const void* w2, const float* s2, const float* b2, int nc, float* y, int64_t sb, int64_t sp,
+                int64_t sc, std::vector<Launch>& ls);
 int prep_bpair(vrs_ctx* ctx, const vrs_nhwc& x, const void* w1, const float* s1, const float* b1, int ch,
                const void* w2, const float* s2, const float* b2, const vrs_nhwc* res, const vrs_nhwc& y,
                std::vector<Launch>& ls);

@@ -98,6 +98,22 @@ typedef struct {
   int32_t x_bytes, y_bytes, res_bytes, w1_bytes, w2_bytes;
 } vrs_bpair_args;
 
+/* Fused pointwise pair (pwpair.hip): 1x1 C -> CM (+BN, SiLU, bf16) then 1x1
+ * CM -> NC (+scale, shift) into a float32 flat output y[b*sb + p*sp + c*sc]. */
+typedef struct {
+  const void* x;     /* bf16 NHWC view, first channel of pixel 0 */
+  const void* w1;    /* [CM][C] bf16 */
+  const float* s1;
+  const float* b1;
+  const void* w2;    /* [NC][CM] bf16 */
+  const float* s2;
+  const float* b2;
+  float* y;
+  int64_t y_sb, y_sp, y_sc;
+  int32_t M, HW, NC;  /* pixels (N*H*W), pixels per image, output channels */
+  int32_t x_pitch, x_bytes, y_bytes;
+} vrs_pwpair_args;
+
 /* Depthwise 3x3 conv (groups == C), NHWC, weights tap-major [9][C] in the
  * element type. */
 typedef struct {

@@ -39,6 +39,7 @@ TILE_W1_128 = 9
 TILE_64x64 = 10   # bf16: small maps (four times the workgroups of 128x128)
 TILE_STEM_PAIR = 11   # model plans: the conv after a 64-channel stem, fused with it (bf16)
 TILE_BPAIR = 12   # model plans: a bottleneck's second 3x3 conv, fused with the first (bf16)
+TILE_PWPAIR = 13   # model plans: a Detect class output conv fused with the 1x1 conv before it (bf16)
 
 ERRORS = {-1: "EINVAL", -2: "EBADSHAPE", -3: "EUNSUPPORTED", -4: "ENOMODULE", -5: "EHIP", -6: "ENOTFOUND",
           -7: "ESTATE"}
@@ -114,6 +115,8 @@ SIGNATURES = {
                                      _vp, _vp, _vp, _P(Nhwc), _vp]),
     "vrs_conv_bottleneck_pair": (C.c_int, [_vp, _P(ConvDesc), _P(ConvDesc), _P(Nhwc), _vp, _vp, _vp, _i32, _vp, _vp,
                                            _vp, _P(Nhwc), _P(Nhwc), _vp]),
+    "vrs_conv_pointwise_pair": (C.c_int, [_vp, _P(ConvDesc), _P(ConvDesc), _P(Nhwc), _vp, _vp, _vp, _i32, _vp, _vp,
+                                          _vp, _i32, _vp, C.c_int64, C.c_int64, C.c_int64, _vp]),
     "vrs_bn_fold": (C.c_int, [_vp, _vp, _vp, _vp, _f32, _i32, _vp, _vp]),
     "vrs_pack_input": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _P(Nhwc), _i32, _vp]),
     "vrs_unpack_output": (C.c_int, [_vp, _P(Nhwc), _i32, _vp, _vp]),
@@ -289,6 +292,16 @@ class Context:
                                              _ptr(scale1), _ptr(shift1), c_hidden, _ptr(w2), _ptr(scale2),
                                              _ptr(shift2), C.byref(res) if res is not None else None, C.byref(y),
                                              _stream(stream)))
+
+    def conv_pointwise_pair(self, x, w1, scale1, shift1, c_mid, w2, scale2, shift2, nc, y, sb, sp, sc, stream=None):
+        """A Detect class branch's last 1x1 conv (BN + SiLU) and its 1x1 conv_plain in one kernel:
+        x an Nhwc view; w1 / w2 from pack_conv_weight ([c_mid][c], [nc][c_mid]); y a float32 device
+        tensor written at y[b*sb + p*sp + co*sc]."""
+        d1 = ConvDesc(1, 1, 1, ACT_SILU, BF16, TILE_AUTO, 1.0, 0, 0, 0, 0.0, 0.0)
+        d2 = ConvDesc(1, 1, 1, ACT_NONE, BF16, TILE_AUTO, 1.0, 0, 0, 0, 0.0, 0.0)
+        check(lib().vrs_conv_pointwise_pair(self.handle, C.byref(d1), C.byref(d2), C.byref(x), _ptr(w1),
+                                            _ptr(scale1), _ptr(shift1), c_mid, _ptr(w2), _ptr(scale2),
+                                            _ptr(shift2), nc, _ptr(y), sb, sp, sc, _stream(stream)))
 
     def pack_input(self, x_nchw, y, dtype, stream=None):
         n, c, h, w = x_nchw.shape
