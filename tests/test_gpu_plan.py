@@ -344,14 +344,15 @@ def test_pointwise_pair_plan():
     """VRS_TILE_PWPAIR on the three Detect class output convs
     (model.23.one2one_cv3.{0,1,2}.2): one launch each replaces the 1x1
     256 -> 256 conv before it and the 256 -> 80 logits conv, bit-identical
-    to the two launches (the same K order and rounding) at batch 2, where
-    the 64-pixel tiles of the 12x12 and 6x6 maps cross image boundaries;
-    conv_io reports the first conv as launch-less and without output, the
-    second as fused_in without input.  The entry is refused on the box
-    output convs (a 3x3 before them) and on YOLO26n (64 -> 80 class
-    channels)."""
+    to the two launches (the same K order and rounding) at batch 32, 320x320:
+    the P3 pair (800 tiles) on the weight-stationary persistent kernel, P4
+    and P5 on the one-group-per-tile kernel, whose 64-pixel tiles of the
+    20x20 and 10x10 maps cross image boundaries; conv_io reports the first
+    conv as launch-less and without output, the second as fused_in without
+    input.  The entry is refused on the box output convs (a 3x3 before them)
+    and on YOLO26n (64 -> 80 class channels)."""
     import torch
-    B, S = 2, 192
+    B, S = 32, 320
     names = [pre for pre, _, _ in _yolo(B, S, vrs.BF16, autotune=False).conv_info()]
     pairs = [(names.index(f"model.23.one2one_cv3.{i}.1.1"), names.index(f"model.23.one2one_cv3.{i}.2"))
              for i in range(3)]
@@ -373,7 +374,8 @@ def test_pointwise_pair_plan():
                 assert m.get_plan()[i2] == vrs.TILE_PWPAIR
                 assert io1.launch == -1 and io1.y.data is None and io1.x.data is not None
                 assert io2.fused_in == 1 and io2.x.data is None and io2.out_idx == 1
-                assert launches[io2.launch] == f"{names[i2]}:vrs_pwpair_bf16_c256_m256"
+                kern = "vrs_pwpair_w_bf16_c256_m256" if i2 == pairs[0][1] else "vrs_pwpair_bf16_c256_m256"
+                assert launches[io2.launch] == f"{names[i2]}:{kern}"
                 assert not any(l.startswith(names[i1] + ":") for l in launches)
             else:
                 assert io1.launch >= 0 and io2.fused_in == 0
