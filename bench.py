@@ -352,7 +352,8 @@ def layers_summary(path, key="layer"):
         ideal += max(fl / (peak_tflops * 1e12), mb / (PEAK_HBM_GBS * 1e9)) * 1e6
         out.append(f"| {lab} | {sym} | {us:.1f} | {r['gflop']:.2f} | {r['mb']:.1f} | {bound} | {ach} | {frac:.3f} |")
     out += ["", f"{len(rows)} launches, {tot:.0f} us in sum (eager, one launch at a time; the hipGraph replay runs "
-                f"the same launches in order on one hardware queue); at the MI355X peaks the same work needs "
+                f"the same launches, the Detect head's chains as parallel branches beside the trunk); at the MI355X "
+                f"peaks the same work needs "
                 f"{ideal:.0f} us."]
     return "\n".join(out)
 
