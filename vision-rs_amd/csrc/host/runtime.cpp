@@ -1006,15 +1006,15 @@ int prep_pwpair(vrs_ctx* ctx, const vrs_nhwc& x, const void* w1, const float* s1
   a.M = (int32_t)M; a.HW = (int32_t)hw; a.NC = nc;
   a.x_pitch = x.pitch; a.x_bytes = (int32_t)xb; a.y_bytes = (int32_t)(last * 4);
   // maps of at least two tiles per CU: the weight-stationary persistent
-  // kernel (one group per CU, W1 in registers); smaller ones: one group per
-  // 64-pixel tile, two per CU (measured at YOLO26m bs64: 80x80 137 vs 224 us,
-  // 40x40 44 vs 57 us, 20x20 18.7 vs 17.5 us)
+  // kernel (one 8-wave group per CU, W1 and W2 in registers); smaller ones:
+  // one 4-wave group per 64-pixel tile, two per CU (measured at YOLO26m
+  // bs64: 80x80 104 vs 224 us, 40x40 34 vs 57 us)
   const int64_t tiles = (M + 63) / 64;
   const bool ws = tiles >= 2ll * ctx->num_cu;
   const char* name = ws ? "vrs_pwpair_w_bf16_c256_m256" : "vrs_pwpair_bf16_c256_m256";
   hipFunction_t f;
   if ((rc = get_fn(ctx, name, &f))) return rc;
-  ls.push_back(make_launch(name, f, dim3((unsigned)(ws ? ctx->num_cu : tiles)), dim3(256), 0, a));
+  ls.push_back(make_launch(name, f, dim3((unsigned)(ws ? ctx->num_cu : tiles)), dim3(ws ? 512 : 256), 0, a));
   ls.back().flops = 2.0 * M * ((double)x.c * cm + (double)cm * nc);
   ls.back().bytes = M * x.c * 2.0 + M * nc * 4.0 + ((double)cm * x.c + (double)nc * cm) * 2.0 + 8.0 * (cm + nc);
   return VRS_OK;

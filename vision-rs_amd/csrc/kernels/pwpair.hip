@@ -181,75 +181,77 @@ __device__ __forceinline__ void pwpair_body(const vrs_pwpair_args& a) {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// Weight-stationary persistent form (maps of many tiles): one workgroup per
-// CU loops over the tiles t = blockIdx.x + i * gridDim.x.  W1 stays in
-// registers for the whole run (wave w: rows 64w..64w+63, all 256 k -- the
-// A fragments), W2 (rows past NC zero) and the constants in LDS; each tile's
-// 64 pixel rows are staged one tile ahead by direct-to-LDS buffer loads
-// (LDS address M0 + 16 * lane, out-of-range offsets fill zeros), chunk c of
-// pixel p at slot 32p + (c ^ (p & 31)) so that the B fragment reads of 32
-// consecutive pixels hit distinct banks.  These loads are issued by inline
-// assembly, which the compiler does not count: the waits for them are
-// explicit (vmcnt before the stores, which are the only other vector memory
-// operations in the loop), and the barriers are bare s_barriers, since the
-// fence of __syncthreads would wait for the loads of the next tile too.
-// Two barriers per tile: after the GEMM 1 epilogue (m complete) and after
-// the stores (m read, the next tile staged).
+// Weight-stationary persistent form (maps of many tiles): one workgroup of
+// 8 waves per CU loops over the tiles t = blockIdx.x + i * gridDim.x.  W1
+// stays in registers for the whole run (wave w: rows 32w..32w+31, all 256 k
+// -- its A fragments, 64 VGPRs), as do the W2 fragments of the six waves
+// that run the second GEMM (output channel block w % 3 of the 32-pixel half
+// w / 3; rows past NC read zero), two waves per SIMD so that one's epilogue
+// runs under the other's MFMAs.  Each tile's 64 pixel rows are staged one
+// tile ahead by direct-to-LDS buffer loads (LDS address M0 + 16 * lane,
+// out-of-range offsets fill zeros), chunk c of pixel p at slot 32p + (c ^ (p
+// & 31)) so that the B fragment reads of 32 consecutive pixels hit distinct
+// banks.  These loads are issued by inline assembly, which the compiler does
+// not count: the waits for them are explicit (vmcnt before the stores, the
+// only other vector memory operations in the loop), and the barriers are
+// bare s_barriers, since the fence of __syncthreads would wait for the loads
+// of the next tile too.  Two barriers per tile: after the GEMM 1 epilogue (m
+// complete) and after the stores (m read, the next tile staged).
 template <int C, int CM>
 __device__ __forceinline__ void pwpair_w_body(const vrs_pwpair_args& a) {
   using E = Elt<bf16_t>;
   using Gr = E::group;
-  constexpr int NP = 64, NT = 256;
+  constexpr int NP = 64, NT = 512, NW = NT / 64;
   constexpr int XB = NP * C;                 // one x tile (elements, swizzled chunks)
-  constexpr int MROW = CM + 8, WROW = CM + 8;
-  static_assert(C == 256 && CM == 256, "shape");
+  constexpr int MROW = CM + 8;
+  constexpr int NQ = NP * C / 8 / NT;        // direct-to-LDS loads per lane and tile (4)
+  static_assert(C == 256 && CM == 256 && NW * 32 == CM, "shape");
   __shared__ __attribute__((aligned(16))) bf16_t xs[2 * XB];
   __shared__ __attribute__((aligned(16))) bf16_t mid[NP * MROW];
-  __shared__ __attribute__((aligned(16))) bf16_t w2s[96 * WROW];
   __shared__ float s1s[CM], b1s[CM], s2s[96], b2s[96];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hq = lane >> 5;
   const int tiles = (a.M + NP - 1) / NP, G = gridDim.x;   // the host launches at most one group per tile
 
-  // W1 fragments: wave rows 64w + 32cb + l32, k = 16s + 8hq .. +7
-  Gr w1f[2][CM / 16];
+  // W1 fragments: wave rows 32w + l32, k = 16s + 8hq .. +7
+  Gr w1f[C / 16];
   {
     const __amdgpu_buffer_rsrc_t rw1 = make_rsrc(a.w1, CM * C * 2);
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-      for (int s = 0; s < C / 16; ++s)
-        w1f[cb][s] = E::bload(rw1, (uint32_t)(((wave * 64 + cb * 32 + l32) * C + hq * 8) * 2), (uint32_t)(s * 32));
+    for (int s = 0; s < C / 16; ++s)
+      w1f[s] = E::bload(rw1, (uint32_t)(((wave * 32 + l32) * C + hq * 8) * 2), (uint32_t)(s * 32));
   }
-  {
+  // GEMM 2 roles: waves 0-5 own output channel block cb2 = w % 3 (rows past
+  // NC read zero) of the 32-pixel half pb2 = w / 3; their W2 fragments
+  const bool g2 = wave < 6;
+  const int cb2 = wave % 3, pb2 = wave / 3;
+  Gr w2f[CM / 16];
+  if (g2) {
     const __amdgpu_buffer_rsrc_t rw2 = make_rsrc(a.w2, a.NC * CM * 2);
-    for (int i = tid; i < 96 * (CM / 8); i += NT) {   // rows past NC: zero
-      const int r = i / (CM / 8), c = i % (CM / 8);
-      E::store(w2s + r * WROW + c * 8, E::bload(rw2, (uint32_t)((r * CM + c * 8) * 2), 0));
-    }
-    for (int i = tid; i < CM; i += NT) { s1s[i] = a.s1[i]; b1s[i] = a.b1[i]; }
-    for (int i = tid; i < 96; i += NT) {
-      s2s[i] = i < a.NC ? a.s2[i] : 0.f;
-      b2s[i] = i < a.NC ? a.b2[i] : 0.f;
-    }
+#pragma unroll
+    for (int s = 0; s < CM / 16; ++s)
+      w2f[s] = E::bload(rw2, (uint32_t)(((cb2 * 32 + l32) * CM + hq * 8) * 2), (uint32_t)(s * 32));
   }
-  // direct-to-LDS staging of tile t into buffer b: wave w issues slots
-  // (8w + q) * 64 + lane, q = 0..7
+  for (int i = tid; i < CM; i += NT) { s1s[i] = a.s1[i]; b1s[i] = a.b1[i]; }
+  for (int i = tid; i < 96; i += NT) {
+    s2s[i] = i < a.NC ? a.s2[i] : 0.f;
+    b2s[i] = i < a.NC ? a.b2[i] : 0.f;
+  }
   const uint64_t xbase = (uint64_t)(uintptr_t)a.x;
-  const int i32x4r0 = __builtin_amdgcn_readfirstlane((int)(uint32_t)xbase);
-  const int i32x4r1 = __builtin_amdgcn_readfirstlane((int)(uint32_t)(xbase >> 32) & 0xffff);
+  const int base_lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)xbase);
+  const int base_hi = __builtin_amdgcn_readfirstlane((int)(uint32_t)(xbase >> 32) & 0xffff);
   const int xbytes = __builtin_amdgcn_readfirstlane(a.x_bytes);
   typedef int i4_t __attribute__((ext_vector_type(4)));
-  const i4_t rd = {i32x4r0, i32x4r1, xbytes, 0x00020000};
+  const i4_t rd = {base_lo, base_hi, xbytes, 0x00020000};
   auto stage = [&](int t, int b) {
     const int m0 = t * NP;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int slot = (wave * 8 + q) * 64 + lane;
+    for (int q = 0; q < NQ; ++q) {
+      const int slot = (wave * NQ + q) * 64 + lane;
       const int p = slot >> 5, c = (slot & 31) ^ (p & 31);
       const uint32_t off = m0 + p < a.M ? (uint32_t)(((m0 + p) * a.x_pitch + c * 8) * 2) : kOOB;
       const uint32_t la = __builtin_amdgcn_readfirstlane(
-          (uint32_t)(uintptr_t)(lds_void_t*)(xs + b * XB + (wave * 8 + q) * 64 * 8));
+          (uint32_t)(uintptr_t)(lds_void_t*)(xs + b * XB + (wave * NQ + q) * 64 * 8));
       asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" :: "s"(la), "v"(off), "s"(rd)
                    : "memory", "m0");
     }
@@ -262,83 +264,65 @@ __device__ __forceinline__ void pwpair_w_body(const vrs_pwpair_args& a) {
   for (int it = 0; t < tiles; ++it, t += G) {
     const int cur = it & 1;
     if (t + G < tiles) stage(t + G, cur ^ 1);
-    // GEMM 1 from the staged tile
     const bf16_t* xb = xs + cur * XB;
-    f32x16_t acc[2][2];
+    f32x16_t acc[2] = {};
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-      for (int pb = 0; pb < 2; ++pb) acc[cb][pb] = (f32x16_t){};
-#pragma unroll
-    for (int s = 0; s < C / 16; ++s) {
-      Gr bf[2];
+    for (int s = 0; s < C / 16; ++s)
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb) {
         const int p = pb * 32 + l32, c = 2 * s + hq;
-        bf[pb] = E::load(xb + (p * 32 + (c ^ (p & 31))) * 8);
+        acc[pb] = mfma32_k16(w1f[s], E::load(xb + (p * 32 + (c ^ (p & 31))) * 8), acc[pb]);
       }
+    // GEMM 1 epilogue -> mid: register 4g + r is channel 32w + 8g + 4hq + r
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb)
+    for (int g = 0; g < 4; ++g) {
+      const int ch = wave * 32 + g * 8 + hq * 4;
+      float sc[4], sh[4];
 #pragma unroll
-        for (int pb = 0; pb < 2; ++pb) acc[cb][pb] = mfma32_k16(w1f[cb][s], bf[pb], acc[cb][pb]);
-    }
-    // GEMM 1 epilogue -> mid
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int ch = wave * 64 + cb * 32 + g * 8 + hq * 4;
-        float sc[4], sh[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) { sc[r] = s1s[ch + r]; sh[r] = b1s[ch + r]; }
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
-          float v[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) v[r] = silu_fast(acc[cb][pb][g * 4 + r] * sc[r] + sh[r]);
-          *reinterpret_cast<u32x2_t*>(mid + (pb * 32 + l32) * MROW + ch) =
-              (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        }
-      }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (wave < 3) {
-      f32x16_t o[2] = {};
-#pragma unroll
-      for (int s = 0; s < CM / 16; ++s) {
-        const Gr af = E::load(w2s + (wave * 32 + l32) * WROW + s * 16 + hq * 8);
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb) o[pb] = mfma32_k16(af, E::load(mid + (pb * 32 + l32) * MROW + s * 16 + hq * 8), o[pb]);
-      }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the next tile's staging (and earlier stores)
+      for (int r = 0; r < 4; ++r) { sc[r] = s1s[ch + r]; sh[r] = b1s[ch + r]; }
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb) {
-        const int m = t * NP + pb * 32 + l32;
-        const bool ok = m < a.M;
-        const int b = ok ? m / a.HW : 0, p = ok ? m - b * a.HW : 0;
-        const int64_t pix = (int64_t)b * a.y_sb + (int64_t)p * a.y_sp;
+        float v[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int co = wave * 32 + g * 8 + hq * 4 + r;
-            const bool st = ok && co < a.NC;
-            const float v = o[pb][g * 4 + r] * s2s[co] + b2s[co];
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
-                                                  st ? (uint32_t)((pix + (int64_t)co * a.y_sc) * 4) : kOOB, 0, 0);
-          }
+        for (int r = 0; r < 4; ++r) v[r] = silu_fast(acc[pb][g * 4 + r] * sc[r] + sh[r]);
+        *reinterpret_cast<u32x2_t*>(mid + (pb * 32 + l32) * MROW + ch) =
+            (u32x2_t){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
       }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (g2) {
+      f32x16_t o = {};
+#pragma unroll
+      for (int s = 0; s < CM / 16; ++s)
+        o = mfma32_k16(w2f[s], E::load(mid + (pb2 * 32 + l32) * MROW + s * 16 + hq * 8), o);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the next tile's staging (and earlier stores)
+      const int m = t * NP + pb2 * 32 + l32;
+      const bool ok = m < a.M;
+      const int b = ok ? m / a.HW : 0, p = ok ? m - b * a.HW : 0;
+      const int64_t pix = (int64_t)b * a.y_sb + (int64_t)p * a.y_sp;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int co = cb2 * 32 + g * 8 + hq * 4 + r;
+          const bool st = ok && co < a.NC;
+          const float v = o[g * 4 + r] * s2s[co] + b2s[co];
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
+                                                st ? (uint32_t)((pix + (int64_t)co * a.y_sc) * 4) : kOOB, 0, 0);
+        }
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 }
+
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(256, 2) void vrs_pwpair_bf16_c256_m256(vrs_pwpair_args a) {
   pwpair_body<256, 256>(a);
 }
 
-extern "C" __global__ __launch_bounds__(256, 1) void vrs_pwpair_w_bf16_c256_m256(vrs_pwpair_args a) {
+extern "C" __global__ __launch_bounds__(512, 1) void vrs_pwpair_w_bf16_c256_m256(vrs_pwpair_args a) {
   pwpair_w_body<256, 256>(a);
 }
