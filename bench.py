@@ -18,6 +18,10 @@ Prints ONE JSON line.  Besides the contract fields it carries:
                 for one warm forward of the workload's batch (64 images at
                 640x640: about 12 s on 16 cores, inside the 10-30 s bound)
   kernels       per-kernel-symbol time / work breakdown of one forward
+  fp8_run, fp8_forced_run
+                config 5's second run (e4m3 weights and activations), each
+                with `roofline_fp8`: the fp8 kernel with the largest total
+                time, priced at the fp8 MFMA peak
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 """
@@ -864,12 +868,16 @@ def main() -> int:
 
     def fp8_summary(m8, el8, ps8, note):
         top = sorted(ps8.items(), key=lambda kv: -kv[1]["ms"])[:4]
+        # the fp8 kernel with the largest total time per forward, priced at the
+        # fp8 MFMA peak (HBM traffic: profiles/yolo26m_fp8_forced_bs64_traffic.md)
+        f8k = [kv for kv in ps8.items() if "_fp8_" in kv[0]]
+        roof8 = roofline_of(*max(f8k, key=lambda kv: kv[1]["ms"]), PEAK_FP8_TFLOPS) if f8k else None
         ios = [m8.conv_io(i) for i in range(len(m8.conv_info()))]
         return {"value": round(a.batch * a.steps / el8, 1), "unit": "images/s",
                 "ms_per_step": round(el8 * 1e3 / a.steps, 3),
                 "fp8_convs": sum(1 for _, f8, _ in m8.conv_info() if f8), "convs": len(m8.conv_info()),
                 "e4m3_inputs": sum(io.x_e4m3 for io in ios), "e4m3_outputs": sum(io.y_e4m3 for io in ios),
-                "note": note,
+                "note": note, "roofline_fp8": roof8,
                 "kernels": {s: {"launches": d["launches"], "ms": round(d["ms"], 4),
                                 "tflops": round(d["flops"] / max(d["ms"], 1e-9) / 1e9, 2)} for s, d in top}}
 
